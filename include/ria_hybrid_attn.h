@@ -1,0 +1,208 @@
+/*
+ * ria_hybrid_attn.h - C ABI of the MI355X (gfx950) hybrid-attention hot path.
+ *
+ * The library replaces the per-token arithmetic of router-ia's stateful
+ * attention cache (v2/src/router_ia/qwen36_attention_cache.py) for B
+ * sequences at once: the Gated DeltaNet conv + delta-rule recurrence, the
+ * partial-RoPE KV append and the sigmoid-gated GQA decode attention, plus
+ * chunked prefill forms of both.  The reference has no FFI for this path; the
+ * ABI style (opaque status ints, a last-error string, library path taken
+ * from an environment variable on the Python side) follows its native
+ * memory pool, native_memory/router_memory.h:11-94.
+ *
+ * Conventions shared by every entry point
+ *   - All tensor arguments are device pointers on the current HIP device.
+ *   - `stream` is a hipStream_t (NULL = default stream).  Calls are
+ *     asynchronous, never synchronise and never allocate.
+ *   - Return RIA_OK (0) on success, otherwise a RIA_ERR_* code; the message
+ *     is available from ria_last_error() on the calling thread.
+ *   - Activation dtype codes: RIA_DT_BF16, RIA_DT_F16, RIA_DT_F32.
+ *   - `seq_slot` maps batch row b to a row of the state / page-table pools;
+ *     NULL means row b.  Per-row position arrays may be NULL, in which case
+ *     the accompanying *_scalar value is used for every row.
+ *   - Sizes are fixed by the model family: DeltaNet head dim 128 (dk == dv),
+ *     conv kernel 4, full-attention head dim 256, KV pages of 16 tokens.
+ *
+ * Memory layouts
+ *   DeltaNet recurrent state  f32  [pool, Hv, 128 (dk, i), 128 (dv, j)]
+ *                              (the reference layout, :256-265)
+ *   DeltaNet conv ring        bf16 [pool, 4 (slot), conv_dim]; the input of
+ *                              step n lives in slot n mod 4.  The reference
+ *                              keeps the same four inputs as a shifting
+ *                              window [1, conv_dim, 4] (:207-209).
+ *   conv weight               bf16 [conv_dim, 4] (== [conv_dim, 1, 4])
+ *   K cache (one layer)       bf16 [num_pages, Hkv, 16 (token), 256 (dim)]
+ *   V cache (one layer)       bf16 [num_pages, Hkv, 256 (dim), 16 (token)]
+ *   page table                i32  [pool, page_table_stride]; logical token
+ *                              t of a sequence lives in physical slot
+ *                              page_table[row][t / 16] * 16 + t % 16.  The
+ *                              stride is the row's page capacity: kernels
+ *                              never read entries at or past it, and treat
+ *                              entries outside [0, num_pages) as absent.
+ */
+#ifndef RIA_HYBRID_ATTN_H
+#define RIA_HYBRID_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RIA_ABI_VERSION 1
+
+enum ria_dtype { RIA_DT_BF16 = 0, RIA_DT_F16 = 1, RIA_DT_F32 = 2 };
+
+enum ria_status {
+  RIA_OK = 0,
+  RIA_ERR_INVALID = 1,   /* bad argument (shape, dtype, null pointer) */
+  RIA_ERR_LAUNCH = 2,    /* HIP launch or runtime error */
+  RIA_ERR_WORKSPACE = 3  /* caller workspace too small */
+};
+
+enum ria_gate_mode {
+  /* gate_a holds g (log decay), gate_b holds beta; A_log/dt_bias unused. */
+  RIA_GATE_PRECOMPUTED = 0,
+  /* gate_a = a_raw, gate_b = b_raw; beta = sigmoid(b),
+   * g = -exp(A_log) * softplus(a + dt_bias)   (qwen36_attention_cache.py:242-250) */
+  RIA_GATE_RAW = 1
+};
+
+/* ABI version of the loaded library (RIA_ABI_VERSION). */
+int ria_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* ria_last_error(void);
+
+/*
+ * Gated DeltaNet decode: one token for each of `batch` sequences, one layer.
+ * Replaces qwen36_attention_cache.py:235-266 (_causal_conv1d_step, q/k/v
+ * split with the 2:1 QK->V head sharing, gating, l2norm, delta-rule update of
+ * the recurrent state and read-out from the updated state).
+ *
+ * mixed_qkv  [batch, conv_dim] of x_dtype, row stride x_row_stride elements.
+ *            fuse_conv=1: projection output before the conv (the conv, SiLU,
+ *            conv-ring update run here, in bf16 like the reference's bf16
+ *            conv weight); fuse_conv=0: already-convolved q|k|v.
+ * conv_weight, conv_ring      used only when fuse_conv=1.
+ * conv_pos   [batch] step index n of this token (ring slot n mod 4), or NULL
+ *            to use conv_pos_scalar for every row.
+ * state      recurrent state pool, updated in place.
+ * gate_a/b   [batch, Hv] f32 with row stride gate_row_stride (see gate_mode).
+ * out        [batch, Hv, 128] of out_dtype: read-out o = S_new^T q.
+ * conv_dim = 2 * num_k_heads * 128 + num_v_heads * 128.
+ */
+int ria_gdn_decode(int batch, int num_k_heads, int num_v_heads,
+                   const void* mixed_qkv, int x_dtype, int64_t x_row_stride, int fuse_conv,
+                   const void* conv_weight, void* conv_ring,
+                   const int32_t* conv_pos, int32_t conv_pos_scalar,
+                   float* state, const int32_t* seq_slot,
+                   const float* gate_a, const float* gate_b, int64_t gate_row_stride,
+                   int gate_mode, const float* A_log, const float* dt_bias,
+                   void* out, int out_dtype, void* stream);
+
+/*
+ * Depthwise causal conv1d step alone (kernel 4, SiLU), for `batch` rows of
+ * `channels` channels.  Replaces qwen36_attention_cache.py:176-221
+ * (_causal_conv1d_step): out = SiLU(sum_j w[c,j] * hist[c, j]) over the three
+ * previous inputs and the current one, computed in bf16 and cast to
+ * out_dtype; the current input is written to ring slot conv_pos mod 4.
+ */
+int ria_conv1d_step(int batch, int channels,
+                    const void* x, int x_dtype, int64_t x_row_stride,
+                    const void* conv_weight, void* conv_ring, const int32_t* seq_slot,
+                    const int32_t* conv_pos, int32_t conv_pos_scalar,
+                    void* out, int out_dtype, void* stream);
+
+/*
+ * Row-wise l2 normalisation x * rsqrt(sum(x^2) + eps) in fp32 over rows of
+ * `dim` elements.  Replaces qwen36_attention_cache.py:169-173 (_l2norm).
+ */
+int ria_l2norm(int64_t rows, int dim, const void* x, int x_dtype, float eps,
+               float* out, void* stream);
+
+/*
+ * RoPE tables for one position: cos/sin of position * inv_freq duplicated
+ * over both halves, `rope_dim` fp32 values each.  inv_freq holds rope_dim/2
+ * fp32 frequencies.  Replaces qwen36_attention_cache.py:137-146 (_rope).
+ */
+int ria_rope_table(int32_t position, const float* inv_freq, int rope_dim,
+                   float* cos_out, float* sin_out, void* stream);
+
+/*
+ * Partial half-split (NeoX) rotary embedding on rows of `head_dim` fp32
+ * values: dims [0, rope_dim) rotate, the rest pass through.  One position
+ * for all rows.  Replaces qwen36_attention_cache.py:149-162 (_apply_rope).
+ */
+int ria_rope_apply(int64_t rows, int head_dim, int rope_dim, const float* x,
+                   float* out, const float* inv_freq, int32_t position, void* stream);
+
+/*
+ * Append one token per sequence into a layer's paged bf16 KV cache, with
+ * partial RoPE applied to k.  Replaces qwen36_attention_cache.py:306-308
+ * (_apply_rope on k + _append_full_kv's torch.cat).  Capacity limits are host
+ * policy and are checked by the caller before this call.
+ *
+ * k, v       [batch, Hkv, 256] of k_dtype / v_dtype (row stride in elements).
+ * positions  RoPE position of the token (tokens_seen), per row or scalar.
+ * slots      logical index of the token in its sequence (tokens resident
+ *            before the append), per row or scalar.
+ */
+int ria_kv_append(int batch, int num_kv_heads,
+                  const void* k, int k_dtype, int64_t k_row_stride,
+                  const void* v, int v_dtype, int64_t v_row_stride,
+                  void* k_cache, void* v_cache, int num_pages,
+                  const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                  const int32_t* positions, int32_t position_scalar,
+                  const int32_t* slots, int32_t slot_scalar,
+                  const float* inv_freq, int rope_dim, void* stream);
+
+/*
+ * Workspace bytes ria_attn_decode needs for these sizes (split_tokens = 0
+ * selects the automatic split size, as in ria_attn_decode).
+ */
+int64_t ria_attn_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads,
+                                        int max_ctx, int split_tokens);
+
+/*
+ * Split-K GQA decode attention over a paged bf16 KV cache with partial RoPE
+ * on q and a sigmoid output gate.  Replaces qwen36_attention_cache.py:306,
+ * 309-317: q is rotated at `positions`, scores = q K^T * scale over the
+ * ctx_lens tokens of each sequence (the just-appended token included), fp32
+ * softmax, P V, then attn * sigmoid(gate) elementwise per (head, dim).
+ * Query head h reads KV head h / (num_q_heads / num_kv_heads); at most 8
+ * query heads per KV head; rope_dim is 0 or 64.
+ *
+ * q, gate    [batch, Hq, 256] of q_dtype / gate_dtype (row stride in elements).
+ * ctx_lens   tokens attended per row (or scalar); max_ctx bounds them.
+ * split_tokens  tokens per split (multiple of 64) or 0 for automatic.
+ * workspace  caller buffer of ria_attn_decode_workspace_bytes() bytes.
+ * out        [batch, Hq, 256] of out_dtype.
+ */
+int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads,
+                    const void* q, int q_dtype, int64_t q_row_stride,
+                    const void* gate, int gate_dtype, int64_t gate_row_stride,
+                    const void* k_cache, const void* v_cache, int num_pages,
+                    const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                    const int32_t* positions, int32_t position_scalar,
+                    const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
+                    const float* inv_freq, int rope_dim, float scale, int split_tokens,
+                    void* workspace, int64_t workspace_bytes,
+                    void* out, int out_dtype, void* stream);
+
+/*
+ * Copy tokens [start, start + count) of each sequence out of the paged cache
+ * into logical order: k_out, v_out bf16 [batch, Hkv, count, 256].  The
+ * inverse of the append's slot mapping; used to materialise the reference's
+ * contiguous full_keys / full_values view (qwen36_attention_cache.py:365-372).
+ */
+int ria_kv_gather(int batch, int num_kv_heads,
+                  const void* k_cache, const void* v_cache, int num_pages,
+                  const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                  int32_t start, int32_t count, void* k_out, void* v_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RIA_HYBRID_ATTN_H */

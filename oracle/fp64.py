@@ -1,0 +1,89 @@
+"""Float64 brute-force forms of the hot-path math, written from the equations.
+
+TEST INFRASTRUCTURE ONLY (see oracle/qwen36_cpu.py).  These loops share no
+code with qwen36_cpu.py: they are the independent check that pins it.  Each
+function states the equation it evaluates; sizes are kept small by the tests.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def rope_tables(position: int, rope_dim: int = 64, theta: float = 1e7) -> tuple[np.ndarray, np.ndarray]:
+    """cos/sin of position * theta^(-2i/d), i < d/2, duplicated over both halves."""
+    half = rope_dim // 2
+    ang = np.array([position * theta ** (-(2.0 * i) / rope_dim) for i in range(half)], dtype=np.float64)
+    ang = np.concatenate([ang, ang])
+    return np.cos(ang), np.sin(ang)
+
+
+def apply_rope(x: np.ndarray, position: int, rope_dim: int = 64, theta: float = 1e7) -> np.ndarray:
+    """Rotate pairs (i, i + d/2) of the first rope_dim dims by angle position*theta^(-2i/d)."""
+    x = np.asarray(x, dtype=np.float64)
+    out = x.copy()
+    half = rope_dim // 2
+    for i in range(half):
+        a = position * theta ** (-(2.0 * i) / rope_dim)
+        c, s = math.cos(a), math.sin(a)
+        x1, x2 = x[..., i], x[..., i + half]
+        out[..., i] = x1 * c - x2 * s
+        out[..., i + half] = x2 * c + x1 * s
+    return out
+
+
+def l2norm(x: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float64)
+    return x / np.sqrt((x * x).sum(axis=-1, keepdims=True) + eps)
+
+
+def conv_step(prev3: np.ndarray, x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """SiLU(w[c,0] x_{t-3} + w[c,1] x_{t-2} + w[c,2] x_{t-1} + w[c,3] x_t) per channel.
+
+    prev3 [C, 3] holds x_{t-3}, x_{t-2}, x_{t-1}; x [C]; w [C, 4].
+    """
+    acc = np.zeros(x.shape[0], dtype=np.float64)
+    for c in range(x.shape[0]):
+        hist = [prev3[c, 0], prev3[c, 1], prev3[c, 2], x[c]]
+        acc[c] = sum(float(w[c, j]) * float(hist[j]) for j in range(4))
+    return acc / (1.0 + np.exp(-acc))
+
+
+def delta_step(S: np.ndarray, q: np.ndarray, k: np.ndarray, v: np.ndarray, beta: float, g: float):
+    """One gated delta-rule step for one head, element by element.
+
+    S [dk, dv]; q, k already normalised (q scaled).  Returns (o [dv], S_new).
+        S' = exp(g) S ; r_j = sum_i S'[i,j] k_i ; d_j = beta (v_j - r_j)
+        S_new[i,j] = S'[i,j] + k_i d_j ; o_j = sum_i S_new[i,j] q_i
+    """
+    dk, dv = S.shape
+    Sp = np.exp(g) * S.astype(np.float64)
+    r = np.zeros(dv)
+    for j in range(dv):
+        for i in range(dk):
+            r[j] += Sp[i, j] * k[i]
+    d = beta * (v - r)
+    Sn = Sp.copy()
+    for i in range(dk):
+        for j in range(dv):
+            Sn[i, j] += k[i] * d[j]
+    o = np.zeros(dv)
+    for j in range(dv):
+        for i in range(dk):
+            o[j] += Sn[i, j] * q[i]
+    return o, Sn
+
+
+def attention(q: np.ndarray, K: np.ndarray, V: np.ndarray, scale: float) -> np.ndarray:
+    """softmax(q K^T * scale) V for one head: q [d], K, V [T, d]."""
+    s = np.array([scale * float(np.dot(q, K[t])) for t in range(K.shape[0])], dtype=np.float64)
+    m = s.max()
+    p = np.exp(s - m)
+    p /= p.sum()
+    return (p[:, None] * V.astype(np.float64)).sum(axis=0)
+
+
+def sigmoid(x: np.ndarray) -> np.ndarray:
+    return 1.0 / (1.0 + np.exp(-np.asarray(x, dtype=np.float64)))

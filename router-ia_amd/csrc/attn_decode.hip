@@ -1,0 +1,513 @@
+// Full-attention decode over a paged bf16 KV cache for gfx950.
+//
+// Reference semantics (v2/src/router_ia/qwen36_attention_cache.py:285-373):
+//   k_rot  = RoPE(k, tokens_seen) on dims [0, 64)           (:306, :154-162)
+//   K, V  += k_rot, v  at slot `resident`                    (:334-373)
+//   s_t    = q_rot . K_t * 256^-0.5  over every resident token (:312)
+//   attn   = softmax(s) V ; out = attn * sigmoid(gate)       (:313-317)
+// with query head h reading KV head h / 8 (repeat_interleave, :309-310).
+//
+// Decode is HBM-bound (2 KiB of KV per token per KV head pair, 8 FLOP/B), so
+// the design goal is one streaming pass over K and V:
+//   * pages: K as [page][kv_head][16 tok][256 dim], V transposed as
+//     [page][kv_head][256 dim][16 tok]; each (page, head) tile is 8 KiB and a
+//     wavefront reads it as one contiguous block.
+//   * scores S^T = K Q^T on MFMA 16x16x32 bf16 (tokens x query heads, the
+//     8 query heads of a KV head padded to 16); the output layout leaves each
+//     lane with 4 tokens of one head, which is exactly the B operand of the
+//     P V product, computed as O^T = V^T P^T on MFMA 16x16x16 bf16.  Softmax
+//     statistics and O^T columns therefore live in the same lane and no
+//     cross-lane transpose is needed.
+//   * split-K: a workgroup (4 waves) owns `split_tokens` tokens of one
+//     (sequence, KV head); waves take pages round-robin with an online
+//     softmax, merge through LDS and emit (max, sum, unnormalised acc); a
+//     combine kernel merges the splits and applies the sigmoid gate.
+#include <math.h>
+
+#include "ria_common.h"
+
+namespace ria {
+
+constexpr int kMaxGroup = 16;  // query heads per KV head handled by one MFMA tile
+
+struct AttnArgs {
+  const void* q;
+  int64_t q_stride;
+  const void* gate;
+  int64_t gate_stride;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  int num_pages;
+  const int32_t* page_table;
+  int64_t pt_stride;
+  const int32_t* seq_slot;
+  const int32_t* positions;
+  int32_t pos_scalar;
+  const int32_t* ctx_lens;
+  int32_t ctx_scalar;
+  const float* inv_freq;
+  int rope_dim;
+  float scale;
+  int split_tokens;
+  int max_splits;
+  float* ws_stats;  // [parts][group][2]  (max, sum)
+  float* ws_acc;    // [parts][group][256]
+  int num_q_heads;
+  int num_kv_heads;
+  int group;
+  void* out;
+};
+
+struct AppendArgs {
+  const void* k;
+  int64_t k_stride;
+  const void* v;
+  int64_t v_stride;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int num_pages;
+  const int32_t* page_table;
+  int64_t pt_stride;
+  const int32_t* seq_slot;
+  const int32_t* positions;
+  int32_t pos_scalar;
+  const int32_t* slots;
+  int32_t slot_scalar;
+  const float* inv_freq;
+  int rope_dim;
+  int num_kv_heads;
+};
+
+// RoPE of element d of a row: (x*cos + rotate_half(x)*sin) on [0, rope_dim),
+// pass-through above (qwen36_attention_cache.py:154-162).
+__device__ __forceinline__ float rope_elem(float xd, float partner, int d, int rope_dim, float pos,
+                                           const float* inv_freq) {
+  if (d >= rope_dim) return xd;
+  const int half = rope_dim >> 1;
+  const float ang = mul_rn(pos, inv_freq[d < half ? d : d - half]);
+  const float c = cosf(ang), s = sinf(ang);
+  const float rot = d < half ? -partner : partner;
+  return add_rn(mul_rn(xd, c), mul_rn(rot, s));
+}
+
+// One workgroup per (sequence, KV head): rotate k, write k and v into the page.
+template <int KT, int VT>
+__global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
+  const int b = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int d = threadIdx.x;
+  const int row = a.seq_slot ? a.seq_slot[b] : b;
+  const int pos = a.positions ? a.positions[b] : a.pos_scalar;
+  const int slot = a.slots ? a.slots[b] : a.slot_scalar;
+  __shared__ float k_s[kAttnHeadDim];
+  const float kv = load_act<KT>(a.k, (int64_t)b * a.k_stride + kvh * kAttnHeadDim + d);
+  const float vv = load_act<VT>(a.v, (int64_t)b * a.v_stride + kvh * kAttnHeadDim + d);
+  k_s[d] = kv;
+  __syncthreads();
+  if (slot < 0 || slot / kPageTokens >= a.pt_stride) return;
+  const int half = a.rope_dim >> 1;
+  const float partner = d < a.rope_dim ? k_s[d < half ? d + half : d - half] : 0.f;
+  const float kr = rope_elem(kv, partner, d, a.rope_dim, static_cast<float>(pos), a.inv_freq);
+  const int phys = a.page_table[(int64_t)row * a.pt_stride + slot / kPageTokens];
+  if (phys < 0 || phys >= a.num_pages) return;  // host guarantees allocation; never write out of the pool
+  const int off = slot % kPageTokens;
+  const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
+  a.k_cache[(tile * kPageTokens + off) * kAttnHeadDim + d] = f32_to_bf16_bits(kr);
+  a.v_cache[(tile * kAttnHeadDim + d) * kPageTokens + off] = f32_to_bf16_bits(vv);
+}
+
+template <int QT>
+__global__ __launch_bounds__(256) void attn_splitk_kernel(AttnArgs a) {
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  // Never read past the row's page-table entries, whatever ctx_lens holds.
+  const int ctx = min(a.ctx_lens ? a.ctx_lens[b] : a.ctx_scalar, (int)min<int64_t>(a.pt_stride * kPageTokens, 1 << 30));
+  const int tok0 = split * a.split_tokens;
+  if (tok0 >= ctx) return;
+  const int tok1 = min(ctx, tok0 + a.split_tokens);
+  const int row = a.seq_slot ? a.seq_slot[b] : b;
+  const float pos = static_cast<float>(a.positions ? a.positions[b] : a.pos_scalar);
+  const int G = a.group;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int n = lane & 15;  // MFMA column: query head (scores) / dim row (PV)
+  const int g4 = lane >> 4; // lane group
+
+  // ---- Q: rotate the group's query heads into LDS (one thread per dim),
+  // then each lane (head n, group g4) packs dims [64*g4, 64*g4 + 64) as bf16.
+  __shared__ float q_lds[8][kAttnHeadDim];
+  for (int h = 0; h < G; ++h) {
+    const int64_t base = (int64_t)b * a.q_stride + (int64_t)(kvh * G + h) * kAttnHeadDim;
+    float x = load_act<QT>(a.q, base + tid);
+    if (a.rope_dim == 64 && tid < 64) {
+      const float partner = load_act<QT>(a.q, base + (tid ^ 32));
+      const float ang = mul_rn(pos, a.inv_freq[tid & 31]);
+      const float c = cosf(ang), s = sinf(ang);
+      x = add_rn(mul_rn(x, c), mul_rn(tid < 32 ? -partner : partner, s));
+    }
+    q_lds[h][tid] = x;
+  }
+  __syncthreads();
+  bf16x8 qop[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = n < G ? q_lds[n & 7][64 * g4 + 8 * kk + j] : 0.f;
+      qop[kk][j] = __builtin_bit_cast(__bf16, f32_to_bf16_bits(v));
+    }
+  }
+
+  f32x4 o[16];
+#pragma unroll
+  for (int db = 0; db < 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int page0 = tok0 / kPageTokens;
+  const int page_end = (tok1 + kPageTokens - 1) / kPageTokens;
+  const int32_t* pt = a.page_table + (int64_t)row * a.pt_stride;
+  for (int p = page0 + wave; p < page_end; p += 4) {
+    int phys = pt[p];
+    phys = (phys < 0 || phys >= a.num_pages) ? 0 : phys;  // unallocated entries never fault
+    const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
+    const uint4* kp = reinterpret_cast<const uint4*>(a.k_cache + (tile * kPageTokens + n) * kAttnHeadDim + 64 * g4);
+    const uint16_t* vp = a.v_cache + tile * (kAttnHeadDim * kPageTokens) + 4 * g4;
+    uint4 kraw[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) kraw[kk] = kp[kk];
+    uint2 vraw[16];
+#pragma unroll
+    for (int db = 0; db < 16; ++db) vraw[db] = *reinterpret_cast<const uint2*>(vp + (db * 16 + n) * kPageTokens);
+
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        __builtin_bit_cast(bf16x8, kraw[kk]), qop[kk], sc, 0, 0, 0);
+
+    const int t_base = p * kPageTokens + 4 * g4;
+    const bool tail = (p + 1) * kPageTokens > tok1;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = (t_base + i < tok1) ? sc[i] * a.scale : -INFINITY;
+      mx = fmaxf(mx, sc[i]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = expf(m_run - m_new);
+    float pr[4];
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pr[i] = expf(sc[i] - m_new);
+      psum += pr[i];
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    s16x4 pb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pb[i] = static_cast<short>(f32_to_bf16_bits(pr[i]));
+    if (tail) {
+      // Tokens past the end of the sequence carry whatever the page holds;
+      // zero their V so 0 * garbage cannot reach the accumulator.
+#pragma unroll
+      for (int db = 0; db < 16; ++db) {
+        uint32_t lo = vraw[db].x, hi = vraw[db].y;
+        if (t_base + 0 >= tok1) lo &= 0xffff0000u;
+        if (t_base + 1 >= tok1) lo &= 0x0000ffffu;
+        if (t_base + 2 >= tok1) hi &= 0xffff0000u;
+        if (t_base + 3 >= tok1) hi &= 0x0000ffffu;
+        vraw[db] = uint2{lo, hi};
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < 16; ++db) {
+      o[db] *= alpha;
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vraw[db]), pb, o[db], 0, 0, 0);
+    }
+  }
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+
+  // ---- merge the four waves through LDS
+  __shared__ float sm_m[4][kMaxGroup];
+  __shared__ float sm_l[4][kMaxGroup];
+  __shared__ float sm_o[4][8][kAttnHeadDim];  // group <= 8 on this path (checked on the host)
+  if (g4 == 0 && n < G) {
+    sm_m[wave][n] = m_run;
+    sm_l[wave][n] = l_run;
+  }
+  if (n < G) {
+#pragma unroll
+    for (int db = 0; db < 16; ++db) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sm_o[wave][n][db * 16 + 4 * g4 + i] = o[db][i];
+    }
+  }
+  __syncthreads();
+  const int64_t part = ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits + split;
+  for (int h = 0; h < G; ++h) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w][h]);
+    float acc = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float wt = (sm_m[w][h] == -INFINITY) ? 0.f : expf(sm_m[w][h] - M);
+      acc = fmaf(wt, sm_o[w][h][tid], acc);
+      L = fmaf(wt, sm_l[w][h], L);
+    }
+    a.ws_acc[(part * G + h) * kAttnHeadDim + tid] = acc;
+    if (tid == 0) {
+      a.ws_stats[(part * G + h) * 2 + 0] = M;
+      a.ws_stats[(part * G + h) * 2 + 1] = L;
+    }
+  }
+}
+
+// Merge the splits of one (sequence, query head) and apply the sigmoid gate.
+template <int GT, int OT>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  const int b = blockIdx.x / a.num_q_heads;
+  const int h = blockIdx.x % a.num_q_heads;
+  const int d = threadIdx.x;
+  const int kvh = h / a.group;
+  const int hi = h % a.group;
+  const int ctx = min(a.ctx_lens ? a.ctx_lens[b] : a.ctx_scalar, (int)min<int64_t>(a.pt_stride * kPageTokens, 1 << 30));
+  const int nsplit = min((ctx + a.split_tokens - 1) / a.split_tokens, a.max_splits);
+  const int64_t part0 = ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits;
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_stats[((part0 + s) * a.group + hi) * 2]);
+  float num = 0.f, den = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const int64_t ph = (part0 + s) * a.group + hi;
+    const float wt = expf(a.ws_stats[ph * 2] - M);
+    num = fmaf(wt, a.ws_acc[ph * kAttnHeadDim + d], num);
+    den = fmaf(wt, a.ws_stats[ph * 2 + 1], den);
+  }
+  const float attn = num / den;
+  const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + d;
+  const float gv = sigmoid_f(load_act<GT>(a.gate, gi));
+  store_act<OT>(a.out, ((int64_t)b * a.num_q_heads + h) * kAttnHeadDim + d, mul_rn(attn, gv));
+}
+
+__global__ __launch_bounds__(256) void kv_gather_kernel(const uint16_t* k_cache, const uint16_t* v_cache,
+                                                        int num_pages, const int32_t* page_table,
+                                                        int64_t pt_stride, const int32_t* seq_slot,
+                                                        int num_kv_heads, int32_t start, int32_t count,
+                                                        uint16_t* k_out, uint16_t* v_out) {
+  const int t = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int d = threadIdx.x;
+  const int row = seq_slot ? seq_slot[b] : b;
+  const int tok = start + t;
+  const int phys = page_table[(int64_t)row * pt_stride + tok / kPageTokens];
+  const int64_t o = (((int64_t)b * num_kv_heads + kvh) * count + t) * kAttnHeadDim + d;
+  if (phys < 0 || phys >= num_pages) {
+    k_out[o] = 0;
+    v_out[o] = 0;
+    return;
+  }
+  const int64_t tile = (int64_t)phys * num_kv_heads + kvh;
+  const int off = tok % kPageTokens;
+  k_out[o] = k_cache[(tile * kPageTokens + off) * kAttnHeadDim + d];
+  v_out[o] = v_cache[(tile * kAttnHeadDim + d) * kPageTokens + off];
+}
+
+static bool valid_dtype(int dt) { return dt == RIA_DT_BF16 || dt == RIA_DT_F16 || dt == RIA_DT_F32; }
+
+static int auto_split_tokens(int batch, int num_kv_heads, int max_ctx) {
+  // Aim for ~2048 workgroups (8 per CU) while keeping at least one page per
+  // wave and at most 8 pages per wave.
+  const int64_t pages = (int64_t)batch * num_kv_heads * ((max_ctx + kPageTokens - 1) / kPageTokens);
+  int64_t pps = pages / 2048;
+  if (pps < 4) pps = 4;
+  if (pps > 32) pps = 32;
+  pps = (pps + 3) / 4 * 4;
+  return static_cast<int>(pps * kPageTokens);
+}
+
+static int resolve_split(int batch, int num_kv_heads, int max_ctx, int split_tokens) {
+  return split_tokens > 0 ? split_tokens : auto_split_tokens(batch, num_kv_heads, max_ctx);
+}
+
+}  // namespace ria
+
+using namespace ria;
+
+extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
+                             const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
+                             int num_pages, const int32_t* page_table, int64_t page_table_stride,
+                             const int32_t* seq_slot, const int32_t* positions, int32_t position_scalar,
+                             const int32_t* slots, int32_t slot_scalar, const float* inv_freq, int rope_dim,
+                             void* stream) {
+  if (batch < 0 || num_kv_heads <= 0) return set_error(RIA_ERR_INVALID, "ria_kv_append: bad batch/num_kv_heads");
+  if (batch == 0) return RIA_OK;
+  if (!valid_dtype(k_dtype) || !valid_dtype(v_dtype)) return set_error(RIA_ERR_INVALID, "ria_kv_append: unknown dtype");
+  if (!k || !v || !k_cache || !v_cache || !page_table) return set_error(RIA_ERR_INVALID, "ria_kv_append: null pointer");
+  if (rope_dim < 0 || rope_dim > 64 || rope_dim % 2) return set_error(RIA_ERR_INVALID, "ria_kv_append: rope_dim must be even and <= 64");
+  if (rope_dim > 0 && !inv_freq) return set_error(RIA_ERR_INVALID, "ria_kv_append: inv_freq is null");
+  if (k_row_stride < (int64_t)num_kv_heads * kAttnHeadDim || v_row_stride < (int64_t)num_kv_heads * kAttnHeadDim)
+    return set_error(RIA_ERR_INVALID, "ria_kv_append: row stride smaller than Hkv*256");
+  if (!slots && slot_scalar < 0) return set_error(RIA_ERR_INVALID, "ria_kv_append: negative slot");
+  AppendArgs a{};
+  a.k = k;
+  a.k_stride = k_row_stride;
+  a.v = v;
+  a.v_stride = v_row_stride;
+  a.k_cache = static_cast<uint16_t*>(k_cache);
+  a.v_cache = static_cast<uint16_t*>(v_cache);
+  a.num_pages = num_pages;
+  a.page_table = page_table;
+  a.pt_stride = page_table_stride;
+  a.seq_slot = seq_slot;
+  a.positions = positions;
+  a.pos_scalar = position_scalar;
+  a.slots = slots;
+  a.slot_scalar = slot_scalar;
+  a.inv_freq = inv_freq;
+  a.rope_dim = rope_dim;
+  a.num_kv_heads = num_kv_heads;
+  dim3 grid(batch, num_kv_heads);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define RIA_APPEND_LAUNCH(KT_, VT_) hipLaunchKernelGGL((kv_append_kernel<KT_, VT_>), grid, dim3(256), 0, st, a)
+#define RIA_APPEND_VT(KT_)                                           \
+  if (v_dtype == RIA_DT_BF16) RIA_APPEND_LAUNCH(KT_, RIA_DT_BF16);    \
+  else if (v_dtype == RIA_DT_F16) RIA_APPEND_LAUNCH(KT_, RIA_DT_F16); \
+  else RIA_APPEND_LAUNCH(KT_, RIA_DT_F32);
+  if (k_dtype == RIA_DT_BF16) {
+    RIA_APPEND_VT(RIA_DT_BF16)
+  } else if (k_dtype == RIA_DT_F16) {
+    RIA_APPEND_VT(RIA_DT_F16)
+  } else {
+    RIA_APPEND_VT(RIA_DT_F32)
+  }
+#undef RIA_APPEND_VT
+#undef RIA_APPEND_LAUNCH
+  return check_launch("ria_kv_append");
+}
+
+extern "C" int64_t ria_attn_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_ctx,
+                                                   int split_tokens) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_ctx <= 0) return 0;
+  const int st = resolve_split(batch, num_kv_heads, max_ctx, split_tokens);
+  const int64_t max_splits = (max_ctx + st - 1) / st;
+  const int64_t parts = (int64_t)batch * num_kv_heads * max_splits;
+  const int64_t group = num_q_heads / num_kv_heads;
+  const int64_t stats = parts * group * 2;
+  const int64_t stats_aligned = (stats + 63) / 64 * 64;
+  return (stats_aligned + parts * group * kAttnHeadDim) * (int64_t)sizeof(float);
+}
+
+extern "C" int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
+                               int64_t q_row_stride, const void* gate, int gate_dtype, int64_t gate_row_stride,
+                               const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
+                               int64_t page_table_stride, const int32_t* seq_slot, const int32_t* positions,
+                               int32_t position_scalar, const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
+                               const float* inv_freq, int rope_dim, float scale, int split_tokens,
+                               void* workspace, int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  if (batch < 0) return set_error(RIA_ERR_INVALID, "ria_attn_decode: batch must be >= 0");
+  if (batch == 0) return RIA_OK;
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
+    return set_error(RIA_ERR_INVALID, "ria_attn_decode: num_q_heads must be a multiple of num_kv_heads");
+  const int group = num_q_heads / num_kv_heads;
+  if (group > 8) return set_error(RIA_ERR_INVALID, "ria_attn_decode: at most 8 query heads per KV head (got %d)", group);
+  if (!valid_dtype(q_dtype) || !valid_dtype(gate_dtype) || !valid_dtype(out_dtype))
+    return set_error(RIA_ERR_INVALID, "ria_attn_decode: unknown dtype code");
+  if (!q || !gate || !k_cache || !v_cache || !page_table || !out || !workspace)
+    return set_error(RIA_ERR_INVALID, "ria_attn_decode: null pointer");
+  if (rope_dim != 0 && rope_dim != 64) return set_error(RIA_ERR_INVALID, "ria_attn_decode: rope_dim must be 0 or 64");
+  if (rope_dim > 0 && !inv_freq) return set_error(RIA_ERR_INVALID, "ria_attn_decode: inv_freq is null");
+  if (max_ctx <= 0) return set_error(RIA_ERR_INVALID, "ria_attn_decode: max_ctx must be > 0");
+  if (!ctx_lens && (ctx_scalar <= 0 || ctx_scalar > max_ctx))
+    return set_error(RIA_ERR_INVALID, "ria_attn_decode: ctx_scalar must be in [1, max_ctx]");
+  if (split_tokens < 0 || split_tokens % 64)
+    return set_error(RIA_ERR_INVALID, "ria_attn_decode: split_tokens must be 0 or a multiple of 64");
+  if (q_row_stride < (int64_t)num_q_heads * kAttnHeadDim || gate_row_stride < (int64_t)num_q_heads * kAttnHeadDim)
+    return set_error(RIA_ERR_INVALID, "ria_attn_decode: row stride smaller than Hq*256");
+  if (reinterpret_cast<uintptr_t>(k_cache) % 16 || reinterpret_cast<uintptr_t>(v_cache) % 16)
+    return set_error(RIA_ERR_INVALID, "ria_attn_decode: KV caches must be 16-byte aligned");
+  const int64_t need = ria_attn_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_ctx, split_tokens);
+  if (workspace_bytes < need)
+    return set_error(RIA_ERR_WORKSPACE, "ria_attn_decode: workspace %lld bytes < required %lld",
+                     (long long)workspace_bytes, (long long)need);
+
+  AttnArgs a{};
+  a.q = q;
+  a.q_stride = q_row_stride;
+  a.gate = gate;
+  a.gate_stride = gate_row_stride;
+  a.k_cache = static_cast<const uint16_t*>(k_cache);
+  a.v_cache = static_cast<const uint16_t*>(v_cache);
+  a.num_pages = num_pages;
+  a.page_table = page_table;
+  a.pt_stride = page_table_stride;
+  a.seq_slot = seq_slot;
+  a.positions = positions;
+  a.pos_scalar = position_scalar;
+  a.ctx_lens = ctx_lens;
+  a.ctx_scalar = ctx_scalar;
+  a.inv_freq = inv_freq;
+  a.rope_dim = rope_dim;
+  a.scale = scale;
+  a.split_tokens = resolve_split(batch, num_kv_heads, max_ctx, split_tokens);
+  a.max_splits = (max_ctx + a.split_tokens - 1) / a.split_tokens;
+  const int64_t parts = (int64_t)batch * num_kv_heads * a.max_splits;
+  const int64_t stats = parts * group * 2;
+  a.ws_stats = static_cast<float*>(workspace);
+  a.ws_acc = a.ws_stats + (stats + 63) / 64 * 64;
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.group = group;
+  a.out = out;
+  if (a.max_splits > 65535 || batch > 65535) return set_error(RIA_ERR_INVALID, "ria_attn_decode: grid too large");
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(a.max_splits, num_kv_heads, batch);
+  if (q_dtype == RIA_DT_BF16)
+    hipLaunchKernelGGL((attn_splitk_kernel<RIA_DT_BF16>), grid, dim3(256), 0, st, a);
+  else if (q_dtype == RIA_DT_F16)
+    hipLaunchKernelGGL((attn_splitk_kernel<RIA_DT_F16>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_splitk_kernel<RIA_DT_F32>), grid, dim3(256), 0, st, a);
+  int rc = check_launch("ria_attn_decode (split-K)");
+  if (rc != RIA_OK) return rc;
+
+  dim3 cgrid(batch * num_q_heads);
+#define RIA_COMB_LAUNCH(GT_, OT_) hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_>), cgrid, dim3(256), 0, st, a)
+#define RIA_COMB_OT(GT_)                                          \
+  if (out_dtype == RIA_DT_BF16) RIA_COMB_LAUNCH(GT_, RIA_DT_BF16); \
+  else if (out_dtype == RIA_DT_F16) RIA_COMB_LAUNCH(GT_, RIA_DT_F16); \
+  else RIA_COMB_LAUNCH(GT_, RIA_DT_F32);
+  if (gate_dtype == RIA_DT_BF16) {
+    RIA_COMB_OT(RIA_DT_BF16)
+  } else if (gate_dtype == RIA_DT_F16) {
+    RIA_COMB_OT(RIA_DT_F16)
+  } else {
+    RIA_COMB_OT(RIA_DT_F32)
+  }
+#undef RIA_COMB_OT
+#undef RIA_COMB_LAUNCH
+  return check_launch("ria_attn_decode (combine)");
+}
+
+extern "C" int ria_kv_gather(int batch, int num_kv_heads, const void* k_cache, const void* v_cache, int num_pages,
+                             const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                             int32_t start, int32_t count, void* k_out, void* v_out, void* stream) {
+  if (batch < 0 || num_kv_heads <= 0 || start < 0 || count < 0)
+    return set_error(RIA_ERR_INVALID, "ria_kv_gather: bad sizes");
+  if (batch == 0 || count == 0) return RIA_OK;
+  if (!k_cache || !v_cache || !page_table || !k_out || !v_out) return set_error(RIA_ERR_INVALID, "ria_kv_gather: null pointer");
+  if (batch > 65535 || num_kv_heads > 65535) return set_error(RIA_ERR_INVALID, "ria_kv_gather: grid too large");
+  dim3 grid(count, num_kv_heads, batch);
+  hipLaunchKernelGGL(kv_gather_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(k_cache), static_cast<const uint16_t*>(v_cache), num_pages,
+                     page_table, page_table_stride, seq_slot, num_kv_heads, start, count,
+                     static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out));
+  return check_launch("ria_kv_gather");
+}

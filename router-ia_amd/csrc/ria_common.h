@@ -1,0 +1,108 @@
+// Shared device helpers for the gfx950 hybrid-attention kernels.
+//
+// Numeric conventions follow the PyTorch ops the reference path uses
+// (v2/src/router_ia/qwen36_attention_cache.py): bf16 <-> fp32 conversion is
+// round-to-nearest-even on the bit pattern (c10::BFloat16), fp16 uses the
+// hardware RNE conversion, and elementwise products/sums that torch evaluates
+// as separate kernels are written with non-contracting intrinsics so the
+// compiler cannot fuse them into an FMA with a different rounding.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ria_hybrid_attn.h"
+
+namespace ria {
+
+// Head geometry fixed by the model family (v2/src/router_ia/qwen36_40layer_loop.py:36-50).
+constexpr int kGdnHeadDim = 128;   // DeltaNet dk == dv
+constexpr int kConvTaps = 4;       // LINEAR_CONV_KERNEL
+constexpr int kConvRing = 4;       // ring slots per channel (slot = step mod 4)
+constexpr int kAttnHeadDim = 256;  // FULL_HEAD_DIM
+constexpr int kPageTokens = 16;    // tokens per KV page
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet), identical to c10::BFloat16.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  _Float16 h = __builtin_bit_cast(_Float16, b);
+  return static_cast<float>(h);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+// Load element `i` of an activation tensor with dtype code DT and widen to fp32.
+template <int DT>
+__device__ __forceinline__ float load_act(const void* p, int64_t i) {
+  if constexpr (DT == RIA_DT_BF16) {
+    return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  } else if constexpr (DT == RIA_DT_F16) {
+    return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  } else {
+    return static_cast<const float*>(p)[i];
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
+  if constexpr (DT == RIA_DT_BF16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
+  } else if constexpr (DT == RIA_DT_F16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_f16_bits(v);
+  } else {
+    static_cast<float*>(p)[i] = v;
+  }
+}
+
+// Value of an fp32 number after a round trip through dtype DT (torch `.to(dt)`).
+template <int DT>
+__device__ __forceinline__ float through_dtype(float v) {
+  if constexpr (DT == RIA_DT_BF16) {
+    return round_bf16(v);
+  } else if constexpr (DT == RIA_DT_F16) {
+    return f16_bits_to_f32(f32_to_f16_bits(v));
+  } else {
+    return v;
+  }
+}
+
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+
+// torch.sigmoid / F.softplus(beta=1, threshold=20) / F.silu on fp32.
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace ria
+
+// Host-side error plumbing shared by every entry point (defined in abi.hip).
+namespace ria {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace ria

@@ -1,0 +1,102 @@
+// Small elementwise entry points behind the module-level helpers of the
+// attention cache: _rope, _apply_rope and _l2norm
+// (v2/src/router_ia/qwen36_attention_cache.py:137-173).
+#include <math.h>
+
+#include "ria_common.h"
+
+namespace ria {
+
+__global__ void rope_table_kernel(int32_t position, const float* inv_freq, int rope_dim, float* cos_out,
+                                  float* sin_out) {
+  const int d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= rope_dim) return;
+  const int half = rope_dim >> 1;
+  // angles = float(position) * inv_freq ; emb = cat(angles, angles)
+  const float ang = mul_rn(static_cast<float>(position), inv_freq[d < half ? d : d - half]);
+  cos_out[d] = cosf(ang);
+  sin_out[d] = sinf(ang);
+}
+
+// One workgroup per row; rows of up to 1024 elements held in LDS.
+__global__ __launch_bounds__(256) void rope_apply_kernel(int head_dim, int rope_dim, const float* x, float* out,
+                                                         const float* inv_freq, int32_t position) {
+  __shared__ float row_s[1024];
+  const int64_t r = blockIdx.x;
+  const float* xr = x + r * head_dim;
+  for (int d = threadIdx.x; d < head_dim; d += blockDim.x) row_s[d] = xr[d];
+  __syncthreads();
+  const int half = rope_dim >> 1;
+  const float pos = static_cast<float>(position);
+  for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
+    float y = row_s[d];
+    if (d < rope_dim) {
+      const float ang = mul_rn(pos, inv_freq[d < half ? d : d - half]);
+      const float c = cosf(ang), s = sinf(ang);
+      const float rot = d < half ? -row_s[d + half] : row_s[d - half];
+      y = add_rn(mul_rn(row_s[d], c), mul_rn(rot, s));
+    }
+    out[r * head_dim + d] = y;
+  }
+}
+
+// One wavefront per row: x * (1 / sqrt(sum(x*x) + eps)).
+template <int XT>
+__global__ __launch_bounds__(256) void l2norm_kernel(int64_t rows, int dim, const void* x, float eps, float* out) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  float ss = 0.f;
+  for (int d = lane; d < dim; d += 64) {
+    const float v = load_act<XT>(x, r * dim + d);
+    ss += mul_rn(v, v);
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss + eps);
+  for (int d = lane; d < dim; d += 64) out[r * dim + d] = mul_rn(load_act<XT>(x, r * dim + d), inv);
+}
+
+}  // namespace ria
+
+using namespace ria;
+
+extern "C" int ria_rope_table(int32_t position, const float* inv_freq, int rope_dim, float* cos_out,
+                              float* sin_out, void* stream) {
+  if (rope_dim <= 0 || rope_dim % 2) return set_error(RIA_ERR_INVALID, "ria_rope_table: rope_dim must be positive and even");
+  if (!inv_freq || !cos_out || !sin_out) return set_error(RIA_ERR_INVALID, "ria_rope_table: null pointer");
+  hipLaunchKernelGGL(rope_table_kernel, dim3((rope_dim + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), position, inv_freq, rope_dim, cos_out, sin_out);
+  return check_launch("ria_rope_table");
+}
+
+extern "C" int ria_rope_apply(int64_t rows, int head_dim, int rope_dim, const float* x, float* out,
+                              const float* inv_freq, int32_t position, void* stream) {
+  if (rows < 0 || head_dim <= 0 || head_dim > 1024) return set_error(RIA_ERR_INVALID, "ria_rope_apply: head_dim must be in [1, 1024]");
+  if (rope_dim < 0 || rope_dim % 2 || rope_dim > head_dim)
+    return set_error(RIA_ERR_INVALID, "ria_rope_apply: rope_dim must be even and <= head_dim");
+  if (rows == 0) return RIA_OK;
+  if (!x || !out || (rope_dim > 0 && !inv_freq)) return set_error(RIA_ERR_INVALID, "ria_rope_apply: null pointer");
+  if (rows > 0x7fffffff) return set_error(RIA_ERR_INVALID, "ria_rope_apply: too many rows");
+  hipLaunchKernelGGL(rope_apply_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), head_dim, rope_dim, x, out, inv_freq, position);
+  return check_launch("ria_rope_apply");
+}
+
+extern "C" int ria_l2norm(int64_t rows, int dim, const void* x, int x_dtype, float eps, float* out, void* stream) {
+  if (rows < 0 || dim <= 0) return set_error(RIA_ERR_INVALID, "ria_l2norm: bad sizes");
+  if (rows == 0) return RIA_OK;
+  if (!x || !out) return set_error(RIA_ERR_INVALID, "ria_l2norm: null pointer");
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > 0x7fffffff) return set_error(RIA_ERR_INVALID, "ria_l2norm: too many rows");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(blocks));
+  if (x_dtype == RIA_DT_BF16)
+    hipLaunchKernelGGL((l2norm_kernel<RIA_DT_BF16>), grid, dim3(256), 0, st, rows, dim, x, eps, out);
+  else if (x_dtype == RIA_DT_F16)
+    hipLaunchKernelGGL((l2norm_kernel<RIA_DT_F16>), grid, dim3(256), 0, st, rows, dim, x, eps, out);
+  else if (x_dtype == RIA_DT_F32)
+    hipLaunchKernelGGL((l2norm_kernel<RIA_DT_F32>), grid, dim3(256), 0, st, rows, dim, x, eps, out);
+  else
+    return set_error(RIA_ERR_INVALID, "ria_l2norm: unknown dtype code");
+  return check_launch("ria_l2norm");
+}

@@ -1,0 +1,104 @@
+"""ctypes binding of the gfx950 hybrid-attention library (include/ria_hybrid_attn.h).
+
+The library is located the way the reference locates its native memory pool
+(src/router_ia/qwen36_native_memory.py:29-45): an explicit path in the
+``RIA_HIP_LIB`` environment variable wins, otherwise the in-tree build
+``router_ia/_lib/libria_hip.so`` is used.  There is no fallback: if the
+library cannot be loaded every compute entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_ENV = "RIA_HIP_LIB"
+DEFAULT_LIB = Path(__file__).resolve().parent / "_lib" / "libria_hip.so"
+ABI_VERSION = 1
+
+RIA_DT_BF16 = 0
+RIA_DT_F16 = 1
+RIA_DT_F32 = 2
+RIA_GATE_PRECOMPUTED = 0
+RIA_GATE_RAW = 1
+
+_c_int = ctypes.c_int
+_c_i32 = ctypes.c_int32
+_c_i64 = ctypes.c_int64
+_c_f32 = ctypes.c_float
+_vp = ctypes.c_void_p
+
+# name -> (restype, argtypes); mirrors include/ria_hybrid_attn.h.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "ria_abi_version": (_c_int, []),
+    "ria_last_error": (ctypes.c_char_p, []),
+    "ria_gdn_decode": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _c_int, _vp, _vp, _vp, _c_i32, _vp, _vp,
+         _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp, _c_int, _vp],
+    ),
+    "ria_conv1d_step": (
+        _c_int,
+        [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _vp, _vp, _c_i32, _vp, _c_int, _vp],
+    ),
+    "ria_l2norm": (_c_int, [_c_i64, _c_int, _vp, _c_int, _c_f32, _vp, _vp]),
+    "ria_rope_table": (_c_int, [_c_i32, _vp, _c_int, _vp, _vp, _vp]),
+    "ria_rope_apply": (_c_int, [_c_i64, _c_int, _c_int, _vp, _vp, _vp, _c_i32, _vp]),
+    "ria_kv_append": (
+        _c_int,
+        [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _vp, _c_i64,
+         _vp, _vp, _c_i32, _vp, _c_i32, _vp, _c_int, _vp],
+    ),
+    "ria_attn_decode_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ria_attn_decode": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _vp,
+         _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _c_f32, _c_int, _vp, _c_i64,
+         _vp, _c_int, _vp],
+    ),
+    "ria_kv_gather": (
+        _c_int,
+        [_c_int, _c_int, _vp, _vp, _c_int, _vp, _c_i64, _vp, _c_i32, _c_i32, _vp, _vp, _vp],
+    ),
+}
+
+_LIB: ctypes.CDLL | None = None
+
+
+class NativeLibraryError(RuntimeError):
+    """The HIP library is missing, stale or failed a call."""
+
+
+def library_path() -> Path:
+    override = os.environ.get(LIB_ENV)
+    return Path(override) if override else DEFAULT_LIB
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and type the HIP library; raise if it is absent or stale."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = library_path()
+    if not path.is_file():
+        raise NativeLibraryError(
+            f"HIP library not found at {path}; build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+            f"or `make -C router-ia_amd/csrc`, or point {LIB_ENV} at a built libria_hip.so"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = lib.ria_abi_version()
+    if version != ABI_VERSION:
+        raise NativeLibraryError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+    _LIB = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().ria_last_error().decode(errors="replace")
+        raise NativeLibraryError(f"{what} failed (status {rc}): {msg}")

@@ -1,0 +1,186 @@
+"""Batched attention state: B sequences decoding the 40-layer hybrid stack together.
+
+The reference keeps one ``AttentionState`` per sequence with per-layer dicts
+of tensors (v2/src/router_ia/qwen36_attention_cache.py:27-92) and advances it
+one sequence at a time.  Here all sequences live in fixed HBM pools so every
+layer is one kernel launch over the whole batch:
+
+    DeltaNet state   f32  [L_lin, B, Hv, 128, 128]   (2 MiB per sequence-layer)
+    conv ring        bf16 [L_lin, B, 4, conv_dim]     (slot = token index mod 4)
+    K / V pages      bf16 per full layer (see paged_kv)
+    tokens_seen      i32  [B] absolute position of the next token (RoPE
+                     position, conv ring index and KV slot of that token)
+
+Per token the caller runs ``linear_step`` / ``full_step`` for each layer and
+then ``advance()``, the batched equivalent of the reference caller bumping
+``tokens_seen`` after all 40 layers (v2/src/router_ia/qwen36_chat_batch.py:204-206).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+from . import kernels as K
+from .paged_kv import PagedKVCache
+
+
+def rope_inv_freq(theta: float, rope_dim: int) -> torch.Tensor:
+    """inv_freq exactly as the reference computes it in fp32 (qwen36_attention_cache.py:140-143)."""
+    if rope_dim <= 0 or rope_dim % 2:
+        raise ValueError(f"Invalid rotary dimension: {rope_dim}")
+    return 1.0 / (theta ** (torch.arange(0, rope_dim, 2, dtype=torch.float32) / rope_dim))
+
+
+class BatchedAttentionState:
+    def __init__(
+        self,
+        max_seqs: int,
+        max_context: int,
+        *,
+        num_linear_layers: int = 30,
+        num_full_layers: int = 10,
+        num_k_heads: int = 16,
+        num_v_heads: int = 32,
+        num_q_heads: int = 16,
+        num_kv_heads: int = 2,
+        rope_theta: float = 10_000_000.0,
+        rope_dim: int = 64,
+        num_pages: int | None = None,
+        device: str | torch.device = "cuda",
+        page_shuffle_seed: int | None = None,
+        split_tokens: int = 0,
+    ):
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError("BatchedAttentionState needs a ROCm GPU device; there is no CPU implementation")
+        nat.load()
+        self.max_seqs = int(max_seqs)
+        self.max_context = int(max_context)
+        self.num_linear_layers = num_linear_layers
+        self.num_full_layers = num_full_layers
+        self.num_k_heads = num_k_heads
+        self.num_v_heads = num_v_heads
+        self.num_q_heads = num_q_heads
+        self.num_kv_heads = num_kv_heads
+        self.conv_dim = K.conv_dim(num_k_heads, num_v_heads)
+        self.split_tokens = split_tokens
+        dev = self.device
+        self.linear_states = torch.zeros((num_linear_layers, max_seqs, num_v_heads, 128, 128),
+                                         dtype=torch.float32, device=dev)
+        self.conv_rings = torch.zeros((num_linear_layers, max_seqs, K.CONV_RING, self.conv_dim),
+                                      dtype=torch.bfloat16, device=dev)
+        max_pages_per_seq = (max_context + K.PAGE_TOKENS - 1) // K.PAGE_TOKENS
+        if num_pages is None:
+            num_pages = max_seqs * max_pages_per_seq
+        self.kv = PagedKVCache(num_full_layers, num_pages, max_seqs, max_pages_per_seq,
+                               num_kv_heads=num_kv_heads, device=dev, shuffle_seed=page_shuffle_seed)
+        self.tokens_seen = torch.zeros(max_seqs, dtype=torch.int32, device=dev)
+        self.ctx_lens = torch.ones(max_seqs, dtype=torch.int32, device=dev)
+        self._host_seen = [0] * max_seqs
+        self._min_headroom = 0  # min over rows of (KV capacity - tokens seen)
+        self.inv_freq = rope_inv_freq(rope_theta, rope_dim).to(dev)
+        self.scale = 256 ** -0.5
+        ws = K.attn_decode_workspace_bytes(max_seqs, num_q_heads, num_kv_heads, max_context, split_tokens)
+        self.workspace = torch.empty(max(ws, 4), dtype=torch.uint8, device=dev)
+
+    # ---------------------------------------------------------------- bookkeeping
+    def set_positions(self, lengths: list[int]) -> None:
+        """Declare that row b already holds lengths[b] tokens of state and KV."""
+        if len(lengths) != self.max_seqs:
+            raise ValueError("one length per sequence row is required")
+        if max(lengths) >= self.max_context:
+            raise ValueError("a context length reaches max_context")
+        self._host_seen = [int(x) for x in lengths]
+        self._ensure([n + 1 for n in self._host_seen])
+        self.tokens_seen.copy_(torch.tensor(self._host_seen, dtype=torch.int32))
+        self.ctx_lens.copy_(self.tokens_seen + 1)
+
+    def reserve(self, extra_tokens: int) -> None:
+        """Allocate KV pages so every row can take `extra_tokens` more tokens without host work."""
+        self._ensure([min(n + extra_tokens, self.max_context) for n in self._host_seen])
+
+    def _ensure(self, n_tokens: list[int]) -> None:
+        self.kv.ensure_many(n_tokens)
+        self._min_headroom = min(self.kv.alloc.capacity_tokens(r) - self._host_seen[r] for r in range(self.max_seqs))
+
+    def reset_row(self, row: int) -> None:
+        self.linear_states[:, row].zero_()
+        self.conv_rings[:, row].zero_()
+        self.kv.release(row)
+        self._min_headroom = 0
+        self._host_seen[row] = 0
+        self.tokens_seen[row] = 0
+        self.ctx_lens[row] = 1
+
+    def advance(self) -> None:
+        self._host_seen = [n + 1 for n in self._host_seen]
+        self._min_headroom -= 1
+        self.tokens_seen.add_(1)
+        self.ctx_lens.add_(1)
+
+    @property
+    def max_seen(self) -> int:
+        return max(self._host_seen)
+
+    # ---------------------------------------------------------------- layer steps
+    def linear_step(
+        self,
+        layer: int,
+        mixed_qkv: torch.Tensor,
+        conv_weight: torch.Tensor,
+        gate_a: torch.Tensor,
+        gate_b: torch.Tensor,
+        *,
+        gate_mode: int = nat.RIA_GATE_PRECOMPUTED,
+        A_log: torch.Tensor | None = None,
+        dt_bias: torch.Tensor | None = None,
+        out: torch.Tensor | None = None,
+        out_dtype: torch.dtype = torch.bfloat16,
+    ) -> torch.Tensor:
+        """One Gated DeltaNet token for every row (conv + recurrence + read-out)."""
+        if out is None:
+            out = torch.empty((self.max_seqs, self.num_v_heads, 128), dtype=out_dtype, device=self.device)
+        return K.gdn_decode(
+            mixed_qkv, self.linear_states[layer], gate_a, gate_b, out,
+            num_k_heads=self.num_k_heads, num_v_heads=self.num_v_heads, fuse_conv=True,
+            conv_weight=conv_weight, conv_ring=self.conv_rings[layer], conv_pos=self.tokens_seen,
+            gate_mode=gate_mode, A_log=A_log, dt_bias=dt_bias)
+
+    def full_step(
+        self,
+        layer: int,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        gate: torch.Tensor,
+        *,
+        out: torch.Tensor | None = None,
+        out_dtype: torch.dtype = torch.bfloat16,
+    ) -> torch.Tensor:
+        """Append this token's k, v (RoPE on k) and attend over each row's whole context."""
+        max_ctx = self.max_seen + 1
+        if max_ctx > self.max_context:
+            raise RuntimeError(f"context {max_ctx} exceeds max_context={self.max_context}")
+        if self._min_headroom < 1:
+            self._ensure([n + 1 for n in self._host_seen])
+        k_cache, v_cache = self.kv.layer(layer)
+        K.kv_append(k, v, k_cache, v_cache, self.kv.page_table, positions=self.tokens_seen,
+                    slots=self.tokens_seen, inv_freq=self.inv_freq)
+        if out is None:
+            out = torch.empty((self.max_seqs, self.num_q_heads, 256), dtype=out_dtype, device=self.device)
+        return K.attn_decode(q, gate, k_cache, v_cache, self.kv.page_table, out, positions=self.tokens_seen,
+                             ctx_lens=self.ctx_lens, max_ctx=max_ctx, inv_freq=self.inv_freq, scale=self.scale,
+                             workspace=self.workspace, split_tokens=self.split_tokens)
+
+    # ---------------------------------------------------------------- inspection
+    def gather_kv(self, layer: int, start: int, count: int) -> tuple[torch.Tensor, torch.Tensor]:
+        k_cache, v_cache = self.kv.layer(layer)
+        return K.kv_gather(k_cache, v_cache, self.kv.page_table, batch=self.max_seqs, start=start, count=count)
+
+    def resident_bytes(self) -> dict[str, int]:
+        return {
+            "linear_bytes": self.linear_states.numel() * 4,
+            "linear_conv_bytes": self.conv_rings.numel() * 2,
+            "full_bytes_allocated": self.kv.k.numel() * 2 + self.kv.v.numel() * 2,
+        }

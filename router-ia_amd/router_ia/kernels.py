@@ -1,0 +1,359 @@
+"""Typed torch-tensor wrappers over the C ABI (include/ria_hybrid_attn.h).
+
+Each wrapper checks shapes, dtypes, devices and strides on the host, then
+launches on the current HIP stream of the tensors' device.  Tensors must live
+on a ROCm GPU: there is no CPU implementation behind these calls.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native as nat
+
+GDN_HEAD_DIM = 128
+CONV_TAPS = 4
+CONV_RING = 4
+ATTN_HEAD_DIM = 256
+PAGE_TOKENS = 16
+
+_DTYPE_CODE = {torch.bfloat16: nat.RIA_DT_BF16, torch.float16: nat.RIA_DT_F16, torch.float32: nat.RIA_DT_F32}
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported activation dtype {t.dtype}; expected bf16, fp16 or fp32") from None
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _require_gpu(name: str, t: torch.Tensor | None, device: torch.device | None = None) -> None:
+    if t is None:
+        return
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"{name} is on {t.device}; the hybrid-attention kernels run only on a ROCm GPU (no CPU path)"
+        )
+    if device is not None and t.device != device:
+        raise RuntimeError(f"{name} is on {t.device}, expected {device}")
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _rows_i32(name: str, t: torch.Tensor | int | None, batch: int, device: torch.device) -> tuple[torch.Tensor | None, int]:
+    """Per-row int32 tensor or scalar -> (tensor or None, scalar)."""
+    if t is None:
+        return None, 0
+    if isinstance(t, int):
+        return None, int(t)
+    _require_gpu(name, t, device)
+    if t.dtype != torch.int32 or t.dim() != 1 or t.shape[0] < batch or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous int32 vector of length >= {batch}")
+    return t, 0
+
+
+def _row_stride(name: str, t: torch.Tensor, batch: int, row_elems: int) -> int:
+    """Row stride (elements) of a [batch, ...] tensor whose rows are contiguous."""
+    flat = t.reshape(t.shape[0], -1) if t.dim() > 2 else t
+    if flat.dim() != 2 or flat.shape[0] != batch or flat.shape[1] != row_elems:
+        raise ValueError(f"{name} must have {batch} rows of {row_elems} elements, got {tuple(t.shape)}")
+    if flat.shape[1] > 1 and flat.stride(1) != 1:
+        raise ValueError(f"{name} rows must be contiguous")
+    if t.dim() > 2 and not t[0].is_contiguous():
+        raise ValueError(f"{name} rows must be contiguous")
+    return int(flat.stride(0)) if batch > 1 else row_elems
+
+
+def conv_dim(num_k_heads: int, num_v_heads: int) -> int:
+    return (2 * num_k_heads + num_v_heads) * GDN_HEAD_DIM
+
+
+def gdn_decode(
+    mixed_qkv: torch.Tensor,
+    state: torch.Tensor,
+    gate_a: torch.Tensor,
+    gate_b: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    num_k_heads: int,
+    num_v_heads: int,
+    fuse_conv: bool = True,
+    conv_weight: torch.Tensor | None = None,
+    conv_ring: torch.Tensor | None = None,
+    conv_pos: torch.Tensor | int = 0,
+    seq_slot: torch.Tensor | None = None,
+    gate_mode: int = nat.RIA_GATE_PRECOMPUTED,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Fused conv + gated delta-rule decode step (ria_gdn_decode)."""
+    batch = int(mixed_qkv.shape[0])
+    dev = mixed_qkv.device
+    cdim = conv_dim(num_k_heads, num_v_heads)
+    for name, t in (("mixed_qkv", mixed_qkv), ("state", state), ("gate_a", gate_a), ("gate_b", gate_b),
+                    ("out", out), ("conv_weight", conv_weight), ("conv_ring", conv_ring), ("seq_slot", seq_slot),
+                    ("A_log", A_log), ("dt_bias", dt_bias)):
+        _require_gpu(name, t, dev)
+    x_stride = _row_stride("mixed_qkv", mixed_qkv, batch, cdim)
+    if state.dtype != torch.float32 or state.dim() != 4 or tuple(state.shape[1:]) != (num_v_heads, 128, 128) \
+            or not state.is_contiguous():
+        raise ValueError(f"state must be contiguous fp32 [pool, {num_v_heads}, 128, 128], got {tuple(state.shape)}")
+    if seq_slot is None and state.shape[0] < batch:
+        raise ValueError("state pool smaller than batch")
+    if gate_a.dtype != torch.float32 or gate_b.dtype != torch.float32:
+        raise ValueError("gate_a / gate_b must be fp32")
+    g_stride = _row_stride("gate_a", gate_a, batch, num_v_heads)
+    if _row_stride("gate_b", gate_b, batch, num_v_heads) != g_stride:
+        raise ValueError("gate_a and gate_b must share a row stride")
+    if tuple(out.shape) != (batch, num_v_heads, GDN_HEAD_DIM) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{batch}, {num_v_heads}, 128]")
+    if fuse_conv:
+        if conv_weight is None or conv_ring is None:
+            raise ValueError("fuse_conv needs conv_weight and conv_ring")
+        _check_conv_tensors(conv_weight, conv_ring, cdim, batch if seq_slot is None else 0)
+    if gate_mode == nat.RIA_GATE_RAW:
+        for name, t in (("A_log", A_log), ("dt_bias", dt_bias)):
+            if t is None or t.dtype != torch.float32 or t.numel() != num_v_heads or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous fp32 tensor of {num_v_heads} values")
+    if seq_slot is not None:
+        _rows_i32("seq_slot", seq_slot, batch, dev)
+    pos_t, pos_s = _rows_i32("conv_pos", conv_pos, batch, dev)
+    lib = nat.load()
+    rc = lib.ria_gdn_decode(
+        batch, num_k_heads, num_v_heads, _ptr(mixed_qkv), dtype_code(mixed_qkv), x_stride, int(bool(fuse_conv)),
+        _ptr(conv_weight) if fuse_conv else None, _ptr(conv_ring) if fuse_conv else None, _ptr(pos_t), pos_s,
+        _ptr(state), _ptr(seq_slot), _ptr(gate_a), _ptr(gate_b), g_stride, int(gate_mode),
+        _ptr(A_log) if gate_mode == nat.RIA_GATE_RAW else None,
+        _ptr(dt_bias) if gate_mode == nat.RIA_GATE_RAW else None,
+        _ptr(out), dtype_code(out), _stream(dev))
+    nat.check(rc, "ria_gdn_decode")
+    return out
+
+
+def _check_conv_tensors(conv_weight: torch.Tensor, conv_ring: torch.Tensor, channels: int, min_pool: int) -> None:
+    if conv_weight.dtype != torch.bfloat16 or conv_weight.numel() != channels * CONV_TAPS \
+            or not conv_weight.is_contiguous():
+        raise ValueError(f"conv_weight must be contiguous bf16 [{channels}, 1, 4]")
+    if conv_ring.dtype != torch.bfloat16 or conv_ring.dim() != 3 or tuple(conv_ring.shape[1:]) != (CONV_RING, channels) \
+            or not conv_ring.is_contiguous():
+        raise ValueError(f"conv_ring must be contiguous bf16 [pool, 4, {channels}], got {tuple(conv_ring.shape)}")
+    if conv_ring.shape[0] < min_pool:
+        raise ValueError("conv ring pool smaller than batch")
+
+
+def conv1d_step(
+    x: torch.Tensor,
+    conv_weight: torch.Tensor,
+    conv_ring: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    conv_pos: torch.Tensor | int,
+    seq_slot: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Depthwise causal conv step + SiLU with the conv ring (ria_conv1d_step)."""
+    batch, channels = int(x.shape[0]), int(x.shape[-1])
+    dev = x.device
+    for name, t in (("x", x), ("conv_weight", conv_weight), ("conv_ring", conv_ring), ("out", out),
+                    ("seq_slot", seq_slot)):
+        _require_gpu(name, t, dev)
+    stride = _row_stride("x", x, batch, channels)
+    _check_conv_tensors(conv_weight, conv_ring, channels, batch if seq_slot is None else 0)
+    if tuple(out.shape) != (batch, channels) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{batch}, {channels}]")
+    if seq_slot is not None:
+        _rows_i32("seq_slot", seq_slot, batch, dev)
+    pos_t, pos_s = _rows_i32("conv_pos", conv_pos, batch, dev)
+    rc = nat.load().ria_conv1d_step(batch, channels, _ptr(x), dtype_code(x), stride, _ptr(conv_weight),
+                                    _ptr(conv_ring), _ptr(seq_slot), _ptr(pos_t), pos_s, _ptr(out), dtype_code(out),
+                                    _stream(dev))
+    nat.check(rc, "ria_conv1d_step")
+    return out
+
+
+def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """x * rsqrt(sum(x^2, -1) + eps) in fp32 (ria_l2norm)."""
+    _require_gpu("x", x)
+    xc = x.contiguous()
+    out = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    dim = int(x.shape[-1])
+    rows = xc.numel() // dim if dim else 0
+    rc = nat.load().ria_l2norm(rows, dim, _ptr(xc), dtype_code(xc), float(eps), _ptr(out), _stream(x.device))
+    nat.check(rc, "ria_l2norm")
+    return out
+
+
+def rope_table(position: int, inv_freq: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(cos, sin) of position * inv_freq over both halves, fp32 (ria_rope_table)."""
+    _require_gpu("inv_freq", inv_freq)
+    rope_dim = 2 * int(inv_freq.numel())
+    cos = torch.empty(rope_dim, device=inv_freq.device, dtype=torch.float32)
+    sin = torch.empty_like(cos)
+    rc = nat.load().ria_rope_table(int(position), _ptr(inv_freq), rope_dim, _ptr(cos), _ptr(sin),
+                                   _stream(inv_freq.device))
+    nat.check(rc, "ria_rope_table")
+    return cos, sin
+
+
+def rope_apply(x: torch.Tensor, position: int, inv_freq: torch.Tensor) -> torch.Tensor:
+    """Partial half-split rotary embedding of fp32 rows (ria_rope_apply)."""
+    _require_gpu("x", x)
+    _require_gpu("inv_freq", inv_freq, x.device)
+    if x.dtype != torch.float32:
+        raise ValueError("rope_apply expects fp32 input")
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    head_dim = int(x.shape[-1])
+    rows = xc.numel() // head_dim
+    rc = nat.load().ria_rope_apply(rows, head_dim, 2 * int(inv_freq.numel()), _ptr(xc), _ptr(out), _ptr(inv_freq),
+                                   int(position), _stream(x.device))
+    nat.check(rc, "ria_rope_apply")
+    return out
+
+
+def _check_kv_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, num_kv_heads: int) -> int:
+    if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise ValueError("KV caches must be bf16")
+    if k_cache.dim() != 4 or tuple(k_cache.shape[1:]) != (num_kv_heads, PAGE_TOKENS, ATTN_HEAD_DIM):
+        raise ValueError(f"k_cache must be [pages, {num_kv_heads}, 16, 256], got {tuple(k_cache.shape)}")
+    if v_cache.dim() != 4 or tuple(v_cache.shape[1:]) != (num_kv_heads, ATTN_HEAD_DIM, PAGE_TOKENS):
+        raise ValueError(f"v_cache must be [pages, {num_kv_heads}, 256, 16], got {tuple(v_cache.shape)}")
+    if k_cache.shape[0] != v_cache.shape[0] or not k_cache.is_contiguous() or not v_cache.is_contiguous():
+        raise ValueError("k_cache / v_cache must be contiguous with equal page counts")
+    return int(k_cache.shape[0])
+
+
+def _check_page_table(page_table: torch.Tensor, dev: torch.device) -> int:
+    _require_gpu("page_table", page_table, dev)
+    if page_table.dtype != torch.int32 or page_table.dim() != 2 or page_table.stride(1) != 1:
+        raise ValueError("page_table must be int32 [pool, max_pages] with contiguous rows")
+    return int(page_table.stride(0))
+
+
+def kv_append(
+    k: torch.Tensor,
+    v: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    *,
+    positions: torch.Tensor | int,
+    slots: torch.Tensor | int,
+    inv_freq: torch.Tensor,
+    seq_slot: torch.Tensor | None = None,
+) -> None:
+    """RoPE k and append k, v of one token per sequence into the paged cache (ria_kv_append)."""
+    batch = int(k.shape[0])
+    num_kv_heads = int(k.shape[1]) if k.dim() == 3 else int(k.numel() // max(batch, 1) // ATTN_HEAD_DIM)
+    dev = k.device
+    for name, t in (("k", k), ("v", v), ("k_cache", k_cache), ("v_cache", v_cache), ("inv_freq", inv_freq),
+                    ("seq_slot", seq_slot)):
+        _require_gpu(name, t, dev)
+    ks = _row_stride("k", k, batch, num_kv_heads * ATTN_HEAD_DIM)
+    vs = _row_stride("v", v, batch, num_kv_heads * ATTN_HEAD_DIM)
+    pages = _check_kv_cache(k_cache, v_cache, num_kv_heads)
+    pts = _check_page_table(page_table, dev)
+    if seq_slot is None and page_table.shape[0] < batch:
+        raise ValueError("page table has fewer rows than batch")
+    pos_t, pos_s = _rows_i32("positions", positions, batch, dev)
+    slot_t, slot_s = _rows_i32("slots", slots, batch, dev)
+    if slot_t is None and slot_s >= page_table.shape[1] * PAGE_TOKENS:
+        raise ValueError(f"slot {slot_s} beyond the page table's {page_table.shape[1] * PAGE_TOKENS} tokens")
+    if seq_slot is not None:
+        _rows_i32("seq_slot", seq_slot, batch, dev)
+    rc = nat.load().ria_kv_append(batch, num_kv_heads, _ptr(k), dtype_code(k), ks, _ptr(v), dtype_code(v), vs,
+                                  _ptr(k_cache), _ptr(v_cache), pages, _ptr(page_table), pts, _ptr(seq_slot),
+                                  _ptr(pos_t), pos_s, _ptr(slot_t), slot_s, _ptr(inv_freq), 2 * int(inv_freq.numel()),
+                                  _stream(dev))
+    nat.check(rc, "ria_kv_append")
+
+
+def attn_decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, max_ctx: int,
+                                split_tokens: int = 0) -> int:
+    return int(nat.load().ria_attn_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_ctx, split_tokens))
+
+
+def attn_decode(
+    q: torch.Tensor,
+    gate: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    positions: torch.Tensor | int,
+    ctx_lens: torch.Tensor | int,
+    max_ctx: int,
+    inv_freq: torch.Tensor | None,
+    scale: float,
+    workspace: torch.Tensor,
+    seq_slot: torch.Tensor | None = None,
+    split_tokens: int = 0,
+) -> torch.Tensor:
+    """Split-K paged GQA decode with RoPE on q and a sigmoid gate (ria_attn_decode)."""
+    batch = int(q.shape[0])
+    num_q_heads = int(q.shape[1])
+    num_kv_heads = int(k_cache.shape[1])
+    dev = q.device
+    for name, t in (("q", q), ("gate", gate), ("k_cache", k_cache), ("v_cache", v_cache), ("out", out),
+                    ("inv_freq", inv_freq), ("workspace", workspace), ("seq_slot", seq_slot)):
+        _require_gpu(name, t, dev)
+    qs = _row_stride("q", q, batch, num_q_heads * ATTN_HEAD_DIM)
+    gs = _row_stride("gate", gate, batch, num_q_heads * ATTN_HEAD_DIM)
+    pages = _check_kv_cache(k_cache, v_cache, num_kv_heads)
+    pts = _check_page_table(page_table, dev)
+    if max_ctx > page_table.shape[1] * PAGE_TOKENS:
+        raise ValueError(f"max_ctx {max_ctx} exceeds the page table capacity {page_table.shape[1] * PAGE_TOKENS}")
+    if seq_slot is None and page_table.shape[0] < batch:
+        raise ValueError("page table has fewer rows than batch")
+    if tuple(out.shape) != (batch, num_q_heads, ATTN_HEAD_DIM) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{batch}, {num_q_heads}, 256]")
+    if not workspace.is_contiguous():
+        raise ValueError("workspace must be contiguous")
+    pos_t, pos_s = _rows_i32("positions", positions, batch, dev)
+    ctx_t, ctx_s = _rows_i32("ctx_lens", ctx_lens, batch, dev)
+    if seq_slot is not None:
+        _rows_i32("seq_slot", seq_slot, batch, dev)
+    rope_dim = 0 if inv_freq is None else 2 * int(inv_freq.numel())
+    ws_bytes = workspace.numel() * workspace.element_size()
+    rc = nat.load().ria_attn_decode(batch, num_q_heads, num_kv_heads, _ptr(q), dtype_code(q), qs, _ptr(gate),
+                                    dtype_code(gate), gs, _ptr(k_cache), _ptr(v_cache), pages, _ptr(page_table), pts,
+                                    _ptr(seq_slot), _ptr(pos_t), pos_s, _ptr(ctx_t), ctx_s, int(max_ctx),
+                                    _ptr(inv_freq), rope_dim, float(scale), int(split_tokens), _ptr(workspace),
+                                    ws_bytes, _ptr(out), dtype_code(out), _stream(dev))
+    nat.check(rc, "ria_attn_decode")
+    return out
+
+
+def kv_gather(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    *,
+    batch: int,
+    start: int,
+    count: int,
+    seq_slot: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Logical-order copy of tokens [start, start+count) out of the paged cache (ria_kv_gather)."""
+    num_kv_heads = int(k_cache.shape[1])
+    dev = k_cache.device
+    pages = _check_kv_cache(k_cache, v_cache, num_kv_heads)
+    pts = _check_page_table(page_table, dev)
+    if start < 0 or count < 0 or start + count > page_table.shape[1] * PAGE_TOKENS:
+        raise ValueError("gather range outside the page table")
+    if seq_slot is not None:
+        _rows_i32("seq_slot", seq_slot, batch, dev)
+    k_out = torch.empty((batch, num_kv_heads, count, ATTN_HEAD_DIM), device=dev, dtype=torch.bfloat16)
+    v_out = torch.empty_like(k_out)
+    rc = nat.load().ria_kv_gather(batch, num_kv_heads, _ptr(k_cache), _ptr(v_cache), pages, _ptr(page_table), pts,
+                                  _ptr(seq_slot), int(start), int(count), _ptr(k_out), _ptr(v_out), _stream(dev))
+    nat.check(rc, "ria_kv_gather")
+    return k_out, v_out

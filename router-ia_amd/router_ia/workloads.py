@@ -1,0 +1,73 @@
+"""Seeded synthetic inputs for the hybrid-attention workloads.
+
+Shapes are the model family's (16 QK heads x 128, 32 V heads x 128, conv over
+8192 channels; full attention 16 Q / 2 KV heads x 256).  Projections are
+excluded: each layer step gets its q/k/v, gate and decay inputs directly.
+
+Gating inputs are drawn so that the raw-gate formula of the reference
+(qwen36_attention_cache.py:242-250) reproduces the requested distributions:
+    b_raw ~ N(0,1)         -> beta = sigmoid(b_raw)
+    a_raw ~ N(0,1), A_log ~ U(-4,0) per head, dt_bias = 0
+                           -> g = -exp(A_log) * softplus(a_raw) = -softplus(N(0,1)) * exp(U(-4,0))
+"""
+
+from __future__ import annotations
+
+import torch
+
+NUM_K_HEADS = 16
+NUM_V_HEADS = 32
+HEAD_DIM = 128
+CONV_DIM = (2 * NUM_K_HEADS + NUM_V_HEADS) * HEAD_DIM
+FULL_Q_HEADS = 16
+FULL_KV_HEADS = 2
+FULL_HEAD_DIM = 256
+
+
+def _gen(seed: int, device: torch.device | str) -> torch.Generator:
+    g = torch.Generator(device=torch.device(device))
+    g.manual_seed(seed)
+    return g
+
+
+def gdn_layer_params(seed: int, device="cpu") -> dict[str, torch.Tensor]:
+    """Per-layer constants: conv weight ~N(0, 0.5) bf16 [8192,1,4], A_log ~U(-4,0), dt_bias = 0."""
+    g = _gen(seed, device)
+    conv_weight = (torch.randn((CONV_DIM, 1, 4), generator=g, device=device) * 0.5).to(torch.bfloat16)
+    a_log = torch.rand((NUM_V_HEADS,), generator=g, device=device) * 4.0 - 4.0
+    dt_bias = torch.zeros((NUM_V_HEADS,), device=device)
+    return {"conv_weight": conv_weight, "A_log": a_log, "dt_bias": dt_bias}
+
+
+def gdn_step_inputs(seed: int, steps: int, batch: int, device="cpu") -> dict[str, torch.Tensor]:
+    """Per-token inputs: mixed q|k|v bf16 ~N(0,1) [steps,B,8192], a_raw, b_raw ~N(0,1) [steps,B,32]."""
+    g = _gen(seed, device)
+    mixed = torch.randn((steps, batch, CONV_DIM), generator=g, device=device).to(torch.bfloat16)
+    a_raw = torch.randn((steps, batch, NUM_V_HEADS), generator=g, device=device)
+    b_raw = torch.randn((steps, batch, NUM_V_HEADS), generator=g, device=device)
+    return {"mixed": mixed, "a_raw": a_raw, "b_raw": b_raw}
+
+
+def attn_step_inputs(seed: int, steps: int, batch: int, device="cpu") -> dict[str, torch.Tensor]:
+    """Per-token inputs: q, gate bf16 [steps,B,16,256]; k, v bf16 [steps,B,2,256]; all ~N(0,1)."""
+    g = _gen(seed, device)
+    q = torch.randn((steps, batch, FULL_Q_HEADS, FULL_HEAD_DIM), generator=g, device=device).to(torch.bfloat16)
+    k = torch.randn((steps, batch, FULL_KV_HEADS, FULL_HEAD_DIM), generator=g, device=device).to(torch.bfloat16)
+    v = torch.randn((steps, batch, FULL_KV_HEADS, FULL_HEAD_DIM), generator=g, device=device).to(torch.bfloat16)
+    gate = torch.randn((steps, batch, FULL_Q_HEADS, FULL_HEAD_DIM), generator=g, device=device).to(torch.bfloat16)
+    return {"q": q, "k": k, "v": v, "gate": gate}
+
+
+def prefilled_kv(seed: int, batch: int, tokens: int, device="cpu") -> tuple[torch.Tensor, torch.Tensor]:
+    """Resident KV content bf16 ~N(0,1) [B, 2, T, 256] (keys already positioned)."""
+    g = _gen(seed, device)
+    k = torch.randn((batch, FULL_KV_HEADS, tokens, FULL_HEAD_DIM), generator=g, device=device).to(torch.bfloat16)
+    v = torch.randn((batch, FULL_KV_HEADS, tokens, FULL_HEAD_DIM), generator=g, device=device).to(torch.bfloat16)
+    return k, v
+
+
+def ragged_lengths(seed: int, batch: int, lo: int, hi: int) -> list[int]:
+    """Context lengths uniform in [lo, hi] (inclusive), one per sequence."""
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return [int(x) for x in torch.randint(lo, hi + 1, (batch,), generator=g)]

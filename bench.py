@@ -1,0 +1,343 @@
+#!/usr/bin/env python3
+"""Decode throughput of the 40-layer hybrid attention stack on one MI355X.
+
+Workload (default ``ragged128``): 128 concurrent sequences, context lengths
+uniform in [1024, 32768] (seed 4), 30 Gated DeltaNet layers + 10 GQA
+full-attention layers (layer 4i+3 is full attention), 16-token KV pages with a
+shuffled page table.  Every sequence starts with resident state: DeltaNet
+states ~N(0, 0.02) fp32, conv rings ~N(0, 1) bf16, KV ~N(0, 1) bf16.  Each
+decode step gives every layer fresh synthetic inputs (projections excluded):
+DeltaNet q|k|v + gate logits, attention q, k, v and gate logits, all
+pre-generated in HBM before timing.
+
+One step = one token for every sequence through all 40 layers (append, conv,
+recurrence, attention, gate) followed by the position advance.  Output: one
+JSON line with tok/s, the roofline of the dominant kernel (split-K attention)
+from HIP events around each of its launches, the step-level HBM fraction, and
+the reference CPU path (the oracle's torch-CPU restatement) timed on a
+bounded sample of the same workload on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "router-ia_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+METRIC = "attn-stack decode tok/s (40 layers, B=1..128); state+KV HBM GB/s % of peak"
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, AMD specification
+LAYERS = 40
+NUM_V_HEADS = 32
+NUM_Q_HEADS = 16
+NUM_KV_HEADS = 2
+HEAD_DIM_ATTN = 256
+CONV_DIM = 8192
+
+# Algorithmic bytes (state + KV + activations), per (sequence, layer, token).
+GDN_BYTES_PER_SEQ = 2 * 2_097_152 + 49_152 + 16_384 + 16_384 + 256 + 8_192  # 4,284,672
+GDN_BYTES_PER_LAYER = 65_536  # conv weight, shared by the batch
+ATTN_KV_BYTES_PER_TOKEN = 2 * NUM_KV_HEADS * HEAD_DIM_ATTN * 2  # 2048 B of K+V per context token
+ATTN_APPEND_BYTES = 2_048
+ATTN_ACT_BYTES = 3 * NUM_Q_HEADS * HEAD_DIM_ATTN * 2  # q, gate, out in bf16: 24,576
+SPLITK_Q_BYTES = NUM_Q_HEADS * HEAD_DIM_ATTN * 2  # the split-K launch reads q only
+
+WORKLOADS = {
+    "ragged128": dict(batch=128, lo=1024, hi=32768, seed=4,
+                      desc="40-layer stack, B=128, context U[1024,32768] (seed 4), 16-token pages, shuffled page table"),
+    "batch32": dict(batch=32, lo=8192, hi=8192, seed=2,
+                    desc="40-layer stack, B=32, context 8192 (seed 2), 16-token pages, shuffled page table"),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def is_full(layer: int) -> bool:
+    return layer % 4 == 3
+
+
+def step_bytes(ctx: list[int]) -> int:
+    """Algorithmic bytes of one decode step; ctx[b] = context incl. the new token."""
+    n_lin = sum(1 for layer in range(LAYERS) if not is_full(layer))
+    n_full = LAYERS - n_lin
+    b = len(ctx)
+    lin = n_lin * (b * GDN_BYTES_PER_SEQ + GDN_BYTES_PER_LAYER)
+    full = n_full * sum(ATTN_KV_BYTES_PER_TOKEN * t + ATTN_APPEND_BYTES + ATTN_ACT_BYTES for t in ctx)
+    return lin + full
+
+
+def run_gpu(args, wl) -> dict:
+    from router_ia import _native as nat
+    from router_ia import kernels as K
+    from router_ia import workloads as W
+    from router_ia.batched_state import BatchedAttentionState
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    batch = wl["batch"]
+    lengths = W.ragged_lengths(wl["seed"], batch, wl["lo"], wl["hi"])
+    total_new = args.warmup + args.steps
+    max_context = max(lengths) + total_new + 16
+    num_pages = sum((n + total_new + 15) // 16 for n in lengths) + batch
+    log(f"[bench] {wl['desc']}: B={batch}, mean context {sum(lengths) / batch:.0f}, max {max(lengths)}, "
+        f"{num_pages} pages/layer")
+    st = BatchedAttentionState(batch, max_context, num_pages=num_pages, device=dev, page_shuffle_seed=wl["seed"])
+    st.set_positions(lengths)
+    st.reserve(total_new)
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(wl["seed"])
+    # Resident state.
+    for li in range(st.num_linear_layers):
+        st.linear_states[li].normal_(0.0, 0.02, generator=gen)
+        st.conv_rings[li].normal_(0.0, 1.0, generator=gen)
+    for fi in range(st.num_full_layers):
+        st.kv.k[fi].normal_(0.0, 1.0, generator=gen)
+        st.kv.v[fi].normal_(0.0, 1.0, generator=gen)
+    # Per-layer constants.
+    conv_w = [(torch.randn((CONV_DIM, 1, 4), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+              for _ in range(st.num_linear_layers)]
+    a_log = [torch.rand((NUM_V_HEADS,), generator=gen, device=dev) * 4.0 - 4.0 for _ in range(st.num_linear_layers)]
+    dt_bias = [torch.zeros((NUM_V_HEADS,), device=dev) for _ in range(st.num_linear_layers)]
+    # Per-step inputs for every layer, resident before timing.
+    n_lin, n_full = st.num_linear_layers, st.num_full_layers
+    mixed = torch.randn((total_new, n_lin, batch, CONV_DIM), generator=gen, device=dev, dtype=torch.bfloat16)
+    gate_ab = torch.randn((total_new, n_lin, 2, batch, NUM_V_HEADS), generator=gen, device=dev)
+    qg = torch.randn((total_new, n_full, 2, batch, NUM_Q_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev,
+                     dtype=torch.bfloat16)
+    kv_in = torch.randn((total_new, n_full, 2, batch, NUM_KV_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev,
+                        dtype=torch.bfloat16)
+    gdn_out = torch.empty((batch, NUM_V_HEADS, 128), device=dev, dtype=torch.bfloat16)
+    attn_out = torch.empty((batch, NUM_Q_HEADS, HEAD_DIM_ATTN), device=dev, dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    log(f"[bench] resident: {torch.cuda.memory_allocated(dev) / 2**30:.1f} GiB allocated")
+
+    attn_events: list[tuple[torch.cuda.Event, torch.cuda.Event, int]] = []
+    gdn_events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
+
+    def one_step(s: int, timed: bool) -> None:
+        max_ctx = st.max_seen + 1
+        ctx_bytes = None
+        for layer in range(LAYERS):
+            if is_full(layer):
+                fi = layer // 4
+                kc, vc = st.kv.layer(fi)
+                K.kv_append(kv_in[s, fi, 0], kv_in[s, fi, 1], kc, vc, st.kv.page_table, positions=st.tokens_seen,
+                            slots=st.tokens_seen, inv_freq=st.inv_freq)
+                kw = dict(positions=st.tokens_seen, ctx_lens=st.ctx_lens, max_ctx=max_ctx, inv_freq=st.inv_freq,
+                          scale=st.scale, workspace=st.workspace)
+                if timed:
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                K.attn_decode(qg[s, fi, 0], qg[s, fi, 1], kc, vc, st.kv.page_table, attn_out,
+                              phase=nat.RIA_ATTN_SPLITK, **kw)
+                if timed:
+                    e1.record()
+                    if ctx_bytes is None:
+                        ctx_bytes = sum(ATTN_KV_BYTES_PER_TOKEN * (n + 1) + SPLITK_Q_BYTES for n in st._host_seen)
+                    attn_events.append((e0, e1, ctx_bytes))
+                K.attn_decode(qg[s, fi, 0], qg[s, fi, 1], kc, vc, st.kv.page_table, attn_out,
+                              phase=nat.RIA_ATTN_COMBINE, **kw)
+            else:
+                li = layer - layer // 4
+                if timed:
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                K.gdn_decode(mixed[s, li], st.linear_states[li], gate_ab[s, li, 0], gate_ab[s, li, 1], gdn_out,
+                             num_k_heads=st.num_k_heads, num_v_heads=st.num_v_heads, conv_weight=conv_w[li],
+                             conv_ring=st.conv_rings[li], conv_pos=st.tokens_seen, gate_mode=nat.RIA_GATE_RAW,
+                             A_log=a_log[li], dt_bias=dt_bias[li])
+                if timed:
+                    e1.record()
+                    gdn_events.append((e0, e1))
+        st.advance()
+
+    for s in range(args.warmup):
+        one_step(s, False)
+    torch.cuda.synchronize()
+    ctx_at_start = [n + 1 for n in st._host_seen]
+    algo_bytes = sum(step_bytes([c + i for c in ctx_at_start]) for i in range(args.steps))
+    log(f"[bench] warmup {args.warmup} steps done; timing {args.steps} steps")
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record()
+    for s in range(args.warmup, args.warmup + args.steps):
+        one_step(s, True)
+        if (s - args.warmup) % 64 == 63:
+            log(f"[bench] step {s - args.warmup + 1}/{args.steps} issued")
+    t_end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    elapsed_s = t_start.elapsed_time(t_end) / 1e3
+    attn_ms = [e0.elapsed_time(e1) for e0, e1, _ in attn_events]
+    attn_bytes = [nb for _, _, nb in attn_events]
+    gdn_ms = [e0.elapsed_time(e1) for e0, e1 in gdn_events]
+    attn_avg_s = sum(attn_ms) / len(attn_ms) / 1e3
+    attn_bytes_avg = sum(attn_bytes) / len(attn_bytes)
+    gdn_avg_s = sum(gdn_ms) / len(gdn_ms) / 1e3
+    gdn_bytes = batch * GDN_BYTES_PER_SEQ + GDN_BYTES_PER_LAYER
+    achieved = attn_bytes_avg / attn_avg_s / 1e9
+    step_gbps = algo_bytes / elapsed_s / 1e9
+    return {
+        "batch": batch,
+        "lengths": lengths,
+        "elapsed_s": elapsed_s,
+        "wall_s": wall,
+        "tok_s": batch * args.steps / elapsed_s,
+        "ms_per_step": elapsed_s / args.steps * 1e3,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attn_splitk_kernel (ria_attn_decode split-K phase)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": round(attn_bytes_avg),
+            "avg_launch_us": round(attn_avg_s * 1e6, 2),
+            "launches": len(attn_ms),
+        },
+        "kernels": {
+            "gdn_decode_kernel": {
+                "avg_launch_us": round(gdn_avg_s * 1e6, 2),
+                "algorithmic_bytes_per_launch": gdn_bytes,
+                "achieved_GBps": round(gdn_bytes / gdn_avg_s / 1e9, 1),
+                "frac": round(gdn_bytes / gdn_avg_s / 1e9 / HBM_PEAK_GBPS, 4),
+                "launches": len(gdn_ms),
+            },
+            "attn_splitk_kernel_share_of_step": round(sum(attn_ms) / 1e3 / elapsed_s, 4),
+            "gdn_decode_kernel_share_of_step": round(sum(gdn_ms) / 1e3 / elapsed_s, 4),
+        },
+        "step_hbm": {
+            "algorithmic_bytes_per_step": round(algo_bytes / args.steps),
+            "achieved_GBps": round(step_gbps, 1),
+            "frac": round(step_gbps / HBM_PEAK_GBPS, 4),
+        },
+    }
+
+
+def run_cpu_baseline(wl, lengths: list[int], n_seqs: int, n_steps: int) -> dict:
+    """The reference CPU path (oracle restatement: fp32, torch.cat KV) on a sample of the workload."""
+    from oracle import qwen36_cpu as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    sample = lengths[:n_seqs]
+    gen = torch.Generator().manual_seed(wl["seed"])
+    states = []
+    for n in sample:
+        s = O.SequenceState()
+        s.tokens_seen = n
+        for li in range(30):
+            s.linear[li] = torch.randn((1, 32, 128, 128), generator=gen) * 0.02
+            s.conv[li] = torch.randn((1, CONV_DIM, 4), generator=gen).to(torch.bfloat16)
+        for fi in range(10):
+            s.keys[fi] = torch.randn((1, NUM_KV_HEADS, n, HEAD_DIM_ATTN), generator=gen).to(torch.bfloat16).float()
+            s.values[fi] = torch.randn((1, NUM_KV_HEADS, n, HEAD_DIM_ATTN), generator=gen).to(torch.bfloat16).float()
+        states.append(s)
+    conv_w = [(torch.randn((CONV_DIM, 1, 4), generator=gen) * 0.5).to(torch.bfloat16) for _ in range(30)]
+    a_log = [torch.rand((32,), generator=gen) * 4.0 - 4.0 for _ in range(30)]
+    b = len(sample)
+    inputs = []
+    for _ in range(n_steps):
+        per_layer = []
+        for layer in range(LAYERS):
+            if is_full(layer):
+                per_layer.append(tuple(torch.randn(shape, generator=gen).to(torch.bfloat16) for shape in (
+                    (b, 16, 256), (b, 2, 256), (b, 2, 256), (b, 16, 256))))
+            else:
+                per_layer.append((torch.randn((b, CONV_DIM), generator=gen).to(torch.bfloat16),
+                                  torch.randn((b, 32), generator=gen), torch.randn((b, 32), generator=gen)))
+        inputs.append(per_layer)
+    zero_bias = torch.zeros(32)
+    t0 = time.perf_counter()
+    for step in range(n_steps):
+        for layer in range(LAYERS):
+            x = inputs[step][layer]
+            if is_full(layer):
+                O.full_step_batched(states, layer // 4, x[0], x[1], x[2], x[3])
+            else:
+                li = layer - layer // 4
+                beta, g = O.gating(x[1], x[2], a_log[li], zero_bias)
+                O.linear_step_batched(states, li, x[0], conv_w[li], beta, g)
+        for s in states:
+            s.tokens_seen += 1
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(b * n_steps / dt, 4),
+        "unit": "tok/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{b} sequences (rows 0..{b - 1} of the seeded lengths: {sample}), all 40 layers, "
+                   f"{n_steps} decode steps, torch-CPU restatement of the reference (fp32 state and KV, "
+                   f"torch.cat KV append); {dt:.1f} s"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="ragged128")
+    ap.add_argument("--cpu-seqs", type=int, default=8)
+    ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (sequences shard across GPUs "
+              "with no communication; see the sharding design). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    wl = WORKLOADS[args.workload]
+    gpu = run_gpu(args, wl)
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU reference path on a sample")
+        cpu = run_cpu_baseline(wl, gpu["lengths"], args.cpu_seqs, args.cpu_steps)
+    result = {
+        "metric": METRIC,
+        "value": round(gpu["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 state + bf16 KV/activations (fp32 accumulate)",
+        "data": "synthetic (seeded random state, KV and per-layer inputs; projections excluded)",
+        "config": {
+            "workload": wl["desc"],
+            "batch": gpu["batch"],
+            "layers": "30 Gated DeltaNet + 10 GQA full attention",
+            "mean_context": round(sum(gpu["lengths"]) / len(gpu["lengths"])),
+            "decode_steps": args.steps,
+            "parallelism": "single GPU",
+        },
+        "roofline": gpu["roofline"],
+        "step_hbm": gpu["step_hbm"],
+        "kernels": gpu["kernels"],
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

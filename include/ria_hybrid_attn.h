@@ -31,7 +31,10 @@
  *                              keeps the same four inputs as a shifting
  *                              window [1, conv_dim, 4] (:207-209).
  *   conv weight               bf16 [conv_dim, 4] (== [conv_dim, 1, 4])
- *   K cache (one layer)       bf16 [num_pages, Hkv, 16 (token), 256 (dim)]
+ *   K cache (one layer)       bf16 [num_pages, Hkv, 8, 4, 16 (token), 8]: the
+ *                              (page, head) tile in MFMA operand order; key
+ *                              element (token t, dim d) sits at
+ *                              [.., (d % 64) / 8, d / 64, t, d % 8]
  *   V cache (one layer)       bf16 [num_pages, Hkv, 256 (dim), 16 (token)]
  *   page table                i32  [pool, page_table_stride]; logical token
  *                              t of a sequence lives in physical slot
@@ -158,6 +161,16 @@ int ria_kv_append(int batch, int num_kv_heads,
                   const float* inv_freq, int rope_dim, void* stream);
 
 /*
+ * Split size ria_attn_decode would choose for these context lengths (a host
+ * array of `batch` tokens-attended counts): long splits, down to one page
+ * per wave when the batch holds too few pages to occupy the GPU.  Passing
+ * the result as split_tokens lets callers size the workspace once for a
+ * batch they know.  split_tokens = 0 applies the same rule to max_ctx for
+ * every row.
+ */
+int ria_attn_decode_split_tokens(int num_kv_heads, const int32_t* ctx_lens_host, int batch);
+
+/*
  * Workspace bytes ria_attn_decode needs for these sizes (split_tokens = 0
  * selects the automatic split size, as in ria_attn_decode).
  */
@@ -189,6 +202,25 @@ int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads,
                     const float* inv_freq, int rope_dim, float scale, int split_tokens,
                     void* workspace, int64_t workspace_bytes,
                     void* out, int out_dtype, void* stream);
+
+/*
+ * ria_attn_decode in two launches that can be timed apart: RIA_ATTN_SPLITK
+ * writes the per-split partials into the workspace, RIA_ATTN_COMBINE merges
+ * them and applies the gate (it must follow a SPLITK call with the same
+ * arguments on the same stream); RIA_ATTN_BOTH is ria_attn_decode.
+ */
+enum ria_attn_phase { RIA_ATTN_SPLITK = 1, RIA_ATTN_COMBINE = 2, RIA_ATTN_BOTH = 3 };
+
+int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads,
+                          const void* q, int q_dtype, int64_t q_row_stride,
+                          const void* gate, int gate_dtype, int64_t gate_row_stride,
+                          const void* k_cache, const void* v_cache, int num_pages,
+                          const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                          const int32_t* positions, int32_t position_scalar,
+                          const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
+                          const float* inv_freq, int rope_dim, float scale, int split_tokens,
+                          void* workspace, int64_t workspace_bytes,
+                          void* out, int out_dtype, int phase, void* stream);
 
 /*
  * Copy tokens [start, start + count) of each sequence out of the paged cache

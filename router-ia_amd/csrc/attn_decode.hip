@@ -9,9 +9,11 @@
 //
 // Decode is HBM-bound (2 KiB of KV per token per KV head pair, 8 FLOP/B), so
 // the design goal is one streaming pass over K and V:
-//   * pages: K as [page][kv_head][16 tok][256 dim], V transposed as
-//     [page][kv_head][256 dim][16 tok]; each (page, head) tile is 8 KiB and a
-//     wavefront reads it as one contiguous block.
+//   * pages: each (page, KV head) tile is 8 KiB.  K is stored in the MFMA
+//     A-operand order [kk 8][g 4][tok 16][8 dims] (dim d -> kk = (d%64)/8,
+//     g = d/64), so the eight 16-byte loads of a lane are each part of one
+//     contiguous 1 KiB wavefront read; V is stored transposed,
+//     [256 dim][16 tok], so the P V operand is a contiguous 512 B read.
 //   * scores S^T = K Q^T on MFMA 16x16x32 bf16 (tokens x query heads, the
 //     8 query heads of a KV head padded to 16); the output layout leaves each
 //     lane with 4 tokens of one head, which is exactly the B operand of the
@@ -29,6 +31,12 @@
 namespace ria {
 
 constexpr int kMaxGroup = 16;  // query heads per KV head handled by one MFMA tile
+constexpr int kTileElems = kPageTokens * kAttnHeadDim;  // 4096 bf16 per (page, KV head)
+
+// Offset of K element (token t, dim d) inside its (page, KV head) tile.
+__host__ __device__ __forceinline__ int k_tile_offset(int t, int d) {
+  return ((((d & 63) >> 3) * 4 + (d >> 6)) * kPageTokens + t) * 8 + (d & 7);
+}
 
 struct AttnArgs {
   const void* q;
@@ -50,7 +58,7 @@ struct AttnArgs {
   float scale;
   int split_tokens;
   int max_splits;
-  float* ws_stats;  // [parts][group][2]  (max, sum)
+  float* ws_stats;  // [parts][group][2]  (max in log2 units, sum)
   float* ws_acc;    // [parts][group][256]
   int num_q_heads;
   int num_kv_heads;
@@ -112,12 +120,12 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   if (phys < 0 || phys >= a.num_pages) return;  // host guarantees allocation; never write out of the pool
   const int off = slot % kPageTokens;
   const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
-  a.k_cache[(tile * kPageTokens + off) * kAttnHeadDim + d] = f32_to_bf16_bits(kr);
+  a.k_cache[tile * kTileElems + k_tile_offset(off, d)] = f32_to_bf16_bits(kr);
   a.v_cache[(tile * kAttnHeadDim + d) * kPageTokens + off] = f32_to_bf16_bits(vv);
 }
 
 template <int QT>
-__global__ __launch_bounds__(256) void attn_splitk_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
@@ -133,34 +141,52 @@ __global__ __launch_bounds__(256) void attn_splitk_kernel(AttnArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int n = lane & 15;  // MFMA column: query head (scores) / dim row (PV)
-  const int g4 = lane >> 4; // lane group
+  const int n = lane & 15;   // MFMA column: query head (scores) / dim row (PV)
+  const int g4 = lane >> 4;  // lane group
 
-  // ---- Q: rotate the group's query heads into LDS (one thread per dim),
-  // then each lane (head n, group g4) packs dims [64*g4, 64*g4 + 64) as bf16.
-  __shared__ float q_lds[8][kAttnHeadDim];
+  // LDS: the fp32 rotated query rows share space with the end-of-split merge.
+  __shared__ float sm_o[4][8][kAttnHeadDim];  // group <= 8 on this path (checked on the host)
+  __shared__ uint4 q_pk[8][64];               // bf16 Q operand, [kk][lane]
+  __shared__ float sm_m[4][kMaxGroup];
+  __shared__ float sm_l[4][kMaxGroup];
+  float (*q_lds)[kAttnHeadDim] = sm_o[0];
+
+  // ---- Q: rotate the group's query heads into LDS (one thread per dim).
+  float rc = 1.f, rs = 0.f;
+  if (a.rope_dim == 64 && tid < 64) {
+    const float ang = mul_rn(pos, a.inv_freq[tid & 31]);
+    rc = cosf(ang);
+    rs = sinf(ang);
+  }
   for (int h = 0; h < G; ++h) {
     const int64_t base = (int64_t)b * a.q_stride + (int64_t)(kvh * G + h) * kAttnHeadDim;
     float x = load_act<QT>(a.q, base + tid);
     if (a.rope_dim == 64 && tid < 64) {
       const float partner = load_act<QT>(a.q, base + (tid ^ 32));
-      const float ang = mul_rn(pos, a.inv_freq[tid & 31]);
-      const float c = cosf(ang), s = sinf(ang);
-      x = add_rn(mul_rn(x, c), mul_rn(tid < 32 ? -partner : partner, s));
+      x = add_rn(mul_rn(x, rc), mul_rn(tid < 32 ? -partner : partner, rs));
     }
     q_lds[h][tid] = x;
   }
   __syncthreads();
-  bf16x8 qop[8];
+  // Pack the B operand: lane (head n, group g4) holds dims 64*g4 + 8*kk + j.
+  if (wave < 2) {
+    const int kk = wave * 4;  // waves 0 and 1 pack kk 0-3 and 4-7
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) {
+    for (int k2 = 0; k2 < 4; ++k2) {
+      uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float v = n < G ? q_lds[n & 7][64 * g4 + 8 * kk + j] : 0.f;
-      qop[kk][j] = __builtin_bit_cast(__bf16, f32_to_bf16_bits(v));
+      for (int j = 0; j < 4; ++j) {
+        const float lo = n < G ? q_lds[n & 7][64 * g4 + 8 * (kk + k2) + 2 * j] : 0.f;
+        const float hi = n < G ? q_lds[n & 7][64 * g4 + 8 * (kk + k2) + 2 * j + 1] : 0.f;
+        w[j] = static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+      }
+      q_pk[kk + k2][lane] = uint4{w[0], w[1], w[2], w[3]};
     }
   }
+  __syncthreads();
 
+  // Scores are kept in log2 units: s2 = (q . k) * scale * log2(e).
+  const float sl2 = a.scale * 1.4426950408889634f;
   f32x4 o[16];
 #pragma unroll
   for (int db = 0; db < 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -169,74 +195,94 @@ __global__ __launch_bounds__(256) void attn_splitk_kernel(AttnArgs a) {
   const int page0 = tok0 / kPageTokens;
   const int page_end = (tok1 + kPageTokens - 1) / kPageTokens;
   const int32_t* pt = a.page_table + (int64_t)row * a.pt_stride;
-  for (int p = page0 + wave; p < page_end; p += 4) {
+
+  auto load_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
     int phys = pt[p];
     phys = (phys < 0 || phys >= a.num_pages) ? 0 : phys;  // unallocated entries never fault
     const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
-    const uint4* kp = reinterpret_cast<const uint4*>(a.k_cache + (tile * kPageTokens + n) * kAttnHeadDim + 64 * g4);
-    const uint16_t* vp = a.v_cache + tile * (kAttnHeadDim * kPageTokens) + 4 * g4;
-    uint4 kraw[8];
+    const u32x4* kp = reinterpret_cast<const u32x4*>(a.k_cache + tile * kTileElems) + lane;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) kraw[kk] = kp[kk];
-    uint2 vraw[16];
+    for (int kk = 0; kk < 8; ++kk) kr[kk] = ld_stream(kp + kk * 64);
+    const uint16_t* vp = a.v_cache + tile * kTileElems + n * kPageTokens + 4 * g4;
 #pragma unroll
-    for (int db = 0; db < 16; ++db) vraw[db] = *reinterpret_cast<const uint2*>(vp + (db * 16 + n) * kPageTokens);
+    for (int db = 0; db < 16; ++db) vr[db] = ld_stream(reinterpret_cast<const u32x2*>(vp + db * 16 * kPageTokens));
+  };
 
+  auto compute_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-        __builtin_bit_cast(bf16x8, kraw[kk]), qop[kk], sc, 0, 0, 0);
-
+    for (int kk = 0; kk < 8; ++kk)
+      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[kk]),
+                                                   __builtin_bit_cast(bf16x8, q_pk[kk][lane]), sc, 0, 0, 0);
     const int t_base = p * kPageTokens + 4 * g4;
-    const bool tail = (p + 1) * kPageTokens > tok1;
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      sc[i] = (t_base + i < tok1) ? sc[i] * a.scale : -INFINITY;
+      sc[i] = (t_base + i < tok1) ? sc[i] * sl2 : -INFINITY;
       mx = fmaxf(mx, sc[i]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = expf(m_run - m_new);
-    float pr[4];
-    float psum = 0.f;
+    // Lazy rescale: keep the reference max while the page max stays within
+    // 2^8 of it, so the accumulator is rescaled only when it has to be.
+    const bool grow = mx > m_run + 8.0f;
+    if (__any(grow)) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = exp2f(m_run - m_new);
+      l_run *= alpha;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      pr[i] = expf(sc[i] - m_new);
-      psum += pr[i];
+      for (int db = 0; db < 16; ++db) o[db] *= alpha;
+      m_run = m_new;
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
     s16x4 pb;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pb[i] = static_cast<short>(f32_to_bf16_bits(pr[i]));
-    if (tail) {
+    for (int i = 0; i < 4; ++i) {
+      const float pr = exp2f(sc[i] - m_run);
+      l_run += pr;
+      pb[i] = static_cast<short>(f32_to_bf16_bits(pr));
+    }
+    if ((p + 1) * kPageTokens > tok1) {
       // Tokens past the end of the sequence carry whatever the page holds;
       // zero their V so 0 * garbage cannot reach the accumulator.
 #pragma unroll
       for (int db = 0; db < 16; ++db) {
-        uint32_t lo = vraw[db].x, hi = vraw[db].y;
+        uint32_t lo = vr[db].x, hi = vr[db].y;
         if (t_base + 0 >= tok1) lo &= 0xffff0000u;
         if (t_base + 1 >= tok1) lo &= 0x0000ffffu;
         if (t_base + 2 >= tok1) hi &= 0xffff0000u;
         if (t_base + 3 >= tok1) hi &= 0x0000ffffu;
-        vraw[db] = uint2{lo, hi};
+        vr[db] = u32x2{lo, hi};
       }
     }
 #pragma unroll
-    for (int db = 0; db < 16; ++db) {
-      o[db] *= alpha;
-      o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vraw[db]), pb, o[db], 0, 0, 0);
+    for (int db = 0; db < 16; ++db)
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vr[db]), pb, o[db], 0, 0, 0);
+  };
+
+  // Pages wave, wave+4, ...: the next page's loads are issued before the
+  // current page is consumed (two register buffers, loop unrolled by two).
+  int p = page0 + wave;
+  if (p < page_end) {
+    u32x4 kA[8], kB[8];
+    u32x2 vA[16], vB[16];
+    load_page(p, kA, vA);
+    while (true) {
+      int pn = p + 4;
+      if (pn < page_end) load_page(pn, kB, vB);
+      compute_page(p, kA, vA);
+      if (pn >= page_end) break;
+      p = pn;
+      pn = p + 4;
+      if (pn < page_end) load_page(pn, kA, vA);
+      compute_page(p, kB, vB);
+      if (pn >= page_end) break;
+      p = pn;
     }
   }
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
 
-  // ---- merge the four waves through LDS
-  __shared__ float sm_m[4][kMaxGroup];
-  __shared__ float sm_l[4][kMaxGroup];
-  __shared__ float sm_o[4][8][kAttnHeadDim];  // group <= 8 on this path (checked on the host)
+  // ---- merge the four waves through LDS (q_lds is dead: every wave passed the barrier above)
   if (g4 == 0 && n < G) {
     sm_m[wave][n] = m_run;
     sm_l[wave][n] = l_run;
@@ -245,7 +291,7 @@ __global__ __launch_bounds__(256) void attn_splitk_kernel(AttnArgs a) {
 #pragma unroll
     for (int db = 0; db < 16; ++db) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sm_o[wave][n][db * 16 + 4 * g4 + i] = o[db][i];
+      for (int i = 0; i < 4; ++i) sm_o[wave][n & 7][db * 16 + 4 * g4 + i] = o[db][i];
     }
   }
   __syncthreads();
@@ -257,7 +303,7 @@ __global__ __launch_bounds__(256) void attn_splitk_kernel(AttnArgs a) {
     float acc = 0.f, L = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float wt = (sm_m[w][h] == -INFINITY) ? 0.f : expf(sm_m[w][h] - M);
+      const float wt = (sm_m[w][h] == -INFINITY) ? 0.f : exp2f(sm_m[w][h] - M);
       acc = fmaf(wt, sm_o[w][h][tid], acc);
       L = fmaf(wt, sm_l[w][h], L);
     }
@@ -285,7 +331,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   float num = 0.f, den = 0.f;
   for (int s = 0; s < nsplit; ++s) {
     const int64_t ph = (part0 + s) * a.group + hi;
-    const float wt = expf(a.ws_stats[ph * 2] - M);
+    const float wt = exp2f(a.ws_stats[ph * 2] - M);  // stats are in log2 units
     num = fmaf(wt, a.ws_acc[ph * kAttnHeadDim + d], num);
     den = fmaf(wt, a.ws_stats[ph * 2 + 1], den);
   }
@@ -315,21 +361,28 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint16_t* k_cache,
   }
   const int64_t tile = (int64_t)phys * num_kv_heads + kvh;
   const int off = tok % kPageTokens;
-  k_out[o] = k_cache[(tile * kPageTokens + off) * kAttnHeadDim + d];
+  k_out[o] = k_cache[tile * kTileElems + k_tile_offset(off, d)];
   v_out[o] = v_cache[(tile * kAttnHeadDim + d) * kPageTokens + off];
 }
 
 static bool valid_dtype(int dt) { return dt == RIA_DT_BF16 || dt == RIA_DT_F16 || dt == RIA_DT_F32; }
 
-static int auto_split_tokens(int batch, int num_kv_heads, int max_ctx) {
-  // Aim for ~2048 workgroups (8 per CU) while keeping at least one page per
-  // wave and at most 8 pages per wave.
-  const int64_t pages = (int64_t)batch * num_kv_heads * ((max_ctx + kPageTokens - 1) / kPageTokens);
-  int64_t pps = pages / 2048;
+// Pages per split: enough splits for ~1024 busy workgroups (4 per CU), but
+// as long as possible (up to 192 pages = 3072 tokens, 48 pages per wave) so
+// the per-split prologue, merge and partial write stay small next to the
+// KV stream.  Measured on MI355X at B=128, contexts U[1k, 32k], with
+// streaming loads: 1024-token splits reach 71% of HBM peak, 2048-token 74%,
+// 3072-token 75%, 6144-token 65% (too few workgroups).
+int auto_split_tokens(int64_t total_pages) {
+  int64_t pps = total_pages / 1024;
   if (pps < 4) pps = 4;
-  if (pps > 32) pps = 32;
+  if (pps > 192) pps = 192;
   pps = (pps + 3) / 4 * 4;
   return static_cast<int>(pps * kPageTokens);
+}
+
+static int auto_split_tokens(int batch, int num_kv_heads, int max_ctx) {
+  return auto_split_tokens((int64_t)batch * num_kv_heads * ((max_ctx + kPageTokens - 1) / kPageTokens));
 }
 
 static int resolve_split(int batch, int num_kv_heads, int max_ctx, int split_tokens) {
@@ -392,6 +445,13 @@ extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_d
   return check_launch("ria_kv_append");
 }
 
+extern "C" int ria_attn_decode_split_tokens(int num_kv_heads, const int32_t* ctx_lens_host, int batch) {
+  if (!ctx_lens_host || batch <= 0 || num_kv_heads <= 0) return 4 * kPageTokens;
+  int64_t pages = 0;
+  for (int b = 0; b < batch; ++b) pages += (ctx_lens_host[b] + kPageTokens - 1) / kPageTokens;
+  return auto_split_tokens(pages * num_kv_heads);
+}
+
 extern "C" int64_t ria_attn_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_ctx,
                                                    int split_tokens) {
   if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_ctx <= 0) return 0;
@@ -404,13 +464,16 @@ extern "C" int64_t ria_attn_decode_workspace_bytes(int batch, int num_q_heads, i
   return (stats_aligned + parts * group * kAttnHeadDim) * (int64_t)sizeof(float);
 }
 
-extern "C" int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
-                               int64_t q_row_stride, const void* gate, int gate_dtype, int64_t gate_row_stride,
-                               const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
-                               int64_t page_table_stride, const int32_t* seq_slot, const int32_t* positions,
-                               int32_t position_scalar, const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
-                               const float* inv_freq, int rope_dim, float scale, int split_tokens,
-                               void* workspace, int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
+                                     int64_t q_row_stride, const void* gate, int gate_dtype, int64_t gate_row_stride,
+                                     const void* k_cache, const void* v_cache, int num_pages,
+                                     const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                                     const int32_t* positions, int32_t position_scalar, const int32_t* ctx_lens,
+                                     int32_t ctx_scalar, int max_ctx, const float* inv_freq, int rope_dim,
+                                     float scale, int split_tokens, void* workspace, int64_t workspace_bytes,
+                                     void* out, int out_dtype, int phase, void* stream) {
+  if (phase < RIA_ATTN_SPLITK || phase > RIA_ATTN_BOTH)
+    return set_error(RIA_ERR_INVALID, "ria_attn_decode: unknown phase %d", phase);
   if (batch < 0) return set_error(RIA_ERR_INVALID, "ria_attn_decode: batch must be >= 0");
   if (batch == 0) return RIA_OK;
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
@@ -468,6 +531,7 @@ extern "C" int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads, con
   if (a.max_splits > 65535 || batch > 65535) return set_error(RIA_ERR_INVALID, "ria_attn_decode: grid too large");
 
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (phase & RIA_ATTN_SPLITK) {
   dim3 grid(a.max_splits, num_kv_heads, batch);
   if (q_dtype == RIA_DT_BF16)
     hipLaunchKernelGGL((attn_splitk_kernel<RIA_DT_BF16>), grid, dim3(256), 0, st, a);
@@ -477,6 +541,8 @@ extern "C" int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads, con
     hipLaunchKernelGGL((attn_splitk_kernel<RIA_DT_F32>), grid, dim3(256), 0, st, a);
   int rc = check_launch("ria_attn_decode (split-K)");
   if (rc != RIA_OK) return rc;
+  }
+  if (!(phase & RIA_ATTN_COMBINE)) return RIA_OK;
 
   dim3 cgrid(batch * num_q_heads);
 #define RIA_COMB_LAUNCH(GT_, OT_) hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_>), cgrid, dim3(256), 0, st, a)
@@ -494,6 +560,19 @@ extern "C" int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads, con
 #undef RIA_COMB_OT
 #undef RIA_COMB_LAUNCH
   return check_launch("ria_attn_decode (combine)");
+}
+
+extern "C" int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
+                               int64_t q_row_stride, const void* gate, int gate_dtype, int64_t gate_row_stride,
+                               const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
+                               int64_t page_table_stride, const int32_t* seq_slot, const int32_t* positions,
+                               int32_t position_scalar, const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
+                               const float* inv_freq, int rope_dim, float scale, int split_tokens,
+                               void* workspace, int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+  return ria_attn_decode_phase(batch, num_q_heads, num_kv_heads, q, q_dtype, q_row_stride, gate, gate_dtype,
+                               gate_row_stride, k_cache, v_cache, num_pages, page_table, page_table_stride, seq_slot,
+                               positions, position_scalar, ctx_lens, ctx_scalar, max_ctx, inv_freq, rope_dim, scale,
+                               split_tokens, workspace, workspace_bytes, out, out_dtype, RIA_ATTN_BOTH, stream);
 }
 
 extern "C" int ria_kv_gather(int batch, int num_kv_heads, const void* k_cache, const void* v_cache, int num_pages,

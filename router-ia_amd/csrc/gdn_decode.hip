@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
   f32x4 s[RPT];
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
-    s[r] = *reinterpret_cast<const f32x4*>(S + (rg + RG * r) * kGdnHeadDim + col0 + jl);
+    s[r] = ld_stream(reinterpret_cast<const f32x4*>(S + (rg + RG * r) * kGdnHeadDim + col0 + jl));
   }
 
   // Gating (every thread computes the same two scalars).
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     const float ki = k_s[i];
 #pragma unroll
     for (int c = 0; c < 4; ++c) s[r][c] = add_rn(s[r][c], mul_rn(ki, dj[c]));
-    *reinterpret_cast<f32x4*>(S + i * kGdnHeadDim + col0 + jl) = s[r];
+    st_stream(reinterpret_cast<f32x4*>(S + i * kGdnHeadDim + col0 + jl), s[r]);
   }
 
   if (rg == 0) {

@@ -22,6 +22,9 @@ RIA_DT_F16 = 1
 RIA_DT_F32 = 2
 RIA_GATE_PRECOMPUTED = 0
 RIA_GATE_RAW = 1
+RIA_ATTN_SPLITK = 1
+RIA_ATTN_COMBINE = 2
+RIA_ATTN_BOTH = 3
 
 _c_int = ctypes.c_int
 _c_i32 = ctypes.c_int32
@@ -50,12 +53,19 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _vp, _c_i64,
          _vp, _vp, _c_i32, _vp, _c_i32, _vp, _c_int, _vp],
     ),
+    "ria_attn_decode_split_tokens": (_c_int, [_c_int, _vp, _c_int]),
     "ria_attn_decode_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "ria_attn_decode": (
         _c_int,
         [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _vp,
          _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _c_f32, _c_int, _vp, _c_i64,
          _vp, _c_int, _vp],
+    ),
+    "ria_attn_decode_phase": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _vp,
+         _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _c_f32, _c_int, _vp, _c_i64,
+         _vp, _c_int, _c_int, _vp],
     ),
     "ria_kv_gather": (
         _c_int,

@@ -81,8 +81,13 @@ class BatchedAttentionState:
         self._min_headroom = 0  # min over rows of (KV capacity - tokens seen)
         self.inv_freq = rope_inv_freq(rope_theta, rope_dim).to(dev)
         self.scale = 256 ** -0.5
-        ws = K.attn_decode_workspace_bytes(max_seqs, num_q_heads, num_kv_heads, max_context, split_tokens)
-        self.workspace = torch.empty(max(ws, 4), dtype=torch.uint8, device=dev)
+        self._fixed_split = split_tokens > 0
+        self._size_workspace()
+
+    def _size_workspace(self) -> None:
+        ws = K.attn_decode_workspace_bytes(self.max_seqs, self.num_q_heads, self.num_kv_heads, self.max_context,
+                                           self.split_tokens)
+        self.workspace = torch.empty(max(ws, 4), dtype=torch.uint8, device=self.device)
 
     # ---------------------------------------------------------------- bookkeeping
     def set_positions(self, lengths: list[int]) -> None:
@@ -95,6 +100,11 @@ class BatchedAttentionState:
         self._ensure([n + 1 for n in self._host_seen])
         self.tokens_seen.copy_(torch.tensor(self._host_seen, dtype=torch.int32))
         self.ctx_lens.copy_(self.tokens_seen + 1)
+        if not self._fixed_split and self.num_full_layers > 0:
+            # Choose the split once for this batch's real lengths (the kernel's
+            # own default only sees the longest context).
+            self.split_tokens = K.attn_decode_split_tokens(self.num_kv_heads, [n + 1 for n in self._host_seen])
+            self._size_workspace()
 
     def reserve(self, extra_tokens: int) -> None:
         """Allocate KV pages so every row can take `extra_tokens` more tokens without host work."""

@@ -218,11 +218,19 @@ def rope_apply(x: torch.Tensor, position: int, inv_freq: torch.Tensor) -> torch.
     return out
 
 
+K_TILE_SHAPE = (8, 4, PAGE_TOKENS, 8)  # (dim % 64) // 8, dim // 64, token, dim % 8
+
+
+def k_tile_index(token: torch.Tensor | int, dim: torch.Tensor | int):
+    """Index of key element (token, dim) inside a K page tile of shape K_TILE_SHAPE."""
+    return (dim % 64) // 8, dim // 64, token, dim % 8
+
+
 def _check_kv_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, num_kv_heads: int) -> int:
     if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
         raise ValueError("KV caches must be bf16")
-    if k_cache.dim() != 4 or tuple(k_cache.shape[1:]) != (num_kv_heads, PAGE_TOKENS, ATTN_HEAD_DIM):
-        raise ValueError(f"k_cache must be [pages, {num_kv_heads}, 16, 256], got {tuple(k_cache.shape)}")
+    if k_cache.dim() != 6 or tuple(k_cache.shape[1:]) != (num_kv_heads, *K_TILE_SHAPE):
+        raise ValueError(f"k_cache must be [pages, {num_kv_heads}, 8, 4, 16, 8], got {tuple(k_cache.shape)}")
     if v_cache.dim() != 4 or tuple(v_cache.shape[1:]) != (num_kv_heads, ATTN_HEAD_DIM, PAGE_TOKENS):
         raise ValueError(f"v_cache must be [pages, {num_kv_heads}, 256, 16], got {tuple(v_cache.shape)}")
     if k_cache.shape[0] != v_cache.shape[0] or not k_cache.is_contiguous() or not v_cache.is_contiguous():
@@ -275,6 +283,12 @@ def kv_append(
     nat.check(rc, "ria_kv_append")
 
 
+def attn_decode_split_tokens(num_kv_heads: int, ctx_lens: list[int]) -> int:
+    """Split size the decode kernel's heuristic picks for these context lengths."""
+    arr = (ctypes.c_int32 * len(ctx_lens))(*[int(x) for x in ctx_lens])
+    return int(nat.load().ria_attn_decode_split_tokens(num_kv_heads, ctypes.cast(arr, ctypes.c_void_p), len(ctx_lens)))
+
+
 def attn_decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, max_ctx: int,
                                 split_tokens: int = 0) -> int:
     return int(nat.load().ria_attn_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_ctx, split_tokens))
@@ -296,8 +310,12 @@ def attn_decode(
     workspace: torch.Tensor,
     seq_slot: torch.Tensor | None = None,
     split_tokens: int = 0,
+    phase: int = nat.RIA_ATTN_BOTH,
 ) -> torch.Tensor:
-    """Split-K paged GQA decode with RoPE on q and a sigmoid gate (ria_attn_decode)."""
+    """Split-K paged GQA decode with RoPE on q and a sigmoid gate (ria_attn_decode_phase).
+
+    phase selects the split-K launch, the combine launch or both (the default).
+    """
     batch = int(q.shape[0])
     num_q_heads = int(q.shape[1])
     num_kv_heads = int(k_cache.shape[1])
@@ -323,11 +341,11 @@ def attn_decode(
         _rows_i32("seq_slot", seq_slot, batch, dev)
     rope_dim = 0 if inv_freq is None else 2 * int(inv_freq.numel())
     ws_bytes = workspace.numel() * workspace.element_size()
-    rc = nat.load().ria_attn_decode(batch, num_q_heads, num_kv_heads, _ptr(q), dtype_code(q), qs, _ptr(gate),
-                                    dtype_code(gate), gs, _ptr(k_cache), _ptr(v_cache), pages, _ptr(page_table), pts,
-                                    _ptr(seq_slot), _ptr(pos_t), pos_s, _ptr(ctx_t), ctx_s, int(max_ctx),
-                                    _ptr(inv_freq), rope_dim, float(scale), int(split_tokens), _ptr(workspace),
-                                    ws_bytes, _ptr(out), dtype_code(out), _stream(dev))
+    rc = nat.load().ria_attn_decode_phase(batch, num_q_heads, num_kv_heads, _ptr(q), dtype_code(q), qs, _ptr(gate),
+                                          dtype_code(gate), gs, _ptr(k_cache), _ptr(v_cache), pages, _ptr(page_table),
+                                          pts, _ptr(seq_slot), _ptr(pos_t), pos_s, _ptr(ctx_t), ctx_s, int(max_ctx),
+                                          _ptr(inv_freq), rope_dim, float(scale), int(split_tokens), _ptr(workspace),
+                                          ws_bytes, _ptr(out), dtype_code(out), int(phase), _stream(dev))
     nat.check(rc, "ria_attn_decode")
     return out
 

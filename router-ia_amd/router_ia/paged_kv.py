@@ -8,8 +8,10 @@ logical token t to physical slot ``page_table[row][t // 16] * 16 + t % 16``.
 All full layers of a sequence share one page table (they hold the same token
 positions), so pages are allocated once per 16 tokens for all layers.
 
-Page layout per layer (bf16):
-    K  [num_pages, Hkv, 16 tokens, 256 dims]
+Page layout per layer (bf16), one 8 KiB tile per (page, KV head):
+    K  [num_pages, Hkv, 8, 4, 16 tokens, 8]  key (token t, dim d) at
+       [.., (d % 64) // 8, d // 64, t, d % 8]: the order in which the decode
+       kernel's MFMA operand loads read it, one contiguous 1 KiB per load
     V  [num_pages, Hkv, 256 dims, 16 tokens]   (transposed inside the page)
 """
 
@@ -19,7 +21,7 @@ import random
 
 import torch
 
-from .kernels import ATTN_HEAD_DIM, PAGE_TOKENS
+from .kernels import ATTN_HEAD_DIM, K_TILE_SHAPE, PAGE_TOKENS
 
 
 class PageAllocator:
@@ -90,7 +92,7 @@ class PagedKVCache:
         self.num_layers = num_layers
         self.num_kv_heads = num_kv_heads
         self.alloc = PageAllocator(num_pages, max_seqs, max_pages_per_seq, shuffle_seed=shuffle_seed)
-        self.k = torch.zeros((num_layers, num_pages, num_kv_heads, PAGE_TOKENS, ATTN_HEAD_DIM),
+        self.k = torch.zeros((num_layers, num_pages, num_kv_heads, *K_TILE_SHAPE),
                              dtype=torch.bfloat16, device=self.device)
         self.v = torch.zeros((num_layers, num_pages, num_kv_heads, ATTN_HEAD_DIM, PAGE_TOKENS),
                              dtype=torch.bfloat16, device=self.device)
@@ -143,9 +145,17 @@ class PagedKVCache:
         offs = (tok % PAGE_TOKENS).to(self.device)
         kb = k.to(device=self.device, dtype=torch.bfloat16)
         vb = v.to(device=self.device, dtype=torch.bfloat16)
+        dims = torch.arange(ATTN_HEAD_DIM, device=self.device)
+        kk, g, j = (dims % 64) // 8, dims // 64, dims % 8
+        pg, of = pages[:, None], offs[:, None]
         for h in range(self.num_kv_heads):
-            self.k[layer, pages, h, offs, :] = kb[:, h, :]
+            self.k[layer, pg, h, kk[None, :], g[None, :], of, j[None, :]] = kb[:, h, :]
             self.v[layer, pages, h, :, offs] = vb[:, h, :]
+
+    def key_row(self, layer: int, page: int, head: int, offset: int) -> torch.Tensor:
+        """The 256-dim key stored at (page, head, token offset), in dim order."""
+        tile = self.k[layer, page, head]  # [8 (kk), 4 (g), 16, 8 (j)]
+        return tile[:, :, offset, :].permute(1, 0, 2).reshape(ATTN_HEAD_DIM)
 
     def layer(self, idx: int) -> tuple[torch.Tensor, torch.Tensor]:
         return self.k[idx], self.v[idx]

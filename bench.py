@@ -77,6 +77,20 @@ def step_bytes(ctx: list[int]) -> int:
     return lin + full
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_stack_ragged128_hbm_traffic.md"
+
+
+def profiled_traffic(kernel: str) -> dict | None:
+    """HBM bytes per launch of `kernel` from the committed FETCH_SIZE/WRITE_SIZE profile."""
+    if not TRAFFIC_PROFILE.is_file():
+        return None
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 6 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+            return {"bytes": int(parts[3]), "algorithmic": int(parts[5]), "source": TRAFFIC_PROFILE.name}
+    return None
+
+
 def run_gpu(args, wl) -> dict:
     from router_ia import _native as nat
     from router_ia import kernels as K
@@ -206,6 +220,7 @@ def run_gpu(args, wl) -> dict:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": None,
+            "traffic_note": None,
             "algorithmic_bytes_per_launch": round(attn_bytes_avg),
             "avg_launch_us": round(attn_avg_s * 1e6, 2),
             "launches": len(attn_ms),
@@ -295,7 +310,17 @@ def main() -> int:
     ap.add_argument("--cpu-seqs", type=int, default=8)
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="only run a plain device copy of this many bytes three times (counter calibration)")
     args = ap.parse_args()
+    if args.copy_bytes:
+        src = torch.ones(args.copy_bytes // 4, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copied {src.numel() * 4} bytes x3", file=sys.stderr)
+        return 0
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (sequences shard across GPUs "
               "with no communication; see the sharding design). Run with --gpus 1.", file=sys.stderr)
@@ -305,6 +330,12 @@ def main() -> int:
         return 2
     wl = WORKLOADS[args.workload]
     gpu = run_gpu(args, wl)
+    prof = profiled_traffic("attn_splitk_kernel") if args.workload == "ragged128" else None
+    if prof:
+        gpu["roofline"]["traffic"] = prof["bytes"]
+        gpu["roofline"]["traffic_note"] = (
+            f"FETCH_SIZE*2.0 + WRITE_SIZE per launch from {prof['source']} (rocprofv3 --pmc, same workload); "
+            f"algorithmic bytes of those launches {prof['algorithmic']}")
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU reference path on a sample")

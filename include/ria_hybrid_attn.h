@@ -31,11 +31,15 @@
  *                              keeps the same four inputs as a shifting
  *                              window [1, conv_dim, 4] (:207-209).
  *   conv weight               bf16 [conv_dim, 4] (== [conv_dim, 1, 4])
- *   K cache (one layer)       bf16 [num_pages, Hkv, 8, 4, 16 (token), 8]: the
+ *   K cache (one layer)       kv_dtype [num_pages, Hkv, 8, 4, 16 (token), 8]: the
  *                              (page, head) tile in MFMA operand order; key
  *                              element (token t, dim d) sits at
  *                              [.., (d % 64) / 8, d / 64, t, d % 8]
- *   V cache (one layer)       bf16 [num_pages, Hkv, 256 (dim), 16 (token)]
+ *   V cache (one layer)       kv_dtype [num_pages, Hkv, 256 (dim), 16 (token)]
+ *                              kv_dtype is RIA_DT_BF16 or RIA_DT_F16: bf16
+ *                              for bf16 activations, fp16 when the
+ *                              projections run in fp16 (fp16 keeps the
+ *                              reference's fp16 values exactly).
  *   page table                i32  [pool, page_table_stride]; logical token
  *                              t of a sequence lives in physical slot
  *                              page_table[row][t / 16] * 16 + t % 16.  The
@@ -154,7 +158,7 @@ int ria_rope_apply(int64_t rows, int head_dim, int rope_dim, const float* x,
 int ria_kv_append(int batch, int num_kv_heads,
                   const void* k, int k_dtype, int64_t k_row_stride,
                   const void* v, int v_dtype, int64_t v_row_stride,
-                  void* k_cache, void* v_cache, int num_pages,
+                  void* k_cache, void* v_cache, int kv_dtype, int num_pages,
                   const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
                   const int32_t* positions, int32_t position_scalar,
                   const int32_t* slots, int32_t slot_scalar,
@@ -195,7 +199,7 @@ int64_t ria_attn_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_h
 int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads,
                     const void* q, int q_dtype, int64_t q_row_stride,
                     const void* gate, int gate_dtype, int64_t gate_row_stride,
-                    const void* k_cache, const void* v_cache, int num_pages,
+                    const void* k_cache, const void* v_cache, int kv_dtype, int num_pages,
                     const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
                     const int32_t* positions, int32_t position_scalar,
                     const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
@@ -214,7 +218,7 @@ enum ria_attn_phase { RIA_ATTN_SPLITK = 1, RIA_ATTN_COMBINE = 2, RIA_ATTN_BOTH =
 int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads,
                           const void* q, int q_dtype, int64_t q_row_stride,
                           const void* gate, int gate_dtype, int64_t gate_row_stride,
-                          const void* k_cache, const void* v_cache, int num_pages,
+                          const void* k_cache, const void* v_cache, int kv_dtype, int num_pages,
                           const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
                           const int32_t* positions, int32_t position_scalar,
                           const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
@@ -224,7 +228,8 @@ int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads,
 
 /*
  * Copy tokens [start, start + count) of each sequence out of the paged cache
- * into logical order: k_out, v_out bf16 [batch, Hkv, count, 256].  The
+ * into logical order: k_out, v_out [batch, Hkv, count, 256] in the cache's
+ * 16-bit element type (bf16 or fp16; the copy is bit-exact).  The
  * inverse of the append's slot mapping; used to materialise the reference's
  * contiguous full_keys / full_values view (qwen36_attention_cache.py:365-372).
  */

@@ -246,3 +246,67 @@ def full_step_batched(states: list[SequenceState], layer: int, q: torch.Tensor, 
             st.tokens_seen)
         outs.append(out)
     return torch.cat(outs, dim=0)
+
+
+# ----------------------------------------------------------------------------- layer composites
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """v2/src/router_ia/qwen36_op_probe.py:55-67: fp32 RMSNorm with (1 + w), cast back to x's dtype."""
+    x32 = x.float()
+    out = x32 * torch.rsqrt(x32.pow(2).mean(dim=-1, keepdim=True) + EPS)
+    return (out * (1.0 + weight.float())).to(x.dtype)
+
+
+def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """v2/src/router_ia/qwen36_gated_norm_probe.py:19-36 (first output)."""
+    x32 = x.float()
+    normalized = (x32 * torch.rsqrt(x32.pow(2).mean(dim=-1, keepdim=True) + EPS)).to(x.dtype)
+    weighted = weight.reshape(1, 1, -1) * normalized
+    return (weighted * F.silu(z.float())).to(x.dtype)
+
+
+def linear_layer_step(w: dict[str, torch.Tensor], st: SequenceState, layer: int, x0: torch.Tensor,
+                      gpu_dtypes: bool = False) -> torch.Tensor:
+    """qwen36_attention_cache.py:224-282 for one token of one sequence (projections included).
+
+    w holds the layer's tensors under their checkpoint suffixes.  With
+    gpu_dtypes the reference's CUDA-path casts are applied (bf16 h, fp16
+    projections, :229-233); otherwise its CPU path (fp32).
+    """
+    proj = (lambda t: t.to(torch.float16)) if gpu_dtypes else (lambda t: t.float())
+    h = rmsnorm(x0, w["input_layernorm.weight"])
+    h_c = h.to(torch.bfloat16 if gpu_dtypes else torch.float32)
+    qkv_w = proj(w["linear_attn.in_proj_qkv.weight"])
+    mixed = F.linear(h_c.to(qkv_w.dtype), qkv_w).reshape(1, CONV_DIM)
+    mixed, st.conv[layer] = causal_conv1d_step(st.conv.get(layer), mixed, w["linear_attn.conv1d.weight"])
+    q, k, v = split_qkv(mixed)
+    a_w, b_w = proj(w["linear_attn.in_proj_a.weight"]), proj(w["linear_attn.in_proj_b.weight"])
+    a_raw = F.linear(h_c.to(a_w.dtype), a_w).reshape(1, NUM_V_HEADS).float()
+    b_raw = F.linear(h_c.to(b_w.dtype), b_w).reshape(1, NUM_V_HEADS).float()
+    beta, g = gating(a_raw, b_raw, w["linear_attn.A_log"].reshape(1, -1), w["linear_attn.dt_bias"].reshape(1, -1))
+    attn, st.linear[layer] = gated_delta_step(st.linear.get(layer), q, k, v, beta, g)
+    z_w = proj(w["linear_attn.in_proj_z.weight"])
+    z = F.linear(h_c.to(z_w.dtype), z_w).reshape(1, NUM_V_HEADS, 128)
+    gated = gated_rmsnorm(attn, z, w["linear_attn.norm.weight"])
+    out_w = proj(w["linear_attn.out_proj.weight"])
+    g_c = gated.reshape(1, VALUE_DIM).to(out_w.dtype if gpu_dtypes else torch.float32)
+    return x0.reshape(1, -1).float() + F.linear(g_c, out_w).float()
+
+
+def full_layer_step(w: dict[str, torch.Tensor], st: SequenceState, layer: int, x0: torch.Tensor,
+                    gpu_dtypes: bool = False) -> torch.Tensor:
+    """qwen36_attention_cache.py:285-324 for one token of one sequence at position st.tokens_seen."""
+    proj = (lambda t: t.to(torch.float16)) if gpu_dtypes else (lambda t: t.float())
+    h = rmsnorm(x0, w["input_layernorm.weight"])
+    h_c = h.to(torch.float16 if gpu_dtypes else torch.float32)
+    q_w, k_w, v_w = (proj(w[f"self_attn.{n}_proj.weight"]) for n in ("q", "k", "v"))
+    q_gate = F.linear(h_c.to(q_w.dtype), q_w).reshape(1, FULL_NUM_HEADS, FULL_HEAD_DIM * 2)
+    q, gate = torch.chunk(q_gate, 2, dim=-1)
+    k = F.linear(h_c.to(k_w.dtype), k_w).reshape(1, FULL_NUM_KV_HEADS, FULL_HEAD_DIM)
+    v = F.linear(h_c.to(v_w.dtype), v_w).reshape(1, FULL_NUM_KV_HEADS, FULL_HEAD_DIM)
+    q = rmsnorm(q, w["self_attn.q_norm.weight"]).float()
+    k = rmsnorm(k, w["self_attn.k_norm.weight"]).float()
+    attn, st.keys[layer], st.values[layer] = full_decode_step(st.keys.get(layer), st.values.get(layer), q, k,
+                                                              v.float(), gate, st.tokens_seen)
+    o_w = proj(w["self_attn.o_proj.weight"])
+    a_c = attn.reshape(1, -1).to(o_w.dtype if gpu_dtypes else torch.float32)
+    return x0.reshape(1, -1).float() + F.linear(a_c, o_w).float()

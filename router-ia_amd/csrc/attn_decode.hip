@@ -20,6 +20,12 @@
 //     P V product, computed as O^T = V^T P^T on MFMA 16x16x16 bf16.  Softmax
 //     statistics and O^T columns therefore live in the same lane and no
 //     cross-lane transpose is needed.
+//   * precision: K and V are exact 16-bit operands (bf16 or fp16 caches); q
+//     and the probabilities P are fp32 values, each carried as a 16-bit pair
+//     hi + lo (hi = round(x), lo = round(x - hi)), so every product runs
+//     twice on MFMA and the operands keep ~16 (bf16) or ~22 (fp16) mantissa
+//     bits.  The kernel is HBM-bound with MFMA to spare; a single bf16 q and
+//     P alone would cost ~2^-9 relative error.
 //   * split-K: a workgroup (4 waves) owns `split_tokens` tokens of one
 //     (sequence, KV head); waves take pages round-robin with an online
 //     softmax, merge through LDS and emit (max, sum, unnormalised acc); a
@@ -99,7 +105,7 @@ __device__ __forceinline__ float rope_elem(float xd, float partner, int d, int r
 }
 
 // One workgroup per (sequence, KV head): rotate k, write k and v into the page.
-template <int KT, int VT>
+template <int KT, int VT, int KVT>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int b = blockIdx.x;
   const int kvh = blockIdx.y;
@@ -120,12 +126,13 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   if (phys < 0 || phys >= a.num_pages) return;  // host guarantees allocation; never write out of the pool
   const int off = slot % kPageTokens;
   const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
-  a.k_cache[tile * kTileElems + k_tile_offset(off, d)] = f32_to_bf16_bits(kr);
-  a.v_cache[(tile * kAttnHeadDim + d) * kPageTokens + off] = f32_to_bf16_bits(vv);
+  a.k_cache[tile * kTileElems + k_tile_offset(off, d)] = Kv16<KVT>::from_f32(kr);
+  a.v_cache[(tile * kAttnHeadDim + d) * kPageTokens + off] = Kv16<KVT>::from_f32(vv);
 }
 
-template <int QT>
+template <int QT, int KVT>
 __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
+  using KV = Kv16<KVT>;
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
@@ -146,7 +153,7 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
 
   // LDS: the fp32 rotated query rows share space with the end-of-split merge.
   __shared__ float sm_o[4][8][kAttnHeadDim];  // group <= 8 on this path (checked on the host)
-  __shared__ uint4 q_pk[8][64];               // bf16 Q operand, [kk][lane]
+  __shared__ uint4 q_pk[2][8][64];            // bf16 Q operand hi / lo, [part][kk][lane]
   __shared__ float sm_m[4][kMaxGroup];
   __shared__ float sm_l[4][kMaxGroup];
   float (*q_lds)[kAttnHeadDim] = sm_o[0];
@@ -168,19 +175,25 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
     q_lds[h][tid] = x;
   }
   __syncthreads();
-  // Pack the B operand: lane (head n, group g4) holds dims 64*g4 + 8*kk + j.
-  if (wave < 2) {
-    const int kk = wave * 4;  // waves 0 and 1 pack kk 0-3 and 4-7
+  // Pack the B operand: lane (head n, group g4) holds dims 64*g4 + 8*kk + j,
+  // as a bf16 hi part and a bf16 remainder.
+  {
+    const int kk0 = wave * 2;  // each wave packs two kk blocks
 #pragma unroll
-    for (int k2 = 0; k2 < 4; ++k2) {
-      uint32_t w[4];
+    for (int k2 = 0; k2 < 2; ++k2) {
+      uint32_t wh[4], wl[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float lo = n < G ? q_lds[n & 7][64 * g4 + 8 * (kk + k2) + 2 * j] : 0.f;
-        const float hi = n < G ? q_lds[n & 7][64 * g4 + 8 * (kk + k2) + 2 * j + 1] : 0.f;
-        w[j] = static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+        const float x0 = n < G ? q_lds[n & 7][64 * g4 + 8 * (kk0 + k2) + 2 * j] : 0.f;
+        const float x1 = n < G ? q_lds[n & 7][64 * g4 + 8 * (kk0 + k2) + 2 * j + 1] : 0.f;
+        const uint16_t h0 = KV::from_f32(x0), h1 = KV::from_f32(x1);
+        const uint16_t l0 = KV::from_f32(x0 - KV::to_f32(h0));
+        const uint16_t l1 = KV::from_f32(x1 - KV::to_f32(h1));
+        wh[j] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+        wl[j] = static_cast<uint32_t>(l0) | (static_cast<uint32_t>(l1) << 16);
       }
-      q_pk[kk + k2][lane] = uint4{w[0], w[1], w[2], w[3]};
+      q_pk[0][kk0 + k2][lane] = uint4{wh[0], wh[1], wh[2], wh[3]};
+      q_pk[1][kk0 + k2][lane] = uint4{wl[0], wl[1], wl[2], wl[3]};
     }
   }
   __syncthreads();
@@ -209,11 +222,17 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
   };
 
   auto compute_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
+    // Re-read the Q operand from LDS every page (an opaque offset keeps the
+    // compiler from hoisting 64 loop-invariant VGPRs out of the page loop).
+    int qoff = lane;
+    asm volatile("" : "+v"(qoff));
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[kk]),
-                                                   __builtin_bit_cast(bf16x8, q_pk[kk][lane]), sc, 0, 0, 0);
+    for (int kk = 0; kk < 8; ++kk) {
+      const uint4 qh = q_pk[0][kk][qoff], ql = q_pk[1][kk][qoff];
+      sc = KV::mfma_k32(kr[kk], u32x4{qh.x, qh.y, qh.z, qh.w}, sc);
+      sc = KV::mfma_k32(kr[kk], u32x4{ql.x, ql.y, ql.z, ql.w}, sc);
+    }
     const int t_base = p * kPageTokens + 4 * g4;
     float mx = -INFINITY;
 #pragma unroll
@@ -234,13 +253,16 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
       for (int db = 0; db < 16; ++db) o[db] *= alpha;
       m_run = m_new;
     }
-    s16x4 pb;
+    uint16_t ph[4], plo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float pr = exp2f(sc[i] - m_run);
       l_run += pr;
-      pb[i] = static_cast<short>(f32_to_bf16_bits(pr));
+      ph[i] = KV::from_f32(pr);
+      plo[i] = KV::from_f32(pr - KV::to_f32(ph[i]));
     }
+    const u32x2 pb = {ph[0] | (uint32_t(ph[1]) << 16), ph[2] | (uint32_t(ph[3]) << 16)};
+    const u32x2 pl = {plo[0] | (uint32_t(plo[1]) << 16), plo[2] | (uint32_t(plo[3]) << 16)};
     if ((p + 1) * kPageTokens > tok1) {
       // Tokens past the end of the sequence carry whatever the page holds;
       // zero their V so 0 * garbage cannot reach the accumulator.
@@ -255,8 +277,10 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
       }
     }
 #pragma unroll
-    for (int db = 0; db < 16; ++db)
-      o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vr[db]), pb, o[db], 0, 0, 0);
+    for (int db = 0; db < 16; ++db) {
+      o[db] = KV::mfma_k16(vr[db], pb, o[db]);
+      o[db] = KV::mfma_k16(vr[db], pl, o[db]);
+    }
   };
 
   // Pages wave, wave+4, ...: the next page's loads are issued before the
@@ -395,13 +419,15 @@ using namespace ria;
 
 extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
                              const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
-                             int num_pages, const int32_t* page_table, int64_t page_table_stride,
+                             int kv_dtype, int num_pages, const int32_t* page_table, int64_t page_table_stride,
                              const int32_t* seq_slot, const int32_t* positions, int32_t position_scalar,
                              const int32_t* slots, int32_t slot_scalar, const float* inv_freq, int rope_dim,
                              void* stream) {
   if (batch < 0 || num_kv_heads <= 0) return set_error(RIA_ERR_INVALID, "ria_kv_append: bad batch/num_kv_heads");
   if (batch == 0) return RIA_OK;
   if (!valid_dtype(k_dtype) || !valid_dtype(v_dtype)) return set_error(RIA_ERR_INVALID, "ria_kv_append: unknown dtype");
+  if (kv_dtype != RIA_DT_BF16 && kv_dtype != RIA_DT_F16)
+    return set_error(RIA_ERR_INVALID, "ria_kv_append: the KV cache must be bf16 or fp16");
   if (!k || !v || !k_cache || !v_cache || !page_table) return set_error(RIA_ERR_INVALID, "ria_kv_append: null pointer");
   if (rope_dim < 0 || rope_dim > 64 || rope_dim % 2) return set_error(RIA_ERR_INVALID, "ria_kv_append: rope_dim must be even and <= 64");
   if (rope_dim > 0 && !inv_freq) return set_error(RIA_ERR_INVALID, "ria_kv_append: inv_freq is null");
@@ -428,11 +454,19 @@ extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_d
   a.num_kv_heads = num_kv_heads;
   dim3 grid(batch, num_kv_heads);
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define RIA_APPEND_LAUNCH(KT_, VT_) hipLaunchKernelGGL((kv_append_kernel<KT_, VT_>), grid, dim3(256), 0, st, a)
-#define RIA_APPEND_VT(KT_)                                           \
-  if (v_dtype == RIA_DT_BF16) RIA_APPEND_LAUNCH(KT_, RIA_DT_BF16);    \
-  else if (v_dtype == RIA_DT_F16) RIA_APPEND_LAUNCH(KT_, RIA_DT_F16); \
-  else RIA_APPEND_LAUNCH(KT_, RIA_DT_F32);
+#define RIA_APPEND_LAUNCH(KT_, VT_)                                                              \
+  if (kv_dtype == RIA_DT_F16)                                                                    \
+    hipLaunchKernelGGL((kv_append_kernel<KT_, VT_, RIA_DT_F16>), grid, dim3(256), 0, st, a);     \
+  else                                                                                           \
+    hipLaunchKernelGGL((kv_append_kernel<KT_, VT_, RIA_DT_BF16>), grid, dim3(256), 0, st, a)
+#define RIA_APPEND_VT(KT_)                 \
+  if (v_dtype == RIA_DT_BF16) {             \
+    RIA_APPEND_LAUNCH(KT_, RIA_DT_BF16);    \
+  } else if (v_dtype == RIA_DT_F16) {       \
+    RIA_APPEND_LAUNCH(KT_, RIA_DT_F16);     \
+  } else {                                  \
+    RIA_APPEND_LAUNCH(KT_, RIA_DT_F32);     \
+  }
   if (k_dtype == RIA_DT_BF16) {
     RIA_APPEND_VT(RIA_DT_BF16)
   } else if (k_dtype == RIA_DT_F16) {
@@ -466,7 +500,7 @@ extern "C" int64_t ria_attn_decode_workspace_bytes(int batch, int num_q_heads, i
 
 extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
                                      int64_t q_row_stride, const void* gate, int gate_dtype, int64_t gate_row_stride,
-                                     const void* k_cache, const void* v_cache, int num_pages,
+                                     const void* k_cache, const void* v_cache, int kv_dtype, int num_pages,
                                      const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
                                      const int32_t* positions, int32_t position_scalar, const int32_t* ctx_lens,
                                      int32_t ctx_scalar, int max_ctx, const float* inv_freq, int rope_dim,
@@ -482,6 +516,8 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
   if (group > 8) return set_error(RIA_ERR_INVALID, "ria_attn_decode: at most 8 query heads per KV head (got %d)", group);
   if (!valid_dtype(q_dtype) || !valid_dtype(gate_dtype) || !valid_dtype(out_dtype))
     return set_error(RIA_ERR_INVALID, "ria_attn_decode: unknown dtype code");
+  if (kv_dtype != RIA_DT_BF16 && kv_dtype != RIA_DT_F16)
+    return set_error(RIA_ERR_INVALID, "ria_attn_decode: the KV cache must be bf16 or fp16");
   if (!q || !gate || !k_cache || !v_cache || !page_table || !out || !workspace)
     return set_error(RIA_ERR_INVALID, "ria_attn_decode: null pointer");
   if (rope_dim != 0 && rope_dim != 64) return set_error(RIA_ERR_INVALID, "ria_attn_decode: rope_dim must be 0 or 64");
@@ -533,12 +569,19 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (phase & RIA_ATTN_SPLITK) {
   dim3 grid(a.max_splits, num_kv_heads, batch);
-  if (q_dtype == RIA_DT_BF16)
-    hipLaunchKernelGGL((attn_splitk_kernel<RIA_DT_BF16>), grid, dim3(256), 0, st, a);
-  else if (q_dtype == RIA_DT_F16)
-    hipLaunchKernelGGL((attn_splitk_kernel<RIA_DT_F16>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((attn_splitk_kernel<RIA_DT_F32>), grid, dim3(256), 0, st, a);
+#define RIA_SPLITK_LAUNCH(QT_)                                                                   \
+  if (kv_dtype == RIA_DT_F16)                                                                    \
+    hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_F16>), grid, dim3(256), 0, st, a);        \
+  else                                                                                           \
+    hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_BF16>), grid, dim3(256), 0, st, a)
+  if (q_dtype == RIA_DT_BF16) {
+    RIA_SPLITK_LAUNCH(RIA_DT_BF16);
+  } else if (q_dtype == RIA_DT_F16) {
+    RIA_SPLITK_LAUNCH(RIA_DT_F16);
+  } else {
+    RIA_SPLITK_LAUNCH(RIA_DT_F32);
+  }
+#undef RIA_SPLITK_LAUNCH
   int rc = check_launch("ria_attn_decode (split-K)");
   if (rc != RIA_OK) return rc;
   }
@@ -564,13 +607,15 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
 
 extern "C" int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
                                int64_t q_row_stride, const void* gate, int gate_dtype, int64_t gate_row_stride,
-                               const void* k_cache, const void* v_cache, int num_pages, const int32_t* page_table,
-                               int64_t page_table_stride, const int32_t* seq_slot, const int32_t* positions,
-                               int32_t position_scalar, const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
-                               const float* inv_freq, int rope_dim, float scale, int split_tokens,
-                               void* workspace, int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
+                               const void* k_cache, const void* v_cache, int kv_dtype, int num_pages,
+                               const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                               const int32_t* positions, int32_t position_scalar, const int32_t* ctx_lens,
+                               int32_t ctx_scalar, int max_ctx, const float* inv_freq, int rope_dim, float scale,
+                               int split_tokens, void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
+                               void* stream) {
   return ria_attn_decode_phase(batch, num_q_heads, num_kv_heads, q, q_dtype, q_row_stride, gate, gate_dtype,
-                               gate_row_stride, k_cache, v_cache, num_pages, page_table, page_table_stride, seq_slot,
+                               gate_row_stride, k_cache, v_cache, kv_dtype, num_pages, page_table, page_table_stride,
+                               seq_slot,
                                positions, position_scalar, ctx_lens, ctx_scalar, max_ctx, inv_freq, rope_dim, scale,
                                split_tokens, workspace, workspace_bytes, out, out_dtype, RIA_ATTN_BOTH, stream);
 }

@@ -50,20 +50,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ria_rope_apply": (_c_int, [_c_i64, _c_int, _c_int, _vp, _vp, _vp, _c_i32, _vp]),
     "ria_kv_append": (
         _c_int,
-        [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _vp, _c_i64,
+        [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp, _c_i64,
          _vp, _vp, _c_i32, _vp, _c_i32, _vp, _c_int, _vp],
     ),
     "ria_attn_decode_split_tokens": (_c_int, [_c_int, _vp, _c_int]),
     "ria_attn_decode_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "ria_attn_decode": (
         _c_int,
-        [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _vp,
+        [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp,
          _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _c_f32, _c_int, _vp, _c_i64,
          _vp, _c_int, _vp],
     ),
     "ria_attn_decode_phase": (
         _c_int,
-        [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _vp,
+        [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp,
          _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _c_f32, _c_int, _vp, _c_i64,
          _vp, _c_int, _c_int, _vp],
     ),

@@ -50,6 +50,7 @@ class BatchedAttentionState:
         device: str | torch.device = "cuda",
         page_shuffle_seed: int | None = None,
         split_tokens: int = 0,
+        kv_dtype: torch.dtype = torch.bfloat16,
     ):
         self.device = torch.device(device)
         if self.device.type != "cuda":
@@ -74,7 +75,8 @@ class BatchedAttentionState:
         if num_pages is None:
             num_pages = max_seqs * max_pages_per_seq
         self.kv = PagedKVCache(num_full_layers, num_pages, max_seqs, max_pages_per_seq,
-                               num_kv_heads=num_kv_heads, device=dev, shuffle_seed=page_shuffle_seed)
+                               num_kv_heads=num_kv_heads, device=dev, shuffle_seed=page_shuffle_seed,
+                               dtype=kv_dtype)
         self.tokens_seen = torch.zeros(max_seqs, dtype=torch.int32, device=dev)
         self.ctx_lens = torch.ones(max_seqs, dtype=torch.int32, device=dev)
         self._host_seen = [0] * max_seqs

@@ -226,9 +226,12 @@ def k_tile_index(token: torch.Tensor | int, dim: torch.Tensor | int):
     return (dim % 64) // 8, dim // 64, token, dim % 8
 
 
+KV_DTYPES = (torch.bfloat16, torch.float16)
+
+
 def _check_kv_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, num_kv_heads: int) -> int:
-    if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
-        raise ValueError("KV caches must be bf16")
+    if k_cache.dtype not in KV_DTYPES or v_cache.dtype != k_cache.dtype:
+        raise ValueError("KV caches must both be bf16 or both fp16")
     if k_cache.dim() != 6 or tuple(k_cache.shape[1:]) != (num_kv_heads, *K_TILE_SHAPE):
         raise ValueError(f"k_cache must be [pages, {num_kv_heads}, 8, 4, 16, 8], got {tuple(k_cache.shape)}")
     if v_cache.dim() != 4 or tuple(v_cache.shape[1:]) != (num_kv_heads, ATTN_HEAD_DIM, PAGE_TOKENS):
@@ -277,7 +280,8 @@ def kv_append(
     if seq_slot is not None:
         _rows_i32("seq_slot", seq_slot, batch, dev)
     rc = nat.load().ria_kv_append(batch, num_kv_heads, _ptr(k), dtype_code(k), ks, _ptr(v), dtype_code(v), vs,
-                                  _ptr(k_cache), _ptr(v_cache), pages, _ptr(page_table), pts, _ptr(seq_slot),
+                                  _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table), pts,
+                                  _ptr(seq_slot),
                                   _ptr(pos_t), pos_s, _ptr(slot_t), slot_s, _ptr(inv_freq), 2 * int(inv_freq.numel()),
                                   _stream(dev))
     nat.check(rc, "ria_kv_append")
@@ -342,8 +346,8 @@ def attn_decode(
     rope_dim = 0 if inv_freq is None else 2 * int(inv_freq.numel())
     ws_bytes = workspace.numel() * workspace.element_size()
     rc = nat.load().ria_attn_decode_phase(batch, num_q_heads, num_kv_heads, _ptr(q), dtype_code(q), qs, _ptr(gate),
-                                          dtype_code(gate), gs, _ptr(k_cache), _ptr(v_cache), pages, _ptr(page_table),
-                                          pts, _ptr(seq_slot), _ptr(pos_t), pos_s, _ptr(ctx_t), ctx_s, int(max_ctx),
+                                          dtype_code(gate), gs, _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache),
+                                          pages, _ptr(page_table), pts, _ptr(seq_slot), _ptr(pos_t), pos_s, _ptr(ctx_t), ctx_s, int(max_ctx),
                                           _ptr(inv_freq), rope_dim, float(scale), int(split_tokens), _ptr(workspace),
                                           ws_bytes, _ptr(out), dtype_code(out), int(phase), _stream(dev))
     nat.check(rc, "ria_attn_decode")
@@ -369,7 +373,7 @@ def kv_gather(
         raise ValueError("gather range outside the page table")
     if seq_slot is not None:
         _rows_i32("seq_slot", seq_slot, batch, dev)
-    k_out = torch.empty((batch, num_kv_heads, count, ATTN_HEAD_DIM), device=dev, dtype=torch.bfloat16)
+    k_out = torch.empty((batch, num_kv_heads, count, ATTN_HEAD_DIM), device=dev, dtype=k_cache.dtype)
     v_out = torch.empty_like(k_out)
     rc = nat.load().ria_kv_gather(batch, num_kv_heads, _ptr(k_cache), _ptr(v_cache), pages, _ptr(page_table), pts,
                                   _ptr(seq_slot), int(start), int(count), _ptr(k_out), _ptr(v_out), _stream(dev))

@@ -8,7 +8,8 @@ logical token t to physical slot ``page_table[row][t // 16] * 16 + t % 16``.
 All full layers of a sequence share one page table (they hold the same token
 positions), so pages are allocated once per 16 tokens for all layers.
 
-Page layout per layer (bf16), one 8 KiB tile per (page, KV head):
+Page layout per layer (bf16, or fp16 for fp16 activations), one 8 KiB tile
+per (page, KV head):
     K  [num_pages, Hkv, 8, 4, 16 tokens, 8]  key (token t, dim d) at
        [.., (d % 64) // 8, d // 64, t, d % 8]: the order in which the decode
        kernel's MFMA operand loads read it, one contiguous 1 KiB per load
@@ -55,10 +56,12 @@ class PageAllocator:
                 f"sequence row {row} needs {need} pages, page table holds {self.max_pages_per_seq}"
             )
         table = self.tables[row]
+        if need - len(table) > len(self._free):
+            # all-or-nothing: a failed request leaves the row and the free list unchanged
+            raise RuntimeError(f"KV page pool exhausted: row {row} needs {need - len(table)} more pages, "
+                               f"{len(self._free)} free")
         added = []
         while len(table) < need:
-            if not self._free:
-                raise RuntimeError("KV page pool exhausted")
             page = self._free.pop()
             added.append((len(table), page))
             table.append(page)
@@ -87,15 +90,18 @@ class PagedKVCache:
         num_kv_heads: int,
         device: torch.device | str,
         shuffle_seed: int | None = None,
+        dtype: torch.dtype = torch.bfloat16,
     ):
+        if dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("the KV cache holds bf16 or fp16")
         self.device = torch.device(device)
+        self.dtype = dtype
         self.num_layers = num_layers
         self.num_kv_heads = num_kv_heads
         self.alloc = PageAllocator(num_pages, max_seqs, max_pages_per_seq, shuffle_seed=shuffle_seed)
-        self.k = torch.zeros((num_layers, num_pages, num_kv_heads, *K_TILE_SHAPE),
-                             dtype=torch.bfloat16, device=self.device)
-        self.v = torch.zeros((num_layers, num_pages, num_kv_heads, ATTN_HEAD_DIM, PAGE_TOKENS),
-                             dtype=torch.bfloat16, device=self.device)
+        self.k = torch.zeros((num_layers, num_pages, num_kv_heads, *K_TILE_SHAPE), dtype=dtype, device=self.device)
+        self.v = torch.zeros((num_layers, num_pages, num_kv_heads, ATTN_HEAD_DIM, PAGE_TOKENS), dtype=dtype,
+                             device=self.device)
         self.page_table = torch.full((max_seqs, max_pages_per_seq), -1, dtype=torch.int32, device=self.device)
 
     def ensure(self, row: int, n_tokens: int) -> None:
@@ -143,8 +149,8 @@ class PagedKVCache:
         tok = torch.arange(start, start + count)
         pages = torch.tensor(table, dtype=torch.long)[tok // PAGE_TOKENS].to(self.device)
         offs = (tok % PAGE_TOKENS).to(self.device)
-        kb = k.to(device=self.device, dtype=torch.bfloat16)
-        vb = v.to(device=self.device, dtype=torch.bfloat16)
+        kb = k.to(device=self.device, dtype=self.dtype)
+        vb = v.to(device=self.device, dtype=self.dtype)
         dims = torch.arange(ATTN_HEAD_DIM, device=self.device)
         kk, g, j = (dims % 64) // 8, dims // 64, dims % 8
         pg, of = pages[:, None], offs[:, None]

@@ -1,0 +1,60 @@
+"""The C-ABI library loads on the host and exports every declared entry point.
+
+No compute call is made here: only entry points that validate arguments on
+the host and return before touching a GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from router_ia import _native as nat
+
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
+
+
+def _declared() -> set[str]:
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ria_\w+)\s*\(", text, flags=re.M))
+    return names
+
+
+def test_header_declares_entry_points() -> None:
+    names = _declared()
+    assert {"ria_gdn_decode", "ria_attn_decode", "ria_kv_append", "ria_last_error", "ria_abi_version"} <= names
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    lib = ctypes.CDLL(str(nat.library_path()))
+    missing = [n for n in sorted(_declared()) if not hasattr(lib, n)]
+    assert not missing, f"declared in include/ but not exported: {missing}"
+
+
+def test_binding_covers_every_declared_symbol() -> None:
+    assert _declared() == set(nat.SIGNATURES), set(nat.SIGNATURES) ^ _declared()
+
+
+def test_abi_version_and_host_side_validation() -> None:
+    lib = nat.load()
+    assert lib.ria_abi_version() == nat.ABI_VERSION
+    rc = lib.ria_gdn_decode(-1, 16, 32, None, 0, 0, 1, None, None, None, 0, None, None, None, None, 0, 0,
+                            None, None, None, 0, None)
+    assert rc == 1 and b"batch" in lib.ria_last_error()
+    rc = lib.ria_attn_decode(1, 16, 2, None, 0, 4096, None, 0, 4096, None, None, 0, 1, None, 1, None, None, 0,
+                             None, 1, 1, None, 64, 0.0625, 0, None, 0, None, 0, None)
+    assert rc == 1 and b"null" in lib.ria_last_error()
+    assert lib.ria_attn_decode_workspace_bytes(0, 16, 2, 10, 0) == 0
+    assert lib.ria_attn_decode_workspace_bytes(1, 16, 2, 64, 64) > 0
+
+
+@pytest.mark.parametrize("ctx,expect", [([4097], 64), ([8193] * 32, 512), ([32768] * 128, 3072)])
+def test_split_heuristic(ctx, expect) -> None:
+    from router_ia import kernels as K
+
+    assert K.attn_decode_split_tokens(2, ctx) == expect

@@ -227,6 +227,37 @@ int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads,
                           void* out, int out_dtype, int phase, void* stream);
 
 /*
+ * Workspace bytes ria_gdn_prefill needs to process `segment_tokens` tokens
+ * per pass (it walks longer prompts in segments of whole 64-token chunks).
+ */
+int64_t ria_gdn_prefill_workspace_bytes(int num_k_heads, int num_v_heads, int segment_tokens);
+
+/*
+ * Chunked (WY form, chunk 64) Gated DeltaNet prefill of `length` tokens of
+ * one sequence, one layer.  Equal to `length` calls of ria_gdn_decode with
+ * fuse_conv=1, which is the reference's token-by-token prefill
+ * (qwen36_chat_batch.py:255-258 -> qwen36_attention_cache.py:176-266); the
+ * chunk algebra is the one transformers' torch_chunk_gated_delta_rule
+ * evaluates for the reference's HF path (qwen36_linear_attention_hf.py:91-100).
+ *
+ * mixed_qkv  [length, conv_dim] projection outputs before the conv.
+ * conv_ring  bf16 [4, conv_dim] of this sequence; conv_pos = step of token 0.
+ * state      f32 [Hv, 128, 128] of this sequence, updated in place.
+ * gate_a/b   [length, Hv] f32 per token (gate_mode as in ria_gdn_decode).
+ * out        [length, Hv, 128] of out_dtype.
+ * workspace  >= ria_gdn_prefill_workspace_bytes(.., 64) bytes, 256-byte
+ *            aligned; larger workspaces take longer segments.
+ */
+int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads,
+                    const void* mixed_qkv, int x_dtype, int64_t x_row_stride,
+                    const void* conv_weight, void* conv_ring, int32_t conv_pos,
+                    float* state,
+                    const float* gate_a, const float* gate_b, int64_t gate_row_stride,
+                    int gate_mode, const float* A_log, const float* dt_bias,
+                    void* out, int out_dtype,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Copy tokens [start, start + count) of each sequence out of the paged cache
  * into logical order: k_out, v_out [batch, Hkv, count, 256] in the cache's
  * 16-bit element type (bf16 or fp16; the copy is bit-exact).  The

@@ -67,6 +67,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _c_f32, _c_int, _vp, _c_i64,
          _vp, _c_int, _c_int, _vp],
     ),
+    "ria_gdn_prefill_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int]),
+    "ria_gdn_prefill": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _c_i32, _vp, _vp, _vp, _c_i64, _c_int,
+         _vp, _vp, _vp, _c_int, _vp, _c_i64, _vp],
+    ),
     "ria_kv_gather": (
         _c_int,
         [_c_int, _c_int, _vp, _vp, _c_int, _vp, _c_i64, _vp, _c_i32, _c_i32, _vp, _vp, _vp],

@@ -379,3 +379,63 @@ def kv_gather(
                                   _ptr(seq_slot), int(start), int(count), _ptr(k_out), _ptr(v_out), _stream(dev))
     nat.check(rc, "ria_kv_gather")
     return k_out, v_out
+
+
+def gdn_prefill_workspace_bytes(num_k_heads: int, num_v_heads: int, segment_tokens: int) -> int:
+    return int(nat.load().ria_gdn_prefill_workspace_bytes(num_k_heads, num_v_heads, segment_tokens))
+
+
+def gdn_prefill(
+    mixed_qkv: torch.Tensor,
+    state: torch.Tensor,
+    gate_a: torch.Tensor,
+    gate_b: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    num_k_heads: int,
+    num_v_heads: int,
+    conv_weight: torch.Tensor,
+    conv_ring: torch.Tensor,
+    conv_pos: int,
+    workspace: torch.Tensor,
+    gate_mode: int = nat.RIA_GATE_PRECOMPUTED,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Chunked Gated DeltaNet prefill of one sequence (ria_gdn_prefill).
+
+    mixed_qkv [L, conv_dim]; state [Hv, 128, 128] fp32 (updated in place);
+    conv_ring [4, conv_dim] bf16 (updated); gate_a/b [L, Hv]; out [L, Hv, 128].
+    """
+    length = int(mixed_qkv.shape[0])
+    dev = mixed_qkv.device
+    cdim = conv_dim(num_k_heads, num_v_heads)
+    for name, t in (("mixed_qkv", mixed_qkv), ("state", state), ("gate_a", gate_a), ("gate_b", gate_b),
+                    ("out", out), ("conv_weight", conv_weight), ("conv_ring", conv_ring), ("workspace", workspace),
+                    ("A_log", A_log), ("dt_bias", dt_bias)):
+        _require_gpu(name, t, dev)
+    xs = _row_stride("mixed_qkv", mixed_qkv, length, cdim)
+    if state.dtype != torch.float32 or tuple(state.shape) != (num_v_heads, 128, 128) or not state.is_contiguous():
+        raise ValueError(f"state must be contiguous fp32 [{num_v_heads}, 128, 128]")
+    _check_conv_tensors(conv_weight, conv_ring.reshape(1, CONV_RING, cdim), cdim, 1)
+    if gate_a.dtype != torch.float32 or gate_b.dtype != torch.float32:
+        raise ValueError("gate_a / gate_b must be fp32")
+    gs = _row_stride("gate_a", gate_a, length, num_v_heads)
+    if _row_stride("gate_b", gate_b, length, num_v_heads) != gs:
+        raise ValueError("gate_a and gate_b must share a row stride")
+    if tuple(out.shape) != (length, num_v_heads, GDN_HEAD_DIM) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{length}, {num_v_heads}, 128]")
+    if gate_mode == nat.RIA_GATE_RAW:
+        for name, t in (("A_log", A_log), ("dt_bias", dt_bias)):
+            if t is None or t.dtype != torch.float32 or t.numel() != num_v_heads or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous fp32 tensor of {num_v_heads} values")
+    if not workspace.is_contiguous():
+        raise ValueError("workspace must be contiguous")
+    raw = gate_mode == nat.RIA_GATE_RAW
+    rc = nat.load().ria_gdn_prefill(length, num_k_heads, num_v_heads, _ptr(mixed_qkv), dtype_code(mixed_qkv), xs,
+                                    _ptr(conv_weight), _ptr(conv_ring), int(conv_pos), _ptr(state), _ptr(gate_a),
+                                    _ptr(gate_b), gs, int(gate_mode), _ptr(A_log) if raw else None,
+                                    _ptr(dt_bias) if raw else None, _ptr(out), dtype_code(out), _ptr(workspace),
+                                    workspace.numel() * workspace.element_size(), _stream(dev))
+    nat.check(rc, "ria_gdn_prefill")
+    return out

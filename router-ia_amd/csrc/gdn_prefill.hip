@@ -38,14 +38,22 @@ constexpr int kDim = kGdnHeadDim;  // 128
 constexpr int kPadQ = 132;          // fp32 row stride of q / k / v tiles in LDS
 constexpr int kPadT = 68;           // fp32 row stride of the 64x64 matrices in LDS
 
-// Per (chunk, head) phase-A outputs, fp32, in this order inside one record.
-constexpr int kRecWn = 0;                         // -W            [64][128]
-constexpr int kRecU = kRecWn + kChunk * kDim;     //  U            [64][128]
-constexpr int kRecQt = kRecU + kChunk * kDim;     //  exp(G) q     [64][128]
-constexpr int kRecKtT = kRecQt + kChunk * kDim;   //  (exp(G_C-G) k)^T [128][64]
-constexpr int kRecQK = kRecKtT + kDim * kChunk;   //  (q k^T) o D  [64][64]
-constexpr int kRecGl = kRecQK + kChunk * kChunk;  //  exp(G_C)
-constexpr int kRecFloats = kRecGl + 64;           // padded to 256 B
+// Per (chunk, head) phase-A record, consumed by phase B.  Operands are stored
+// pre-split (bf16 hi, bf16 lo) in MFMA 16x16x32 operand order, one 16-byte
+// unit per lane, so phase B loads them as contiguous 1 KiB wavefront reads:
+//   Qt  exp(G) q        A operand, [token tile 4][k-step 4][hi/lo][lane]
+//   Wn  -W              A operand, [token tile 4][k-step 4][hi/lo][lane]
+//   QK  (q k^T) o D     A operand, [token tile 4][k-step 2][hi/lo][lane]
+//   Kt  (exp(G_C-G) k)^T A operand, [dk tile 8][k-step 2][hi/lo][lane]
+//   U   T (beta v)      C tiles in accumulator order, [token tile 4][dim tile 8][lane] x 4 fp32
+//   gl  exp(G_C)
+constexpr int kRecQt = 0;
+constexpr int kRecWn = kRecQt + 4 * 4 * 2 * 64 * 16;
+constexpr int kRecQK = kRecWn + 4 * 4 * 2 * 64 * 16;
+constexpr int kRecKt = kRecQK + 4 * 2 * 2 * 64 * 16;
+constexpr int kRecU = kRecKt + 8 * 2 * 2 * 64 * 16;
+constexpr int kRecGl = kRecU + 4 * 8 * 64 * 16;
+constexpr int kRecBytes = kRecGl + 256;
 
 struct PrefillArgs {
   const void* x;  // [L, conv_dim] projection output (pre-conv), x_dtype
@@ -65,7 +73,7 @@ struct PrefillArgs {
   int64_t gate_stride;
   const float* A_log;
   const float* dt_bias;
-  float* rec;  // [seg_chunks, Hv, kRecFloats]
+  char* rec;   // [seg_chunks, Hv, kRecBytes]
   void* out;   // [L, Hv, 128]
   int num_k_heads;
   int num_v_heads;
@@ -96,6 +104,11 @@ __device__ __forceinline__ f32x4 mfma3(u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl, f
   return acc;
 }
 
+__device__ __forceinline__ u32x4 lds16(const uint16_t* p) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  return u32x4{v.x, v.y, v.z, v.w};
+}
+
 __device__ __forceinline__ void load8(const float* p, float* v) {
   const float4 a = *reinterpret_cast<const float4*>(p);
   const float4 b = *reinterpret_cast<const float4*>(p + 4);
@@ -104,33 +117,56 @@ __device__ __forceinline__ void load8(const float* p, float* v) {
 }
 
 // ---------------------------------------------------------------- conv
-// One thread per channel, a tile of tokens per workgroup row.
+// Two adjacent channels per thread (one 32-bit load per token for bf16
+// inputs), tokens in batches of 8 so several loads are in flight.
 constexpr int kConvTile = 64;
 
 template <int XT>
 __global__ __launch_bounds__(256) void prefill_conv_kernel(PrefillArgs a) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int c = 2 * (blockIdx.x * 256 + threadIdx.x);
   if (c >= a.conv_dim) return;
   const int t_begin = a.tok0 + blockIdx.y * kConvTile;
   const int t_end = min(t_begin + kConvTile, a.tok0 + a.seg_tokens);
-  const uint2 wv = *reinterpret_cast<const uint2*>(a.conv_w + (int64_t)c * kConvTaps);
-  const float w0 = bf16_bits_to_f32(wv.x & 0xffffu), w1 = bf16_bits_to_f32(wv.x >> 16);
-  const float w2 = bf16_bits_to_f32(wv.y & 0xffffu), w3 = bf16_bits_to_f32(wv.y >> 16);
-  auto input = [&](int t) -> float {
-    if (t >= 0) return bf16_bits_to_f32(f32_to_bf16_bits(load_act<XT>(a.x, (int64_t)t * a.x_stride + c)));
-    return bf16_bits_to_f32(a.conv_ring[((a.n0 + t) & 3) * a.conv_dim + c]);
+  const uint4 wv = *reinterpret_cast<const uint4*>(a.conv_w + (int64_t)c * kConvTaps);  // 2 channels x 4 taps
+  const float wa[4] = {bf16_bits_to_f32(wv.x & 0xffffu), bf16_bits_to_f32(wv.x >> 16),
+                       bf16_bits_to_f32(wv.y & 0xffffu), bf16_bits_to_f32(wv.y >> 16)};
+  const float wb[4] = {bf16_bits_to_f32(wv.z & 0xffffu), bf16_bits_to_f32(wv.z >> 16),
+                       bf16_bits_to_f32(wv.w & 0xffffu), bf16_bits_to_f32(wv.w >> 16)};
+  auto input = [&](int t, float& xa, float& xb) {
+    if (t >= 0) {
+      xa = bf16_bits_to_f32(f32_to_bf16_bits(load_act<XT>(a.x, (int64_t)t * a.x_stride + c)));
+      xb = bf16_bits_to_f32(f32_to_bf16_bits(load_act<XT>(a.x, (int64_t)t * a.x_stride + c + 1)));
+    } else {
+      const uint32_t r = *reinterpret_cast<const uint32_t*>(a.conv_ring + ((a.n0 + t) & 3) * a.conv_dim + c);
+      xa = bf16_bits_to_f32(r & 0xffffu);
+      xb = bf16_bits_to_f32(r >> 16);
+    }
   };
-  float h0 = input(t_begin - 3), h1 = input(t_begin - 2), h2 = input(t_begin - 1);
-  for (int t = t_begin; t < t_end; ++t) {
-    const float xv = input(t);
-    float acc = w0 * h0;
-    acc = fmaf(w1, h1, acc);
-    acc = fmaf(w2, h2, acc);
-    acc = fmaf(w3, xv, acc);
-    a.post[(int64_t)(t - a.tok0) * a.conv_dim + c] = f32_to_bf16_bits(silu_f(round_bf16(acc)));
-    h0 = h1;
-    h1 = h2;
-    h2 = xv;
+  float ha[3], hb[3];
+  for (int i = 0; i < 3; ++i) input(t_begin - 3 + i, ha[i], hb[i]);
+  for (int tb = t_begin; tb < t_end; tb += 8) {
+    float xa[8], xb[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (tb + u < t_end) input(tb + u, xa[u], xb[u]);
+      else xa[u] = xb[u] = 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (tb + u >= t_end) break;
+      float acc_a = wa[0] * ha[0], acc_b = wb[0] * hb[0];
+      acc_a = fmaf(wa[1], ha[1], acc_a);
+      acc_b = fmaf(wb[1], hb[1], acc_b);
+      acc_a = fmaf(wa[2], ha[2], acc_a);
+      acc_b = fmaf(wb[2], hb[2], acc_b);
+      acc_a = fmaf(wa[3], xa[u], acc_a);
+      acc_b = fmaf(wb[3], xb[u], acc_b);
+      const uint32_t y = f32_to_bf16_bits(silu_f(round_bf16(acc_a))) |
+                         (uint32_t(f32_to_bf16_bits(silu_f(round_bf16(acc_b)))) << 16);
+      *reinterpret_cast<uint32_t*>(a.post + (int64_t)(tb + u - a.tok0) * a.conv_dim + c) = y;
+      ha[0] = ha[1]; ha[1] = ha[2]; ha[2] = xa[u];
+      hb[0] = hb[1]; hb[1] = hb[2]; hb[2] = xb[u];
+    }
   }
 }
 
@@ -146,52 +182,79 @@ __global__ __launch_bounds__(256) void conv_ring_tail_kernel(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------- phase A
+// LDS regions (bytes) and what they hold over the kernel's steps.
+constexpr int kR1 = 0;                   // q hi/lo [64][136] bf16 -> (beta v)^T hi/lo [128][68] bf16
+constexpr int kR2 = kR1 + 34816;         // k hi/lo [64][136] bf16 -> (beta e^G k)^T hi/lo [128][68]
+constexpr int kR3 = kR2 + 34816;         // L fp32 [64][68]       -> T hi/lo [64][68] bf16
+constexpr int kR4 = kR3 + 17408;         // (q k^T) o D fp32 [64][68] -> -W fp32 [64][132] (with R5)
+constexpr int kR5 = kR4 + 17408;         // (e^{G_C-G} k)^T fp32 [128][68] -> T fp32 [64][68]
+constexpr int kRScal = kR5 + 34816;      // beta, G, scratch
+constexpr int kPrepLdsBytes = kRScal + 4 * 64 * 2 + 4 * 4 * 16 * 17;
+
 template <int XT, int GM>
 __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
   const int cl = blockIdx.x;  // chunk within the segment
   const int h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g4 = lane >> 4;
-  const int chunk = a.chunk0 + cl;
-  const int t0 = chunk * kChunk;  // absolute first token
+  const int t0 = (a.chunk0 + cl) * kChunk;  // absolute first token of the chunk
   const int group = a.num_v_heads / a.num_k_heads;
   const int hk = h / group;
   const int kdim = a.num_k_heads * kDim;
 
-  __shared__ __attribute__((aligned(16))) float smem[3 * kChunk * kPadQ + 2 * kChunk * kPadT + 4 * 16 * 17 + 5 * kChunk];
-  float* qs = smem;                   // [64][kPadQ] q, then exp(G) q
-  float* ks = qs + kChunk * kPadQ;    // [64][kPadQ] k
-  float* vs = ks + kChunk * kPadQ;    // [64][kPadQ] v
-  float* Lm = vs + kChunk * kPadQ;    // [64][kPadT] L
-  float* Tm = Lm + kChunk * kPadT;    // [64][kPadT] T
-  float* Xs = Tm + kChunk * kPadT;    // [4][16][17] per-wave scratch
-  float* beta_s = Xs + 4 * 16 * 17;   // [64]
-  float* G_s = beta_s + kChunk;       // [64]
-  float* eg_s = G_s + kChunk;         // [64] exp(G)
-  float* ss_s = eg_s + kChunk;        // [128] row sums of squares
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kPrepLdsBytes];
+  uint16_t* qhl = reinterpret_cast<uint16_t*>(lds + kR1);  // hi at [0, 64*136), lo after
+  uint16_t* khl = reinterpret_cast<uint16_t*>(lds + kR2);
+  float* Lm = reinterpret_cast<float*>(lds + kR3);
+  float* QKs = reinterpret_cast<float*>(lds + kR4);
+  float* KtS = reinterpret_cast<float*>(lds + kR5);
+  float* beta_s = reinterpret_cast<float*>(lds + kRScal);
+  float* G_s = beta_s + 64;
+  float* Xs = G_s + 64;  // [4][16][17]
+  char* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecBytes;
 
-  // 1. q, k, v rows (post-conv values as the reference sees them), zeros past L.
-  for (int e = tid; e < kChunk * 3 * kDim; e += 256) {
-    const int r = e / (3 * kDim), col = e % (3 * kDim);
-    const int t = t0 + r;
-    float val = 0.f;
-    if (t < a.length) {
-      int c;
-      if (col < kDim) c = hk * kDim + col;
-      else if (col < 2 * kDim) c = kdim + hk * kDim + (col - kDim);
-      else c = 2 * kdim + h * kDim + (col - 2 * kDim);
-      val = through_dtype<XT>(bf16_bits_to_f32(a.post[(int64_t)(t - a.tok0) * a.conv_dim + c]));
+  // Step 1: lane (n, g4) of wave w loads token 16w + n, dims 32s + 8g4 .. +8 of
+  // q, k and v: the MFMA A-operand order, so no transpose is needed later.
+  const int row = 16 * wave + n;
+  const int t = t0 + row;
+  const bool valid = t < a.length;
+  float qv[4][8], kv[4][8], vv[4][8];
+  {
+    const uint16_t* base = a.post + (int64_t)(t - a.tok0) * a.conv_dim;
+    uint4 rq[4], rk[4], rv[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int d = 32 * s + 8 * g4;
+      if (valid) {
+        rq[s] = *reinterpret_cast<const uint4*>(base + hk * kDim + d);
+        rk[s] = *reinterpret_cast<const uint4*>(base + kdim + hk * kDim + d);
+        rv[s] = *reinterpret_cast<const uint4*>(base + 2 * kdim + h * kDim + d);
+      } else {
+        rq[s] = rk[s] = rv[s] = uint4{0u, 0u, 0u, 0u};
+      }
     }
-    float* dst = col < kDim ? qs : (col < 2 * kDim ? ks : vs);
-    dst[r * kPadQ + (col % kDim)] = val;
+    auto unpack = [](uint4 r, float* o) {
+      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o[2 * j] = through_dtype<XT>(bf16_bits_to_f32(w[j] & 0xffffu));
+        o[2 * j + 1] = through_dtype<XT>(bf16_bits_to_f32(w[j] >> 16));
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      unpack(rq[s], qv[s]);
+      unpack(rk[s], kv[s]);
+      unpack(rv[s], vv[s]);
+    }
   }
-  // 2. gates
-  if (tid < kChunk) {
-    const int t = t0 + tid;
+  // Gates and the cumulative decay (sequential, like torch.cumsum).
+  if (wave == 0) {
+    const int tt = t0 + lane;
     float beta = 0.f, g = 0.f;
-    if (t < a.length) {
-      const float ga = a.gate_a[(int64_t)t * a.gate_stride + h];
-      const float gb = a.gate_b[(int64_t)t * a.gate_stride + h];
+    if (tt < a.length) {
+      const float ga = a.gate_a[(int64_t)tt * a.gate_stride + h];
+      const float gb = a.gate_b[(int64_t)tt * a.gate_stride + h];
       if constexpr (GM == RIA_GATE_RAW) {
         beta = sigmoid_f(gb);
         g = -expf(a.A_log[h]) * softplus_f(ga + a.dt_bias[h]);
@@ -200,46 +263,80 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
         g = ga;
       }
     }
-    beta_s[tid] = beta;
-    G_s[tid] = g;
-  }
-  __syncthreads();
-  // 3. cumulative decay (sequential, as torch.cumsum) and row sums of squares
-  if (tid == 0) {
-    float acc = 0.f;
-    for (int i = 0; i < kChunk; ++i) {
-      acc += G_s[i];
-      G_s[i] = acc;
+    beta_s[lane] = beta;
+    G_s[lane] = g;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {
+      float acc = 0.f;
+      for (int i = 0; i < kChunk; ++i) {
+        acc += G_s[i];
+        G_s[i] = acc;
+      }
     }
   }
+  // Step 2: l2norm of the q and k rows (a row is spread over the 4 lane groups).
+  float sq = 0.f, sk = 0.f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sq += mul_rn(qv[s][j], qv[s][j]);
+      sk += mul_rn(kv[s][j], kv[s][j]);
+    }
+  sq += __shfl_xor(sq, 16, 64);
+  sq += __shfl_xor(sq, 32, 64);
+  sk += __shfl_xor(sk, 16, 64);
+  sk += __shfl_xor(sk, 32, 64);
+  const float iq = 1.0f / sqrtf(sq + 1e-6f), ik = 1.0f / sqrtf(sk + 1e-6f);
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      qv[s][j] = mul_rn(mul_rn(qv[s][j], iq), 0.08838834764831845f);
+      kv[s][j] = mul_rn(kv[s][j], ik);
+    }
+  __syncthreads();  // G_s, beta_s ready
+  const float eg = expf(G_s[row]);                    // e^{G_t}
+  const float ekl = expf(G_s[kChunk - 1] - G_s[row]);  // e^{G_C - G_t}
+  const float bt = beta_s[row];
+  // q, k hi/lo rows into LDS; exp(G) q straight to the record (A-operand order).
   {
-    // waves 0-1: q rows, waves 2-3: k rows; 32 rows per wave
-    float* base = wave < 2 ? qs : ks;
-    const int r0 = (wave & 1) * 32;
-    for (int r = 0; r < 32; ++r) {
-      const float* row = base + (r0 + r) * kPadQ;
-      const float s = wave_sum(mul_rn(row[lane], row[lane]) + mul_rn(row[lane + 64], row[lane + 64]));
-      if (lane == 0) ss_s[(wave < 2 ? 0 : 64) + r0 + r] = s;
+    u32x4* qt_rec = reinterpret_cast<u32x4*>(rec + kRecQt);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int d = 32 * s + 8 * g4;
+      u32x4 hi, lo;
+      split8(qv[s], hi, lo);
+      *reinterpret_cast<u32x4*>(qhl + row * 136 + d) = hi;
+      *reinterpret_cast<u32x4*>(qhl + 64 * 136 + row * 136 + d) = lo;
+      split8(kv[s], hi, lo);
+      *reinterpret_cast<u32x4*>(khl + row * 136 + d) = hi;
+      *reinterpret_cast<u32x4*>(khl + 64 * 136 + row * 136 + d) = lo;
+      float tmp[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tmp[j] = qv[s][j] * eg;
+      split8(tmp, hi, lo);
+      qt_rec[((wave * 4 + s) * 2 + 0) * 64 + lane] = hi;
+      qt_rec[((wave * 4 + s) * 2 + 1) * 64 + lane] = lo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) KtS[(d + j) * 68 + row] = kv[s][j] * ekl;  // transposed
     }
   }
   __syncthreads();
-  if (tid < kChunk) eg_s[tid] = expf(G_s[tid]);
-  // 4. l2norm (q also scaled by 128^-0.5)
-  for (int e = tid; e < 2 * kChunk * kDim; e += 256) {
-    const int which = e / (kChunk * kDim), rem = e % (kChunk * kDim);
-    const int r = rem / kDim, d = rem % kDim;
-    float* p = (which == 0 ? qs : ks) + r * kPadQ + d;
-    const float inv = 1.0f / sqrtf(ss_s[which * 64 + r] + 1e-6f);
-    float y = mul_rn(*p, inv);
-    if (which == 0) y = mul_rn(y, 0.08838834764831845f);
-    *p = y;
+  // Step 3: Kt operand to the record; K K^T -> L and Q K^T -> (q k^T) o D.
+  {
+    u32x4* kt_rec = reinterpret_cast<u32x4*>(rec + kRecKt);
+    for (int job = wave; job < 16; job += 4) {
+      const int dt = job >> 1, s = job & 1;
+      float tmp[8];
+      load8(KtS + (16 * dt + n) * 68 + 32 * s + 8 * g4, tmp);
+      u32x4 hi, lo;
+      split8(tmp, hi, lo);
+      kt_rec[((dt * 2 + s) * 2 + 0) * 64 + lane] = hi;
+      kt_rec[((dt * 2 + s) * 2 + 1) * 64 + lane] = lo;
+    }
   }
-  __syncthreads();
-
-  float* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecFloats;
-
-  // 5. K K^T -> L (strict lower, beta_i D_ij) and Q K^T -> (q k^T) o D (j <= i).
-  // 10 lower tiles of each; wave w takes tiles (ti, tj) with index % 4 == w.
   for (int job = wave; job < 20; job += 4) {
     const bool is_q = job >= 10;
     int idx = job % 10, ti = 0;
@@ -248,139 +345,165 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
       ++ti;
     }
     const int tj = idx;
-    const float* A = (is_q ? qs : ks) + (16 * ti + n) * kPadQ;
-    const float* B = ks + (16 * tj + n) * kPadQ;
+    const uint16_t* A = is_q ? qhl : khl;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      float av[8], bv[8];
-      load8(A + 32 * s + 8 * g4, av);
-      load8(B + 32 * s + 8 * g4, bv);
-      u32x4 ah, al, bh, bl;
-      split8(av, ah, al);
-      split8(bv, bh, bl);
-      acc = mfma3(ah, al, bh, bl, acc);
+      const int d = 32 * s + 8 * g4;
+      acc = mfma3(lds16(A + (16 * ti + n) * 136 + d), lds16(A + 64 * 136 + (16 * ti + n) * 136 + d),
+                  lds16(khl + (16 * tj + n) * 136 + d), lds16(khl + 64 * 136 + (16 * tj + n) * 136 + d), acc);
     }
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int i = 16 * ti + 4 * g4 + i4, j = 16 * tj + n;
       const float dec = j <= i ? expf(G_s[i] - G_s[j]) : 0.f;
-      if (is_q) {
-        rec[kRecQK + i * kChunk + j] = j <= i ? acc[i4] * dec : 0.f;
-      } else {
-        Lm[i * kPadT + j] = j < i ? beta_s[i] * acc[i4] * dec : 0.f;
-      }
+      if (is_q) QKs[i * 68 + j] = j <= i ? acc[i4] * dec : 0.f;
+      else Lm[i * 68 + j] = j < i ? beta_s[i] * acc[i4] * dec : 0.f;
     }
   }
-  // Q K^T tiles above the diagonal are zero.
-  for (int e = tid; e < kChunk * kChunk; e += 256) {
-    const int i = e / kChunk, j = e % kChunk;
-    if ((j >> 4) > (i >> 4)) rec[kRecQK + e] = 0.f;
+  for (int e = tid; e < kChunk * kChunk; e += 256) {  // upper tiles of (q k^T) o D are zero
+    const int i = e >> 6, j = e & 63;
+    if ((j >> 4) > (i >> 4)) QKs[i * 68 + j] = 0.f;
   }
   __syncthreads();
-
-  // 6. T = (I + L)^-1, blocked 4x4 over 16x16 blocks.
-  // 6a. diagonal blocks: wave w inverts block w; lane j (< 16) owns column j.
-  if (n == lane) {  // lanes 0..15
+  // Step 4: QK operand to the record; T = (I + L)^-1 into R5 (blocked 4x4 of 16x16).
+  float* Tm = KtS;
+  {
+    u32x4* qk_rec = reinterpret_cast<u32x4*>(rec + kRecQK);
+    for (int job = wave; job < 8; job += 4) {
+      const int w = job >> 1, s = job & 1;
+      float tmp[8];
+      load8(QKs + (16 * w + n) * 68 + 32 * s + 8 * g4, tmp);
+      u32x4 hi, lo;
+      split8(tmp, hi, lo);
+      qk_rec[((w * 2 + s) * 2 + 0) * 64 + lane] = hi;
+      qk_rec[((w * 2 + s) * 2 + 1) * 64 + lane] = lo;
+    }
+  }
+  if (n == lane) {  // lanes 0..15: wave w inverts diagonal block w, lane j owns column j
     const int b0 = 16 * wave;
     float col[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      float s = 0.f;
+      float sacc = 0.f;
 #pragma unroll
-      for (int m = 0; m < i; ++m) s = fmaf(Lm[(b0 + i) * kPadT + b0 + m], col[m], s);
-      col[i] = (i == lane) ? 1.f : (i < lane ? 0.f : -s);
+      for (int m = 0; m < i; ++m) sacc = fmaf(Lm[(b0 + i) * 68 + b0 + m], col[m], sacc);
+      col[i] = (i == lane) ? 1.f : (i < lane ? 0.f : -sacc);
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) Tm[(b0 + i) * kPadT + b0 + lane] = col[i];
+    for (int i = 0; i < 16; ++i) Tm[(b0 + i) * 68 + b0 + lane] = col[i];
   }
   __syncthreads();
-  // 6b. off-diagonal blocks by distance: T_ij = -T_ii (sum_{m=j}^{i-1} L_im T_mj)
-  for (int dist = 1; dist < 4; ++dist) {
+  for (int dist = 1; dist < 4; ++dist) {  // T_ij = -T_ii sum_{m=j}^{i-1} L_im T_mj
     const int bi = wave + dist, bj = wave;
     if (bi < 4) {
       float* X = Xs + wave * 16 * 17;
-      // X = sum_m L_im T_mj ; lane computes 4 entries (r = lane/4*... )
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int e = lane * 4 + q4, r = e >> 4, c = e & 15;
-        float s = 0.f;
+        float sacc = 0.f;
         for (int bm = bj; bm < bi; ++bm)
 #pragma unroll
           for (int m = 0; m < 16; ++m)
-            s = fmaf(Lm[(16 * bi + r) * kPadT + 16 * bm + m], Tm[(16 * bm + m) * kPadT + 16 * bj + c], s);
-        X[r * 17 + c] = s;
+            sacc = fmaf(Lm[(16 * bi + r) * 68 + 16 * bm + m], Tm[(16 * bm + m) * 68 + 16 * bj + c], sacc);
+        X[r * 17 + c] = sacc;
       }
-      __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int e = lane * 4 + q4, r = e >> 4, c = e & 15;
-        float s = 0.f;
+        float sacc = 0.f;
 #pragma unroll
-        for (int m = 0; m < 16; ++m) s = fmaf(Tm[(16 * bi + r) * kPadT + 16 * bi + m], X[m * 17 + c], s);
-        Tm[(16 * bi + r) * kPadT + 16 * bj + c] = -s;
+        for (int m = 0; m < 16; ++m) sacc = fmaf(Tm[(16 * bi + r) * 68 + 16 * bi + m], X[m * 17 + c], sacc);
+        Tm[(16 * bi + r) * 68 + 16 * bj + c] = -sacc;
       }
     }
     __syncthreads();
   }
-  // upper blocks of T are zero (read by the U/W products below)
+  // Step 5: T hi/lo into R3 (L is dead); (beta v)^T and (beta e^G k)^T hi/lo
+  // into R1 / R2 (q, k rows are dead), from the rows still in registers.
+  uint16_t* Thl = reinterpret_cast<uint16_t*>(lds + kR3);  // hi [64][68], lo after
   for (int e = tid; e < kChunk * kChunk; e += 256) {
-    const int i = e / kChunk, j = e % kChunk;
-    if ((j >> 4) > (i >> 4)) Tm[i * kPadT + j] = 0.f;
+    const int i = e >> 6, j = e & 63;
+    const float v = (j >> 4) > (i >> 4) ? 0.f : Tm[i * 68 + j];
+    const uint16_t hb = f32_to_bf16_bits(v);
+    Thl[i * 68 + j] = hb;
+    Thl[64 * 68 + i * 68 + j] = f32_to_bf16_bits(v - bf16_bits_to_f32(hb));
   }
+  uint16_t* vbT = qhl;  // hi [128][68], lo after
+  uint16_t* kbT = khl;
+  __syncthreads();  // q/k rows in R1/R2 no longer read
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = 32 * s + 8 * g4 + j;
+      const float vb = vv[s][j] * bt;
+      const float kb = kv[s][j] * (bt * eg);
+      uint16_t hb = f32_to_bf16_bits(vb);
+      vbT[d * 68 + row] = hb;
+      vbT[128 * 68 + d * 68 + row] = f32_to_bf16_bits(vb - bf16_bits_to_f32(hb));
+      hb = f32_to_bf16_bits(kb);
+      kbT[d * 68 + row] = hb;
+      kbT[128 * 68 + d * 68 + row] = f32_to_bf16_bits(kb - bf16_bits_to_f32(hb));
+    }
   __syncthreads();
-
-  // 7. U = T (beta v) and W = T (beta exp(G) k): 2 x 32 output tiles of 16x16.
+  // Step 6: U = T (beta v) and W = T (beta e^G k), 32 + 32 tiles of 16x16.
+  float* Wst = QKs;  // -W staging [64][132] over R4 + R5 (QK and T fp32 are dead)
+  f32x4* u_rec = reinterpret_cast<f32x4*>(rec + kRecU);
   for (int job = wave; job < 64; job += 4) {
     const bool is_w = job >= 32;
-    const int tt = (job & 31) >> 3, td = job & 7;  // token tile, dim tile
-    const float* src = is_w ? ks : vs;
+    const int tt = (job & 31) >> 3, td = job & 7;
+    const uint16_t* B = is_w ? kbT : vbT;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     const int nsteps = (16 * tt + 15) / 32 + 1;  // T is lower triangular
     for (int s = 0; s < nsteps; ++s) {
-      float av[8], bv[8];
-      load8(Tm + (16 * tt + n) * kPadT + 32 * s + 8 * g4, av);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = 32 * s + 8 * g4 + j;
-        const float sc = is_w ? beta_s[t] * eg_s[t] : beta_s[t];
-        bv[j] = src[t * kPadQ + 16 * td + n] * sc;
-      }
-      u32x4 ah, al, bh, bl;
-      split8(av, ah, al);
-      split8(bv, bh, bl);
-      acc = mfma3(ah, al, bh, bl, acc);
+      const int kofs = 32 * s + 8 * g4;
+      acc = mfma3(lds16(Thl + (16 * tt + n) * 68 + kofs), lds16(Thl + 64 * 68 + (16 * tt + n) * 68 + kofs),
+                  lds16(B + (16 * td + n) * 68 + kofs), lds16(B + 128 * 68 + (16 * td + n) * 68 + kofs), acc);
     }
+    if (is_w) {
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const int r = 16 * tt + 4 * g4 + i4, d = 16 * td + n;
-      if (is_w) rec[kRecWn + r * kDim + d] = -acc[i4];
-      else rec[kRecU + r * kDim + d] = acc[i4];
+      for (int i4 = 0; i4 < 4; ++i4) Wst[(16 * tt + 4 * g4 + i4) * 132 + 16 * td + n] = -acc[i4];
+    } else {
+      u_rec[(tt * 8 + td) * 64 + lane] = acc;
     }
   }
-  // 8. exp(G) q, (exp(G_C - G) k)^T and exp(G_C)
-  const float g_last = G_s[kChunk - 1];
-  for (int e = tid; e < kChunk * kDim; e += 256) {
-    const int r = e / kDim, d = e % kDim;
-    rec[kRecQt + e] = qs[r * kPadQ + d] * eg_s[r];
-    const int dd = e / kChunk, rr = e % kChunk;  // transposed walk for KtT
-    rec[kRecKtT + e] = ks[rr * kPadQ + dd] * expf(g_last - G_s[rr]);
+  __syncthreads();
+  // Step 7: -W operand to the record.
+  {
+    u32x4* wn_rec = reinterpret_cast<u32x4*>(rec + kRecWn);
+    for (int job = wave; job < 16; job += 4) {
+      const int w = job >> 2, s = job & 3;
+      float tmp[8];
+      load8(Wst + (16 * w + n) * 132 + 32 * s + 8 * g4, tmp);
+      u32x4 hi, lo;
+      split8(tmp, hi, lo);
+      wn_rec[((w * 4 + s) * 2 + 0) * 64 + lane] = hi;
+      wn_rec[((w * 4 + s) * 2 + 1) * 64 + lane] = lo;
+    }
   }
-  if (tid == 0) rec[kRecGl] = expf(g_last);
+  if (tid == 0) *reinterpret_cast<float*>(rec + kRecGl) = expf(G_s[kChunk - 1]);
 }
 
 // ---------------------------------------------------------------- phase B
+struct ChunkOps {
+  u32x4 qt[4][2], wn[4][2], qk[2][2], kt[2][2][2];
+  f32x4 u;
+  float gl;
+};
+
 template <int OT>
-__global__ __launch_bounds__(256) void chunk_scan_kernel(PrefillArgs a) {
-  // Workgroup id -> (column block, head) with the 8 column blocks of a head
-  // sharing an XCD (ids congruent mod 8 run on one XCD; 32 heads * cb + h).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void chunk_scan_kernel(PrefillArgs a) {
+  // The 8 column blocks of a head share an XCD (workgroup ids congruent mod 8
+  // run on one XCD; id = 32 * cb + h), so its records are fetched once per L2.
   const int h = blockIdx.x % a.num_v_heads;
   const int cb = blockIdx.x / a.num_v_heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g4 = lane >> 4;
 
-  __shared__ float S32[kDim][17];                                  // state block S[:, cb*16 + c]
+  __shared__ float S32[kDim][17];  // state block S[:, 16 cb + c], fp32
   __shared__ __attribute__((aligned(16))) uint16_t STh[16][kDim + 8];  // S^T hi / lo (bf16)
   __shared__ __attribute__((aligned(16))) uint16_t STl[16][kDim + 8];
   __shared__ __attribute__((aligned(16))) uint16_t VTh[16][kChunk + 8];  // v'^T hi / lo (bf16)
@@ -397,26 +520,40 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(PrefillArgs a) {
   }
   __syncthreads();
 
-  for (int cl = 0; cl < a.seg_chunks; ++cl) {
-    const int chunk = a.chunk0 + cl;
-    const float* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecFloats;
-    // (i) v' = U + Wn S and o_inter = Qt S for token tile `wave`.
-    f32x4 vn, oi = {0.f, 0.f, 0.f, 0.f};
+  auto load_ops = [&](int cl, ChunkOps& o) {
+    const char* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecBytes;
+    const u32x4* qt = reinterpret_cast<const u32x4*>(rec + kRecQt);
+    const u32x4* wn = reinterpret_cast<const u32x4*>(rec + kRecWn);
+    const u32x4* qk = reinterpret_cast<const u32x4*>(rec + kRecQK);
+    const u32x4* kt = reinterpret_cast<const u32x4*>(rec + kRecKt);
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) vn[i4] = rec[kRecU + (16 * wave + 4 * g4 + i4) * kDim + cb * 16 + n];
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        o.qt[s][p] = qt[((wave * 4 + s) * 2 + p) * 64 + lane];
+        o.wn[s][p] = wn[((wave * 4 + s) * 2 + p) * 64 + lane];
+      }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        o.qk[s][p] = qk[((wave * 2 + s) * 2 + p) * 64 + lane];
+#pragma unroll
+        for (int tk = 0; tk < 2; ++tk) o.kt[tk][s][p] = kt[(((2 * wave + tk) * 2 + s) * 2 + p) * 64 + lane];
+      }
+    o.u = reinterpret_cast<const f32x4*>(rec + kRecU)[(wave * 8 + cb) * 64 + lane];
+    o.gl = *reinterpret_cast<const float*>(rec + kRecGl);
+  };
+
+  auto process = [&](int cl, const ChunkOps& o) {
+    const int chunk = a.chunk0 + cl;
+    // (i) v' = U - W S and o_inter = exp(G) q S for token tile `wave`
+    f32x4 vn = o.u, oi = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const uint4 bh4 = *reinterpret_cast<const uint4*>(&STh[n][32 * s + 8 * g4]);
-      const uint4 bl4 = *reinterpret_cast<const uint4*>(&STl[n][32 * s + 8 * g4]);
-      const u32x4 bh = {bh4.x, bh4.y, bh4.z, bh4.w}, bl = {bl4.x, bl4.y, bl4.z, bl4.w};
-      float av[8];
-      u32x4 ah, al;
-      load8(rec + kRecWn + (16 * wave + n) * kDim + 32 * s + 8 * g4, av);
-      split8(av, ah, al);
-      vn = mfma3(ah, al, bh, bl, vn);
-      load8(rec + kRecQt + (16 * wave + n) * kDim + 32 * s + 8 * g4, av);
-      split8(av, ah, al);
-      oi = mfma3(ah, al, bh, bl, oi);
+      const u32x4 bh = lds16(&STh[n][32 * s + 8 * g4]), bl = lds16(&STl[n][32 * s + 8 * g4]);
+      vn = mfma3(o.wn[s][0], o.wn[s][1], bh, bl, vn);
+      oi = mfma3(o.qt[s][0], o.qt[s][1], bh, bl, oi);
     }
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
@@ -425,41 +562,30 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(PrefillArgs a) {
       VTl[n][16 * wave + 4 * g4 + i4] = f32_to_bf16_bits(vn[i4] - bf16_bits_to_f32(hb));
     }
     __syncthreads();
-    // (ii) o = o_inter + (q k^T o D) v'
-    const int nsteps = (16 * wave + 15) / 32 + 1;
-    for (int s = 0; s < nsteps; ++s) {
-      const uint4 bh4 = *reinterpret_cast<const uint4*>(&VTh[n][32 * s + 8 * g4]);
-      const uint4 bl4 = *reinterpret_cast<const uint4*>(&VTl[n][32 * s + 8 * g4]);
-      const u32x4 bh = {bh4.x, bh4.y, bh4.z, bh4.w}, bl = {bl4.x, bl4.y, bl4.z, bl4.w};
-      float av[8];
-      u32x4 ah, al;
-      load8(rec + kRecQK + (16 * wave + n) * kChunk + 32 * s + 8 * g4, av);
-      split8(av, ah, al);
-      oi = mfma3(ah, al, bh, bl, oi);
+    // (ii) o = o_inter + ((q k^T) o D) v'   (lower triangular: token tiles <= wave)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (32 * s <= 16 * wave + 15) {
+        const u32x4 bh = lds16(&VTh[n][32 * s + 8 * g4]), bl = lds16(&VTl[n][32 * s + 8 * g4]);
+        oi = mfma3(o.qk[s][0], o.qk[s][1], bh, bl, oi);
+      }
     }
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int t = chunk * kChunk + 16 * wave + 4 * g4 + i4;
       if (t < a.length) store_act<OT>(a.out, ((int64_t)t * a.num_v_heads + h) * kDim + cb * 16 + n, oi[i4]);
     }
-    // (iii) S <- exp(G_C) S + Kt^T v' for dk tiles 2*wave, 2*wave + 1.
-    const float gl = rec[kRecGl];
+    // (iii) S <- exp(G_C) S + Kt^T v' for dk tiles 2 wave, 2 wave + 1
 #pragma unroll
     for (int tk = 0; tk < 2; ++tk) {
       const int dt = 2 * wave + tk;
       f32x4 sn;
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) sn[i4] = gl * S32[16 * dt + 4 * g4 + i4][n];
+      for (int i4 = 0; i4 < 4; ++i4) sn[i4] = o.gl * S32[16 * dt + 4 * g4 + i4][n];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const uint4 bh4 = *reinterpret_cast<const uint4*>(&VTh[n][32 * s + 8 * g4]);
-        const uint4 bl4 = *reinterpret_cast<const uint4*>(&VTl[n][32 * s + 8 * g4]);
-        const u32x4 bh = {bh4.x, bh4.y, bh4.z, bh4.w}, bl = {bl4.x, bl4.y, bl4.z, bl4.w};
-        float av[8];
-        u32x4 ah, al;
-        load8(rec + kRecKtT + (16 * dt + n) * kChunk + 32 * s + 8 * g4, av);
-        split8(av, ah, al);
-        sn = mfma3(ah, al, bh, bl, sn);
+        const u32x4 bh = lds16(&VTh[n][32 * s + 8 * g4]), bl = lds16(&VTl[n][32 * s + 8 * g4]);
+        sn = mfma3(o.kt[tk][s][0], o.kt[tk][s][1], bh, bl, sn);
       }
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
@@ -471,6 +597,17 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(PrefillArgs a) {
       }
     }
     __syncthreads();
+  };
+
+  // Chunk cl + 1's operands load while chunk cl computes (unrolled by two).
+  ChunkOps A, B;
+  load_ops(0, A);
+  for (int cl = 0; cl < a.seg_chunks; cl += 2) {
+    if (cl + 1 < a.seg_chunks) load_ops(cl + 1, B);
+    process(cl, A);
+    if (cl + 1 >= a.seg_chunks) break;
+    if (cl + 2 < a.seg_chunks) load_ops(cl + 2, A);
+    process(cl + 1, B);
   }
   for (int e = tid; e < kDim * 16; e += 256) {
     const int r = e >> 4, c = e & 15;
@@ -484,7 +621,7 @@ int64_t prefill_segment_bytes(int num_k_heads, int num_v_heads, int seg_tokens) 
   const int64_t conv_dim = (int64_t)(2 * num_k_heads + num_v_heads) * kDim;
   const int64_t chunks = (seg_tokens + kChunk - 1) / kChunk;
   const int64_t post = ((int64_t)chunks * kChunk * conv_dim * 2 + 255) / 256 * 256;
-  return post + chunks * num_v_heads * (int64_t)kRecFloats * 4;
+  return post + chunks * num_v_heads * (int64_t)kRecBytes;
 }
 
 }  // namespace ria
@@ -545,7 +682,7 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
   a.conv_dim = conv_dim;
   const int64_t post_bytes = ((int64_t)seg_chunks * kChunk * conv_dim * 2 + 255) / 256 * 256;
   a.post = static_cast<uint16_t*>(workspace);
-  a.rec = reinterpret_cast<float*>(static_cast<char*>(workspace) + post_bytes);
+  a.rec = static_cast<char*>(workspace) + post_bytes;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   const int total_chunks = (length + kChunk - 1) / kChunk;
@@ -554,7 +691,7 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
     a.seg_chunks = min(seg_chunks, total_chunks - c0);
     a.tok0 = c0 * kChunk;
     a.seg_tokens = min(a.seg_chunks * kChunk, length - a.tok0);
-    dim3 cgrid((conv_dim + 255) / 256, (a.seg_tokens + kConvTile - 1) / kConvTile);
+    dim3 cgrid((conv_dim / 2 + 255) / 256, (a.seg_tokens + kConvTile - 1) / kConvTile);
     dim3 pgrid(a.seg_chunks, num_v_heads);
     dim3 sgrid(num_v_heads * (kDim / 16));
 #define RIA_PREFILL_PHASES(XT_)                                                                          \

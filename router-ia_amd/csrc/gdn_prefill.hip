@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
       qv[s][j] = mul_rn(mul_rn(qv[s][j], iq), 0.08838834764831845f);
       kv[s][j] = mul_rn(kv[s][j], ik);
     }
-  __syncthreads();  // G_s, beta_s ready
+  lds_barrier();  // G_s, beta_s ready
   const float eg = expf(G_s[row]);                    // e^{G_t}
   const float ekl = expf(G_s[kChunk - 1] - G_s[row]);  // e^{G_C - G_t}
   const float bt = beta_s[row];
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
       for (int j = 0; j < 8; ++j) KtS[(d + j) * 68 + row] = kv[s][j] * ekl;  // transposed
     }
   }
-  __syncthreads();
+  lds_barrier();
   // Step 3: Kt operand to the record; K K^T -> L and Q K^T -> (q k^T) o D.
   {
     u32x4* kt_rec = reinterpret_cast<u32x4*>(rec + kRecKt);
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     const int i = e >> 6, j = e & 63;
     if ((j >> 4) > (i >> 4)) QKs[i * 68 + j] = 0.f;
   }
-  __syncthreads();
+  lds_barrier();
   // Step 4: QK operand to the record; T = (I + L)^-1 into R5 (blocked 4x4 of 16x16).
   float* Tm = KtS;
   {
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) Tm[(b0 + i) * 68 + b0 + lane] = col[i];
   }
-  __syncthreads();
+  lds_barrier();
   for (int dist = 1; dist < 4; ++dist) {  // T_ij = -T_ii sum_{m=j}^{i-1} L_im T_mj
     const int bi = wave + dist, bj = wave;
     if (bi < 4) {
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
         Tm[(16 * bi + r) * 68 + 16 * bj + c] = -sacc;
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   // Step 5: T hi/lo into R3 (L is dead); (beta v)^T and (beta e^G k)^T hi/lo
   // into R1 / R2 (q, k rows are dead), from the rows still in registers.
@@ -433,7 +433,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
   }
   uint16_t* vbT = qhl;  // hi [128][68], lo after
   uint16_t* kbT = khl;
-  __syncthreads();  // q/k rows in R1/R2 no longer read
+  lds_barrier();  // q/k rows in R1/R2 no longer read
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
       kbT[d * 68 + row] = hb;
       kbT[128 * 68 + d * 68 + row] = f32_to_bf16_bits(kb - bf16_bits_to_f32(hb));
     }
-  __syncthreads();
+  lds_barrier();
   // Step 6: U = T (beta v) and W = T (beta e^G k), 32 + 32 tiles of 16x16.
   float* Wst = QKs;  // -W staging [64][132] over R4 + R5 (QK and T fp32 are dead)
   f32x4* u_rec = reinterpret_cast<f32x4*>(rec + kRecU);
@@ -470,7 +470,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
       u_rec[(tt * 8 + td) * 64 + lane] = acc;
     }
   }
-  __syncthreads();
+  lds_barrier();
   // Step 7: -W operand to the record.
   {
     u32x4* wn_rec = reinterpret_cast<u32x4*>(rec + kRecWn);
@@ -518,7 +518,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     STh[c][r] = hb;
     STl[c][r] = f32_to_bf16_bits(v - bf16_bits_to_f32(hb));
   }
-  __syncthreads();
+  lds_barrier();
 
   auto load_ops = [&](int cl, ChunkOps& o) {
     const char* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecBytes;
@@ -561,7 +561,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       VTh[n][16 * wave + 4 * g4 + i4] = hb;
       VTl[n][16 * wave + 4 * g4 + i4] = f32_to_bf16_bits(vn[i4] - bf16_bits_to_f32(hb));
     }
-    __syncthreads();
+    lds_barrier();
     // (ii) o = o_inter + ((q k^T) o D) v'   (lower triangular: token tiles <= wave)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -596,7 +596,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         STl[n][r] = f32_to_bf16_bits(sn[i4] - bf16_bits_to_f32(hb));
       }
     }
-    __syncthreads();
+    lds_barrier();
   };
 
   // Chunk cl + 1's operands load while chunk cl computes (unrolled by two).

@@ -34,12 +34,10 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet), identical to c10::BFloat16.
+// Round-to-nearest-even fp32 -> bf16, as c10::BFloat16 rounds finite values.
+// gfx950 converts in hardware (v_cvt_pk_bf16_f32, two values per instruction).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
@@ -136,6 +134,11 @@ __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_no
 __device__ __forceinline__ u32x2 ld_stream(const u32x2* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ f32x4 ld_stream(const f32x4* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_stream(f32x4* p, f32x4 v) { __builtin_nontemporal_store(v, p); }
+
+// Workgroup barrier for LDS traffic only: it waits for this wave's LDS (and
+// scalar) operations but not for outstanding global loads or stores, which
+// __syncthreads() would also drain (exposing prefetches and store latency).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

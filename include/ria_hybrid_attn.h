@@ -165,6 +165,47 @@ int ria_kv_append(int batch, int num_kv_heads,
                   const float* inv_freq, int rope_dim, void* stream);
 
 /*
+ * Append `length` consecutive tokens of ONE sequence (a prompt) into its
+ * pages: token i goes to logical slot start_pos + i with RoPE position
+ * start_pos + i.  Equal to `length` ria_kv_append calls, i.e. the
+ * reference's per-token prefill of :306-308 and :365-372
+ * (qwen36_chat_batch.py:255-258 drives one decode step per prompt token).
+ *
+ * k, v            [length, Hkv, 256] of k_dtype / v_dtype.
+ * page_table_row  this sequence's page-table row, page_capacity entries;
+ *                 start_pos + length must fit in page_capacity * 16.
+ */
+int ria_kv_append_seq(int length, int num_kv_heads,
+                      const void* k, int k_dtype, int64_t k_row_stride,
+                      const void* v, int v_dtype, int64_t v_row_stride,
+                      void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                      const int32_t* page_table_row, int64_t page_capacity,
+                      int32_t start_pos, const float* inv_freq, int rope_dim, void* stream);
+
+/*
+ * Causal GQA attention prefill of `length` prompt tokens of one sequence,
+ * one layer: appends the prompt's k (RoPE) and v to the pages exactly as
+ * ria_kv_append_seq, then token i (position start_pos + i) attends to keys
+ * 0 .. start_pos + i, and out = softmax(q_rot K^T * scale) V * sigmoid(gate).
+ * Equal to `length` ria_kv_append + ria_attn_decode steps, the reference's
+ * token-by-token prefill of qwen36_attention_cache.py:306-317.
+ *
+ * q, gate   [length, Hq, 256] (row strides in elements); k, v [length, Hkv, 256].
+ *           q, k, v, gate and out share act_dtype.
+ * out       [length, Hq, 256] of act_dtype, contiguous.
+ * Hq / Hkv <= 8; rope_dim is 0 or 64.
+ */
+int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads,
+                     const void* q, int64_t q_row_stride,
+                     const void* k, int64_t k_row_stride,
+                     const void* v, int64_t v_row_stride,
+                     const void* gate, int64_t gate_row_stride, int act_dtype,
+                     void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                     const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
+                     const float* inv_freq, int rope_dim, float scale,
+                     void* out, void* stream);
+
+/*
  * Split size ria_attn_decode would choose for these context lengths (a host
  * array of `batch` tokens-attended counts): long splits, down to one page
  * per wave when the batch holds too few pages to occupy the GPU.  Passing

@@ -90,6 +90,7 @@ struct AppendArgs {
   const float* inv_freq;
   int rope_dim;
   int num_kv_heads;
+  int seq_mode;  // 1: blockIdx.x is token i of one sequence at position (and slot) pos_scalar + i
 };
 
 // RoPE of element d of a row: (x*cos + rotate_half(x)*sin) on [0, rope_dim),
@@ -110,9 +111,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int b = blockIdx.x;
   const int kvh = blockIdx.y;
   const int d = threadIdx.x;
-  const int row = a.seq_slot ? a.seq_slot[b] : b;
-  const int pos = a.positions ? a.positions[b] : a.pos_scalar;
-  const int slot = a.slots ? a.slots[b] : a.slot_scalar;
+  const int row = a.seq_mode ? 0 : (a.seq_slot ? a.seq_slot[b] : b);
+  const int pos = a.seq_mode ? a.pos_scalar + b : (a.positions ? a.positions[b] : a.pos_scalar);
+  const int slot = a.seq_mode ? a.pos_scalar + b : (a.slots ? a.slots[b] : a.slot_scalar);
   __shared__ float k_s[kAttnHeadDim];
   const float kv = load_act<KT>(a.k, (int64_t)b * a.k_stride + kvh * kAttnHeadDim + d);
   const float vv = load_act<VT>(a.v, (int64_t)b * a.v_stride + kvh * kAttnHeadDim + d);
@@ -413,47 +414,8 @@ static int resolve_split(int batch, int num_kv_heads, int max_ctx, int split_tok
   return split_tokens > 0 ? split_tokens : auto_split_tokens(batch, num_kv_heads, max_ctx);
 }
 
-}  // namespace ria
-
-using namespace ria;
-
-extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
-                             const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
-                             int kv_dtype, int num_pages, const int32_t* page_table, int64_t page_table_stride,
-                             const int32_t* seq_slot, const int32_t* positions, int32_t position_scalar,
-                             const int32_t* slots, int32_t slot_scalar, const float* inv_freq, int rope_dim,
-                             void* stream) {
-  if (batch < 0 || num_kv_heads <= 0) return set_error(RIA_ERR_INVALID, "ria_kv_append: bad batch/num_kv_heads");
-  if (batch == 0) return RIA_OK;
-  if (!valid_dtype(k_dtype) || !valid_dtype(v_dtype)) return set_error(RIA_ERR_INVALID, "ria_kv_append: unknown dtype");
-  if (kv_dtype != RIA_DT_BF16 && kv_dtype != RIA_DT_F16)
-    return set_error(RIA_ERR_INVALID, "ria_kv_append: the KV cache must be bf16 or fp16");
-  if (!k || !v || !k_cache || !v_cache || !page_table) return set_error(RIA_ERR_INVALID, "ria_kv_append: null pointer");
-  if (rope_dim < 0 || rope_dim > 64 || rope_dim % 2) return set_error(RIA_ERR_INVALID, "ria_kv_append: rope_dim must be even and <= 64");
-  if (rope_dim > 0 && !inv_freq) return set_error(RIA_ERR_INVALID, "ria_kv_append: inv_freq is null");
-  if (k_row_stride < (int64_t)num_kv_heads * kAttnHeadDim || v_row_stride < (int64_t)num_kv_heads * kAttnHeadDim)
-    return set_error(RIA_ERR_INVALID, "ria_kv_append: row stride smaller than Hkv*256");
-  if (!slots && slot_scalar < 0) return set_error(RIA_ERR_INVALID, "ria_kv_append: negative slot");
-  AppendArgs a{};
-  a.k = k;
-  a.k_stride = k_row_stride;
-  a.v = v;
-  a.v_stride = v_row_stride;
-  a.k_cache = static_cast<uint16_t*>(k_cache);
-  a.v_cache = static_cast<uint16_t*>(v_cache);
-  a.num_pages = num_pages;
-  a.page_table = page_table;
-  a.pt_stride = page_table_stride;
-  a.seq_slot = seq_slot;
-  a.positions = positions;
-  a.pos_scalar = position_scalar;
-  a.slots = slots;
-  a.slot_scalar = slot_scalar;
-  a.inv_freq = inv_freq;
-  a.rope_dim = rope_dim;
-  a.num_kv_heads = num_kv_heads;
-  dim3 grid(batch, num_kv_heads);
-  hipStream_t st = static_cast<hipStream_t>(stream);
+static void launch_append(const AppendArgs& a, int rows, int k_dtype, int v_dtype, int kv_dtype, hipStream_t st) {
+  dim3 grid(rows, a.num_kv_heads);
 #define RIA_APPEND_LAUNCH(KT_, VT_)                                                              \
   if (kv_dtype == RIA_DT_F16)                                                                    \
     hipLaunchKernelGGL((kv_append_kernel<KT_, VT_, RIA_DT_F16>), grid, dim3(256), 0, st, a);     \
@@ -476,7 +438,93 @@ extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_d
   }
 #undef RIA_APPEND_VT
 #undef RIA_APPEND_LAUNCH
+}
+
+static int check_append_common(const char* who, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
+                               const void* v, int v_dtype, int64_t v_row_stride, const void* k_cache,
+                               const void* v_cache, int kv_dtype, const int32_t* page_table, const float* inv_freq,
+                               int rope_dim) {
+  if (num_kv_heads <= 0) return set_error(RIA_ERR_INVALID, "%s: bad num_kv_heads", who);
+  if (!valid_dtype(k_dtype) || !valid_dtype(v_dtype)) return set_error(RIA_ERR_INVALID, "%s: unknown dtype", who);
+  if (kv_dtype != RIA_DT_BF16 && kv_dtype != RIA_DT_F16)
+    return set_error(RIA_ERR_INVALID, "%s: the KV cache must be bf16 or fp16", who);
+  if (!k || !v || !k_cache || !v_cache || !page_table) return set_error(RIA_ERR_INVALID, "%s: null pointer", who);
+  if (rope_dim < 0 || rope_dim > 64 || rope_dim % 2)
+    return set_error(RIA_ERR_INVALID, "%s: rope_dim must be even and <= 64", who);
+  if (rope_dim > 0 && !inv_freq) return set_error(RIA_ERR_INVALID, "%s: inv_freq is null", who);
+  if (k_row_stride < (int64_t)num_kv_heads * kAttnHeadDim || v_row_stride < (int64_t)num_kv_heads * kAttnHeadDim)
+    return set_error(RIA_ERR_INVALID, "%s: row stride smaller than Hkv*256", who);
+  return RIA_OK;
+}
+
+}  // namespace ria
+
+using namespace ria;
+
+extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
+                             const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
+                             int kv_dtype, int num_pages, const int32_t* page_table, int64_t page_table_stride,
+                             const int32_t* seq_slot, const int32_t* positions, int32_t position_scalar,
+                             const int32_t* slots, int32_t slot_scalar, const float* inv_freq, int rope_dim,
+                             void* stream) {
+  if (batch < 0) return set_error(RIA_ERR_INVALID, "ria_kv_append: bad batch");
+  int rc = check_append_common("ria_kv_append", num_kv_heads, k, k_dtype, k_row_stride, v, v_dtype, v_row_stride,
+                               k_cache, v_cache, kv_dtype, page_table, inv_freq, rope_dim);
+  if (rc != RIA_OK) return rc;
+  if (batch == 0) return RIA_OK;
+  if (!slots && slot_scalar < 0) return set_error(RIA_ERR_INVALID, "ria_kv_append: negative slot");
+  AppendArgs a{};
+  a.k = k;
+  a.k_stride = k_row_stride;
+  a.v = v;
+  a.v_stride = v_row_stride;
+  a.k_cache = static_cast<uint16_t*>(k_cache);
+  a.v_cache = static_cast<uint16_t*>(v_cache);
+  a.num_pages = num_pages;
+  a.page_table = page_table;
+  a.pt_stride = page_table_stride;
+  a.seq_slot = seq_slot;
+  a.positions = positions;
+  a.pos_scalar = position_scalar;
+  a.slots = slots;
+  a.slot_scalar = slot_scalar;
+  a.inv_freq = inv_freq;
+  a.rope_dim = rope_dim;
+  a.num_kv_heads = num_kv_heads;
+  a.seq_mode = 0;
+  launch_append(a, batch, k_dtype, v_dtype, kv_dtype, static_cast<hipStream_t>(stream));
   return check_launch("ria_kv_append");
+}
+
+extern "C" int ria_kv_append_seq(int length, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
+                                 const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
+                                 int kv_dtype, int num_pages, const int32_t* page_table_row, int64_t page_capacity,
+                                 int32_t start_pos, const float* inv_freq, int rope_dim, void* stream) {
+  if (length < 0 || start_pos < 0) return set_error(RIA_ERR_INVALID, "ria_kv_append_seq: negative length or start");
+  int rc = check_append_common("ria_kv_append_seq", num_kv_heads, k, k_dtype, k_row_stride, v, v_dtype,
+                               v_row_stride, k_cache, v_cache, kv_dtype, page_table_row, inv_freq, rope_dim);
+  if (rc != RIA_OK) return rc;
+  if (length == 0) return RIA_OK;
+  if ((int64_t)start_pos + length > page_capacity * kPageTokens)
+    return set_error(RIA_ERR_INVALID, "ria_kv_append_seq: %d + %d tokens exceed the row's %lld pages", start_pos,
+                     length, (long long)page_capacity);
+  AppendArgs a{};
+  a.k = k;
+  a.k_stride = k_row_stride;
+  a.v = v;
+  a.v_stride = v_row_stride;
+  a.k_cache = static_cast<uint16_t*>(k_cache);
+  a.v_cache = static_cast<uint16_t*>(v_cache);
+  a.num_pages = num_pages;
+  a.page_table = page_table_row;
+  a.pt_stride = page_capacity;
+  a.pos_scalar = start_pos;
+  a.inv_freq = inv_freq;
+  a.rope_dim = rope_dim;
+  a.num_kv_heads = num_kv_heads;
+  a.seq_mode = 1;
+  launch_append(a, length, k_dtype, v_dtype, kv_dtype, static_cast<hipStream_t>(stream));
+  return check_launch("ria_kv_append_seq");
 }
 
 extern "C" int ria_attn_decode_split_tokens(int num_kv_heads, const int32_t* ctx_lens_host, int batch) {

@@ -77,6 +77,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_int, _c_int, _vp, _vp, _c_int, _vp, _c_i64, _vp, _c_i32, _c_i32, _vp, _vp, _vp],
     ),
+    "ria_kv_append_seq": (
+        _c_int,
+        [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp, _c_i64,
+         _c_i32, _vp, _c_int, _vp],
+    ),
+    "ria_attn_prefill": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _vp, _vp,
+         _c_int, _c_int, _vp, _c_i64, _c_i32, _vp, _c_int, _c_f32, _vp, _vp],
+    ),
 }
 
 _LIB: ctypes.CDLL | None = None

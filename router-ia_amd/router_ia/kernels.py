@@ -439,3 +439,94 @@ def gdn_prefill(
                                     workspace.numel() * workspace.element_size(), _stream(dev))
     nat.check(rc, "ria_gdn_prefill")
     return out
+
+
+def _page_row(page_table: torch.Tensor, dev: torch.device) -> int:
+    """Check a single sequence's page-table row (1-D int32); returns its capacity in pages."""
+    _require_gpu("page_table", page_table, dev)
+    if page_table.dtype != torch.int32 or page_table.dim() != 1 or not page_table.is_contiguous():
+        raise ValueError("page_table must be one contiguous int32 row")
+    return int(page_table.numel())
+
+
+def kv_append_seq(
+    k: torch.Tensor,
+    v: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    *,
+    start: int,
+    inv_freq: torch.Tensor | None,
+) -> None:
+    """Append a prompt's k (RoPE at start + i) and v at slots start + i of one sequence (ria_kv_append_seq).
+
+    k, v [L, Hkv, 256]; page_table is the sequence's page-table row.
+    """
+    length = int(k.shape[0])
+    num_kv_heads = int(k_cache.shape[1])
+    dev = k.device
+    for name, t in (("k", k), ("v", v), ("k_cache", k_cache), ("v_cache", v_cache), ("inv_freq", inv_freq)):
+        _require_gpu(name, t, dev)
+    ks = _row_stride("k", k, length, num_kv_heads * ATTN_HEAD_DIM)
+    vs = _row_stride("v", v, length, num_kv_heads * ATTN_HEAD_DIM)
+    pages = _check_kv_cache(k_cache, v_cache, num_kv_heads)
+    cap = _page_row(page_table, dev)
+    if start < 0 or start + length > cap * PAGE_TOKENS:
+        raise ValueError(f"{start} + {length} tokens exceed the row's {cap} pages")
+    rope_dim = 0 if inv_freq is None else 2 * int(inv_freq.numel())
+    rc = nat.load().ria_kv_append_seq(length, num_kv_heads, _ptr(k), dtype_code(k), ks, _ptr(v), dtype_code(v), vs,
+                                      _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table),
+                                      cap, int(start), _ptr(inv_freq), rope_dim, _stream(dev))
+    nat.check(rc, "ria_kv_append_seq")
+
+
+def attn_prefill(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    gate: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    out: torch.Tensor | None = None,
+    *,
+    start: int,
+    inv_freq: torch.Tensor | None,
+    scale: float,
+) -> torch.Tensor:
+    """Causal GQA prefill of one sequence's prompt over its paged cache (ria_attn_prefill).
+
+    q, gate [L, Hq, 256]; k, v [L, Hkv, 256], all of one dtype; the prompt's
+    k/v are appended at slots start .. start + L - 1 first.  Returns out
+    [L, Hq, 256] in that dtype.
+    """
+    length = int(q.shape[0])
+    num_q_heads = int(q.shape[1])
+    num_kv_heads = int(k_cache.shape[1])
+    dev = q.device
+    for name, t in (("q", q), ("k", k), ("v", v), ("gate", gate), ("k_cache", k_cache), ("v_cache", v_cache),
+                    ("inv_freq", inv_freq)):
+        _require_gpu(name, t, dev)
+    if len({q.dtype, k.dtype, v.dtype, gate.dtype}) != 1:
+        raise ValueError("q, k, v and gate must share a dtype")
+    qs = _row_stride("q", q, length, num_q_heads * ATTN_HEAD_DIM)
+    gs = _row_stride("gate", gate, length, num_q_heads * ATTN_HEAD_DIM)
+    ks = _row_stride("k", k, length, num_kv_heads * ATTN_HEAD_DIM)
+    vs = _row_stride("v", v, length, num_kv_heads * ATTN_HEAD_DIM)
+    pages = _check_kv_cache(k_cache, v_cache, num_kv_heads)
+    cap = _page_row(page_table, dev)
+    if start < 0 or start + length > cap * PAGE_TOKENS:
+        raise ValueError(f"{start} + {length} tokens exceed the row's {cap} pages")
+    if out is None:
+        out = torch.empty((length, num_q_heads, ATTN_HEAD_DIM), device=dev, dtype=q.dtype)
+    _require_gpu("out", out, dev)
+    if tuple(out.shape) != (length, num_q_heads, ATTN_HEAD_DIM) or not out.is_contiguous() or out.dtype != q.dtype:
+        raise ValueError(f"out must be contiguous [{length}, {num_q_heads}, 256] of q's dtype")
+    rope_dim = 0 if inv_freq is None else 2 * int(inv_freq.numel())
+    rc = nat.load().ria_attn_prefill(length, num_q_heads, num_kv_heads, _ptr(q), qs, _ptr(k), ks, _ptr(v), vs,
+                                     _ptr(gate), gs, dtype_code(q), _ptr(k_cache), _ptr(v_cache),
+                                     dtype_code(k_cache), pages, _ptr(page_table), cap, int(start), _ptr(inv_freq),
+                                     rope_dim, float(scale), _ptr(out), _stream(dev))
+    nat.check(rc, "ria_attn_prefill")
+    return out

@@ -58,3 +58,21 @@ def test_split_heuristic(ctx, expect) -> None:
     from router_ia import kernels as K
 
     assert K.attn_decode_split_tokens(2, ctx) == expect
+
+
+def test_prefill_attention_host_validation() -> None:
+    lib = nat.load()
+    # 16 query heads per KV head is beyond the kernel's group limit
+    rc = lib.ria_attn_prefill(16, 32, 2, None, 8192, None, 512, None, 512, None, 8192, 0, None, None, 0, 4, None,
+                              4, 0, None, 64, 0.0625, None, None)
+    assert rc == 1 and b"at most 8" in lib.ria_last_error()
+    # the prompt must fit in the row's pages: 60 + 10 tokens > 4 pages of 16
+    fake = ctypes.c_void_p(256)
+    rc = lib.ria_attn_prefill(10, 16, 2, fake, 4096, fake, 512, fake, 512, fake, 4096, 0, fake, fake, 0, 4, fake,
+                              4, 60, fake, 64, 0.0625, fake, None)
+    assert rc == 1 and b"exceed" in lib.ria_last_error()
+    rc = lib.ria_kv_append_seq(10, 2, fake, 0, 512, fake, 0, 512, fake, fake, 0, 4, fake, 4, 60, fake, 64, None)
+    assert rc == 1 and b"exceed" in lib.ria_last_error()
+    # zero-length prompts are a no-op
+    assert lib.ria_attn_prefill(0, 16, 2, fake, 4096, fake, 512, fake, 512, fake, 4096, 0, fake, fake, 0, 4, fake,
+                                4, 0, fake, 64, 0.0625, fake, None) == 0

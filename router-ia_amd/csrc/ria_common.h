@@ -23,6 +23,7 @@ constexpr int kAttnHeadDim = 256;  // FULL_HEAD_DIM
 constexpr int kPageTokens = 16;    // tokens per KV page
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -75,6 +76,73 @@ __device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
   }
 }
 
+// Eight consecutive activation elements starting at element i (i a multiple
+// of 8, base pointer 16-byte aligned), widened to fp32.
+template <int DT>
+__device__ __forceinline__ void load_act8(const void* p, int64_t i, float (&x)[8]) {
+  if constexpr (DT == RIA_DT_F32) {
+    const f32x4* v = reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
+    const f32x4 a = v[0], b = v[1];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = a[j];
+      x[4 + j] = b[j];
+    }
+  } else {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p) + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint16_t lo = static_cast<uint16_t>(w[j] & 0xffffu), hi = static_cast<uint16_t>(w[j] >> 16);
+      if constexpr (DT == RIA_DT_BF16) {
+        x[2 * j] = bf16_bits_to_f32(lo);
+        x[2 * j + 1] = bf16_bits_to_f32(hi);
+      } else {
+        x[2 * j] = f16_bits_to_f32(lo);
+        x[2 * j + 1] = f16_bits_to_f32(hi);
+      }
+    }
+  }
+}
+
+// Four consecutive elements at i (a multiple of 4, base 16-byte aligned).
+template <int DT>
+__device__ __forceinline__ void load_act4(const void* p, int64_t i, float (&x)[4]) {
+  if constexpr (DT == RIA_DT_F32) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = a[j];
+  } else {
+    const u32x2 w = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(p) + i);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint16_t lo = static_cast<uint16_t>(w[j] & 0xffffu), hi = static_cast<uint16_t>(w[j] >> 16);
+      if constexpr (DT == RIA_DT_BF16) {
+        x[2 * j] = bf16_bits_to_f32(lo);
+        x[2 * j + 1] = bf16_bits_to_f32(hi);
+      } else {
+        x[2 * j] = f16_bits_to_f32(lo);
+        x[2 * j + 1] = f16_bits_to_f32(hi);
+      }
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store_act4(void* p, int64_t i, const float (&x)[4]) {
+  if constexpr (DT == RIA_DT_F32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(p) + i) = f32x4{x[0], x[1], x[2], x[3]};
+  } else {
+    uint32_t w[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint16_t lo = DT == RIA_DT_BF16 ? f32_to_bf16_bits(x[2 * j]) : f32_to_f16_bits(x[2 * j]);
+      const uint16_t hi = DT == RIA_DT_BF16 ? f32_to_bf16_bits(x[2 * j + 1]) : f32_to_f16_bits(x[2 * j + 1]);
+      w[j] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+    }
+    *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p) + i) = u32x2{w[0], w[1]};
+  }
+}
+
 // Value of an fp32 number after a round trip through dtype DT (torch `.to(dt)`).
 template <int DT>
 __device__ __forceinline__ float through_dtype(float v) {
@@ -112,6 +180,10 @@ struct Kv16<RIA_DT_BF16> {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
                                                      0, 0, 0);
   }
+  static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
 };
 
 template <>
@@ -125,6 +197,10 @@ struct Kv16<RIA_DT_F16> {
   static __device__ __forceinline__ f32x4 mfma_k16(u32x2 a, u32x2 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0,
                                                  0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
   }
 };
 

@@ -51,7 +51,21 @@ ATTN_APPEND_BYTES = 2_048
 ATTN_ACT_BYTES = 3 * NUM_Q_HEADS * HEAD_DIM_ATTN * 2  # q, gate, out in bf16: 24,576
 SPLITK_Q_BYTES = NUM_Q_HEADS * HEAD_DIM_ATTN * 2  # the split-K launch reads q only
 
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, AMD specification
+PREFILL_METRIC = "prefill tok/s (1 Gated DeltaNet + 1 full-attention layer, one 16384-token prompt); MFMA TFLOP/s % of peak"
+GDN_CHUNK_FLOP = 11_710_000  # chunked WY form, per (V head, 64-token chunk): KK^T, QK^T, T, U, W, scan
+PREFILL_LEN = 16384
+
+
+def attn_prefill_flop(length: int) -> int:
+    """Causal GQA attention FLOPs: QK^T and PV over keys 0..t for every query t, 16 heads x 256 dims."""
+    return NUM_Q_HEADS * length * (length + 1) // 2 * HEAD_DIM_ATTN * 4
+
+
 WORKLOADS = {
+    "prefill16k": dict(batch=1, lo=PREFILL_LEN, hi=PREFILL_LEN, seed=3, prefill=True,
+                       desc="prefill of one 16384-token prompt through 1 Gated DeltaNet layer (chunk 64) and "
+                            "1 GQA full-attention layer (causal, fills 16-token KV pages, shuffled page table)"),
     "ragged128": dict(batch=128, lo=1024, hi=32768, seed=4,
                       desc="40-layer stack, B=128, context U[1024,32768] (seed 4), 16-token pages, shuffled page table"),
     "batch32": dict(batch=32, lo=8192, hi=8192, seed=2,
@@ -301,6 +315,148 @@ def run_cpu_baseline(wl, lengths: list[int], n_seqs: int, n_steps: int) -> dict:
     }
 
 
+def run_prefill_gpu(args, wl) -> dict:
+    """One 16384-token prompt through one DeltaNet layer and one attention layer, `steps` times."""
+    from router_ia import _native as nat
+    from router_ia import kernels as K
+    from router_ia.batched_state import rope_inv_freq
+    from router_ia.paged_kv import PagedKVCache
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = PREFILL_LEN
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(wl["seed"])
+    mixed = torch.randn((L, CONV_DIM), generator=gen, device=dev).to(torch.bfloat16)
+    a_raw = torch.randn((L, NUM_V_HEADS), generator=gen, device=dev)
+    b_raw = torch.randn((L, NUM_V_HEADS), generator=gen, device=dev)
+    conv_w = (torch.randn((CONV_DIM, 1, 4), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    a_log = torch.rand((NUM_V_HEADS,), generator=gen, device=dev) * 4.0 - 4.0
+    dt_bias = torch.zeros((NUM_V_HEADS,), device=dev)
+    state = torch.zeros((NUM_V_HEADS, 128, 128), device=dev)
+    ring = torch.zeros((4, CONV_DIM), dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(K.gdn_prefill_workspace_bytes(16, NUM_V_HEADS, L), dtype=torch.uint8, device=dev)
+    gdn_out = torch.empty((L, NUM_V_HEADS, 128), device=dev, dtype=torch.bfloat16)
+    q = torch.randn((L, NUM_Q_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev).to(torch.bfloat16)
+    gate = torch.randn((L, NUM_Q_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev).to(torch.bfloat16)
+    k = torch.randn((L, NUM_KV_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn((L, NUM_KV_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev).to(torch.bfloat16)
+    pages = L // 16 + 2
+    kv = PagedKVCache(1, pages, 1, pages, num_kv_heads=NUM_KV_HEADS, device=dev, shuffle_seed=wl["seed"])
+    kv.ensure(0, L)
+    inv_freq = rope_inv_freq(1e7, 64).to(dev)
+    attn_out = torch.empty((L, NUM_Q_HEADS, HEAD_DIM_ATTN), device=dev, dtype=torch.bfloat16)
+    log(f"[bench] {wl['desc']}")
+
+    def gdn():
+        K.gdn_prefill(mixed, state, a_raw, b_raw, gdn_out, num_k_heads=16, num_v_heads=NUM_V_HEADS,
+                      conv_weight=conv_w, conv_ring=ring, conv_pos=0, workspace=ws, gate_mode=nat.RIA_GATE_RAW,
+                      A_log=a_log, dt_bias=dt_bias)
+
+    def attn(phase):
+        K.attn_prefill(q, k, v, gate, kv.k[0], kv.v[0], kv.page_table[0], attn_out, start=0, inv_freq=inv_freq,
+                       scale=HEAD_DIM_ATTN ** -0.5, phase=phase)
+
+    for _ in range(args.warmup):
+        gdn()
+        attn(nat.RIA_PREFILL_BOTH)
+    torch.cuda.synchronize()
+    ev = {name: [] for name in ("gdn", "append", "attend")}
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t_start.record()
+    for _ in range(args.steps):
+        for name, fn in (("gdn", gdn), ("append", lambda: attn(nat.RIA_PREFILL_APPEND)),
+                         ("attend", lambda: attn(nat.RIA_PREFILL_ATTEND))):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            ev[name].append((e0, e1))
+    t_end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    elapsed_s = t_start.elapsed_time(t_end) / 1e3
+    avg = {name: sum(a.elapsed_time(b) for a, b in pairs) / len(pairs) / 1e3 for name, pairs in ev.items()}
+    attn_flop = attn_prefill_flop(L)
+    gdn_flop = GDN_CHUNK_FLOP * NUM_V_HEADS * (L // 64)
+    achieved = attn_flop / avg["attend"] / 1e12
+    return {
+        "batch": 1,
+        "lengths": [L],
+        "elapsed_s": elapsed_s,
+        "wall_s": wall,
+        "tok_s": L * args.steps / elapsed_s,
+        "ms_per_step": elapsed_s / args.steps * 1e3,
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "attn_prefill_kernel (ria_attn_prefill_phase, attention launch)",
+            "achieved": round(achieved, 1),
+            "peak": MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "algorithmic_flop_per_launch": attn_flop,
+            "avg_launch_us": round(avg["attend"] * 1e6, 1),
+            "launches": len(ev["attend"]),
+            "mfma_work_note": ("q and the probabilities run as bf16 hi+lo pairs, so the MFMA pipe executes "
+                               "2x the algorithmic FLOPs"),
+        },
+        "kernels": {
+            "gdn_prefill (conv + chunk prep + chunk scan)": {
+                "avg_call_us": round(avg["gdn"] * 1e6, 1),
+                "algorithmic_flop": gdn_flop,
+                "achieved_TFLOPs": round(gdn_flop / avg["gdn"] / 1e12, 1),
+                "frac": round(gdn_flop / avg["gdn"] / 1e12 / MFMA_PEAK_TFLOPS, 4),
+            },
+            "kv_append_kernel (prompt k/v into pages)": {"avg_call_us": round(avg["append"] * 1e6, 1)},
+        },
+    }
+
+
+def run_prefill_cpu(wl, n_gdn: int, n_attn: int) -> dict:
+    """The reference's token-by-token prefill (oracle restatement) timed per token on this host.
+
+    Per token the reference runs one DeltaNet decode step (position independent)
+    and one attention decode step over every earlier token; over a 16384-token
+    prompt the mean attention context is 8192, so the attention step is timed
+    at positions 8192.. with an 8192-token fp32 cache.
+    """
+    from oracle import qwen36_cpu as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    gen = torch.Generator().manual_seed(wl["seed"])
+    conv_w = (torch.randn((CONV_DIM, 1, 4), generator=gen) * 0.5).to(torch.bfloat16)
+    a_log = torch.rand((NUM_V_HEADS,), generator=gen) * 4.0 - 4.0
+    zero_bias = torch.zeros(NUM_V_HEADS)
+    xs = torch.randn((n_gdn, 1, CONV_DIM), generator=gen).to(torch.bfloat16)
+    ab = torch.randn((n_gdn, 2, 1, NUM_V_HEADS), generator=gen)
+    conv_state = lin_state = None
+    t0 = time.perf_counter()
+    for i in range(n_gdn):
+        beta, g = O.gating(ab[i, 0], ab[i, 1], a_log, zero_bias)
+        _, conv_state, lin_state = O.linear_decode_step(conv_state, lin_state, xs[i], conv_w, beta, g)
+    t_gdn = (time.perf_counter() - t0) / n_gdn
+    ctx = PREFILL_LEN // 2
+    fk = torch.randn((1, NUM_KV_HEADS, ctx, HEAD_DIM_ATTN), generator=gen).to(torch.bfloat16).float()
+    fv = torch.randn((1, NUM_KV_HEADS, ctx, HEAD_DIM_ATTN), generator=gen).to(torch.bfloat16).float()
+    qa = torch.randn((n_attn, 2, 1, NUM_Q_HEADS, HEAD_DIM_ATTN), generator=gen).to(torch.bfloat16)
+    kva = torch.randn((n_attn, 2, 1, NUM_KV_HEADS, HEAD_DIM_ATTN), generator=gen).to(torch.bfloat16)
+    t0 = time.perf_counter()
+    for i in range(n_attn):
+        _, fk, fv = O.full_decode_step(fk, fv, qa[i, 0], kva[i, 0], kva[i, 1], qa[i, 1], ctx + i)
+    t_attn = (time.perf_counter() - t0) / n_attn
+    return {
+        "value": round(1.0 / (t_gdn + t_attn), 3),
+        "unit": "tok/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"token-by-token prefill as the reference runs it (torch-CPU restatement, fp32): {n_gdn} DeltaNet "
+                   f"decode steps ({t_gdn * 1e3:.2f} ms/token) + {n_attn} attention decode steps at positions "
+                   f"{ctx}..{ctx + n_attn - 1}, the prompt's mean context ({t_attn * 1e3:.2f} ms/token)"),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -329,6 +485,8 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     wl = WORKLOADS[args.workload]
+    if wl.get("prefill"):
+        return prefill_main(args, wl)
     gpu = run_gpu(args, wl)
     prof = profiled_traffic("attn_splitk_kernel") if args.workload == "ragged128" else None
     if prof:
@@ -363,6 +521,39 @@ def main() -> int:
         },
         "roofline": gpu["roofline"],
         "step_hbm": gpu["step_hbm"],
+        "kernels": gpu["kernels"],
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def prefill_main(args, wl) -> int:
+    gpu = run_prefill_gpu(args, wl)
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU reference path (token-by-token prefill) on a sample")
+        cpu = run_prefill_cpu(wl, 96, 96)
+    result = {
+        "metric": PREFILL_METRIC,
+        "value": round(gpu["tok_s"], 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 activations and KV, fp32 state and accumulate (MFMA bf16 hi+lo operands)",
+        "data": "synthetic (seeded random prompt inputs; projections excluded)",
+        "config": {
+            "workload": wl["desc"],
+            "prompt_tokens": PREFILL_LEN,
+            "layers": "1 Gated DeltaNet (chunk 64) + 1 GQA full attention (16 Q / 2 KV heads x 256)",
+            "parallelism": "single GPU",
+        },
+        "roofline": gpu["roofline"],
         "kernels": gpu["kernels"],
         "cpu_baseline": cpu,
     }

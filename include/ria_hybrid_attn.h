@@ -67,6 +67,8 @@ enum ria_status {
   RIA_ERR_WORKSPACE = 3  /* caller workspace too small */
 };
 
+enum ria_prefill_phase { RIA_PREFILL_APPEND = 1, RIA_PREFILL_ATTEND = 2, RIA_PREFILL_BOTH = 3 };
+
 enum ria_gate_mode {
   /* gate_a holds g (log decay), gate_b holds beta; A_log/dt_bias unused. */
   RIA_GATE_PRECOMPUTED = 0,
@@ -193,7 +195,8 @@ int ria_kv_append_seq(int length, int num_kv_heads,
  * q, gate   [length, Hq, 256] (row strides in elements); k, v [length, Hkv, 256].
  *           q, k, v, gate and out share act_dtype.
  * out       [length, Hq, 256] of act_dtype, contiguous.
- * Hq / Hkv <= 8; rope_dim is 0 or 64.
+ * Hq / Hkv <= 8; rope_dim is 0 or 64.  q, gate and out 16-byte aligned, row
+ * strides multiples of 8 elements.
  */
 int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads,
                      const void* q, int64_t q_row_stride,
@@ -204,6 +207,26 @@ int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads,
                      const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
                      const float* inv_freq, int rope_dim, float scale,
                      void* out, void* stream);
+
+/*
+ * ria_attn_prefill split in its two launches: RIA_PREFILL_APPEND writes the
+ * prompt's k/v into the pages, RIA_PREFILL_ATTEND computes the attention over
+ * pages already holding them, RIA_PREFILL_BOTH does both (== ria_attn_prefill).
+ * Lets a caller time or overlap the phases; the arguments are those of
+ * ria_attn_prefill (k, v unused by RIA_PREFILL_ATTEND, q, gate, out unused by
+ * RIA_PREFILL_APPEND, but all are validated).
+ * Also requires q, gate and out 16-byte aligned with row strides that are
+ * multiples of 8 elements (ria_attn_prefill has the same requirement).
+ */
+int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_heads,
+                           const void* q, int64_t q_row_stride,
+                           const void* k, int64_t k_row_stride,
+                           const void* v, int64_t v_row_stride,
+                           const void* gate, int64_t gate_row_stride, int act_dtype,
+                           void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                           const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
+                           const float* inv_freq, int rope_dim, float scale,
+                           void* out, int phase, void* stream);
 
 /*
  * Split size ria_attn_decode would choose for these context lengths (a host

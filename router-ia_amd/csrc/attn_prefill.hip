@@ -10,22 +10,23 @@
 // append kernel in sequence mode), then one workgroup per (16-token query
 // block, KV head) streams the keys 0 .. last query of the block in blocks of
 // 32 keys (two pages).
-//   * the 4 waves own two query heads each (GQA group <= 8): a wave's 32
-//     columns are (head, token) pairs, so one 32x32x16 MFMA covers 32 keys x
-//     32 queries and every key block fetched serves 16 tokens x 8 heads;
-//   * key blocks travel HBM/L2 -> LDS by direct-to-LDS loads into a 3-slot
-//     ring, two blocks ahead of the one being computed, with no registers
-//     in flight;
-//   * scores S^T = K Q^T: the K tile is already in A-operand order (8 dims
-//     of one token are 16 contiguous bytes); the rows of a 32-key block take
-//     the tokens of each page in the order 0-3, 8-11, 4-7, 12-15, which makes
-//     a lane's 16 score rows exactly the 8 + 8 consecutive tokens whose V^T
-//     columns it reads as one 16-byte operand for O^T = V^T P^T;
+//   * 8 waves, one query head each (GQA group <= 8), two waves per SIMD: one
+//     wave's softmax (VALU, transcendental) overlaps the other's MFMAs, and
+//     every key block fetched serves 16 tokens x 8 heads;
+//   * key blocks travel HBM/L2 -> LDS by direct-to-LDS loads into a 4-slot
+//     ring, two blocks ahead of the one being computed, with no registers in
+//     flight;
+//   * scores S^T = K Q^T on 16x16x32 MFMA (16 keys x 16 tokens per tile): the
+//     K tile is already in A-operand order (8 dims of one token are 16
+//     contiguous bytes); the two score tiles of a block take their rows from
+//     the block's tokens in an order that leaves lane group g with exactly 8
+//     consecutive tokens of one page, whose V^T column is then one 16-byte
+//     operand of O^T = V^T P^T (16x16x32, k = those 32 keys);
 //   * the rotated q and the probabilities are carried as 16-bit hi + lo
 //     pairs (near-fp32 operands on MFMA); the online softmax is kept in log2
-//     units with a lazy rescale (only when a block max exceeds the running
-//     max by 2^8); row statistics combine across the two lane halves with
-//     permlane32 swaps;
+//     units (q is pre-scaled) with a lazy rescale (only when a block max
+//     exceeds the running max by 2^8); row statistics combine across lane
+//     groups with permlane swaps;
 //   * the gated result leaves through LDS so the output stores are coalesced;
 //   * query blocks are scheduled from the last (most keys) to the first.
 #include <math.h>
@@ -37,9 +38,11 @@ namespace ria {
 constexpr int kTile = kPageTokens * kAttnHeadDim;  // elements per (page, KV head) tile
 constexpr int kTileVec = kTile * 2 / 16;           // 16-byte vectors per tile (512)
 constexpr int kSlotVec = 4 * kTileVec;             // ring slot: K page 0, K page 1, V page 0, V page 1
-constexpr int kRingSlots = 3;
+constexpr int kRingSlots = 4;
+constexpr int kPrefillWaves = 8;                   // one query head per wave
+constexpr int kPrefillThreads = 64 * kPrefillWaves;
 constexpr int kStagePitch = kAttnHeadDim + 4;      // floats per staged output row
-constexpr int kPrefillLds = 4 * 32 * kStagePitch * 4;  // output stage; the ring (96 KiB) aliases it
+constexpr int kPrefillLds = kPrefillWaves * 16 * kStagePitch * 4;  // output stage; the ring (128 KiB) aliases it
 static_assert(kRingSlots * kSlotVec * 16 <= kPrefillLds, "ring must fit in the LDS block");
 
 struct PrefillAttnArgs {
@@ -62,67 +65,70 @@ struct PrefillAttnArgs {
   void* out;
 };
 
-// Token of a page held by row i (0..15) of a key block: groups of four in the
-// order 0-3, 8-11, 4-7, 12-15.
-__device__ __forceinline__ int block_row_token(int i) { return 4 * (((i >> 2) & 1) * 2 + (i >> 3)) + (i & 3); }
+// Key held by row r (0..15) of score tile m (0, 1) of a 32-key block, as
+// (page of the block, token): lane group g = r / 4 of both tiles together
+// holds tokens 8 (g % 2) .. 8 (g % 2) + 7 of page g / 2, tile m the half
+// 8 (g % 2) + 4 m .. + 3.
+__device__ __forceinline__ int tile_row_page(int r) { return r >> 3; }
+__device__ __forceinline__ int tile_row_token(int m, int r) { return 8 * ((r >> 2) & 1) + 4 * m + (r & 3); }
 
-__device__ __forceinline__ float swap32_max(float x) {
-  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+__device__ __forceinline__ float swap_max(float x, bool rows16) {
+  const auto s = rows16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
+                        : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
 
-__device__ __forceinline__ float swap32_sum(float x) {
-  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+__device__ __forceinline__ float swap_sum(float x, bool rows16) {
+  const auto s = rows16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
+                        : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
 template <int AT, int KVT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_prefill_kernel(
+__global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(
     PrefillAttnArgs a, const int32_t* __restrict__ pt) {
   using KV = Kv16<KVT>;
   const int nqb = (a.length + 15) / 16;
   const int qb = nqb - 1 - static_cast<int>(blockIdx.x) / a.num_kv_heads;  // heaviest blocks first
   const int kvh = static_cast<int>(blockIdx.x) % a.num_kv_heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c = lane & 31;  // MFMA column: (head 2 wave + c/16, token c%16); PV: dim row
-  const int h = lane >> 5;  // k half of the MFMA operands
+  const int n = lane & 15;   // MFMA column (token 16 qb + n) / row (key or dim)
+  const int g4 = lane >> 4;  // lane group: k slice of the operands, row group of the results
 
   __shared__ __attribute__((aligned(16))) unsigned char smem[kPrefillLds];
   u32x4* ring = reinterpret_cast<u32x4*>(smem);
   float* stage = reinterpret_cast<float*>(smem);
 
-  const int hh = c >> 4;
-  const bool head_ok = 2 * wave + hh < a.group;
-  const int head = kvh * a.group + 2 * wave + hh;
-  const int t_row = 16 * qb + (c & 15);
+  const bool head_ok = wave < a.group;
+  const int head = kvh * a.group + wave;
+  const int t_row = 16 * qb + n;
   const bool row_ok = head_ok && t_row < a.length;
   const int qpos = a.start + t_row;
-  const int ctx_total = a.start + a.length;  // keys that exist
+  const int ctx_total = a.start + a.length;   // keys that exist
   const int qlim = min(qpos, ctx_total - 1);  // last key this column sees
 
-  // ---- q operands: column c, dims 16 kd + 8 h + j, RoPE'd, as hi + lo pairs
-  u32x4 qh[16], ql[16];
+  // ---- q operands: column n, dims 32 kd + 8 g4 + j, RoPE'd, scaled by
+  //      scale * log2(e) (scores come out in log2 units), as hi + lo pairs
+  u32x4 qh[8], ql[8];
   auto pack = [&](const float (&x)[8], u32x4& hi, u32x4& lo) {
     uint32_t h4[4], l4[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint16_t a0 = KV::from_f32(x[2 * j]), a1 = KV::from_f32(x[2 * j + 1]);
-      const uint16_t b0 = KV::from_f32(x[2 * j] - KV::to_f32(a0));
-      const uint16_t b1 = KV::from_f32(x[2 * j + 1] - KV::to_f32(a1));
-      h4[j] = a0 | (uint32_t(a1) << 16);
-      l4[j] = b0 | (uint32_t(b1) << 16);
+      h4[j] = KV::pack2(x[2 * j], x[2 * j + 1]);
+      l4[j] = KV::pack2(x[2 * j] - KV::lo_f32(h4[j]), x[2 * j + 1] - KV::hi_f32(h4[j]));
     }
     hi = u32x4{h4[0], h4[1], h4[2], h4[3]};
     lo = u32x4{l4[0], l4[1], l4[2], l4[3]};
   };
+  const float sl2 = a.scale * 1.4426950408889634f;
   {
-    const int64_t base = (int64_t)t_row * a.q_stride + (int64_t)head * kAttnHeadDim + 8 * h;
-    // dims [0, 64): kd 0..3; rotate_half pairs kd with kd ^ 2 at the same j
-    float x[4][8];
+    const int64_t base = (int64_t)t_row * a.q_stride + (int64_t)head * kAttnHeadDim + 8 * g4;
+    // dims [0, 64) are kd 0, 1; rotate_half pairs dim 8 g4 + j with 32 + 8 g4 + j
+    float x[2][8];
 #pragma unroll
-    for (int kd = 0; kd < 4; ++kd) {
+    for (int kd = 0; kd < 2; ++kd) {
       if (row_ok) {
-        load_act8<AT>(a.q, base + 16 * kd, x[kd]);
+        load_act8<AT>(a.q, base + 32 * kd, x[kd]);
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[kd][j] = 0.f;
@@ -131,28 +137,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if (a.rope_dim == 64) {
       const float pos = static_cast<float>(qpos);
 #pragma unroll
-      for (int kd = 0; kd < 2; ++kd) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float ang = mul_rn(pos, a.inv_freq[16 * kd + 8 * h + j]);
-          const float cs = cosf(ang), sn = sinf(ang);
-          const float x1 = x[kd][j], x2 = x[kd + 2][j];
-          x[kd][j] = add_rn(mul_rn(x1, cs), mul_rn(-x2, sn));
-          x[kd + 2][j] = add_rn(mul_rn(x2, cs), mul_rn(x1, sn));
-        }
+      for (int j = 0; j < 8; ++j) {
+        const float ang = mul_rn(pos, a.inv_freq[8 * g4 + j]);
+        const float cs = cosf(ang), sn = sinf(ang);
+        const float x1 = x[0][j], x2 = x[1][j];
+        x[0][j] = add_rn(mul_rn(x1, cs), mul_rn(-x2, sn));
+        x[1][j] = add_rn(mul_rn(x2, cs), mul_rn(x1, sn));
       }
     }
 #pragma unroll
-    for (int kd = 0; kd < 4; ++kd) pack(x[kd], qh[kd], ql[kd]);
+    for (int kd = 0; kd < 2; ++kd) {
 #pragma unroll
-    for (int kd = 4; kd < 16; ++kd) {
+      for (int j = 0; j < 8; ++j) x[kd][j] *= sl2;
+      pack(x[kd], qh[kd], ql[kd]);
+    }
+#pragma unroll
+    for (int kd = 2; kd < 8; ++kd) {
       float y[8];
       if (row_ok) {
-        load_act8<AT>(a.q, base + 16 * kd, y);
+        load_act8<AT>(a.q, base + 32 * kd, y);
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) y[j] = 0.f;
       }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] *= sl2;
       pack(y, qh[kd], ql[kd]);
     }
   }
@@ -161,13 +170,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int npages = q_last / kPageTokens + 1;                   // <= pt_len (checked on the host)
   const int nblk = (npages + 1) / 2;
   const int kmax = min(q_last, ctx_total - 1);  // last key any column of the block uses
+  const int q_first = a.start + 16 * qb;         // first query position of the block
 
   // Direct-to-LDS copy of key block b (K and V tiles of pages 2b, 2b+1) into
-  // ring slot b % 3: 8 loads of 16 bytes per thread, always 8 so that the
+  // ring slot b % 4: 4 loads of 16 bytes per thread, always 4 so that the
   // wait counts below hold; a page past the block's range reads page 0 and
   // is masked out.
+  auto slot_of = [&](int b) { return ring + (b % kRingSlots) * kSlotVec; };
   auto issue = [&](int b) {
-    u32x4* slot = ring + (b % kRingSlots) * kSlotVec;
+    u32x4* slot = slot_of(b);
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg) {
       const int p = 2 * b + pg;
@@ -176,48 +187,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
       const u32x4* kp = reinterpret_cast<const u32x4*>(a.k_cache + tile * kTile);
       const u32x4* vp = reinterpret_cast<const u32x4*>(a.v_cache + tile * kTile);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int v = i * 256 + wave * 64;  // this wave's 64 vectors; lane l lands at +l
-        __builtin_amdgcn_global_load_lds(kp + v + lane, slot + pg * kTileVec + v, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vp + v + lane, slot + (2 + pg) * kTileVec + v, 16, 0, 0);
-      }
+      const int v = wave * 64;  // this wave's 64 vectors of each tile; lane l lands at +l
+      __builtin_amdgcn_global_load_lds(kp + v + lane, slot + pg * kTileVec + v, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vp + v + lane, slot + (2 + pg) * kTileVec + v, 16, 0, 0);
     }
   };
 
-  const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
-  f32x16 o[8];
+  f32x4 o[16];  // O^T tiles: dims 16 dt + 4 g4 + i, column n
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
+  for (int dt = 0; dt < 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  // K operand of lane (c, h) for dim block kd: key row c -> page c / 16,
-  // token block_row_token(c % 16); dims 16 kd + 8 h .. + 7 -> vector
-  // ((g % 8) * 4 + g / 8) * 16 + token of the K tile, g = 2 kd + h.
-  const int k_row_vec = (c >> 4) * kTileVec + block_row_token(c & 15);
+  // K operand rows of this lane (row n of both score tiles): vector offset of
+  // token tile_row_token(m, n) of page tile_row_page(n); dims 32 kd + 8 g4 ..
+  // + 7 are dim group q8 = 4 kd + g4 at vector ((q8 % 8) * 4 + q8 / 8) * 16.
+  const int k_row0 = tile_row_page(n) * kTileVec + tile_row_token(0, n);
+  const int k_row1 = tile_row_page(n) * kTileVec + tile_row_token(1, n);
+  // V^T operand of this lane for dim tile dt: dim 16 dt + n, tokens
+  // 8 (g4 % 2) .. + 7 of page g4 / 2 (16 contiguous bytes of the V tile).
+  const int v_vec = (2 + (g4 >> 1)) * kTileVec + 2 * n + (g4 & 1);
+  // key of result row i of score tile m in this lane: 32 b + 8 g4 + 4 m + i
 
   issue(0);
   if (nblk > 1) issue(1);
   for (int b = 0; b < nblk; ++b) {
     // this thread's copies of block b have landed; after the barrier every
-    // thread's have, and every wave is done with slot (b + 2) % 3
+    // thread's have, and every wave is done with slot (b + 2) % 4 (block b - 2)
     if (b + 1 < nblk)
-      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     else
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (b + 2 < nblk) issue(b + 2);
-    u32x4* slot = ring + (b % kRingSlots) * kSlotVec;
+    u32x4* slot = slot_of(b);
     if (32 * b + 31 > kmax) {
       // last block: zero V of keys past the last one used, so that
       // 0-probability keys cannot bring NaN/Inf from unwritten slots
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int vi = i * 256 + tid;            // vector of the block's two V tiles
-        const int m = vi / kTileVec;             // page of the block
-        const int tok0 = 8 * (vi & 1);           // tokens tok0 .. tok0 + 7 of one dim
-        const int k0 = 32 * b + 16 * m + tok0;
+      for (int j2 = 0; j2 < 2; ++j2) {
+        const int vi = j2 * kPrefillThreads + tid;  // vector of the block's two V tiles
+        const int m = vi / kTileVec;                 // page of the block
+        const int k0 = 32 * b + 16 * m + 8 * (vi & 1);  // tokens k0 .. k0 + 7 of one dim
         u32x4 w = slot[2 * kTileVec + vi];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -230,145 +239,97 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       }
       lds_barrier();
     }
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) asm volatile("" : "+a"(o[dt]));
 
-    f32x16 sh, sl;
+    // ---- scores: two 16-key tiles, q_hi and q_lo products into one accumulator
+    f32x4 sc[2];
+    sc[0] = sc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sh[r] = sl[r] = 0.f;
-    auto k_operand = [&](int kd) {
-      const int g = 2 * kd + h;
-      return slot[k_row_vec + ((g & 7) * 4 + (g >> 3)) * kPageTokens];
-    };
-    u32x4 kb[2][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) kb[0][i] = k_operand(i);
-#pragma unroll
-    for (int grp = 0; grp < 4; ++grp) {
-      if (grp + 1 < 4) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kb[(grp + 1) & 1][i] = k_operand(4 * (grp + 1) + i);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sh = KV::mfma32(kb[grp & 1][i], qh[4 * grp + i], sh);
-        sl = KV::mfma32(kb[grp & 1][i], ql[4 * grp + i], sl);
-      }
+    for (int kd = 0; kd < 8; ++kd) {
+      const int q8 = 4 * kd + g4;
+      const int goff = ((q8 & 7) * 4 + (q8 >> 3)) * kPageTokens;
+      const u32x4 k0 = slot[k_row0 + goff];
+      const u32x4 k1 = slot[k_row1 + goff];
+      sc[0] = KV::mfma_k32(k0, qh[kd], sc[0]);
+      sc[1] = KV::mfma_k32(k1, qh[kd], sc[1]);
+      sc[0] = KV::mfma_k32(k0, ql[kd], sc[0]);
+      sc[1] = KV::mfma_k32(k1, ql[kd], sc[1]);
     }
-    // keep four LDS reads in flight ahead of the MFMAs that consume them
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+
+    // ---- online softmax over the block (log2 units)
+    float s[8];
 #pragma unroll
-    for (int grp = 0; grp < 4; ++grp) {
-      if (grp + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    }
-    // row r of this lane holds key 32 b + 16 (r / 8) + 8 h + r % 8
-    const int key0 = 32 * b + 8 * h;
-    float s[16];
-    float mx = -INFINITY;
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kpos = key0 + 16 * (r >> 3) + (r & 7);
-      s[r] = kpos <= qlim ? (sh[r] + sl[r]) * sl2 : -INFINITY;
-      mx = fmaxf(mx, s[r]);
+      for (int i = 0; i < 4; ++i) s[4 * m + i] = sc[m][i];
+    if (32 * b + 31 > q_first) {
+      // blocks reaching past the block's first query need the causal mask
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (32 * b + 8 * g4 + 4 * m + i > qlim) s[4 * m + i] = -INFINITY;
     }
-    mx = swap32_max(mx);
+    float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    mx = swap_max(mx, true);
+    mx = swap_max(mx, false);
+    // m_run is finite from the first block on (key 0 is visible to every
+    // column), so masked scores give exp2(-inf) = 0
     const bool grow = mx > m_run + 8.0f;
     if (__any(grow)) {
       const float m_new = grow ? mx : m_run;
-      const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block, where o and l are 0
       l_run *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        // through VGPRs here only; the accumulators otherwise stay in AGPRs
-        f32x16 t = o[dt];
-        asm volatile("" : "+v"(t));
-        t *= alpha;
-        o[dt] = t;
-        asm volatile("" : "+a"(o[dt]));
-      }
+      for (int dt = 0; dt < 16; ++dt) o[dt] *= alpha;
       m_run = m_new;
     }
-    u32x4 ph[2], pl[2];
+    float pr[8];
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      float pr[8];
+    for (int j = 0; j < 8; ++j) pr[j] = __builtin_amdgcn_exp2f(s[j] - m_run);
+    l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+    u32x4 ph, pl;
+    pack(pr, ph, pl);
+
+    // ---- O^T += V^T P^T over the block's 32 keys
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float sv = s[8 * m + j];
-        pr[j] = sv == -INFINITY ? 0.f : exp2f(sv - m_run);
-        l_run += pr[j];
-      }
-      pack(pr, ph[m], pl[m]);
+    for (int dt = 0; dt < 16; ++dt) {
+      const u32x4 vop = slot[v_vec + 32 * dt];
+      o[dt] = KV::mfma_k32(vop, ph, o[dt]);
+      o[dt] = KV::mfma_k32(vop, pl, o[dt]);
     }
-    // V^T operand of lane (c, h), dim block dt, page m: dim 32 dt + c,
-    // tokens 8 h .. 8 h + 7 (16 contiguous bytes of the V tile)
-    auto v_operand = [&](int dt, int m) { return slot[(2 + m) * kTileVec + (32 * dt + c) * 2 + h]; };
-    u32x4 vb[2][2];
-    vb[0][0] = v_operand(0, 0);
-    vb[0][1] = v_operand(0, 1);
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      if (dt + 1 < 8) {
-        vb[(dt + 1) & 1][0] = v_operand(dt + 1, 0);
-        vb[(dt + 1) & 1][1] = v_operand(dt + 1, 1);
-      }
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        o[dt] = KV::mfma32(vb[dt & 1][m], ph[m], o[dt]);
-        o[dt] = KV::mfma32(vb[dt & 1][m], pl[m], o[dt]);
-      }
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      if (dt + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    }
-    // keep the accumulators resident in AGPRs across iterations (the rare
-    // rescale above then copies them out and back only when it runs)
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) asm volatile("" : "+a"(o[dt]));
   }
 
   // ---- normalise, stage (the ring is dead once every wave has left the loop), gate, store
   lds_barrier();
-  const float l_tot = swap32_sum(l_run);
+  const float l_tot = swap_sum(swap_sum(l_run, true), false);
   const float inv = 1.0f / l_tot;  // every valid query sees at least itself
-  float* st = stage + (wave * 32 + c) * kStagePitch;
+  float* st = stage + (wave * 16 + n) * kStagePitch;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int a4 = 0; a4 < 4; ++a4) {
-      // rows 8 a4 + 4 h + i of MFMA tile dt are dims 32 dt + 8 a4 + 4 h + i
-      const f32x4 v = {o[dt][4 * a4] * inv, o[dt][4 * a4 + 1] * inv, o[dt][4 * a4 + 2] * inv,
-                       o[dt][4 * a4 + 3] * inv};
-      *reinterpret_cast<f32x4*>(st + 32 * dt + 8 * a4 + 4 * h) = v;
-    }
+  for (int dt = 0; dt < 16; ++dt)
+    *reinterpret_cast<f32x4*>(st + 16 * dt + 4 * g4) = o[dt] * inv;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  for (int col = 0; col < 32; ++col) {
-    const int t = 16 * qb + (col & 15);
-    const int hw = 2 * wave + (col >> 4);
-    if (t >= a.length || hw >= a.group) continue;
-    const int hd = kvh * a.group + hw;
+  if (!head_ok) return;
+  for (int r = 0; r < 16; ++r) {
+    const int t = 16 * qb + r;
+    if (t >= a.length) break;
     const int d = 4 * lane;
-    const float* row = stage + (wave * 32 + col) * kStagePitch + d;
+    const float* row = stage + (wave * 16 + r) * kStagePitch + d;
     float g[4], y[4];
-    load_act4<AT>(a.gate, (int64_t)t * a.gate_stride + (int64_t)hd * kAttnHeadDim + d, g);
+    load_act4<AT>(a.gate, (int64_t)t * a.gate_stride + (int64_t)head * kAttnHeadDim + d, g);
 #pragma unroll
     for (int i = 0; i < 4; ++i) y[i] = mul_rn(row[i], sigmoid_f(g[i]));
-    store_act4<AT>(a.out, ((int64_t)t * a.num_q_heads + hd) * kAttnHeadDim + d, y);
+    store_act4<AT>(a.out, ((int64_t)t * a.num_q_heads + head) * kAttnHeadDim + d, y);
   }
 }
 
 template <int AT>
 static void launch_prefill(const PrefillAttnArgs& a, const int32_t* pt, int kv_dtype, dim3 grid, hipStream_t st) {
   if (kv_dtype == RIA_DT_F16)
-    hipLaunchKernelGGL((attn_prefill_kernel<AT, RIA_DT_F16>), grid, dim3(256), 0, st, a, pt);
+    hipLaunchKernelGGL((attn_prefill_kernel<AT, RIA_DT_F16>), grid, dim3(kPrefillThreads), 0, st, a, pt);
   else
-    hipLaunchKernelGGL((attn_prefill_kernel<AT, RIA_DT_BF16>), grid, dim3(256), 0, st, a, pt);
+    hipLaunchKernelGGL((attn_prefill_kernel<AT, RIA_DT_BF16>), grid, dim3(kPrefillThreads), 0, st, a, pt);
 }
 
 }  // namespace ria
@@ -380,12 +341,15 @@ extern "C" int ria_kv_append_seq(int length, int num_kv_heads, const void* k, in
                                  int kv_dtype, int num_pages, const int32_t* page_table_row, int64_t page_capacity,
                                  int32_t start_pos, const float* inv_freq, int rope_dim, void* stream);
 
-extern "C" int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads, const void* q, int64_t q_row_stride,
-                                const void* k, int64_t k_row_stride, const void* v, int64_t v_row_stride,
-                                const void* gate, int64_t gate_row_stride, int act_dtype, void* k_cache,
-                                void* v_cache, int kv_dtype, int num_pages, const int32_t* page_table_row,
-                                int64_t page_capacity, int32_t start_pos, const float* inv_freq, int rope_dim,
-                                float scale, void* out, void* stream) {
+extern "C" int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_heads, const void* q,
+                                      int64_t q_row_stride, const void* k, int64_t k_row_stride, const void* v,
+                                      int64_t v_row_stride, const void* gate, int64_t gate_row_stride, int act_dtype,
+                                      void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                                      const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
+                                      const float* inv_freq, int rope_dim, float scale, void* out, int phase,
+                                      void* stream) {
+  if (phase < RIA_PREFILL_APPEND || phase > RIA_PREFILL_BOTH)
+    return set_error(RIA_ERR_INVALID, "ria_attn_prefill: phase must be 1 (append), 2 (attention) or 3 (both)");
   if (length < 0 || start_pos < 0) return set_error(RIA_ERR_INVALID, "ria_attn_prefill: negative length or start");
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
     return set_error(RIA_ERR_INVALID, "ria_attn_prefill: num_q_heads must be a multiple of num_kv_heads");
@@ -411,10 +375,13 @@ extern "C" int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads, c
   if (length == 0) return RIA_OK;
   const int64_t blocks = (int64_t)((length + 15) / 16) * num_kv_heads;
   if (blocks > 0x7fffffff) return set_error(RIA_ERR_INVALID, "ria_attn_prefill: grid too large");
-  int rc = ria_kv_append_seq(length, num_kv_heads, k, act_dtype, k_row_stride, v, act_dtype, v_row_stride, k_cache,
-                             v_cache, kv_dtype, num_pages, page_table_row, page_capacity, start_pos, inv_freq,
-                             rope_dim, stream);
-  if (rc != RIA_OK) return rc;
+  if (phase & RIA_PREFILL_APPEND) {
+    int rc = ria_kv_append_seq(length, num_kv_heads, k, act_dtype, k_row_stride, v, act_dtype, v_row_stride,
+                               k_cache, v_cache, kv_dtype, num_pages, page_table_row, page_capacity, start_pos,
+                               inv_freq, rope_dim, stream);
+    if (rc != RIA_OK) return rc;
+  }
+  if (!(phase & RIA_PREFILL_ATTEND)) return RIA_OK;
   PrefillAttnArgs a{};
   a.q = q;
   a.q_stride = q_row_stride;
@@ -442,4 +409,16 @@ extern "C" int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads, c
   else
     launch_prefill<RIA_DT_F32>(a, page_table_row, kv_dtype, grid, st);
   return check_launch("ria_attn_prefill");
+}
+
+extern "C" int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads, const void* q, int64_t q_row_stride,
+                                const void* k, int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                const void* gate, int64_t gate_row_stride, int act_dtype, void* k_cache,
+                                void* v_cache, int kv_dtype, int num_pages, const int32_t* page_table_row,
+                                int64_t page_capacity, int32_t start_pos, const float* inv_freq, int rope_dim,
+                                float scale, void* out, void* stream) {
+  return ria_attn_prefill_phase(length, num_q_heads, num_kv_heads, q, q_row_stride, k, k_row_stride, v, v_row_stride,
+                                gate, gate_row_stride, act_dtype, k_cache, v_cache, kv_dtype, num_pages,
+                                page_table_row, page_capacity, start_pos, inv_freq, rope_dim, scale, out,
+                                RIA_PREFILL_BOTH, stream);
 }

@@ -24,6 +24,8 @@ constexpr int kPageTokens = 16;    // tokens per KV page
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -172,6 +174,12 @@ template <>
 struct Kv16<RIA_DT_BF16> {
   static __device__ __forceinline__ uint16_t from_f32(float f) { return f32_to_bf16_bits(f); }
   static __device__ __forceinline__ float to_f32(uint16_t b) { return bf16_bits_to_f32(b); }
+  // two values rounded to nearest-even in one instruction: a in the low half
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+  }
+  static __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
   static __device__ __forceinline__ f32x4 mfma_k32(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
@@ -190,6 +198,11 @@ template <>
 struct Kv16<RIA_DT_F16> {
   static __device__ __forceinline__ uint16_t from_f32(float f) { return f32_to_f16_bits(f); }
   static __device__ __forceinline__ float to_f32(uint16_t b) { return f16_bits_to_f32(b); }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return static_cast<uint32_t>(f32_to_f16_bits(a)) | (static_cast<uint32_t>(f32_to_f16_bits(b)) << 16);
+  }
+  static __device__ __forceinline__ float lo_f32(uint32_t w) { return f16_bits_to_f32(static_cast<uint16_t>(w)); }
+  static __device__ __forceinline__ float hi_f32(uint32_t w) { return f16_bits_to_f32(static_cast<uint16_t>(w >> 16)); }
   static __device__ __forceinline__ f32x4 mfma_k32(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
                                                   0);

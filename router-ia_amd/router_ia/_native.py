@@ -25,6 +25,9 @@ RIA_GATE_RAW = 1
 RIA_ATTN_SPLITK = 1
 RIA_ATTN_COMBINE = 2
 RIA_ATTN_BOTH = 3
+RIA_PREFILL_APPEND = 1
+RIA_PREFILL_ATTEND = 2
+RIA_PREFILL_BOTH = 3
 
 _c_int = ctypes.c_int
 _c_i32 = ctypes.c_int32
@@ -86,6 +89,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_int, _c_int, _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _vp, _vp,
          _c_int, _c_int, _vp, _c_i64, _c_i32, _vp, _c_int, _c_f32, _vp, _vp],
+    ),
+    "ria_attn_prefill_phase": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _vp, _vp,
+         _c_int, _c_int, _vp, _c_i64, _c_i32, _vp, _c_int, _c_f32, _vp, _c_int, _vp],
     ),
 }
 

@@ -494,12 +494,14 @@ def attn_prefill(
     start: int,
     inv_freq: torch.Tensor | None,
     scale: float,
+    phase: int = nat.RIA_PREFILL_BOTH,
 ) -> torch.Tensor:
-    """Causal GQA prefill of one sequence's prompt over its paged cache (ria_attn_prefill).
+    """Causal GQA prefill of one sequence's prompt over its paged cache (ria_attn_prefill_phase).
 
     q, gate [L, Hq, 256]; k, v [L, Hkv, 256], all of one dtype; the prompt's
     k/v are appended at slots start .. start + L - 1 first.  Returns out
-    [L, Hq, 256] in that dtype.
+    [L, Hq, 256] in that dtype.  phase selects the append launch, the
+    attention launch or both (the default).
     """
     length = int(q.shape[0])
     num_q_heads = int(q.shape[1])
@@ -524,9 +526,10 @@ def attn_prefill(
     if tuple(out.shape) != (length, num_q_heads, ATTN_HEAD_DIM) or not out.is_contiguous() or out.dtype != q.dtype:
         raise ValueError(f"out must be contiguous [{length}, {num_q_heads}, 256] of q's dtype")
     rope_dim = 0 if inv_freq is None else 2 * int(inv_freq.numel())
-    rc = nat.load().ria_attn_prefill(length, num_q_heads, num_kv_heads, _ptr(q), qs, _ptr(k), ks, _ptr(v), vs,
-                                     _ptr(gate), gs, dtype_code(q), _ptr(k_cache), _ptr(v_cache),
-                                     dtype_code(k_cache), pages, _ptr(page_table), cap, int(start), _ptr(inv_freq),
-                                     rope_dim, float(scale), _ptr(out), _stream(dev))
+    rc = nat.load().ria_attn_prefill_phase(length, num_q_heads, num_kv_heads, _ptr(q), qs, _ptr(k), ks, _ptr(v),
+                                           vs, _ptr(gate), gs, dtype_code(q), _ptr(k_cache), _ptr(v_cache),
+                                           dtype_code(k_cache), pages, _ptr(page_table), cap, int(start),
+                                           _ptr(inv_freq), rope_dim, float(scale), _ptr(out), int(phase),
+                                           _stream(dev))
     nat.check(rc, "ria_attn_prefill")
     return out

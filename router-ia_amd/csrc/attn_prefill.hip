@@ -22,8 +22,9 @@
 //     the block's tokens in an order that leaves lane group g with exactly 8
 //     consecutive tokens of one page, whose V^T column is then one 16-byte
 //     operand of O^T = V^T P^T (16x16x32, k = those 32 keys);
-//   * the rotated q and the probabilities are carried as 16-bit hi + lo
-//     pairs (near-fp32 operands on MFMA); the online softmax is kept in log2
+//   * with a bf16 cache the rotated q and the probabilities are carried as
+//     bf16 hi + lo pairs (near-fp32 operands on MFMA); with an fp16 cache the
+//     fp16 hi part alone (11 significant bits); the online softmax is kept in log2
 //     units (q is pre-scaled) with a lazy rescale (only when a block max
 //     exceeds the running max by 2^8); row statistics combine across lane
 //     groups with permlane swaps;
@@ -37,7 +38,13 @@ namespace ria {
 
 constexpr int kTile = kPageTokens * kAttnHeadDim;  // elements per (page, KV head) tile
 constexpr int kTileVec = kTile * 2 / 16;           // 16-byte vectors per tile (512)
-constexpr int kSlotVec = 4 * kTileVec;             // ring slot: K page 0, K page 1, V page 0, V page 1
+// Ring slot layout (16-byte vectors): K page 0 at 0, K page 1 at kSlotK1 (64
+// bytes further than back-to-back, so the rows of the two pages that one
+// 16-lane read pass touches fall on different banks), V^T pages 0 and 1 at
+// kSlotV + 512 m, each stored as [token half][dim][8 tokens].
+constexpr int kSlotK1 = kTileVec + 4;
+constexpr int kSlotV = kSlotK1 + kTileVec;
+constexpr int kSlotVec = kSlotV + 2 * kTileVec;
 constexpr int kRingSlots = 4;
 constexpr int kPrefillWaves = 8;                   // one query head per wave
 constexpr int kPrefillThreads = 64 * kPrefillWaves;
@@ -88,6 +95,9 @@ template <int AT, int KVT>
 __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(
     PrefillAttnArgs a, const int32_t* __restrict__ pt) {
   using KV = Kv16<KVT>;
+  // bf16 operands carry q and the probabilities as hi + lo pairs; fp16 ones
+  // keep 11 significant bits in the hi part alone, which is enough here
+  constexpr bool kSplit = KVT == RIA_DT_BF16;
   const int nqb = (a.length + 15) / 16;
   const int qb = nqb - 1 - static_cast<int>(blockIdx.x) / a.num_kv_heads;  // heaviest blocks first
   const int kvh = static_cast<int>(blockIdx.x) % a.num_kv_heads;
@@ -188,8 +198,10 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
       const u32x4* kp = reinterpret_cast<const u32x4*>(a.k_cache + tile * kTile);
       const u32x4* vp = reinterpret_cast<const u32x4*>(a.v_cache + tile * kTile);
       const int v = wave * 64;  // this wave's 64 vectors of each tile; lane l lands at +l
-      __builtin_amdgcn_global_load_lds(kp + v + lane, slot + pg * kTileVec + v, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vp + v + lane, slot + (2 + pg) * kTileVec + v, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(kp + v + lane, slot + pg * kSlotK1 + v, 16, 0, 0);
+      // V^T position (half, dim) = v + lane holds tile vector 2 dim + half
+      const int vdim = (wave & 3) * 64 + lane, vhalf = wave >> 2;
+      __builtin_amdgcn_global_load_lds(vp + 2 * vdim + vhalf, slot + kSlotV + pg * kTileVec + v, 16, 0, 0);
     }
   };
 
@@ -201,61 +213,58 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   // K operand rows of this lane (row n of both score tiles): vector offset of
   // token tile_row_token(m, n) of page tile_row_page(n); dims 32 kd + 8 g4 ..
   // + 7 are dim group q8 = 4 kd + g4 at vector ((q8 % 8) * 4 + q8 / 8) * 16.
-  const int k_row0 = tile_row_page(n) * kTileVec + tile_row_token(0, n);
-  const int k_row1 = tile_row_page(n) * kTileVec + tile_row_token(1, n);
+  const int k_row0 = tile_row_page(n) * kSlotK1 + tile_row_token(0, n);
+  const int k_row1 = tile_row_page(n) * kSlotK1 + tile_row_token(1, n);
   // V^T operand of this lane for dim tile dt: dim 16 dt + n, tokens
-  // 8 (g4 % 2) .. + 7 of page g4 / 2 (16 contiguous bytes of the V tile).
-  const int v_vec = (2 + (g4 >> 1)) * kTileVec + 2 * n + (g4 & 1);
+  // 8 (g4 % 2) .. + 7 of page g4 / 2 (one 16-byte vector).
+  const int v_vec = kSlotV + (g4 >> 1) * kTileVec + (g4 & 1) * 256 + n;
   // key of result row i of score tile m in this lane: 32 b + 8 g4 + 4 m + i
 
-  issue(0);
-  if (nblk > 1) issue(1);
-  for (int b = 0; b < nblk; ++b) {
-    // this thread's copies of block b have landed; after the barrier every
-    // thread's have, and every wave is done with slot (b + 2) % 4 (block b - 2)
-    if (b + 1 < nblk)
-      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (b + 2 < nblk) issue(b + 2);
-    u32x4* slot = slot_of(b);
-    if (32 * b + 31 > kmax) {
-      // last block: zero V of keys past the last one used, so that
-      // 0-probability keys cannot bring NaN/Inf from unwritten slots
-#pragma unroll
-      for (int j2 = 0; j2 < 2; ++j2) {
-        const int vi = j2 * kPrefillThreads + tid;  // vector of the block's two V tiles
-        const int m = vi / kTileVec;                 // page of the block
-        const int k0 = 32 * b + 16 * m + 8 * (vi & 1);  // tokens k0 .. k0 + 7 of one dim
-        u32x4 w = slot[2 * kTileVec + vi];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uint32_t x = w[j];
-          if (k0 + 2 * j > kmax) x &= 0xffff0000u;
-          if (k0 + 2 * j + 1 > kmax) x &= 0x0000ffffu;
-          w[j] = x;
-        }
-        slot[2 * kTileVec + vi] = w;
-      }
-      lds_barrier();
-    }
-
-    // ---- scores: two 16-key tiles, q_hi and q_lo products into one accumulator
-    f32x4 sc[2];
-    sc[0] = sc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Each phase first issues all of its LDS operand reads, then its MFMAs
+  // (scheduling barriers keep the compiler from re-serialising them); the
+  // V^T reads of a block go out before its softmax so they land meanwhile.
+  //
+  // ---- scores of block b: two 16-key tiles; q_hi and q_lo products in separate
+  //      accumulators so no MFMA waits on the one just before it
+  auto qk = [&](int b, f32x4 (&sc)[2]) {
+    const u32x4* slot = slot_of(b);
+    u32x4 kop[8][2];
 #pragma unroll
     for (int kd = 0; kd < 8; ++kd) {
       const int q8 = 4 * kd + g4;
       const int goff = ((q8 & 7) * 4 + (q8 >> 3)) * kPageTokens;
-      const u32x4 k0 = slot[k_row0 + goff];
-      const u32x4 k1 = slot[k_row1 + goff];
-      sc[0] = KV::mfma_k32(k0, qh[kd], sc[0]);
-      sc[1] = KV::mfma_k32(k1, qh[kd], sc[1]);
-      sc[0] = KV::mfma_k32(k0, ql[kd], sc[0]);
-      sc[1] = KV::mfma_k32(k1, ql[kd], sc[1]);
+      kop[kd][0] = slot[k_row0 + goff];
+      kop[kd][1] = slot[k_row1 + goff];
     }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kd = 0; kd < 8; ++kd) {
+      acc[0] = KV::mfma_k32(kop[kd][0], qh[kd], acc[0]);
+      acc[1] = KV::mfma_k32(kop[kd][1], qh[kd], acc[1]);
+      if (kSplit) {
+        acc[2] = KV::mfma_k32(kop[kd][0], ql[kd], acc[2]);
+        acc[3] = KV::mfma_k32(kop[kd][1], ql[kd], acc[3]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    sc[0] = acc[0] + acc[2];
+    sc[1] = acc[1] + acc[3];
+  };
 
-    // ---- online softmax over the block (log2 units)
+  auto load_v = [&](int b, u32x4 (&vop)[16]) {
+    const u32x4* slot = slot_of(b);
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) vop[dt] = slot[v_vec + 16 * dt];
+  };
+
+  // ---- online softmax of block b (log2 units), then O^T += V^T P^T over its 32 keys
+  auto softmax_pv = [&](int b, const f32x4 (&sc)[2]) {
+    u32x4 vop[16];
+    load_v(b, vop);
+    __builtin_amdgcn_sched_barrier(0);
     float s[8];
 #pragma unroll
     for (int m = 0; m < 2; ++m)
@@ -289,15 +298,66 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
     u32x4 ph, pl;
     pack(pr, ph, pl);
-
-    // ---- O^T += V^T P^T over the block's 32 keys
+    __builtin_amdgcn_sched_barrier(0);
+    // all hi products, then all lo products: 16 MFMAs between dependent ones
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-      const u32x4 vop = slot[v_vec + 32 * dt];
-      o[dt] = KV::mfma_k32(vop, ph, o[dt]);
-      o[dt] = KV::mfma_k32(vop, pl, o[dt]);
+    for (int dt = 0; dt < 16; ++dt) o[dt] = KV::mfma_k32(vop[dt], ph, o[dt]);
+    if (kSplit) {
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) o[dt] = KV::mfma_k32(vop[dt], pl, o[dt]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Waves w and w + 4 share a SIMD.  Waves 4..7 run half an iteration behind
+  // (softmax and P V of block b - 1 before the scores of block b), so that
+  // on every SIMD one wave's softmax overlaps the other's MFMAs instead of
+  // both waves reaching the same phase between the same two barriers.  The
+  // slot of block b - 1 stays valid through iteration b (4-slot ring).
+  const bool lag = wave >= 4;
+  f32x4 sc[2];
+  issue(0);
+  if (nblk > 1) issue(1);
+  for (int b = 0; b < nblk; ++b) {
+    // this thread's copies of block b have landed; after the barrier every
+    // thread's have, and every wave is done with slot (b + 2) % 4 (block b - 2)
+    if (b + 1 < nblk)
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (b + 2 < nblk) issue(b + 2);
+    u32x4* slot = slot_of(b);
+    if (32 * b + 31 > kmax) {
+      // last block: zero V of keys past the last one used, so that
+      // 0-probability keys cannot bring NaN/Inf from unwritten slots
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2) {
+        const int vi = j2 * kPrefillThreads + tid;  // vector of the block's two V^T tiles
+        const int m = vi / kTileVec;                 // page of the block
+        const int half = (vi % kTileVec) >> 8;       // token half: tokens 8 half .. + 7 of one dim
+        const int k0 = 32 * b + 16 * m + 8 * half;
+        u32x4 w = slot[kSlotV + vi];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint32_t x = w[j];
+          if (k0 + 2 * j > kmax) x &= 0xffff0000u;
+          if (k0 + 2 * j + 1 > kmax) x &= 0x0000ffffu;
+          w[j] = x;
+        }
+        slot[kSlotV + vi] = w;
+      }
+      lds_barrier();
+    }
+
+    if (!lag) {
+      qk(b, sc);
+      softmax_pv(b, sc);
+    } else {
+      if (b > 0) softmax_pv(b - 1, sc);
+      qk(b, sc);
     }
   }
+  if (lag) softmax_pv(nblk - 1, sc);
 
   // ---- normalise, stage (the ring is dead once every wave has left the loop), gate, store
   lds_barrier();

@@ -14,6 +14,9 @@ layer is one kernel launch over the whole batch:
 Per token the caller runs ``linear_step`` / ``full_step`` for each layer and
 then ``advance()``, the batched equivalent of the reference caller bumping
 ``tokens_seen`` after all 40 layers (v2/src/router_ia/qwen36_chat_batch.py:204-206).
+A prompt enters one row at a time through ``begin_prefill`` /
+``linear_prefill`` / ``full_prefill`` / ``end_prefill`` (chunked DeltaNet and
+causal attention prefill), equal to decoding it token by token.
 """
 
 from __future__ import annotations
@@ -51,6 +54,7 @@ class BatchedAttentionState:
         page_shuffle_seed: int | None = None,
         split_tokens: int = 0,
         kv_dtype: torch.dtype = torch.bfloat16,
+        prefill_segment_tokens: int = 4096,
     ):
         self.device = torch.device(device)
         if self.device.type != "cuda":
@@ -85,6 +89,10 @@ class BatchedAttentionState:
         self.scale = 256 ** -0.5
         self._fixed_split = split_tokens > 0
         self._size_workspace()
+        # DeltaNet prefill runs prompts in segments of this many tokens; its
+        # workspace (about 75 KB per token) is allocated on the first prefill
+        self.prefill_segment_tokens = max(64, int(prefill_segment_tokens))
+        self.prefill_workspace: torch.Tensor | None = None
 
     def _size_workspace(self) -> None:
         ws = K.attn_decode_workspace_bytes(self.max_seqs, self.num_q_heads, self.num_kv_heads, self.max_context,
@@ -184,6 +192,73 @@ class BatchedAttentionState:
         return K.attn_decode(q, gate, k_cache, v_cache, self.kv.page_table, out, positions=self.tokens_seen,
                              ctx_lens=self.ctx_lens, max_ctx=max_ctx, inv_freq=self.inv_freq, scale=self.scale,
                              workspace=self.workspace, split_tokens=self.split_tokens)
+
+    # ---------------------------------------------------------------- prompt prefill (one row)
+    # A prompt enters one sequence row at a time: begin_prefill(row, L), then
+    # linear_prefill / full_prefill for every layer, then end_prefill(row, L).
+    # The result equals L decode steps of that row (the reference prefills
+    # token by token, qwen36_chat_batch.py:255-258).
+    def begin_prefill(self, row: int, length: int) -> None:
+        """Reserve KV pages for `length` more tokens of `row` (plus the next decode token)."""
+        target = self._host_seen[row] + length + 1
+        if target > self.max_context:
+            raise RuntimeError(f"prompt of {length} tokens exceeds max_context={self.max_context}")
+        self._ensure([target if r == row else n + 1 for r, n in enumerate(self._host_seen)])
+
+    def _prefill_workspace(self, length: int) -> torch.Tensor:
+        seg = min(length, self.prefill_segment_tokens)
+        need = K.gdn_prefill_workspace_bytes(self.num_k_heads, self.num_v_heads, max(seg, 64))
+        if self.prefill_workspace is None or self.prefill_workspace.numel() < need:
+            self.prefill_workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
+        return self.prefill_workspace
+
+    def linear_prefill(
+        self,
+        layer: int,
+        row: int,
+        mixed_qkv: torch.Tensor,
+        conv_weight: torch.Tensor,
+        gate_a: torch.Tensor,
+        gate_b: torch.Tensor,
+        *,
+        gate_mode: int = nat.RIA_GATE_PRECOMPUTED,
+        A_log: torch.Tensor | None = None,
+        dt_bias: torch.Tensor | None = None,
+        out: torch.Tensor | None = None,
+        out_dtype: torch.dtype = torch.bfloat16,
+    ) -> torch.Tensor:
+        """A prompt's Gated DeltaNet tokens for one row (chunked prefill); mixed_qkv [L, conv_dim]."""
+        length = int(mixed_qkv.shape[0])
+        if out is None:
+            out = torch.empty((length, self.num_v_heads, 128), dtype=out_dtype, device=self.device)
+        return K.gdn_prefill(
+            mixed_qkv, self.linear_states[layer, row], gate_a, gate_b, out,
+            num_k_heads=self.num_k_heads, num_v_heads=self.num_v_heads, conv_weight=conv_weight,
+            conv_ring=self.conv_rings[layer, row], conv_pos=self._host_seen[row],
+            workspace=self._prefill_workspace(length), gate_mode=gate_mode, A_log=A_log, dt_bias=dt_bias)
+
+    def full_prefill(
+        self,
+        layer: int,
+        row: int,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        gate: torch.Tensor,
+        *,
+        out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Append a prompt's k, v (RoPE on k) to one row and run its causal attention; q, gate [L, Hq, 256]."""
+        k_cache, v_cache = self.kv.layer(layer)
+        return K.attn_prefill(q, k, v, gate, k_cache, v_cache, self.kv.page_table[row], out,
+                              start=self._host_seen[row], inv_freq=self.inv_freq, scale=self.scale)
+
+    def end_prefill(self, row: int, length: int) -> None:
+        """The row's position moves past the prompt (after every layer has run it)."""
+        self._host_seen[row] += length
+        self.tokens_seen[row] += length
+        self.ctx_lens[row] += length
+        self._min_headroom = min(self.kv.alloc.capacity_tokens(r) - self._host_seen[r] for r in range(self.max_seqs))
 
     # ---------------------------------------------------------------- inspection
     def gather_kv(self, layer: int, start: int, count: int) -> tuple[torch.Tensor, torch.Tensor]:

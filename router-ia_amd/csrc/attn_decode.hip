@@ -64,8 +64,11 @@ struct AttnArgs {
   float scale;
   int split_tokens;
   int max_splits;
-  float* ws_stats;  // [parts][group][2]  (max in log2 units, sum)
-  float* ws_acc;    // [parts][group][256]
+  int balanced;      // 1: stream-K partition of all (sequence, KV head) pages over the grid
+  int batch;
+  int32_t* ws_units; // balanced: [0] total pages, [1] pages per workgroup, [2 ..] page offset of each unit
+  float* ws_stats;   // [parts][group][2]  (max in log2 units, sum)
+  float* ws_acc;     // [parts][group][256]
   int num_q_heads;
   int num_kv_heads;
   int group;
@@ -131,232 +134,329 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   a.v_cache[(tile * kAttnHeadDim + d) * kPageTokens + off] = Kv16<KVT>::from_f32(vv);
 }
 
-template <int QT, int KVT>
+// Pages of the context of batch row b (never past the row's page-table entries).
+__device__ __forceinline__ int row_ctx(const AttnArgs& a, int b) {
+  return min(a.ctx_lens ? a.ctx_lens[b] : a.ctx_scalar, (int)min<int64_t>(a.pt_stride * kPageTokens, 1 << 30));
+}
+
+// Balanced partition: unit u = b * Hkv + kvh owns pages [off[u], off[u + 1])
+// of one global page stream of `total` pages; workgroup w takes pages
+// [w * chunk, (w + 1) * chunk).  Workgroup w's partial for unit u lives at
+// index w + u, which is unique because the (w, u) pairs that meet form a
+// monotone staircase.
+constexpr int kMaxBalancedUnits = 4096;
+constexpr int kMinChunkPages = 16;
+
+// Inclusive block scan of up to 256 per-thread values through LDS; returns
+// the exclusive prefix of this thread's value.
+__device__ int block_exclusive_scan(int v, int* scratch) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) scratch[wave] = x;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += scratch[w];
+  __syncthreads();
+  return base + x - v;
+}
+
+template <int QT, int KVT, bool BALANCED>
 __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
   using KV = Kv16<KVT>;
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
-  // Never read past the row's page-table entries, whatever ctx_lens holds.
-  const int ctx = min(a.ctx_lens ? a.ctx_lens[b] : a.ctx_scalar, (int)min<int64_t>(a.pt_stride * kPageTokens, 1 << 30));
-  const int tok0 = split * a.split_tokens;
-  if (tok0 >= ctx) return;
-  const int tok1 = min(ctx, tok0 + a.split_tokens);
-  const int row = a.seq_slot ? a.seq_slot[b] : b;
-  const float pos = static_cast<float>(a.positions ? a.positions[b] : a.pos_scalar);
   const int G = a.group;
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int n = lane & 15;   // MFMA column: query head (scores) / dim row (PV)
   const int g4 = lane >> 4;  // lane group
 
-  // LDS: the fp32 rotated query rows share space with the end-of-split merge.
+  // LDS: the fp32 rotated query rows share space with the end-of-range merge.
   __shared__ float sm_o[4][8][kAttnHeadDim];  // group <= 8 on this path (checked on the host)
   __shared__ uint4 q_pk[2][8][64];            // bf16 Q operand hi / lo, [part][kk][lane]
   __shared__ float sm_m[4][kMaxGroup];
   __shared__ float sm_l[4][kMaxGroup];
   float (*q_lds)[kAttnHeadDim] = sm_o[0];
-
-  // ---- Q: rotate the group's query heads into LDS (one thread per dim).
-  float rc = 1.f, rs = 0.f;
-  if (a.rope_dim == 64 && tid < 64) {
-    const float ang = mul_rn(pos, a.inv_freq[tid & 31]);
-    rc = cosf(ang);
-    rs = sinf(ang);
-  }
-  for (int h = 0; h < G; ++h) {
-    const int64_t base = (int64_t)b * a.q_stride + (int64_t)(kvh * G + h) * kAttnHeadDim;
-    float x = load_act<QT>(a.q, base + tid);
-    if (a.rope_dim == 64 && tid < 64) {
-      const float partner = load_act<QT>(a.q, base + (tid ^ 32));
-      x = add_rn(mul_rn(x, rc), mul_rn(tid < 32 ? -partner : partner, rs));
-    }
-    q_lds[h][tid] = x;
-  }
-  __syncthreads();
-  // Pack the B operand: lane (head n, group g4) holds dims 64*g4 + 8*kk + j,
-  // as a bf16 hi part and a bf16 remainder.
-  {
-    const int kk0 = wave * 2;  // each wave packs two kk blocks
-#pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      uint32_t wh[4], wl[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float x0 = n < G ? q_lds[n & 7][64 * g4 + 8 * (kk0 + k2) + 2 * j] : 0.f;
-        const float x1 = n < G ? q_lds[n & 7][64 * g4 + 8 * (kk0 + k2) + 2 * j + 1] : 0.f;
-        const uint16_t h0 = KV::from_f32(x0), h1 = KV::from_f32(x1);
-        const uint16_t l0 = KV::from_f32(x0 - KV::to_f32(h0));
-        const uint16_t l1 = KV::from_f32(x1 - KV::to_f32(h1));
-        wh[j] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
-        wl[j] = static_cast<uint32_t>(l0) | (static_cast<uint32_t>(l1) << 16);
-      }
-      q_pk[0][kk0 + k2][lane] = uint4{wh[0], wh[1], wh[2], wh[3]};
-      q_pk[1][kk0 + k2][lane] = uint4{wl[0], wl[1], wl[2], wl[3]};
-    }
-  }
-  __syncthreads();
-
   // Scores are kept in log2 units: s2 = (q . k) * scale * log2(e).
   const float sl2 = a.scale * 1.4426950408889634f;
-  f32x4 o[16];
-#pragma unroll
-  for (int db = 0; db < 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
 
-  const int page0 = tok0 / kPageTokens;
-  const int page_end = (tok1 + kPageTokens - 1) / kPageTokens;
-  const int32_t* pt = a.page_table + (int64_t)row * a.pt_stride;
+  // One (batch row, KV head, token range) -> partial `part`.
+  auto process = [&](int b, int kvh, int tok0, int tok1, int64_t part) {
+    const int row = a.seq_slot ? a.seq_slot[b] : b;
+    const float pos = static_cast<float>(a.positions ? a.positions[b] : a.pos_scalar);
+    __syncthreads();  // the previous range's merge has been read out of sm_o
 
-  auto load_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
-    int phys = pt[p];
-    phys = (phys < 0 || phys >= a.num_pages) ? 0 : phys;  // unallocated entries never fault
-    const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
-    const u32x4* kp = reinterpret_cast<const u32x4*>(a.k_cache + tile * kTileElems) + lane;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) kr[kk] = ld_stream(kp + kk * 64);
-    const uint16_t* vp = a.v_cache + tile * kTileElems + n * kPageTokens + 4 * g4;
-#pragma unroll
-    for (int db = 0; db < 16; ++db) vr[db] = ld_stream(reinterpret_cast<const u32x2*>(vp + db * 16 * kPageTokens));
-  };
-
-  auto compute_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
-    // Re-read the Q operand from LDS every page (an opaque offset keeps the
-    // compiler from hoisting 64 loop-invariant VGPRs out of the page loop).
-    int qoff = lane;
-    asm volatile("" : "+v"(qoff));
-    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const uint4 qh = q_pk[0][kk][qoff], ql = q_pk[1][kk][qoff];
-      sc = KV::mfma_k32(kr[kk], u32x4{qh.x, qh.y, qh.z, qh.w}, sc);
-      sc = KV::mfma_k32(kr[kk], u32x4{ql.x, ql.y, ql.z, ql.w}, sc);
+    // ---- Q: rotate the group's query heads into LDS (one thread per dim).
+    float rc = 1.f, rs = 0.f;
+    if (a.rope_dim == 64 && tid < 64) {
+      const float ang = mul_rn(pos, a.inv_freq[tid & 31]);
+      rc = cosf(ang);
+      rs = sinf(ang);
     }
-    const int t_base = p * kPageTokens + 4 * g4;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sc[i] = (t_base + i < tok1) ? sc[i] * sl2 : -INFINITY;
-      mx = fmaxf(mx, sc[i]);
+    for (int h = 0; h < G; ++h) {
+      const int64_t base = (int64_t)b * a.q_stride + (int64_t)(kvh * G + h) * kAttnHeadDim;
+      float x = load_act<QT>(a.q, base + tid);
+      if (a.rope_dim == 64 && tid < 64) {
+        const float partner = load_act<QT>(a.q, base + (tid ^ 32));
+        x = add_rn(mul_rn(x, rc), mul_rn(tid < 32 ? -partner : partner, rs));
+      }
+      q_lds[h][tid] = x;
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    // Lazy rescale: keep the reference max while the page max stays within
-    // 2^8 of it, so the accumulator is rescaled only when it has to be.
-    const bool grow = mx > m_run + 8.0f;
-    if (__any(grow)) {
-      const float m_new = grow ? mx : m_run;
-      const float alpha = exp2f(m_run - m_new);
-      l_run *= alpha;
+    __syncthreads();
+    // Pack the B operand: lane (head n, group g4) holds dims 64*g4 + 8*kk + j,
+    // as a bf16 hi part and a bf16 remainder.
+    {
+      const int kk0 = wave * 2;  // each wave packs two kk blocks
 #pragma unroll
-      for (int db = 0; db < 16; ++db) o[db] *= alpha;
-      m_run = m_new;
-    }
-    uint16_t ph[4], plo[4];
+      for (int k2 = 0; k2 < 2; ++k2) {
+        uint32_t wh[4], wl[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float pr = exp2f(sc[i] - m_run);
-      l_run += pr;
-      ph[i] = KV::from_f32(pr);
-      plo[i] = KV::from_f32(pr - KV::to_f32(ph[i]));
-    }
-    const u32x2 pb = {ph[0] | (uint32_t(ph[1]) << 16), ph[2] | (uint32_t(ph[3]) << 16)};
-    const u32x2 pl = {plo[0] | (uint32_t(plo[1]) << 16), plo[2] | (uint32_t(plo[3]) << 16)};
-    if ((p + 1) * kPageTokens > tok1) {
-      // Tokens past the end of the sequence carry whatever the page holds;
-      // zero their V so 0 * garbage cannot reach the accumulator.
-#pragma unroll
-      for (int db = 0; db < 16; ++db) {
-        uint32_t lo = vr[db].x, hi = vr[db].y;
-        if (t_base + 0 >= tok1) lo &= 0xffff0000u;
-        if (t_base + 1 >= tok1) lo &= 0x0000ffffu;
-        if (t_base + 2 >= tok1) hi &= 0xffff0000u;
-        if (t_base + 3 >= tok1) hi &= 0x0000ffffu;
-        vr[db] = u32x2{lo, hi};
+        for (int j = 0; j < 4; ++j) {
+          const float x0 = n < G ? q_lds[n & 7][64 * g4 + 8 * (kk0 + k2) + 2 * j] : 0.f;
+          const float x1 = n < G ? q_lds[n & 7][64 * g4 + 8 * (kk0 + k2) + 2 * j + 1] : 0.f;
+          const uint16_t h0 = KV::from_f32(x0), h1 = KV::from_f32(x1);
+          const uint16_t l0 = KV::from_f32(x0 - KV::to_f32(h0));
+          const uint16_t l1 = KV::from_f32(x1 - KV::to_f32(h1));
+          wh[j] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+          wl[j] = static_cast<uint32_t>(l0) | (static_cast<uint32_t>(l1) << 16);
+        }
+        q_pk[0][kk0 + k2][lane] = uint4{wh[0], wh[1], wh[2], wh[3]};
+        q_pk[1][kk0 + k2][lane] = uint4{wl[0], wl[1], wl[2], wl[3]};
       }
     }
+    __syncthreads();
+
+    f32x4 o[16];
 #pragma unroll
-    for (int db = 0; db < 16; ++db) {
-      o[db] = KV::mfma_k16(vr[db], pb, o[db]);
-      o[db] = KV::mfma_k16(vr[db], pl, o[db]);
+    for (int db = 0; db < 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+
+    const int page0 = tok0 / kPageTokens;
+    const int page_end = (tok1 + kPageTokens - 1) / kPageTokens;
+    const int32_t* pt = a.page_table + (int64_t)row * a.pt_stride;
+
+    auto load_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
+      int phys = pt[p];
+      phys = (phys < 0 || phys >= a.num_pages) ? 0 : phys;  // unallocated entries never fault
+      const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
+      const u32x4* kp = reinterpret_cast<const u32x4*>(a.k_cache + tile * kTileElems) + lane;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) kr[kk] = ld_stream(kp + kk * 64);
+      const uint16_t* vp = a.v_cache + tile * kTileElems + n * kPageTokens + 4 * g4;
+#pragma unroll
+      for (int db = 0; db < 16; ++db) vr[db] = ld_stream(reinterpret_cast<const u32x2*>(vp + db * 16 * kPageTokens));
+    };
+
+    auto compute_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
+      // Re-read the Q operand from LDS every page (an opaque offset keeps the
+      // compiler from hoisting 64 loop-invariant VGPRs out of the page loop).
+      int qoff = lane;
+      asm volatile("" : "+v"(qoff));
+      f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const uint4 qh = q_pk[0][kk][qoff], ql = q_pk[1][kk][qoff];
+        sc = KV::mfma_k32(kr[kk], u32x4{qh.x, qh.y, qh.z, qh.w}, sc);
+        sc = KV::mfma_k32(kr[kk], u32x4{ql.x, ql.y, ql.z, ql.w}, sc);
+      }
+      const int t_base = p * kPageTokens + 4 * g4;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = (t_base + i < tok1) ? sc[i] * sl2 : -INFINITY;
+        mx = fmaxf(mx, sc[i]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // Lazy rescale: keep the reference max while the page max stays within
+      // 2^8 of it, so the accumulator is rescaled only when it has to be.
+      const bool grow = mx > m_run + 8.0f;
+      if (__any(grow)) {
+        const float m_new = grow ? mx : m_run;
+        const float alpha = exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 16; ++db) o[db] *= alpha;
+        m_run = m_new;
+      }
+      uint16_t ph[4], plo[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pr = exp2f(sc[i] - m_run);
+        l_run += pr;
+        ph[i] = KV::from_f32(pr);
+        plo[i] = KV::from_f32(pr - KV::to_f32(ph[i]));
+      }
+      const u32x2 pb = {ph[0] | (uint32_t(ph[1]) << 16), ph[2] | (uint32_t(ph[3]) << 16)};
+      const u32x2 pl = {plo[0] | (uint32_t(plo[1]) << 16), plo[2] | (uint32_t(plo[3]) << 16)};
+      if ((p + 1) * kPageTokens > tok1) {
+        // Tokens past the end of the range carry whatever the page holds;
+        // zero their V so 0 * garbage cannot reach the accumulator.
+#pragma unroll
+        for (int db = 0; db < 16; ++db) {
+          uint32_t lo = vr[db].x, hi = vr[db].y;
+          if (t_base + 0 >= tok1) lo &= 0xffff0000u;
+          if (t_base + 1 >= tok1) lo &= 0x0000ffffu;
+          if (t_base + 2 >= tok1) hi &= 0xffff0000u;
+          if (t_base + 3 >= tok1) hi &= 0x0000ffffu;
+          vr[db] = u32x2{lo, hi};
+        }
+      }
+#pragma unroll
+      for (int db = 0; db < 16; ++db) {
+        o[db] = KV::mfma_k16(vr[db], pb, o[db]);
+        o[db] = KV::mfma_k16(vr[db], pl, o[db]);
+      }
+    };
+
+    // Pages wave, wave+4, ...: the next page's loads are issued before the
+    // current page is consumed (two register buffers, loop unrolled by two).
+    int p = page0 + wave;
+    if (p < page_end) {
+      u32x4 kA[8], kB[8];
+      u32x2 vA[16], vB[16];
+      load_page(p, kA, vA);
+      while (true) {
+        int pn = p + 4;
+        if (pn < page_end) load_page(pn, kB, vB);
+        compute_page(p, kA, vA);
+        if (pn >= page_end) break;
+        p = pn;
+        pn = p + 4;
+        if (pn < page_end) load_page(pn, kA, vA);
+        compute_page(p, kB, vB);
+        if (pn >= page_end) break;
+        p = pn;
+      }
+    }
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+
+    // ---- merge the four waves through LDS (q_lds is dead: every wave passed the barrier above)
+    if (g4 == 0 && n < G) {
+      sm_m[wave][n] = m_run;
+      sm_l[wave][n] = l_run;
+    }
+    if (n < G) {
+#pragma unroll
+      for (int db = 0; db < 16; ++db) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sm_o[wave][n & 7][db * 16 + 4 * g4 + i] = o[db][i];
+      }
+    }
+    __syncthreads();
+    for (int h = 0; h < G; ++h) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w][h]);
+      float acc = 0.f, L = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float wt = (sm_m[w][h] == -INFINITY) ? 0.f : exp2f(sm_m[w][h] - M);
+        acc = fmaf(wt, sm_o[w][h][tid], acc);
+        L = fmaf(wt, sm_l[w][h], L);
+      }
+      a.ws_acc[(part * G + h) * kAttnHeadDim + tid] = acc;
+      if (tid == 0) {
+        a.ws_stats[(part * G + h) * 2 + 0] = M;
+        a.ws_stats[(part * G + h) * 2 + 1] = L;
+      }
     }
   };
 
-  // Pages wave, wave+4, ...: the next page's loads are issued before the
-  // current page is consumed (two register buffers, loop unrolled by two).
-  int p = page0 + wave;
-  if (p < page_end) {
-    u32x4 kA[8], kB[8];
-    u32x2 vA[16], vB[16];
-    load_page(p, kA, vA);
-    while (true) {
-      int pn = p + 4;
-      if (pn < page_end) load_page(pn, kB, vB);
-      compute_page(p, kA, vA);
-      if (pn >= page_end) break;
-      p = pn;
-      pn = p + 4;
-      if (pn < page_end) load_page(pn, kA, vA);
-      compute_page(p, kB, vB);
-      if (pn >= page_end) break;
-      p = pn;
+  if constexpr (!BALANCED) {
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int b = blockIdx.z;
+    const int ctx = row_ctx(a, b);
+    const int tok0 = split * a.split_tokens;
+    if (tok0 >= ctx) return;
+    process(b, kvh, tok0, min(ctx, tok0 + a.split_tokens), ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits + split);
+  } else {
+    // ---- page offsets of every unit (u = b * Hkv + kvh) in LDS
+    __shared__ int off[kMaxBalancedUnits + 1];
+    __shared__ int scan_scratch[4];
+    const int units = a.batch * a.num_kv_heads;
+    const int per = (units + 255) / 256;  // units per thread (<= 16)
+    int mine = 0;
+    for (int i = 0; i < per; ++i) {
+      const int u = tid * per + i;
+      if (u < units) mine += (row_ctx(a, u / a.num_kv_heads) + kPageTokens - 1) / kPageTokens;
     }
-  }
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
-
-  // ---- merge the four waves through LDS (q_lds is dead: every wave passed the barrier above)
-  if (g4 == 0 && n < G) {
-    sm_m[wave][n] = m_run;
-    sm_l[wave][n] = l_run;
-  }
-  if (n < G) {
-#pragma unroll
-    for (int db = 0; db < 16; ++db) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sm_o[wave][n & 7][db * 16 + 4 * g4 + i] = o[db][i];
+    int run = block_exclusive_scan(mine, scan_scratch);
+    for (int i = 0; i < per; ++i) {
+      const int u = tid * per + i;
+      if (u < units) {
+        off[u] = run;
+        run += (row_ctx(a, u / a.num_kv_heads) + kPageTokens - 1) / kPageTokens;
+      }
     }
-  }
-  __syncthreads();
-  const int64_t part = ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits + split;
-  for (int h = 0; h < G; ++h) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w][h]);
-    float acc = 0.f, L = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float wt = (sm_m[w][h] == -INFINITY) ? 0.f : exp2f(sm_m[w][h] - M);
-      acc = fmaf(wt, sm_o[w][h][tid], acc);
-      L = fmaf(wt, sm_l[w][h], L);
+    if (tid == (units - 1) / per) off[units] = run;  // the thread that holds the last unit
+    __syncthreads();
+    const int total = off[units];
+    const int nwg = static_cast<int>(gridDim.x);
+    const int chunk = max((total + nwg - 1) / nwg, kMinChunkPages);
+    if (blockIdx.x == 0) {
+      // publish the partition for the combine kernel
+      for (int u = tid; u <= units; u += 256) a.ws_units[2 + u] = off[u];
+      if (tid == 0) {
+        a.ws_units[0] = total;
+        a.ws_units[1] = chunk;
+      }
     }
-    a.ws_acc[(part * G + h) * kAttnHeadDim + tid] = acc;
-    if (tid == 0) {
-      a.ws_stats[(part * G + h) * 2 + 0] = M;
-      a.ws_stats[(part * G + h) * 2 + 1] = L;
+    const int w = static_cast<int>(blockIdx.x);
+    const int p0 = w * chunk;
+    if (p0 >= total) return;
+    const int p1 = min(p0 + chunk, total);
+    // first unit containing page p0: the last u with off[u] <= p0
+    int lo = 0, hi = units - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (off[mid] <= p0) lo = mid; else hi = mid - 1;
+    }
+    for (int u = lo; u < units && off[u] < p1; ++u) {
+      const int a0 = max(off[u], p0) - off[u], a1 = min(off[u + 1], p1) - off[u];  // unit-local pages
+      if (a1 <= a0) continue;
+      const int b = u / a.num_kv_heads, kvh = u % a.num_kv_heads;
+      const int ctx = row_ctx(a, b);
+      process(b, kvh, a0 * kPageTokens, min(ctx, a1 * kPageTokens), (int64_t)w + u);
     }
   }
 }
 
-// Merge the splits of one (sequence, query head) and apply the sigmoid gate.
-template <int GT, int OT>
+// Merge the partials of one (sequence, query head) and apply the sigmoid gate.
+template <int GT, int OT, bool BALANCED>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const int b = blockIdx.x / a.num_q_heads;
   const int h = blockIdx.x % a.num_q_heads;
   const int d = threadIdx.x;
   const int kvh = h / a.group;
   const int hi = h % a.group;
-  const int ctx = min(a.ctx_lens ? a.ctx_lens[b] : a.ctx_scalar, (int)min<int64_t>(a.pt_stride * kPageTokens, 1 << 30));
-  const int nsplit = min((ctx + a.split_tokens - 1) / a.split_tokens, a.max_splits);
-  const int64_t part0 = ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits;
+  int64_t first, count;
+  if constexpr (BALANCED) {
+    // partials of unit u come from workgroups off[u] / chunk .. (off[u + 1] - 1) / chunk, at index w + u
+    const int u = b * a.num_kv_heads + kvh;
+    const int chunk = a.ws_units[1];
+    const int o0 = a.ws_units[2 + u], o1 = a.ws_units[3 + u];
+    const int w0 = o0 / chunk, w1 = (o1 - 1) / chunk;
+    first = (int64_t)w0 + u;
+    count = o1 > o0 ? w1 - w0 + 1 : 0;
+  } else {
+    const int ctx = row_ctx(a, b);
+    first = ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits;
+    count = min((ctx + a.split_tokens - 1) / a.split_tokens, a.max_splits);
+  }
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_stats[((part0 + s) * a.group + hi) * 2]);
+  for (int64_t s = 0; s < count; ++s) M = fmaxf(M, a.ws_stats[((first + s) * a.group + hi) * 2]);
   float num = 0.f, den = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const int64_t ph = (part0 + s) * a.group + hi;
-    const float wt = exp2f(a.ws_stats[ph * 2] - M);  // stats are in log2 units
+  for (int64_t s = 0; s < count; ++s) {
+    const int64_t ph = (first + s) * a.group + hi;
+    const float mv = a.ws_stats[ph * 2];
+    const float wt = mv == -INFINITY ? 0.f : exp2f(mv - M);  // stats are in log2 units
     num = fmaf(wt, a.ws_acc[ph * kAttnHeadDim + d], num);
     den = fmaf(wt, a.ws_stats[ph * 2 + 1], den);
   }
@@ -534,16 +634,40 @@ extern "C" int ria_attn_decode_split_tokens(int num_kv_heads, const int32_t* ctx
   return auto_split_tokens(pages * num_kv_heads);
 }
 
+// Workgroups of a balanced launch: two per CU (the kernel's occupancy).
+static int balanced_workgroups() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return 2 * cus;
+}
+
+static bool use_balanced(int batch, int num_kv_heads, int split_tokens) {
+  return split_tokens == 0 && (int64_t)batch * num_kv_heads <= kMaxBalancedUnits;
+}
+
+// Workspace: [unit table (balanced only), padded to 64 floats][stats][acc].
+static int64_t decode_parts(int batch, int num_kv_heads, int max_ctx, int split_tokens, int64_t* unit_ints) {
+  if (use_balanced(batch, num_kv_heads, split_tokens)) {
+    const int64_t units = (int64_t)batch * num_kv_heads;
+    *unit_ints = (units + 3 + 63) / 64 * 64;
+    return balanced_workgroups() + units;
+  }
+  *unit_ints = 0;
+  const int st = resolve_split(batch, num_kv_heads, max_ctx, split_tokens);
+  return (int64_t)batch * num_kv_heads * ((max_ctx + st - 1) / st);
+}
+
 extern "C" int64_t ria_attn_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_ctx,
                                                    int split_tokens) {
   if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_ctx <= 0) return 0;
-  const int st = resolve_split(batch, num_kv_heads, max_ctx, split_tokens);
-  const int64_t max_splits = (max_ctx + st - 1) / st;
-  const int64_t parts = (int64_t)batch * num_kv_heads * max_splits;
+  int64_t unit_ints = 0;
+  const int64_t parts = decode_parts(batch, num_kv_heads, max_ctx, split_tokens, &unit_ints);
   const int64_t group = num_q_heads / num_kv_heads;
   const int64_t stats = parts * group * 2;
   const int64_t stats_aligned = (stats + 63) / 64 * 64;
-  return (stats_aligned + parts * group * kAttnHeadDim) * (int64_t)sizeof(float);
+  return (unit_ints + stats_aligned + parts * group * kAttnHeadDim) * (int64_t)sizeof(float);
 }
 
 extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
@@ -602,11 +726,16 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
   a.inv_freq = inv_freq;
   a.rope_dim = rope_dim;
   a.scale = scale;
-  a.split_tokens = resolve_split(batch, num_kv_heads, max_ctx, split_tokens);
-  a.max_splits = (max_ctx + a.split_tokens - 1) / a.split_tokens;
-  const int64_t parts = (int64_t)batch * num_kv_heads * a.max_splits;
+  const bool balanced = use_balanced(batch, num_kv_heads, split_tokens);
+  int64_t unit_ints = 0;
+  const int64_t parts = decode_parts(batch, num_kv_heads, max_ctx, split_tokens, &unit_ints);
+  a.balanced = balanced ? 1 : 0;
+  a.batch = batch;
+  a.split_tokens = balanced ? 0 : resolve_split(batch, num_kv_heads, max_ctx, split_tokens);
+  a.max_splits = balanced ? 0 : (max_ctx + a.split_tokens - 1) / a.split_tokens;
   const int64_t stats = parts * group * 2;
-  a.ws_stats = static_cast<float*>(workspace);
+  a.ws_units = static_cast<int32_t*>(workspace);
+  a.ws_stats = static_cast<float*>(workspace) + unit_ints;
   a.ws_acc = a.ws_stats + (stats + 63) / 64 * 64;
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
@@ -616,12 +745,18 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (phase & RIA_ATTN_SPLITK) {
-  dim3 grid(a.max_splits, num_kv_heads, batch);
-#define RIA_SPLITK_LAUNCH(QT_)                                                                   \
-  if (kv_dtype == RIA_DT_F16)                                                                    \
-    hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_F16>), grid, dim3(256), 0, st, a);        \
-  else                                                                                           \
-    hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_BF16>), grid, dim3(256), 0, st, a)
+  dim3 grid = balanced ? dim3(balanced_workgroups()) : dim3(a.max_splits, num_kv_heads, batch);
+#define RIA_SPLITK_KV(QT_, BAL_)                                                                  \
+  if (kv_dtype == RIA_DT_F16)                                                                     \
+    hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_F16, BAL_>), grid, dim3(256), 0, st, a);   \
+  else                                                                                            \
+    hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_BF16, BAL_>), grid, dim3(256), 0, st, a)
+#define RIA_SPLITK_LAUNCH(QT_)       \
+  if (balanced) {                    \
+    RIA_SPLITK_KV(QT_, true);        \
+  } else {                           \
+    RIA_SPLITK_KV(QT_, false);       \
+  }
   if (q_dtype == RIA_DT_BF16) {
     RIA_SPLITK_LAUNCH(RIA_DT_BF16);
   } else if (q_dtype == RIA_DT_F16) {
@@ -630,17 +765,26 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
     RIA_SPLITK_LAUNCH(RIA_DT_F32);
   }
 #undef RIA_SPLITK_LAUNCH
+#undef RIA_SPLITK_KV
   int rc = check_launch("ria_attn_decode (split-K)");
   if (rc != RIA_OK) return rc;
   }
   if (!(phase & RIA_ATTN_COMBINE)) return RIA_OK;
 
   dim3 cgrid(batch * num_q_heads);
-#define RIA_COMB_LAUNCH(GT_, OT_) hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_>), cgrid, dim3(256), 0, st, a)
-#define RIA_COMB_OT(GT_)                                          \
-  if (out_dtype == RIA_DT_BF16) RIA_COMB_LAUNCH(GT_, RIA_DT_BF16); \
-  else if (out_dtype == RIA_DT_F16) RIA_COMB_LAUNCH(GT_, RIA_DT_F16); \
-  else RIA_COMB_LAUNCH(GT_, RIA_DT_F32);
+#define RIA_COMB_LAUNCH(GT_, OT_)                                                               \
+  if (balanced)                                                                                 \
+    hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_, true>), cgrid, dim3(256), 0, st, a);      \
+  else                                                                                          \
+    hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_, false>), cgrid, dim3(256), 0, st, a)
+#define RIA_COMB_OT(GT_)                     \
+  if (out_dtype == RIA_DT_BF16) {            \
+    RIA_COMB_LAUNCH(GT_, RIA_DT_BF16);       \
+  } else if (out_dtype == RIA_DT_F16) {      \
+    RIA_COMB_LAUNCH(GT_, RIA_DT_F16);        \
+  } else {                                   \
+    RIA_COMB_LAUNCH(GT_, RIA_DT_F32);        \
+  }
   if (gate_dtype == RIA_DT_BF16) {
     RIA_COMB_OT(RIA_DT_BF16)
   } else if (gate_dtype == RIA_DT_F16) {

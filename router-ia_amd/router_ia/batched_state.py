@@ -87,7 +87,6 @@ class BatchedAttentionState:
         self._min_headroom = 0  # min over rows of (KV capacity - tokens seen)
         self.inv_freq = rope_inv_freq(rope_theta, rope_dim).to(dev)
         self.scale = 256 ** -0.5
-        self._fixed_split = split_tokens > 0
         self._size_workspace()
         # DeltaNet prefill runs prompts in segments of this many tokens; its
         # workspace (about 75 KB per token) is allocated on the first prefill
@@ -110,11 +109,6 @@ class BatchedAttentionState:
         self._ensure([n + 1 for n in self._host_seen])
         self.tokens_seen.copy_(torch.tensor(self._host_seen, dtype=torch.int32))
         self.ctx_lens.copy_(self.tokens_seen + 1)
-        if not self._fixed_split and self.num_full_layers > 0:
-            # Choose the split once for this batch's real lengths (the kernel's
-            # own default only sees the longest context).
-            self.split_tokens = K.attn_decode_split_tokens(self.num_kv_heads, [n + 1 for n in self._host_seen])
-            self._size_workspace()
 
     def reserve(self, extra_tokens: int) -> None:
         """Allocate KV pages so every row can take `extra_tokens` more tokens without host work."""

@@ -82,6 +82,33 @@ def test_attn_decode_ragged_shuffled_pages(gpu, split_tokens):
 
 
 @pytest.mark.gpu
+def test_attn_decode_balanced_partition_many_units(gpu):
+    """Balanced (stream-K) decode: 48 ragged rows, ~9.6k pages over the grid, so
+    workgroups cross unit boundaries and units span several workgroups."""
+    announce("attn_decode: balanced partition, B=48, contexts U[200, 3000], shuffled pages")
+    batch, steps = 48, 2
+    lengths = W.ragged_lengths(24, batch, 200, 3000)
+    kpre, vpre = W.prefilled_kv(25, batch, max(lengths))
+    x = W.attn_step_inputs(26, steps, batch)
+    st = _attn_state(gpu, batch, max(lengths) + steps + 32, shuffle_seed=7)
+    assert st.split_tokens == 0  # the balanced partition
+    _prefill(st, lengths, kpre, vpre)
+    states = []
+    for b, n in enumerate(lengths):
+        s = O.SequenceState()
+        s.keys[0], s.values[0], s.tokens_seen = kpre[b:b + 1, :, :n].float(), vpre[b:b + 1, :, :n].float(), n
+        states.append(s)
+    for t in range(steps):
+        out = st.full_step(0, x["q"][t].to(gpu), x["k"][t].to(gpu), x["v"][t].to(gpu), x["gate"][t].to(gpu),
+                           out_dtype=torch.float32)
+        want = O.full_step_batched(states, 0, x["q"][t], x["k"][t], x["v"][t], x["gate"][t])
+        st.advance()
+        for s in states:
+            s.tokens_seen += 1
+        assert_act_close(out, want, f"step {t}")
+
+
+@pytest.mark.gpu
 def test_kv_append_slot_mapping_bit_exact(gpu):
     """Every appended token lands at page_table[row][t // 16] * 16 + t % 16 of its layer pool."""
     announce("kv_append: slot mapping, B=4, shuffled pages")

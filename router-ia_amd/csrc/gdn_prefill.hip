@@ -542,7 +542,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int tk = 0; tk < 2; ++tk) o.kt[tk][s][p] = kt[(((2 * wave + tk) * 2 + s) * 2 + p) * 64 + lane];
       }
     o.u = reinterpret_cast<const f32x4*>(rec + kRecU)[(wave * 8 + cb) * 64 + lane];
-    o.gl = *reinterpret_cast<const float*>(rec + kRecGl);
+    // a vector load (opaque zero lane offset): a scalar load here would be
+    // waited for by the next lds_barrier (lgkmcnt), exposing its latency
+    int zero = 0;
+    asm volatile("" : "+v"(zero));
+    o.gl = reinterpret_cast<const float*>(rec + kRecGl)[zero];
   };
 
   auto process = [&](int cl, const ChunkOps& o) {
@@ -600,13 +604,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   };
 
   // Chunk cl + 1's operands load while chunk cl computes (unrolled by two).
+  // The prefetch is unconditional (the last chunk is simply loaded again):
+  // a conditional one splits the loop into paths the compiler's wait
+  // analysis merges conservatively, draining the prefetch every chunk.
   ChunkOps A, B;
   load_ops(0, A);
+  const int last = a.seg_chunks - 1;
   for (int cl = 0; cl < a.seg_chunks; cl += 2) {
-    if (cl + 1 < a.seg_chunks) load_ops(cl + 1, B);
+    load_ops(min(cl + 1, last), B);
     process(cl, A);
     if (cl + 1 >= a.seg_chunks) break;
-    if (cl + 2 < a.seg_chunks) load_ops(cl + 2, A);
+    load_ops(min(cl + 2, last), A);
     process(cl + 1, B);
   }
   for (int e = tid; e < kDim * 16; e += 256) {

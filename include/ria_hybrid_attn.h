@@ -22,6 +22,10 @@
  *     the accompanying *_scalar value is used for every row.
  *   - Sizes are fixed by the model family: DeltaNet head dim 128 (dk == dv),
  *     conv kernel 4, full-attention head dim 256, KV pages of 16 tokens.
+ *   - Norm weights are f32 device arrays (convert a bf16 checkpoint weight
+ *     once; the reference widens it to fp32 before use).  A NULL norm weight
+ *     on a fused entry point means its input arrives already normalised.
+ *     Fused norms use the model's eps, 1e-6.
  *
  * Memory layouts
  *   DeltaNet recurrent state  f32  [pool, Hv, 128 (dk, i), 128 (dv, j)]
@@ -56,7 +60,7 @@
 extern "C" {
 #endif
 
-#define RIA_ABI_VERSION 1
+#define RIA_ABI_VERSION 2
 
 enum ria_dtype { RIA_DT_BF16 = 0, RIA_DT_F16 = 1, RIA_DT_F32 = 2 };
 
@@ -98,7 +102,12 @@ const char* ria_last_error(void);
  *            to use conv_pos_scalar for every row.
  * state      recurrent state pool, updated in place.
  * gate_a/b   [batch, Hv] f32 with row stride gate_row_stride (see gate_mode).
- * out        [batch, Hv, 128] of out_dtype: read-out o = S_new^T q.
+ * out        [batch, Hv, 128] of out_dtype: read-out o = S_new^T q, or with
+ *            z given the gated RMSNorm of it (qwen36_attention_cache.py:268-271,
+ *            qwen36_gated_norm_probe.py:19-36):
+ *            out = norm_weight * o / sqrt(mean(o^2) + 1e-6) * SiLU(z) per head.
+ * z          NULL, or the gate [batch, Hv, 128] of z_dtype with row stride
+ *            z_row_stride; norm_weight [128] f32.
  * conv_dim = 2 * num_k_heads * 128 + num_v_heads * 128.
  */
 int ria_gdn_decode(int batch, int num_k_heads, int num_v_heads,
@@ -108,7 +117,9 @@ int ria_gdn_decode(int batch, int num_k_heads, int num_v_heads,
                    float* state, const int32_t* seq_slot,
                    const float* gate_a, const float* gate_b, int64_t gate_row_stride,
                    int gate_mode, const float* A_log, const float* dt_bias,
-                   void* out, int out_dtype, void* stream);
+                   void* out, int out_dtype,
+                   const void* z, int z_dtype, int64_t z_row_stride, const float* norm_weight,
+                   void* stream);
 
 /*
  * Depthwise causal conv1d step alone (kernel 4, SiLU), for `batch` rows of
@@ -129,6 +140,31 @@ int ria_conv1d_step(int batch, int channels,
  */
 int ria_l2norm(int64_t rows, int dim, const void* x, int x_dtype, float eps,
                float* out, void* stream);
+
+/*
+ * RMSNorm with the (1 + w) affine of the model's input, q and k norms:
+ * y = x / sqrt(mean(x^2) + eps) * (1 + weight) in fp32, cast back to x_dtype,
+ * stored as out_dtype.  Rows are (token, head) pairs: head h of token t holds
+ * `dim` elements at x + t * x_token_stride + h * dim.  Replaces
+ * qwen36_op_probe.py:55-67 (`rmsnorm`, called at qwen36_attention_cache.py:227
+ * and :302-305).  out may alias x when both have one dtype and one stride.
+ */
+int ria_rmsnorm(int64_t tokens, int heads, int dim,
+                const void* x, int x_dtype, int64_t x_token_stride,
+                const float* weight, float eps,
+                void* out, int out_dtype, int64_t out_token_stride, void* stream);
+
+/*
+ * Gated RMSNorm: n = x / sqrt(mean(x^2) + eps) cast to x_dtype, then
+ * y = weight * n * SiLU(z) in fp32, cast to x_dtype, stored as out_dtype;
+ * rows as in ria_rmsnorm.  Replaces qwen36_gated_norm_probe.py:19-36
+ * (`gated_rmsnorm`, called at qwen36_attention_cache.py:268-271).
+ */
+int ria_gated_rmsnorm(int64_t tokens, int heads, int dim,
+                      const void* x, int x_dtype, int64_t x_token_stride,
+                      const void* z, int z_dtype, int64_t z_token_stride,
+                      const float* weight, float eps,
+                      void* out, int out_dtype, int64_t out_token_stride, void* stream);
 
 /*
  * RoPE tables for one position: cos/sin of position * inv_freq duplicated
@@ -156,6 +192,8 @@ int ria_rope_apply(int64_t rows, int head_dim, int rope_dim, const float* x,
  * positions  RoPE position of the token (tokens_seen), per row or scalar.
  * slots      logical index of the token in its sequence (tokens resident
  *            before the append), per row or scalar.
+ * k_norm_weight  NULL, or the k_norm weight [256] f32: k is RMSNorm'd with
+ *            (1 + w) and cast back to k_dtype before RoPE (:303-305).
  */
 int ria_kv_append(int batch, int num_kv_heads,
                   const void* k, int k_dtype, int64_t k_row_stride,
@@ -164,7 +202,7 @@ int ria_kv_append(int batch, int num_kv_heads,
                   const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
                   const int32_t* positions, int32_t position_scalar,
                   const int32_t* slots, int32_t slot_scalar,
-                  const float* inv_freq, int rope_dim, void* stream);
+                  const float* inv_freq, int rope_dim, const float* k_norm_weight, void* stream);
 
 /*
  * Append `length` consecutive tokens of ONE sequence (a prompt) into its
@@ -176,13 +214,15 @@ int ria_kv_append(int batch, int num_kv_heads,
  * k, v            [length, Hkv, 256] of k_dtype / v_dtype.
  * page_table_row  this sequence's page-table row, page_capacity entries;
  *                 start_pos + length must fit in page_capacity * 16.
+ * k_norm_weight   as in ria_kv_append.
  */
 int ria_kv_append_seq(int length, int num_kv_heads,
                       const void* k, int k_dtype, int64_t k_row_stride,
                       const void* v, int v_dtype, int64_t v_row_stride,
                       void* k_cache, void* v_cache, int kv_dtype, int num_pages,
                       const int32_t* page_table_row, int64_t page_capacity,
-                      int32_t start_pos, const float* inv_freq, int rope_dim, void* stream);
+                      int32_t start_pos, const float* inv_freq, int rope_dim,
+                      const float* k_norm_weight, void* stream);
 
 /*
  * Causal GQA attention prefill of `length` prompt tokens of one sequence,
@@ -197,6 +237,9 @@ int ria_kv_append_seq(int length, int num_kv_heads,
  * out       [length, Hq, 256] of act_dtype, contiguous.
  * Hq / Hkv <= 8; rope_dim is 0 or 64.  q, gate and out 16-byte aligned, row
  * strides multiples of 8 elements.
+ * q_norm_weight, k_norm_weight  NULL, or the q_norm / k_norm weights [256]
+ *           f32 (16-byte aligned): q and k are RMSNorm'd with (1 + w) and cast
+ *           back to act_dtype before RoPE (:302-305).
  */
 int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads,
                      const void* q, int64_t q_row_stride,
@@ -205,7 +248,8 @@ int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads,
                      const void* gate, int64_t gate_row_stride, int act_dtype,
                      void* k_cache, void* v_cache, int kv_dtype, int num_pages,
                      const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
-                     const float* inv_freq, int rope_dim, float scale,
+                     const float* inv_freq, int rope_dim,
+                     const float* q_norm_weight, const float* k_norm_weight, float scale,
                      void* out, void* stream);
 
 /*
@@ -225,7 +269,8 @@ int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_heads,
                            const void* gate, int64_t gate_row_stride, int act_dtype,
                            void* k_cache, void* v_cache, int kv_dtype, int num_pages,
                            const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
-                           const float* inv_freq, int rope_dim, float scale,
+                           const float* inv_freq, int rope_dim,
+                           const float* q_norm_weight, const float* k_norm_weight, float scale,
                            void* out, int phase, void* stream);
 
 /*
@@ -258,6 +303,8 @@ int64_t ria_attn_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_h
  * ctx_lens   tokens attended per row (or scalar); max_ctx bounds them.
  * split_tokens  tokens per split (multiple of 64) or 0 for automatic.
  * workspace  caller buffer of ria_attn_decode_workspace_bytes() bytes.
+ * q_norm_weight  NULL, or the q_norm weight [256] f32: q is RMSNorm'd with
+ *            (1 + w) and cast back to q_dtype before RoPE (:302-304).
  * out        [batch, Hq, 256] of out_dtype.
  */
 int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads,
@@ -267,7 +314,8 @@ int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads,
                     const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
                     const int32_t* positions, int32_t position_scalar,
                     const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
-                    const float* inv_freq, int rope_dim, float scale, int split_tokens,
+                    const float* inv_freq, int rope_dim, const float* q_norm_weight,
+                    float scale, int split_tokens,
                     void* workspace, int64_t workspace_bytes,
                     void* out, int out_dtype, void* stream);
 
@@ -286,7 +334,8 @@ int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads,
                           const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
                           const int32_t* positions, int32_t position_scalar,
                           const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
-                          const float* inv_freq, int rope_dim, float scale, int split_tokens,
+                          const float* inv_freq, int rope_dim, const float* q_norm_weight,
+                          float scale, int split_tokens,
                           void* workspace, int64_t workspace_bytes,
                           void* out, int out_dtype, int phase, void* stream);
 
@@ -308,7 +357,10 @@ int64_t ria_gdn_prefill_workspace_bytes(int num_k_heads, int num_v_heads, int se
  * conv_ring  bf16 [4, conv_dim] of this sequence; conv_pos = step of token 0.
  * state      f32 [Hv, 128, 128] of this sequence, updated in place.
  * gate_a/b   [length, Hv] f32 per token (gate_mode as in ria_gdn_decode).
- * out        [length, Hv, 128] of out_dtype.
+ * out        [length, Hv, 128] of out_dtype: the read-out, or with z given
+ *            its gated RMSNorm as in ria_gdn_decode.
+ * z          NULL, or the gate [length, Hv, 128] of z_dtype (row stride
+ *            z_row_stride); norm_weight [128] f32.
  * workspace  >= ria_gdn_prefill_workspace_bytes(.., 64) bytes, 256-byte
  *            aligned; larger workspaces take longer segments.
  */
@@ -319,6 +371,7 @@ int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads,
                     const float* gate_a, const float* gate_b, int64_t gate_row_stride,
                     int gate_mode, const float* A_log, const float* dt_bias,
                     void* out, int out_dtype,
+                    const void* z, int z_dtype, int64_t z_row_stride, const float* norm_weight,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /*

@@ -87,3 +87,33 @@ def attention(q: np.ndarray, K: np.ndarray, V: np.ndarray, scale: float) -> np.n
 
 def sigmoid(x: np.ndarray) -> np.ndarray:
     return 1.0 / (1.0 + np.exp(-np.asarray(x, dtype=np.float64)))
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """Per row of n elements: y_d = x_d / sqrt(sum_e x_e^2 / n + eps) * (1 + w_d)."""
+    x = np.asarray(x, dtype=np.float64)
+    flat = x.reshape(-1, x.shape[-1])
+    out = np.empty_like(flat)
+    n = flat.shape[1]
+    for r in range(flat.shape[0]):
+        ms = sum(float(v) * float(v) for v in flat[r]) / n
+        scale = 1.0 / math.sqrt(ms + eps)
+        for d in range(n):
+            out[r, d] = flat[r, d] * scale * (1.0 + float(w[d]))
+    return out.reshape(x.shape)
+
+
+def gated_rmsnorm(x: np.ndarray, z: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """Per row of n elements: y_d = w_d * x_d / sqrt(sum_e x_e^2 / n + eps) * z_d / (1 + exp(-z_d))."""
+    x = np.asarray(x, dtype=np.float64)
+    zf = np.asarray(z, dtype=np.float64).reshape(-1, x.shape[-1])
+    flat = x.reshape(-1, x.shape[-1])
+    out = np.empty_like(flat)
+    n = flat.shape[1]
+    for r in range(flat.shape[0]):
+        ms = sum(float(v) * float(v) for v in flat[r]) / n
+        scale = 1.0 / math.sqrt(ms + eps)
+        for d in range(n):
+            zd = zf[r, d]
+            out[r, d] = float(w[d]) * flat[r, d] * scale * zd / (1.0 + math.exp(-zd))
+    return out.reshape(x.shape)

@@ -61,6 +61,7 @@ struct AttnArgs {
   int32_t ctx_scalar;
   const float* inv_freq;
   int rope_dim;
+  const float* q_norm_w;  // q_norm weight [256] f32, or null: q arrives normalised
   float scale;
   int split_tokens;
   int max_splits;
@@ -92,6 +93,7 @@ struct AppendArgs {
   int32_t slot_scalar;
   const float* inv_freq;
   int rope_dim;
+  const float* norm_w;  // k_norm weight [256] f32, or null: k arrives normalised
   int num_kv_heads;
   int seq_mode;  // 1: blockIdx.x is token i of one sequence at position (and slot) pos_scalar + i
 };
@@ -108,7 +110,8 @@ __device__ __forceinline__ float rope_elem(float xd, float partner, int d, int r
   return add_rn(mul_rn(xd, c), mul_rn(rot, s));
 }
 
-// One workgroup per (sequence, KV head): rotate k, write k and v into the page.
+// One workgroup per (sequence, KV head): optionally RMSNorm k (k_norm,
+// qwen36_attention_cache.py:303-305), rotate it, write k and v into the page.
 template <int KT, int VT, int KVT>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int b = blockIdx.x;
@@ -118,8 +121,15 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int pos = a.seq_mode ? a.pos_scalar + b : (a.positions ? a.positions[b] : a.pos_scalar);
   const int slot = a.seq_mode ? a.pos_scalar + b : (a.slots ? a.slots[b] : a.slot_scalar);
   __shared__ float k_s[kAttnHeadDim];
-  const float kv = load_act<KT>(a.k, (int64_t)b * a.k_stride + kvh * kAttnHeadDim + d);
+  __shared__ float ss_s[4];
+  float kv = load_act<KT>(a.k, (int64_t)b * a.k_stride + kvh * kAttnHeadDim + d);
   const float vv = load_act<VT>(a.v, (int64_t)b * a.v_stride + kvh * kAttnHeadDim + d);
+  if (a.norm_w) {  // uniform: one sum of squares over the 256 dims
+    const float ss = wave_sum(mul_rn(kv, kv));
+    if ((d & 63) == 0) ss_s[d >> 6] = ss;
+    __syncthreads();
+    kv = rmsnorm_elem<KT>(kv, rms_scale(ss_s[0] + ss_s[1] + ss_s[2] + ss_s[3], kAttnHeadDim), a.norm_w[d]);
+  }
   k_s[d] = kv;
   __syncthreads();
   if (slot < 0 || slot / kPageTokens >= a.pt_stride) return;
@@ -165,7 +175,7 @@ __device__ int block_exclusive_scan(int v, int* scratch) {
   return base + x - v;
 }
 
-template <int QT, int KVT, bool BALANCED>
+template <int QT, int KVT, bool BALANCED, bool QNORM>
 __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
   using KV = Kv16<KVT>;
   const int G = a.group;
@@ -180,6 +190,7 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
   __shared__ uint4 q_pk[2][8][64];            // bf16 Q operand hi / lo, [part][kk][lane]
   __shared__ float sm_m[4][kMaxGroup];
   __shared__ float sm_l[4][kMaxGroup];
+  __shared__ float qn_s[8];                   // per-head RMSNorm scale of q
   float (*q_lds)[kAttnHeadDim] = sm_o[0];
   // Scores are kept in log2 units: s2 = (q . k) * scale * log2(e).
   const float sl2 = a.scale * 1.4426950408889634f;
@@ -197,14 +208,47 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
       rc = cosf(ang);
       rs = sinf(ang);
     }
-    for (int h = 0; h < G; ++h) {
-      const int64_t base = (int64_t)b * a.q_stride + (int64_t)(kvh * G + h) * kAttnHeadDim;
-      float x = load_act<QT>(a.q, base + tid);
-      if (a.rope_dim == 64 && tid < 64) {
-        const float partner = load_act<QT>(a.q, base + (tid ^ 32));
-        x = add_rn(mul_rn(x, rc), mul_rn(tid < 32 ? -partner : partner, rs));
+    if constexpr (QNORM) {
+      // q_norm (qwen36_attention_cache.py:302-304) before RoPE: raw rows into
+      // the second merge slice (free until this range's merge), one wave per
+      // head for the sum of squares, then each thread normalises its dim (and
+      // its RoPE partner) and rotates.
+      // (an opaque copy of the thread index keeps this branch's addresses
+      // from being hoisted out of the unit loop and held across the page loop)
+      int t = tid;
+      asm volatile("" : "+v"(t));
+      const int tl = t & 63, tw = t >> 6;
+      float (*raw)[kAttnHeadDim] = sm_o[1];
+      for (int h = 0; h < G; ++h)
+        raw[h][t] = load_act<QT>(a.q, (int64_t)b * a.q_stride + (int64_t)(kvh * G + h) * kAttnHeadDim + t);
+      __syncthreads();
+      for (int h = tw; h < G; h += 4) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < kAttnHeadDim; j += 64) ss = add_rn(ss, mul_rn(raw[h][j + tl], raw[h][j + tl]));
+        ss = wave_sum(ss);
+        if (tl == 0) qn_s[h] = rms_scale(ss, kAttnHeadDim);
       }
-      q_lds[h][tid] = x;
+      __syncthreads();
+      const float w_self = a.q_norm_w[t], w_partner = a.q_norm_w[t ^ 32];
+      for (int h = 0; h < G; ++h) {
+        float x = rmsnorm_elem<QT>(raw[h][t], qn_s[h], w_self);
+        if (a.rope_dim == 64 && t < 64) {
+          const float partner = rmsnorm_elem<QT>(raw[h][t ^ 32], qn_s[h], w_partner);
+          x = add_rn(mul_rn(x, rc), mul_rn(t < 32 ? -partner : partner, rs));
+        }
+        q_lds[h][t] = x;
+      }
+    } else {
+      for (int h = 0; h < G; ++h) {
+        const int64_t base = (int64_t)b * a.q_stride + (int64_t)(kvh * G + h) * kAttnHeadDim;
+        float x = load_act<QT>(a.q, base + tid);
+        if (a.rope_dim == 64 && tid < 64) {
+          const float partner = load_act<QT>(a.q, base + (tid ^ 32));
+          x = add_rn(mul_rn(x, rc), mul_rn(tid < 32 ? -partner : partner, rs));
+        }
+        q_lds[h][tid] = x;
+      }
     }
     __syncthreads();
     // Pack the B operand: lane (head n, group g4) holds dims 64*g4 + 8*kk + j,
@@ -566,7 +610,7 @@ extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_d
                              int kv_dtype, int num_pages, const int32_t* page_table, int64_t page_table_stride,
                              const int32_t* seq_slot, const int32_t* positions, int32_t position_scalar,
                              const int32_t* slots, int32_t slot_scalar, const float* inv_freq, int rope_dim,
-                             void* stream) {
+                             const float* k_norm_weight, void* stream) {
   if (batch < 0) return set_error(RIA_ERR_INVALID, "ria_kv_append: bad batch");
   int rc = check_append_common("ria_kv_append", num_kv_heads, k, k_dtype, k_row_stride, v, v_dtype, v_row_stride,
                                k_cache, v_cache, kv_dtype, page_table, inv_freq, rope_dim);
@@ -590,6 +634,7 @@ extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_d
   a.slot_scalar = slot_scalar;
   a.inv_freq = inv_freq;
   a.rope_dim = rope_dim;
+  a.norm_w = k_norm_weight;
   a.num_kv_heads = num_kv_heads;
   a.seq_mode = 0;
   launch_append(a, batch, k_dtype, v_dtype, kv_dtype, static_cast<hipStream_t>(stream));
@@ -599,7 +644,8 @@ extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_d
 extern "C" int ria_kv_append_seq(int length, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
                                  const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
                                  int kv_dtype, int num_pages, const int32_t* page_table_row, int64_t page_capacity,
-                                 int32_t start_pos, const float* inv_freq, int rope_dim, void* stream) {
+                                 int32_t start_pos, const float* inv_freq, int rope_dim,
+                                 const float* k_norm_weight, void* stream) {
   if (length < 0 || start_pos < 0) return set_error(RIA_ERR_INVALID, "ria_kv_append_seq: negative length or start");
   int rc = check_append_common("ria_kv_append_seq", num_kv_heads, k, k_dtype, k_row_stride, v, v_dtype,
                                v_row_stride, k_cache, v_cache, kv_dtype, page_table_row, inv_freq, rope_dim);
@@ -621,6 +667,7 @@ extern "C" int ria_kv_append_seq(int length, int num_kv_heads, const void* k, in
   a.pos_scalar = start_pos;
   a.inv_freq = inv_freq;
   a.rope_dim = rope_dim;
+  a.norm_w = k_norm_weight;
   a.num_kv_heads = num_kv_heads;
   a.seq_mode = 1;
   launch_append(a, length, k_dtype, v_dtype, kv_dtype, static_cast<hipStream_t>(stream));
@@ -676,8 +723,8 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
                                      const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
                                      const int32_t* positions, int32_t position_scalar, const int32_t* ctx_lens,
                                      int32_t ctx_scalar, int max_ctx, const float* inv_freq, int rope_dim,
-                                     float scale, int split_tokens, void* workspace, int64_t workspace_bytes,
-                                     void* out, int out_dtype, int phase, void* stream) {
+                                     const float* q_norm_weight, float scale, int split_tokens, void* workspace,
+                                     int64_t workspace_bytes, void* out, int out_dtype, int phase, void* stream) {
   if (phase < RIA_ATTN_SPLITK || phase > RIA_ATTN_BOTH)
     return set_error(RIA_ERR_INVALID, "ria_attn_decode: unknown phase %d", phase);
   if (batch < 0) return set_error(RIA_ERR_INVALID, "ria_attn_decode: batch must be >= 0");
@@ -725,6 +772,7 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
   a.ctx_scalar = ctx_scalar;
   a.inv_freq = inv_freq;
   a.rope_dim = rope_dim;
+  a.q_norm_w = q_norm_weight;
   a.scale = scale;
   const bool balanced = use_balanced(batch, num_kv_heads, split_tokens);
   int64_t unit_ints = 0;
@@ -746,16 +794,22 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (phase & RIA_ATTN_SPLITK) {
   dim3 grid = balanced ? dim3(balanced_workgroups()) : dim3(a.max_splits, num_kv_heads, batch);
-#define RIA_SPLITK_KV(QT_, BAL_)                                                                  \
-  if (kv_dtype == RIA_DT_F16)                                                                     \
-    hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_F16, BAL_>), grid, dim3(256), 0, st, a);   \
-  else                                                                                            \
-    hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_BF16, BAL_>), grid, dim3(256), 0, st, a)
+#define RIA_SPLITK_KV(QT_, BAL_, QN_)                                                                  \
+  if (kv_dtype == RIA_DT_F16)                                                                          \
+    hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_F16, BAL_, QN_>), grid, dim3(256), 0, st, a);   \
+  else                                                                                                 \
+    hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_BF16, BAL_, QN_>), grid, dim3(256), 0, st, a)
+#define RIA_SPLITK_QN(QT_, BAL_)            \
+  if (q_norm_weight) {                      \
+    RIA_SPLITK_KV(QT_, BAL_, true);         \
+  } else {                                  \
+    RIA_SPLITK_KV(QT_, BAL_, false);        \
+  }
 #define RIA_SPLITK_LAUNCH(QT_)       \
   if (balanced) {                    \
-    RIA_SPLITK_KV(QT_, true);        \
+    RIA_SPLITK_QN(QT_, true)         \
   } else {                           \
-    RIA_SPLITK_KV(QT_, false);       \
+    RIA_SPLITK_QN(QT_, false)        \
   }
   if (q_dtype == RIA_DT_BF16) {
     RIA_SPLITK_LAUNCH(RIA_DT_BF16);
@@ -765,6 +819,7 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
     RIA_SPLITK_LAUNCH(RIA_DT_F32);
   }
 #undef RIA_SPLITK_LAUNCH
+#undef RIA_SPLITK_QN
 #undef RIA_SPLITK_KV
   int rc = check_launch("ria_attn_decode (split-K)");
   if (rc != RIA_OK) return rc;
@@ -802,14 +857,14 @@ extern "C" int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads, con
                                const void* k_cache, const void* v_cache, int kv_dtype, int num_pages,
                                const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
                                const int32_t* positions, int32_t position_scalar, const int32_t* ctx_lens,
-                               int32_t ctx_scalar, int max_ctx, const float* inv_freq, int rope_dim, float scale,
-                               int split_tokens, void* workspace, int64_t workspace_bytes, void* out, int out_dtype,
-                               void* stream) {
+                               int32_t ctx_scalar, int max_ctx, const float* inv_freq, int rope_dim,
+                               const float* q_norm_weight, float scale, int split_tokens, void* workspace,
+                               int64_t workspace_bytes, void* out, int out_dtype, void* stream) {
   return ria_attn_decode_phase(batch, num_q_heads, num_kv_heads, q, q_dtype, q_row_stride, gate, gate_dtype,
                                gate_row_stride, k_cache, v_cache, kv_dtype, num_pages, page_table, page_table_stride,
-                               seq_slot,
-                               positions, position_scalar, ctx_lens, ctx_scalar, max_ctx, inv_freq, rope_dim, scale,
-                               split_tokens, workspace, workspace_bytes, out, out_dtype, RIA_ATTN_BOTH, stream);
+                               seq_slot, positions, position_scalar, ctx_lens, ctx_scalar, max_ctx, inv_freq,
+                               rope_dim, q_norm_weight, scale, split_tokens, workspace, workspace_bytes, out,
+                               out_dtype, RIA_ATTN_BOTH, stream);
 }
 
 extern "C" int ria_kv_gather(int batch, int num_kv_heads, const void* k_cache, const void* v_cache, int num_pages,

@@ -65,6 +65,7 @@ struct PrefillAttnArgs {
   int length;  // prompt tokens
   const float* inv_freq;
   int rope_dim;
+  const float* q_norm_w;  // q_norm weight [256] f32, or null: q arrives normalised
   float scale;
   int num_q_heads;
   int num_kv_heads;
@@ -133,17 +134,45 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   const float sl2 = a.scale * 1.4426950408889634f;
   {
     const int64_t base = (int64_t)t_row * a.q_stride + (int64_t)head * kAttnHeadDim + 8 * g4;
+    auto load_q8 = [&](int kd, float (&y)[8]) {
+      if (row_ok) {
+        load_act8<AT>(a.q, base + 32 * kd, y);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = 0.f;
+      }
+    };
+    // q_norm (qwen36_attention_cache.py:302-304) before RoPE: a first pass
+    // for the row's sum of squares, whose four 64-dim slices sit in lanes
+    // n, n + 16, n + 32, n + 48; the second pass normalises as it loads.
+    float qs = 1.f;
+    if (a.q_norm_w) {
+      float ss = 0.f;
+#pragma unroll
+      for (int kd = 0; kd < 8; ++kd) {
+        float y[8];
+        load_q8(kd, y);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = add_rn(ss, mul_rn(y[j], y[j]));
+      }
+      qs = rms_scale(swap_sum(swap_sum(ss, true), false), kAttnHeadDim);
+    }
+    auto load_qn = [&](int kd, float (&y)[8]) {
+      load_q8(kd, y);
+      if (a.q_norm_w) {
+        const f32x4* wp = reinterpret_cast<const f32x4*>(a.q_norm_w + 32 * kd + 8 * g4);
+        const f32x4 w0 = wp[0], w1 = wp[1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          y[j] = rmsnorm_elem<AT>(y[j], qs, w0[j]);
+          y[4 + j] = rmsnorm_elem<AT>(y[4 + j], qs, w1[j]);
+        }
+      }
+    };
     // dims [0, 64) are kd 0, 1; rotate_half pairs dim 8 g4 + j with 32 + 8 g4 + j
     float x[2][8];
 #pragma unroll
-    for (int kd = 0; kd < 2; ++kd) {
-      if (row_ok) {
-        load_act8<AT>(a.q, base + 32 * kd, x[kd]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[kd][j] = 0.f;
-      }
-    }
+    for (int kd = 0; kd < 2; ++kd) load_qn(kd, x[kd]);
     if (a.rope_dim == 64) {
       const float pos = static_cast<float>(qpos);
 #pragma unroll
@@ -164,12 +193,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
     for (int kd = 2; kd < 8; ++kd) {
       float y[8];
-      if (row_ok) {
-        load_act8<AT>(a.q, base + 32 * kd, y);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = 0.f;
-      }
+      load_qn(kd, y);
 #pragma unroll
       for (int j = 0; j < 8; ++j) y[j] *= sl2;
       pack(y, qh[kd], ql[kd]);
@@ -396,17 +420,15 @@ static void launch_prefill(const PrefillAttnArgs& a, const int32_t* pt, int kv_d
 
 using namespace ria;
 
-extern "C" int ria_kv_append_seq(int length, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
-                                 const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
-                                 int kv_dtype, int num_pages, const int32_t* page_table_row, int64_t page_capacity,
-                                 int32_t start_pos, const float* inv_freq, int rope_dim, void* stream);
+
 
 extern "C" int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_heads, const void* q,
                                       int64_t q_row_stride, const void* k, int64_t k_row_stride, const void* v,
                                       int64_t v_row_stride, const void* gate, int64_t gate_row_stride, int act_dtype,
                                       void* k_cache, void* v_cache, int kv_dtype, int num_pages,
                                       const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
-                                      const float* inv_freq, int rope_dim, float scale, void* out, int phase,
+                                      const float* inv_freq, int rope_dim, const float* q_norm_weight,
+                                      const float* k_norm_weight, float scale, void* out, int phase,
                                       void* stream) {
   if (phase < RIA_PREFILL_APPEND || phase > RIA_PREFILL_BOTH)
     return set_error(RIA_ERR_INVALID, "ria_attn_prefill: phase must be 1 (append), 2 (attention) or 3 (both)");
@@ -423,6 +445,8 @@ extern "C" int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_he
     return set_error(RIA_ERR_INVALID, "ria_attn_prefill: null pointer");
   if (rope_dim != 0 && rope_dim != 64) return set_error(RIA_ERR_INVALID, "ria_attn_prefill: rope_dim must be 0 or 64");
   if (rope_dim && !inv_freq) return set_error(RIA_ERR_INVALID, "ria_attn_prefill: inv_freq is null");
+  if (reinterpret_cast<uintptr_t>(q_norm_weight) % 16)
+    return set_error(RIA_ERR_INVALID, "ria_attn_prefill: q_norm_weight must be 16-byte aligned");
   if ((int64_t)start_pos + length > page_capacity * kPageTokens)
     return set_error(RIA_ERR_INVALID, "ria_attn_prefill: %d + %d tokens exceed the row's %lld pages", start_pos,
                      length, (long long)page_capacity);
@@ -438,7 +462,7 @@ extern "C" int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_he
   if (phase & RIA_PREFILL_APPEND) {
     int rc = ria_kv_append_seq(length, num_kv_heads, k, act_dtype, k_row_stride, v, act_dtype, v_row_stride,
                                k_cache, v_cache, kv_dtype, num_pages, page_table_row, page_capacity, start_pos,
-                               inv_freq, rope_dim, stream);
+                               inv_freq, rope_dim, k_norm_weight, stream);
     if (rc != RIA_OK) return rc;
   }
   if (!(phase & RIA_PREFILL_ATTEND)) return RIA_OK;
@@ -455,6 +479,7 @@ extern "C" int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_he
   a.length = length;
   a.inv_freq = inv_freq;
   a.rope_dim = rope_dim;
+  a.q_norm_w = q_norm_weight;
   a.scale = scale;
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
@@ -476,9 +501,10 @@ extern "C" int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads, c
                                 const void* gate, int64_t gate_row_stride, int act_dtype, void* k_cache,
                                 void* v_cache, int kv_dtype, int num_pages, const int32_t* page_table_row,
                                 int64_t page_capacity, int32_t start_pos, const float* inv_freq, int rope_dim,
-                                float scale, void* out, void* stream) {
+                                const float* q_norm_weight, const float* k_norm_weight, float scale, void* out,
+                                void* stream) {
   return ria_attn_prefill_phase(length, num_q_heads, num_kv_heads, q, q_row_stride, k, k_row_stride, v, v_row_stride,
                                 gate, gate_row_stride, act_dtype, k_cache, v_cache, kv_dtype, num_pages,
-                                page_table_row, page_capacity, start_pos, inv_freq, rope_dim, scale, out,
-                                RIA_PREFILL_BOTH, stream);
+                                page_table_row, page_capacity, start_pos, inv_freq, rope_dim, q_norm_weight,
+                                k_norm_weight, scale, out, RIA_PREFILL_BOTH, stream);
 }

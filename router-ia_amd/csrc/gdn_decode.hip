@@ -13,6 +13,11 @@
 //   S_new  = S' + k_i d_j
 //   o_j    = sum_i S_new[i,j] q_i = sum_i S'[i,j] q_i + d_j (k . q)
 //
+// With a gate z the read-out leaves through the gated RMSNorm
+// (qwen36_attention_cache.py:268-271, qwen36_gated_norm_probe.py:19-36):
+//   out_j  = w_j * o_j / sqrt(mean(o^2) + 1e-6) * SiLU(z_j)
+// which needs the whole head's o in one workgroup (COLS = 128).
+//
 // Work decomposition: one 256-thread workgroup per (sequence, V head, column
 // block of COLS state columns).  Columns of S are independent in this
 // update, so small batches split a head over several workgroups.  Each
@@ -39,6 +44,10 @@ struct GdnDecodeArgs {
   const float* A_log;
   const float* dt_bias;
   void* out;  // [batch, Hv, 128]
+  const void* z;         // gated-norm gate [batch, Hv, 128] (row stride z_stride), or null
+  int64_t z_stride;
+  int z_dtype;
+  const float* norm_w;   // gated-norm weight [128] f32
   int num_k_heads;
   int num_v_heads;
   int conv_dim;
@@ -73,8 +82,9 @@ __device__ __forceinline__ float conv_channel(const GdnDecodeArgs& a, int b, int
   }
 }
 
-template <int COLS, int XT, int OT, bool FUSE, int GM>
+template <int COLS, int XT, int OT, bool FUSE, int GM, bool NORM>
 __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
+  static_assert(!NORM || COLS == kGdnHeadDim, "the gated norm needs whole heads");
   constexpr int TPR = COLS / 4;         // threads per state row
   constexpr int RG = 256 / TPR;         // row groups in the workgroup
   constexpr int RPT = kGdnHeadDim / RG; // rows held per thread
@@ -206,6 +216,21 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     st_stream(reinterpret_cast<f32x4*>(S + i * kGdnHeadDim + col0 + jl), s[r]);
   }
 
+  if constexpr (NORM) {
+    // rows group 0 is lanes 0..31 of wave 0 and holds the head's 128 outputs
+    if (rg == 0) {
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ss = add_rn(ss, mul_rn(oo[c], oo[c]));
+      const float r = rms_scale(half_wave_sum(ss), kGdnHeadDim);
+      {
+        const int64_t zo = (int64_t)b * a.z_stride + h * kGdnHeadDim + jl;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          oo[c] = gated_norm_elem<RIA_DT_F32>(oo[c], r, a.norm_w[jl + c], load_act_dt(a.z, zo + c, a.z_dtype));
+      }
+    }
+  }
   if (rg == 0) {
     const int64_t o = ((int64_t)b * a.num_v_heads + h) * kGdnHeadDim + col0 + jl;
 #pragma unroll
@@ -227,21 +252,33 @@ __global__ __launch_bounds__(256) void conv1d_step_kernel(GdnDecodeArgs a) {
   store_act<OT>(a.out, (int64_t)b * a.conv_dim + c, y);
 }
 
-template <int COLS, int XT, int OT, bool FUSE>
+template <int COLS, int XT, int OT, bool FUSE, bool NORM>
 static void launch_gdn_gm(const GdnDecodeArgs& a, int gate_mode, int blocks, hipStream_t st) {
   if (gate_mode == RIA_GATE_RAW)
-    hipLaunchKernelGGL((gdn_decode_kernel<COLS, XT, OT, FUSE, RIA_GATE_RAW>), dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gdn_decode_kernel<COLS, XT, OT, FUSE, RIA_GATE_RAW, NORM>), dim3(blocks), dim3(256), 0, st,
+                       a);
   else
-    hipLaunchKernelGGL((gdn_decode_kernel<COLS, XT, OT, FUSE, RIA_GATE_PRECOMPUTED>), dim3(blocks), dim3(256), 0,
-                       st, a);
+    hipLaunchKernelGGL((gdn_decode_kernel<COLS, XT, OT, FUSE, RIA_GATE_PRECOMPUTED, NORM>), dim3(blocks), dim3(256),
+                       0, st, a);
+}
+
+template <int COLS, int XT, int OT, bool FUSE>
+static void launch_gdn_norm(const GdnDecodeArgs& a, int gate_mode, int blocks, hipStream_t st) {
+  if constexpr (COLS == kGdnHeadDim) {
+    if (a.z) {
+      launch_gdn_gm<COLS, XT, OT, FUSE, true>(a, gate_mode, blocks, st);
+      return;
+    }
+  }
+  launch_gdn_gm<COLS, XT, OT, FUSE, false>(a, gate_mode, blocks, st);
 }
 
 template <int COLS, int XT, int OT>
 static void launch_gdn_fuse(const GdnDecodeArgs& a, bool fuse, int gate_mode, int blocks, hipStream_t st) {
   if (fuse)
-    launch_gdn_gm<COLS, XT, OT, true>(a, gate_mode, blocks, st);
+    launch_gdn_norm<COLS, XT, OT, true>(a, gate_mode, blocks, st);
   else
-    launch_gdn_gm<COLS, XT, OT, false>(a, gate_mode, blocks, st);
+    launch_gdn_norm<COLS, XT, OT, false>(a, gate_mode, blocks, st);
 }
 
 template <int COLS, int XT>
@@ -276,7 +313,8 @@ extern "C" int ria_gdn_decode(int batch, int num_k_heads, int num_v_heads, const
                               const int32_t* conv_pos, int32_t conv_pos_scalar, float* state,
                               const int32_t* seq_slot, const float* gate_a, const float* gate_b,
                               int64_t gate_row_stride, int gate_mode, const float* A_log, const float* dt_bias,
-                              void* out, int out_dtype, void* stream) {
+                              void* out, int out_dtype, const void* z, int z_dtype, int64_t z_row_stride,
+                              const float* norm_weight, void* stream) {
   if (batch < 0) return set_error(RIA_ERR_INVALID, "ria_gdn_decode: batch must be >= 0");
   if (batch == 0) return RIA_OK;
   if (num_k_heads <= 0 || num_v_heads <= 0 || num_v_heads % num_k_heads != 0)
@@ -297,6 +335,8 @@ extern "C" int ria_gdn_decode(int batch, int num_k_heads, int num_v_heads, const
   const int conv_dim = (2 * num_k_heads + num_v_heads) * kGdnHeadDim;
   if (x_row_stride < conv_dim) return set_error(RIA_ERR_INVALID, "ria_gdn_decode: x_row_stride < conv_dim");
   if (gate_row_stride < num_v_heads) return set_error(RIA_ERR_INVALID, "ria_gdn_decode: gate_row_stride < Hv");
+  if (z && (!norm_weight || !valid_dtype(z_dtype) || z_row_stride < (int64_t)num_v_heads * kGdnHeadDim))
+    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: a gate z needs norm_weight, a dtype code and row stride >= Hv*128");
 
   GdnDecodeArgs a{};
   a.x = mixed_qkv;
@@ -313,15 +353,22 @@ extern "C" int ria_gdn_decode(int batch, int num_k_heads, int num_v_heads, const
   a.A_log = A_log;
   a.dt_bias = dt_bias;
   a.out = out;
+  a.z = z;
+  a.z_stride = z_row_stride;
+  a.z_dtype = z_dtype;
+  a.norm_w = norm_weight;
   a.num_k_heads = num_k_heads;
   a.num_v_heads = num_v_heads;
   a.conv_dim = conv_dim;
 
-  // Column blocking: enough workgroups to cover 256 CUs several times over.
+  // Column blocking: enough workgroups to cover 256 CUs several times over;
+  // the gated norm needs whole heads.
   const int64_t tiles = (int64_t)batch * num_v_heads;
   int cols = 128;
-  if (tiles < 256) cols = 32;
-  else if (tiles < 1024) cols = 64;
+  if (!z) {
+    if (tiles < 256) cols = 32;
+    else if (tiles < 1024) cols = 64;
+  }
   a.ncb = kGdnHeadDim / cols;
   const int64_t blocks64 = tiles * a.ncb;
   if (blocks64 > 0x7fffffff) return set_error(RIA_ERR_INVALID, "ria_gdn_decode: grid too large");

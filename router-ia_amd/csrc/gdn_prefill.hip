@@ -28,6 +28,7 @@
 // operands split as hi + lo bf16 (hi*hi + hi*lo + lo*hi, ~2^-16 relative);
 // the cumulative decay, exponentials and the triangular inverse are fp32.
 #include <math.h>
+#include <algorithm>
 
 #include "ria_common.h"
 
@@ -74,7 +75,8 @@ struct PrefillArgs {
   const float* A_log;
   const float* dt_bias;
   char* rec;   // [seg_chunks, Hv, kRecBytes]
-  void* out;   // [L, Hv, 128]
+  void* out;   // [L, Hv, 128] (or the segment's fp32 read-out before the gated norm)
+  int out_tok0;  // token stored at row 0 of out
   int num_k_heads;
   int num_v_heads;
   int conv_dim;
@@ -577,7 +579,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int t = chunk * kChunk + 16 * wave + 4 * g4 + i4;
-      if (t < a.length) store_act<OT>(a.out, ((int64_t)t * a.num_v_heads + h) * kDim + cb * 16 + n, oi[i4]);
+      if (t < a.length)
+        store_act<OT>(a.out, ((int64_t)(t - a.out_tok0) * a.num_v_heads + h) * kDim + cb * 16 + n, oi[i4]);
     }
     // (iii) S <- exp(G_C) S + Kt^T v' for dk tiles 2 wave, 2 wave + 1
 #pragma unroll
@@ -625,12 +628,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
 static bool valid_dtype(int dt) { return dt == RIA_DT_BF16 || dt == RIA_DT_F16 || dt == RIA_DT_F32; }
 
-int64_t prefill_segment_bytes(int num_k_heads, int num_v_heads, int seg_tokens) {
+// Workspace of one segment: [post-conv activations | phase-A records].  The
+// first region holds the bf16 post-conv q|k|v until phase A has read it, then
+// (with the gated norm) the segment's fp32 read-out between the scan and the
+// norm pass.
+int64_t prefill_post_bytes(int num_k_heads, int num_v_heads, int seg_chunks) {
   const int64_t conv_dim = (int64_t)(2 * num_k_heads + num_v_heads) * kDim;
-  const int64_t chunks = (seg_tokens + kChunk - 1) / kChunk;
-  const int64_t post = ((int64_t)chunks * kChunk * conv_dim * 2 + 255) / 256 * 256;
-  return post + chunks * num_v_heads * (int64_t)kRecBytes;
+  const int64_t tokens = (int64_t)seg_chunks * kChunk;
+  const int64_t bytes = std::max(tokens * conv_dim * 2, tokens * num_v_heads * kDim * 4);
+  return (bytes + 255) / 256 * 256;
 }
+
+int64_t prefill_segment_bytes(int num_k_heads, int num_v_heads, int seg_tokens) {
+  const int chunks = (seg_tokens + kChunk - 1) / kChunk;
+  return prefill_post_bytes(num_k_heads, num_v_heads, chunks) + (int64_t)chunks * num_v_heads * kRecBytes;
+}
+
+static int dtype_bytes(int dt) { return dt == RIA_DT_F32 ? 4 : 2; }
 
 }  // namespace ria
 
@@ -645,6 +659,7 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
                                int64_t x_row_stride, const void* conv_weight, void* conv_ring, int32_t conv_pos,
                                float* state, const float* gate_a, const float* gate_b, int64_t gate_row_stride,
                                int gate_mode, const float* A_log, const float* dt_bias, void* out, int out_dtype,
+                               const void* z, int z_dtype, int64_t z_row_stride, const float* norm_weight,
                                void* workspace, int64_t workspace_bytes, void* stream) {
   if (length < 0) return set_error(RIA_ERR_INVALID, "ria_gdn_prefill: length must be >= 0");
   if (length == 0) return RIA_OK;
@@ -663,6 +678,8 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
   const int conv_dim = (2 * num_k_heads + num_v_heads) * kDim;
   if (x_row_stride < conv_dim || gate_row_stride < num_v_heads)
     return set_error(RIA_ERR_INVALID, "ria_gdn_prefill: row stride too small");
+  if (z && (!norm_weight || !valid_dtype(z_dtype) || z_row_stride < (int64_t)num_v_heads * kDim))
+    return set_error(RIA_ERR_INVALID, "ria_gdn_prefill: a gate z needs norm_weight, a dtype code and row stride >= Hv*128");
   // Largest segment (whole chunks) the workspace holds.
   int seg_chunks = (length + kChunk - 1) / kChunk;
   while (seg_chunks > 0 && prefill_segment_bytes(num_k_heads, num_v_heads, seg_chunks * kChunk) > workspace_bytes)
@@ -688,7 +705,7 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
   a.num_k_heads = num_k_heads;
   a.num_v_heads = num_v_heads;
   a.conv_dim = conv_dim;
-  const int64_t post_bytes = ((int64_t)seg_chunks * kChunk * conv_dim * 2 + 255) / 256 * 256;
+  const int64_t post_bytes = prefill_post_bytes(num_k_heads, num_v_heads, seg_chunks);
   a.post = static_cast<uint16_t*>(workspace);
   a.rec = static_cast<char*>(workspace) + post_bytes;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -716,14 +733,32 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
       RIA_PREFILL_PHASES(RIA_DT_F32);
     }
 #undef RIA_PREFILL_PHASES
-    if (out_dtype == RIA_DT_BF16)
-      hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_BF16>), sgrid, dim3(256), 0, st, a);
-    else if (out_dtype == RIA_DT_F16)
-      hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F16>), sgrid, dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F32>), sgrid, dim3(256), 0, st, a);
-    int rc = check_launch("ria_gdn_prefill");
-    if (rc != RIA_OK) return rc;
+    if (z) {
+      // fp32 read-out of the segment into the (now dead) post-conv region,
+      // then the gated RMSNorm over whole heads into out
+      PrefillArgs sa = a;
+      sa.out = a.post;
+      sa.out_tok0 = a.tok0;
+      hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F32>), sgrid, dim3(256), 0, st, sa);
+      int rc = check_launch("ria_gdn_prefill");
+      if (rc != RIA_OK) return rc;
+      const int64_t head_row = (int64_t)num_v_heads * kDim;
+      rc = ria_gated_rmsnorm(a.seg_tokens, num_v_heads, kDim, a.post, RIA_DT_F32, head_row,
+                             static_cast<const char*>(z) + (int64_t)a.tok0 * z_row_stride * dtype_bytes(z_dtype),
+                             z_dtype, z_row_stride, norm_weight, kNormEps,
+                             static_cast<char*>(out) + (int64_t)a.tok0 * head_row * dtype_bytes(out_dtype), out_dtype,
+                             head_row, stream);
+      if (rc != RIA_OK) return rc;
+    } else {
+      if (out_dtype == RIA_DT_BF16)
+        hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_BF16>), sgrid, dim3(256), 0, st, a);
+      else if (out_dtype == RIA_DT_F16)
+        hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F16>), sgrid, dim3(256), 0, st, a);
+      else
+        hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F32>), sgrid, dim3(256), 0, st, a);
+      int rc = check_launch("ria_gdn_prefill");
+      if (rc != RIA_OK) return rc;
+    }
   }
   dim3 rgrid((conv_dim + 255) / 256);
   if (x_dtype == RIA_DT_BF16)

@@ -67,6 +67,14 @@ __device__ __forceinline__ float load_act(const void* p, int64_t i) {
   }
 }
 
+// load_act with the dtype code known only at run time (side inputs such as
+// the gated norm's z, where a template parameter would multiply instances).
+__device__ __forceinline__ float load_act_dt(const void* p, int64_t i, int dt) {
+  if (dt == RIA_DT_BF16) return load_act<RIA_DT_BF16>(p, i);
+  if (dt == RIA_DT_F16) return load_act<RIA_DT_F16>(p, i);
+  return load_act<RIA_DT_F32>(p, i);
+}
+
 template <int DT>
 __device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
   if constexpr (DT == RIA_DT_BF16) {
@@ -165,6 +173,30 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
+// RMSNorm pieces shared by the standalone and the fused forms.  eps is the
+// model's 1e-6 (qwen36_op_probe.py:32, qwen36_gated_norm_probe.py:16).
+constexpr float kNormEps = 1e-6f;
+
+// 1 / sqrt(mean(x^2) + eps) from the row's sum of squares over n elements.
+__device__ __forceinline__ float rms_scale(float sum_sq, int n, float eps = kNormEps) {
+  return 1.0f / sqrtf(add_rn(__fdiv_rn(sum_sq, static_cast<float>(n)), eps));
+}
+
+// Qwen RMSNorm element (qwen36_op_probe.py:55-67): (x r)(1 + w) in fp32, cast
+// back to the input dtype XT.
+template <int XT>
+__device__ __forceinline__ float rmsnorm_elem(float x, float r, float w) {
+  return through_dtype<XT>(mul_rn(mul_rn(x, r), add_rn(1.0f, w)));
+}
+
+// Gated RMSNorm element (qwen36_gated_norm_probe.py:19-36): the normalised
+// value is cast to the input dtype XT, scaled by w, gated by SiLU(z) in fp32,
+// and the product cast to XT again.
+template <int XT>
+__device__ __forceinline__ float gated_norm_elem(float x, float r, float w, float z) {
+  return through_dtype<XT>(mul_rn(mul_rn(w, through_dtype<XT>(mul_rn(x, r))), silu_f(z)));
+}
+
 // 16-bit KV element formats: conversion and the two MFMA shapes the decode
 // kernel uses (16x16x32 with 8 operands per lane, 16x16x16 with 4).
 template <int KVT>
@@ -232,6 +264,18 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Sum over each half of the wavefront (lanes 0..31 and 32..63 separately),
+// by ds_swizzle in xor mode: the lane pattern is an immediate, so no lane
+// address registers stay live (pattern = and_mask 0x1f | xor_mask << 10).
+__device__ __forceinline__ float half_wave_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (1 << 10)));
+  v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (2 << 10)));
+  v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (4 << 10)));
+  v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (8 << 10)));
+  v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (16 << 10)));
   return v;
 }
 

@@ -1,6 +1,10 @@
 // Small elementwise entry points behind the module-level helpers of the
 // attention cache: _rope, _apply_rope and _l2norm
-// (v2/src/router_ia/qwen36_attention_cache.py:137-173).
+// (v2/src/router_ia/qwen36_attention_cache.py:137-173), and the two RMSNorm
+// forms around it: the (1 + w) RMSNorm of the layer input and of q / k
+// (qwen36_op_probe.py:55-67, used at qwen36_attention_cache.py:227,302-305)
+// and the gated RMSNorm of the DeltaNet read-out (qwen36_gated_norm_probe.py:19-36,
+// used at qwen36_attention_cache.py:268-271).
 #include <math.h>
 
 #include "ria_common.h"
@@ -56,9 +60,122 @@ __global__ __launch_bounds__(256) void l2norm_kernel(int64_t rows, int dim, cons
   for (int d = lane; d < dim; d += 64) out[r * dim + d] = mul_rn(load_act<XT>(x, r * dim + d), inv);
 }
 
+struct NormArgs {
+  const void* x;
+  int64_t x_stride;  // elements between tokens
+  const void* z;     // gated form only
+  int64_t z_stride;
+  int z_dtype;
+  const float* weight;
+  float eps;
+  void* out;
+  int64_t out_stride;
+  int64_t rows;  // tokens * heads
+  int heads;
+  int dim;
+};
+
+// One wavefront per (token, head) row of `dim` elements; head h of a token
+// starts at element h * dim of the token's row.  Each lane reads its own
+// elements in both passes, so `out` may alias `x` when both have one dtype
+// and one stride.
+template <int XT, int OT, bool GATED>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= a.rows) return;
+  const int64_t t = r / a.heads;
+  const int64_t hoff = (r - t * a.heads) * a.dim;
+  const int64_t xo = t * a.x_stride + hoff;
+  float ss = 0.f;
+  for (int d = lane; d < a.dim; d += 64) {
+    const float v = load_act<XT>(a.x, xo + d);
+    ss = add_rn(ss, mul_rn(v, v));
+  }
+  const float rs = rms_scale(wave_sum(ss), a.dim, a.eps);
+  const int64_t oo = t * a.out_stride + hoff;
+  const int64_t zo = t * a.z_stride + hoff;
+  for (int d = lane; d < a.dim; d += 64) {
+    const float v = load_act<XT>(a.x, xo + d);
+    float y;
+    if constexpr (GATED)
+      y = gated_norm_elem<XT>(v, rs, a.weight[d], load_act_dt(a.z, zo + d, a.z_dtype));
+    else
+      y = rmsnorm_elem<XT>(v, rs, a.weight[d]);
+    store_act<OT>(a.out, oo + d, y);
+  }
+}
+
+template <int XT, bool GATED>
+static void launch_norm_ot(const NormArgs& a, int out_dtype, dim3 grid, hipStream_t st) {
+  if (out_dtype == RIA_DT_BF16)
+    hipLaunchKernelGGL((rmsnorm_kernel<XT, RIA_DT_BF16, GATED>), grid, dim3(256), 0, st, a);
+  else if (out_dtype == RIA_DT_F16)
+    hipLaunchKernelGGL((rmsnorm_kernel<XT, RIA_DT_F16, GATED>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<XT, RIA_DT_F32, GATED>), grid, dim3(256), 0, st, a);
+}
+
+static bool norm_dtype_ok(int dt) { return dt == RIA_DT_BF16 || dt == RIA_DT_F16 || dt == RIA_DT_F32; }
+
+template <bool GATED>
+static int launch_norm(const char* who, int64_t tokens, int heads, int dim, const void* x, int x_dtype,
+                       int64_t x_stride, const void* z, int z_dtype, int64_t z_stride, const float* weight, float eps,
+                       void* out, int out_dtype, int64_t out_stride, void* stream) {
+  if (tokens < 0 || heads <= 0 || dim <= 0) return set_error(RIA_ERR_INVALID, "%s: bad sizes", who);
+  if (!norm_dtype_ok(x_dtype) || !norm_dtype_ok(out_dtype) || (GATED && !norm_dtype_ok(z_dtype)))
+    return set_error(RIA_ERR_INVALID, "%s: unknown dtype code", who);
+  const int64_t row = (int64_t)heads * dim;
+  if (x_stride < row || out_stride < row || (GATED && z_stride < row))
+    return set_error(RIA_ERR_INVALID, "%s: token stride smaller than heads * dim", who);
+  if (!(eps >= 0.f)) return set_error(RIA_ERR_INVALID, "%s: eps must be >= 0", who);
+  if (tokens == 0) return RIA_OK;
+  if (!x || !weight || !out || (GATED && !z)) return set_error(RIA_ERR_INVALID, "%s: null pointer", who);
+  const int64_t rows = tokens * heads;
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > 0x7fffffff) return set_error(RIA_ERR_INVALID, "%s: too many rows", who);
+  NormArgs a{};
+  a.x = x;
+  a.x_stride = x_stride;
+  a.z = z;
+  a.z_stride = z_stride;
+  a.z_dtype = z_dtype;
+  a.weight = weight;
+  a.eps = eps;
+  a.out = out;
+  a.out_stride = out_stride;
+  a.rows = rows;
+  a.heads = heads;
+  a.dim = dim;
+  const dim3 grid(static_cast<unsigned>(blocks));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (x_dtype == RIA_DT_BF16)
+    launch_norm_ot<RIA_DT_BF16, GATED>(a, out_dtype, grid, st);
+  else if (x_dtype == RIA_DT_F16)
+    launch_norm_ot<RIA_DT_F16, GATED>(a, out_dtype, grid, st);
+  else
+    launch_norm_ot<RIA_DT_F32, GATED>(a, out_dtype, grid, st);
+  return check_launch(who);
+}
+
 }  // namespace ria
 
 using namespace ria;
+
+extern "C" int ria_rmsnorm(int64_t tokens, int heads, int dim, const void* x, int x_dtype, int64_t x_token_stride,
+                           const float* weight, float eps, void* out, int out_dtype, int64_t out_token_stride,
+                           void* stream) {
+  return launch_norm<false>("ria_rmsnorm", tokens, heads, dim, x, x_dtype, x_token_stride, nullptr, RIA_DT_F32, 0,
+                            weight, eps, out, out_dtype, out_token_stride, stream);
+}
+
+extern "C" int ria_gated_rmsnorm(int64_t tokens, int heads, int dim, const void* x, int x_dtype,
+                                 int64_t x_token_stride, const void* z, int z_dtype, int64_t z_token_stride,
+                                 const float* weight, float eps, void* out, int out_dtype, int64_t out_token_stride,
+                                 void* stream) {
+  return launch_norm<true>("ria_gated_rmsnorm", tokens, heads, dim, x, x_dtype, x_token_stride, z, z_dtype,
+                           z_token_stride, weight, eps, out, out_dtype, out_token_stride, stream);
+}
 
 extern "C" int ria_rope_table(int32_t position, const float* inv_freq, int rope_dim, float* cos_out,
                               float* sin_out, void* stream) {

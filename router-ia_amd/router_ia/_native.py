@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIB_ENV = "RIA_HIP_LIB"
 DEFAULT_LIB = Path(__file__).resolve().parent / "_lib" / "libria_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 RIA_DT_BF16 = 0
 RIA_DT_F16 = 1
@@ -42,39 +42,44 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ria_gdn_decode": (
         _c_int,
         [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _c_int, _vp, _vp, _vp, _c_i32, _vp, _vp,
-         _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp, _c_int, _vp],
+         _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_i64, _vp, _vp],
     ),
     "ria_conv1d_step": (
         _c_int,
         [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _vp, _vp, _c_i32, _vp, _c_int, _vp],
     ),
     "ria_l2norm": (_c_int, [_c_i64, _c_int, _vp, _c_int, _c_f32, _vp, _vp]),
+    "ria_rmsnorm": (_c_int, [_c_i64, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_f32, _vp, _c_int, _c_i64, _vp]),
+    "ria_gated_rmsnorm": (
+        _c_int,
+        [_c_i64, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _c_f32, _vp, _c_int, _c_i64, _vp],
+    ),
     "ria_rope_table": (_c_int, [_c_i32, _vp, _c_int, _vp, _vp, _vp]),
     "ria_rope_apply": (_c_int, [_c_i64, _c_int, _c_int, _vp, _vp, _vp, _c_i32, _vp]),
     "ria_kv_append": (
         _c_int,
         [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp, _c_i64,
-         _vp, _vp, _c_i32, _vp, _c_i32, _vp, _c_int, _vp],
+         _vp, _vp, _c_i32, _vp, _c_i32, _vp, _c_int, _vp, _vp],
     ),
     "ria_attn_decode_split_tokens": (_c_int, [_c_int, _vp, _c_int]),
     "ria_attn_decode_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "ria_attn_decode": (
         _c_int,
         [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp,
-         _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _c_f32, _c_int, _vp, _c_i64,
+         _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _vp, _c_f32, _c_int, _vp, _c_i64,
          _vp, _c_int, _vp],
     ),
     "ria_attn_decode_phase": (
         _c_int,
         [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp,
-         _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _c_f32, _c_int, _vp, _c_i64,
+         _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _vp, _c_f32, _c_int, _vp, _c_i64,
          _vp, _c_int, _c_int, _vp],
     ),
     "ria_gdn_prefill_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int]),
     "ria_gdn_prefill": (
         _c_int,
         [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _c_i32, _vp, _vp, _vp, _c_i64, _c_int,
-         _vp, _vp, _vp, _c_int, _vp, _c_i64, _vp],
+         _vp, _vp, _vp, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _c_i64, _vp],
     ),
     "ria_kv_gather": (
         _c_int,
@@ -83,17 +88,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ria_kv_append_seq": (
         _c_int,
         [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp, _c_i64,
-         _c_i32, _vp, _c_int, _vp],
+         _c_i32, _vp, _c_int, _vp, _vp],
     ),
     "ria_attn_prefill": (
         _c_int,
         [_c_int, _c_int, _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _vp, _vp,
-         _c_int, _c_int, _vp, _c_i64, _c_i32, _vp, _c_int, _c_f32, _vp, _vp],
+         _c_int, _c_int, _vp, _c_i64, _c_i32, _vp, _c_int, _vp, _vp, _c_f32, _vp, _vp],
     ),
     "ria_attn_prefill_phase": (
         _c_int,
         [_c_int, _c_int, _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _vp, _vp,
-         _c_int, _c_int, _vp, _c_i64, _c_i32, _vp, _c_int, _c_f32, _vp, _c_int, _vp],
+         _c_int, _c_int, _vp, _c_i64, _c_i32, _vp, _c_int, _vp, _vp, _c_f32, _vp, _c_int, _vp],
     ),
 }
 

@@ -17,6 +17,11 @@ then ``advance()``, the batched equivalent of the reference caller bumping
 A prompt enters one row at a time through ``begin_prefill`` /
 ``linear_prefill`` / ``full_prefill`` / ``end_prefill`` (chunked DeltaNet and
 causal attention prefill), equal to decoding it token by token.
+
+The norms on either side of the attention arithmetic run inside the same
+launches when their fp32 weights are passed: the gated RMSNorm of the
+DeltaNet read-out (``z``, ``norm_weight``; :268-271) and the q_norm / k_norm
+RMSNorms before RoPE (``q_norm_weight``, ``k_norm_weight``; :302-305).
 """
 
 from __future__ import annotations
@@ -151,15 +156,17 @@ class BatchedAttentionState:
         dt_bias: torch.Tensor | None = None,
         out: torch.Tensor | None = None,
         out_dtype: torch.dtype = torch.bfloat16,
+        z: torch.Tensor | None = None,
+        norm_weight: torch.Tensor | None = None,
     ) -> torch.Tensor:
-        """One Gated DeltaNet token for every row (conv + recurrence + read-out)."""
+        """One Gated DeltaNet token for every row (conv + recurrence + read-out [+ gated RMSNorm])."""
         if out is None:
             out = torch.empty((self.max_seqs, self.num_v_heads, 128), dtype=out_dtype, device=self.device)
         return K.gdn_decode(
             mixed_qkv, self.linear_states[layer], gate_a, gate_b, out,
             num_k_heads=self.num_k_heads, num_v_heads=self.num_v_heads, fuse_conv=True,
             conv_weight=conv_weight, conv_ring=self.conv_rings[layer], conv_pos=self.tokens_seen,
-            gate_mode=gate_mode, A_log=A_log, dt_bias=dt_bias)
+            gate_mode=gate_mode, A_log=A_log, dt_bias=dt_bias, z=z, norm_weight=norm_weight)
 
     def full_step(
         self,
@@ -171,6 +178,8 @@ class BatchedAttentionState:
         *,
         out: torch.Tensor | None = None,
         out_dtype: torch.dtype = torch.bfloat16,
+        q_norm_weight: torch.Tensor | None = None,
+        k_norm_weight: torch.Tensor | None = None,
     ) -> torch.Tensor:
         """Append this token's k, v (RoPE on k) and attend over each row's whole context."""
         max_ctx = self.max_seen + 1
@@ -180,12 +189,12 @@ class BatchedAttentionState:
             self._ensure([n + 1 for n in self._host_seen])
         k_cache, v_cache = self.kv.layer(layer)
         K.kv_append(k, v, k_cache, v_cache, self.kv.page_table, positions=self.tokens_seen,
-                    slots=self.tokens_seen, inv_freq=self.inv_freq)
+                    slots=self.tokens_seen, inv_freq=self.inv_freq, k_norm_weight=k_norm_weight)
         if out is None:
             out = torch.empty((self.max_seqs, self.num_q_heads, 256), dtype=out_dtype, device=self.device)
         return K.attn_decode(q, gate, k_cache, v_cache, self.kv.page_table, out, positions=self.tokens_seen,
                              ctx_lens=self.ctx_lens, max_ctx=max_ctx, inv_freq=self.inv_freq, scale=self.scale,
-                             workspace=self.workspace, split_tokens=self.split_tokens)
+                             workspace=self.workspace, split_tokens=self.split_tokens, q_norm_weight=q_norm_weight)
 
     # ---------------------------------------------------------------- prompt prefill (one row)
     # A prompt enters one sequence row at a time: begin_prefill(row, L), then
@@ -220,6 +229,8 @@ class BatchedAttentionState:
         dt_bias: torch.Tensor | None = None,
         out: torch.Tensor | None = None,
         out_dtype: torch.dtype = torch.bfloat16,
+        z: torch.Tensor | None = None,
+        norm_weight: torch.Tensor | None = None,
     ) -> torch.Tensor:
         """A prompt's Gated DeltaNet tokens for one row (chunked prefill); mixed_qkv [L, conv_dim]."""
         length = int(mixed_qkv.shape[0])
@@ -229,7 +240,8 @@ class BatchedAttentionState:
             mixed_qkv, self.linear_states[layer, row], gate_a, gate_b, out,
             num_k_heads=self.num_k_heads, num_v_heads=self.num_v_heads, conv_weight=conv_weight,
             conv_ring=self.conv_rings[layer, row], conv_pos=self._host_seen[row],
-            workspace=self._prefill_workspace(length), gate_mode=gate_mode, A_log=A_log, dt_bias=dt_bias)
+            workspace=self._prefill_workspace(length), gate_mode=gate_mode, A_log=A_log, dt_bias=dt_bias, z=z,
+            norm_weight=norm_weight)
 
     def full_prefill(
         self,
@@ -241,11 +253,14 @@ class BatchedAttentionState:
         gate: torch.Tensor,
         *,
         out: torch.Tensor | None = None,
+        q_norm_weight: torch.Tensor | None = None,
+        k_norm_weight: torch.Tensor | None = None,
     ) -> torch.Tensor:
         """Append a prompt's k, v (RoPE on k) to one row and run its causal attention; q, gate [L, Hq, 256]."""
         k_cache, v_cache = self.kv.layer(layer)
         return K.attn_prefill(q, k, v, gate, k_cache, v_cache, self.kv.page_table[row], out,
-                              start=self._host_seen[row], inv_freq=self.inv_freq, scale=self.scale)
+                              start=self._host_seen[row], inv_freq=self.inv_freq, scale=self.scale,
+                              q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight)
 
     def end_prefill(self, row: int, length: int) -> None:
         """The row's position moves past the prompt (after every layer has run it)."""

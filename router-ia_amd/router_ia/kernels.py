@@ -76,6 +76,17 @@ def conv_dim(num_k_heads: int, num_v_heads: int) -> int:
     return (2 * num_k_heads + num_v_heads) * GDN_HEAD_DIM
 
 
+def _norm_weight(name: str, w: torch.Tensor | None, n: int, dev: torch.device) -> ctypes.c_void_p | None:
+    """A norm weight as the ABI takes it: contiguous fp32 [n] on the device (16-byte aligned)."""
+    if w is None:
+        return None
+    _require_gpu(name, w, dev)
+    if w.dtype != torch.float32 or w.numel() != n or not w.is_contiguous() or w.data_ptr() % 16:
+        raise ValueError(f"{name} must be a contiguous, 16-byte aligned fp32 tensor of {n} values "
+                         f"(convert the checkpoint weight with .float() once)")
+    return _ptr(w)
+
+
 def gdn_decode(
     mixed_qkv: torch.Tensor,
     state: torch.Tensor,
@@ -93,8 +104,15 @@ def gdn_decode(
     gate_mode: int = nat.RIA_GATE_PRECOMPUTED,
     A_log: torch.Tensor | None = None,
     dt_bias: torch.Tensor | None = None,
+    z: torch.Tensor | None = None,
+    norm_weight: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Fused conv + gated delta-rule decode step (ria_gdn_decode)."""
+    """Fused conv + gated delta-rule decode step (ria_gdn_decode).
+
+    With ``z`` ([batch, Hv, 128] or [batch, >= Hv*128] rows) and the fp32
+    ``norm_weight`` [128], ``out`` receives the gated RMSNorm of the read-out
+    (qwen36_attention_cache.py:268-271) instead of the read-out itself.
+    """
     batch = int(mixed_qkv.shape[0])
     dev = mixed_qkv.device
     cdim = conv_dim(num_k_heads, num_v_heads)
@@ -126,6 +144,15 @@ def gdn_decode(
     if seq_slot is not None:
         _rows_i32("seq_slot", seq_slot, batch, dev)
     pos_t, pos_s = _rows_i32("conv_pos", conv_pos, batch, dev)
+    z_stride = 0
+    if (z is None) != (norm_weight is None):
+        raise ValueError("the gated norm needs both z and norm_weight")
+    if z is not None:
+        _require_gpu("z", z, dev)
+        z_stride = _row_stride("z", z, batch, num_v_heads * GDN_HEAD_DIM) if z.dim() == 3 else int(z.stride(0))
+        if z.dim() == 2 and (z.shape[0] != batch or z.shape[1] < num_v_heads * GDN_HEAD_DIM or z.stride(1) != 1):
+            raise ValueError(f"z must have {batch} rows of >= {num_v_heads * GDN_HEAD_DIM} contiguous elements")
+    w_ptr = _norm_weight("norm_weight", norm_weight, GDN_HEAD_DIM, dev)
     lib = nat.load()
     rc = lib.ria_gdn_decode(
         batch, num_k_heads, num_v_heads, _ptr(mixed_qkv), dtype_code(mixed_qkv), x_stride, int(bool(fuse_conv)),
@@ -133,7 +160,7 @@ def gdn_decode(
         _ptr(state), _ptr(seq_slot), _ptr(gate_a), _ptr(gate_b), g_stride, int(gate_mode),
         _ptr(A_log) if gate_mode == nat.RIA_GATE_RAW else None,
         _ptr(dt_bias) if gate_mode == nat.RIA_GATE_RAW else None,
-        _ptr(out), dtype_code(out), _stream(dev))
+        _ptr(out), dtype_code(out), _ptr(z), dtype_code(z) if z is not None else 0, z_stride, w_ptr, _stream(dev))
     nat.check(rc, "ria_gdn_decode")
     return out
 
@@ -187,6 +214,68 @@ def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     rows = xc.numel() // dim if dim else 0
     rc = nat.load().ria_l2norm(rows, dim, _ptr(xc), dtype_code(xc), float(eps), _ptr(out), _stream(x.device))
     nat.check(rc, "ria_l2norm")
+    return out
+
+
+def _token_rows(name: str, t: torch.Tensor, dim: int) -> tuple[int, int, int]:
+    """[T, D] or [T, H, D] with contiguous heads inside each token -> (T, H, token stride)."""
+    if t.dim() == 2:
+        tokens, heads = int(t.shape[0]), 1
+        inner = t.shape[1] == 1 or t.stride(1) == 1
+    elif t.dim() == 3:
+        tokens, heads = int(t.shape[0]), int(t.shape[1])
+        inner = (t.shape[2] == 1 or t.stride(2) == 1) and (heads == 1 or t.stride(1) == dim)
+    else:
+        raise ValueError(f"{name} must be [tokens, dim] or [tokens, heads, dim], got {tuple(t.shape)}")
+    if int(t.shape[-1]) != dim or not inner:
+        raise ValueError(f"{name} needs rows of {dim} contiguous elements, got shape {tuple(t.shape)} "
+                         f"strides {t.stride()}")
+    return tokens, heads, (int(t.stride(0)) if tokens > 1 else heads * dim)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None = None,
+            eps: float = 1e-6) -> torch.Tensor:
+    """(1 + w) RMSNorm over the last dim in fp32, cast back to x's dtype (ria_rmsnorm).
+
+    x is [tokens, dim] or [tokens, heads, dim]; ``out`` (same shape) may have
+    another dtype, into which the x-dtype result is converted.
+    """
+    _require_gpu("x", x)
+    dim = int(x.shape[-1])
+    tokens, heads, xs = _token_rows("x", x, dim)
+    if out is None:
+        out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+    _require_gpu("out", out, x.device)
+    if tuple(out.shape) != tuple(x.shape):
+        raise ValueError(f"out shape {tuple(out.shape)} != x shape {tuple(x.shape)}")
+    _, _, os_ = _token_rows("out", out, dim)
+    rc = nat.load().ria_rmsnorm(tokens, heads, dim, _ptr(x), dtype_code(x), xs,
+                                _norm_weight("weight", weight, dim, x.device), float(eps), _ptr(out),
+                                dtype_code(out), os_, _stream(x.device))
+    nat.check(rc, "ria_rmsnorm")
+    return out
+
+
+def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None = None,
+                  eps: float = 1e-6) -> torch.Tensor:
+    """weight * RMSNorm(x) * SiLU(z) per row, in x's dtype (ria_gated_rmsnorm)."""
+    _require_gpu("x", x)
+    _require_gpu("z", z, x.device)
+    if tuple(z.shape) != tuple(x.shape):
+        raise ValueError(f"x/z shape mismatch: {tuple(x.shape)} vs {tuple(z.shape)}")
+    dim = int(x.shape[-1])
+    tokens, heads, xs = _token_rows("x", x, dim)
+    _, _, zs = _token_rows("z", z, dim)
+    if out is None:
+        out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+    _require_gpu("out", out, x.device)
+    if tuple(out.shape) != tuple(x.shape):
+        raise ValueError(f"out shape {tuple(out.shape)} != x shape {tuple(x.shape)}")
+    _, _, os_ = _token_rows("out", out, dim)
+    rc = nat.load().ria_gated_rmsnorm(tokens, heads, dim, _ptr(x), dtype_code(x), xs, _ptr(z), dtype_code(z), zs,
+                                      _norm_weight("weight", weight, dim, x.device), float(eps), _ptr(out),
+                                      dtype_code(out), os_, _stream(x.device))
+    nat.check(rc, "ria_gated_rmsnorm")
     return out
 
 
@@ -259,8 +348,13 @@ def kv_append(
     slots: torch.Tensor | int,
     inv_freq: torch.Tensor,
     seq_slot: torch.Tensor | None = None,
+    k_norm_weight: torch.Tensor | None = None,
 ) -> None:
-    """RoPE k and append k, v of one token per sequence into the paged cache (ria_kv_append)."""
+    """RoPE k and append k, v of one token per sequence into the paged cache (ria_kv_append).
+
+    With the fp32 ``k_norm_weight`` [256], k is RMSNorm'd ((1 + w), cast back
+    to k's dtype) before RoPE (qwen36_attention_cache.py:303-305).
+    """
     batch = int(k.shape[0])
     num_kv_heads = int(k.shape[1]) if k.dim() == 3 else int(k.numel() // max(batch, 1) // ATTN_HEAD_DIM)
     dev = k.device
@@ -283,7 +377,7 @@ def kv_append(
                                   _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table), pts,
                                   _ptr(seq_slot),
                                   _ptr(pos_t), pos_s, _ptr(slot_t), slot_s, _ptr(inv_freq), 2 * int(inv_freq.numel()),
-                                  _stream(dev))
+                                  _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev), _stream(dev))
     nat.check(rc, "ria_kv_append")
 
 
@@ -315,10 +409,13 @@ def attn_decode(
     seq_slot: torch.Tensor | None = None,
     split_tokens: int = 0,
     phase: int = nat.RIA_ATTN_BOTH,
+    q_norm_weight: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Split-K paged GQA decode with RoPE on q and a sigmoid gate (ria_attn_decode_phase).
 
     phase selects the split-K launch, the combine launch or both (the default).
+    With the fp32 ``q_norm_weight`` [256], q is RMSNorm'd ((1 + w), cast back
+    to q's dtype) before RoPE (qwen36_attention_cache.py:302-304).
     """
     batch = int(q.shape[0])
     num_q_heads = int(q.shape[1])
@@ -348,7 +445,9 @@ def attn_decode(
     rc = nat.load().ria_attn_decode_phase(batch, num_q_heads, num_kv_heads, _ptr(q), dtype_code(q), qs, _ptr(gate),
                                           dtype_code(gate), gs, _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache),
                                           pages, _ptr(page_table), pts, _ptr(seq_slot), _ptr(pos_t), pos_s, _ptr(ctx_t), ctx_s, int(max_ctx),
-                                          _ptr(inv_freq), rope_dim, float(scale), int(split_tokens), _ptr(workspace),
+                                          _ptr(inv_freq), rope_dim,
+                                          _norm_weight("q_norm_weight", q_norm_weight, ATTN_HEAD_DIM, dev),
+                                          float(scale), int(split_tokens), _ptr(workspace),
                                           ws_bytes, _ptr(out), dtype_code(out), int(phase), _stream(dev))
     nat.check(rc, "ria_attn_decode")
     return out
@@ -401,11 +500,15 @@ def gdn_prefill(
     gate_mode: int = nat.RIA_GATE_PRECOMPUTED,
     A_log: torch.Tensor | None = None,
     dt_bias: torch.Tensor | None = None,
+    z: torch.Tensor | None = None,
+    norm_weight: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Chunked Gated DeltaNet prefill of one sequence (ria_gdn_prefill).
 
     mixed_qkv [L, conv_dim]; state [Hv, 128, 128] fp32 (updated in place);
     conv_ring [4, conv_dim] bf16 (updated); gate_a/b [L, Hv]; out [L, Hv, 128].
+    With ``z`` [L, Hv, 128] (or rows of >= Hv*128) and the fp32 ``norm_weight``
+    [128], out receives the gated RMSNorm of the read-out.
     """
     length = int(mixed_qkv.shape[0])
     dev = mixed_qkv.device
@@ -431,11 +534,24 @@ def gdn_prefill(
                 raise ValueError(f"{name} must be a contiguous fp32 tensor of {num_v_heads} values")
     if not workspace.is_contiguous():
         raise ValueError("workspace must be contiguous")
+    if (z is None) != (norm_weight is None):
+        raise ValueError("the gated norm needs both z and norm_weight")
+    z_stride = 0
+    if z is not None:
+        _require_gpu("z", z, dev)
+        if z.dim() == 3:
+            z_stride = _row_stride("z", z, length, num_v_heads * GDN_HEAD_DIM)
+        elif z.dim() == 2 and z.shape[0] == length and z.shape[1] >= num_v_heads * GDN_HEAD_DIM and z.stride(1) == 1:
+            z_stride = int(z.stride(0))
+        else:
+            raise ValueError(f"z must have {length} rows of >= {num_v_heads * GDN_HEAD_DIM} contiguous elements")
     raw = gate_mode == nat.RIA_GATE_RAW
     rc = nat.load().ria_gdn_prefill(length, num_k_heads, num_v_heads, _ptr(mixed_qkv), dtype_code(mixed_qkv), xs,
                                     _ptr(conv_weight), _ptr(conv_ring), int(conv_pos), _ptr(state), _ptr(gate_a),
                                     _ptr(gate_b), gs, int(gate_mode), _ptr(A_log) if raw else None,
-                                    _ptr(dt_bias) if raw else None, _ptr(out), dtype_code(out), _ptr(workspace),
+                                    _ptr(dt_bias) if raw else None, _ptr(out), dtype_code(out), _ptr(z),
+                                    dtype_code(z) if z is not None else 0, z_stride,
+                                    _norm_weight("norm_weight", norm_weight, GDN_HEAD_DIM, dev), _ptr(workspace),
                                     workspace.numel() * workspace.element_size(), _stream(dev))
     nat.check(rc, "ria_gdn_prefill")
     return out
@@ -458,10 +574,12 @@ def kv_append_seq(
     *,
     start: int,
     inv_freq: torch.Tensor | None,
+    k_norm_weight: torch.Tensor | None = None,
 ) -> None:
     """Append a prompt's k (RoPE at start + i) and v at slots start + i of one sequence (ria_kv_append_seq).
 
-    k, v [L, Hkv, 256]; page_table is the sequence's page-table row.
+    k, v [L, Hkv, 256]; page_table is the sequence's page-table row; with the
+    fp32 ``k_norm_weight`` [256] k is RMSNorm'd before RoPE.
     """
     length = int(k.shape[0])
     num_kv_heads = int(k_cache.shape[1])
@@ -477,7 +595,8 @@ def kv_append_seq(
     rope_dim = 0 if inv_freq is None else 2 * int(inv_freq.numel())
     rc = nat.load().ria_kv_append_seq(length, num_kv_heads, _ptr(k), dtype_code(k), ks, _ptr(v), dtype_code(v), vs,
                                       _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table),
-                                      cap, int(start), _ptr(inv_freq), rope_dim, _stream(dev))
+                                      cap, int(start), _ptr(inv_freq), rope_dim,
+                                      _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev), _stream(dev))
     nat.check(rc, "ria_kv_append_seq")
 
 
@@ -495,13 +614,16 @@ def attn_prefill(
     inv_freq: torch.Tensor | None,
     scale: float,
     phase: int = nat.RIA_PREFILL_BOTH,
+    q_norm_weight: torch.Tensor | None = None,
+    k_norm_weight: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Causal GQA prefill of one sequence's prompt over its paged cache (ria_attn_prefill_phase).
 
     q, gate [L, Hq, 256]; k, v [L, Hkv, 256], all of one dtype; the prompt's
     k/v are appended at slots start .. start + L - 1 first.  Returns out
     [L, Hq, 256] in that dtype.  phase selects the append launch, the
-    attention launch or both (the default).
+    attention launch or both (the default).  With the fp32 q_norm / k_norm
+    weights [256], q and k are RMSNorm'd before RoPE.
     """
     length = int(q.shape[0])
     num_q_heads = int(q.shape[1])
@@ -529,7 +651,9 @@ def attn_prefill(
     rc = nat.load().ria_attn_prefill_phase(length, num_q_heads, num_kv_heads, _ptr(q), qs, _ptr(k), ks, _ptr(v),
                                            vs, _ptr(gate), gs, dtype_code(q), _ptr(k_cache), _ptr(v_cache),
                                            dtype_code(k_cache), pages, _ptr(page_table), cap, int(start),
-                                           _ptr(inv_freq), rope_dim, float(scale), _ptr(out), int(phase),
-                                           _stream(dev))
+                                           _ptr(inv_freq), rope_dim,
+                                           _norm_weight("q_norm_weight", q_norm_weight, ATTN_HEAD_DIM, dev),
+                                           _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev),
+                                           float(scale), _ptr(out), int(phase), _stream(dev))
     nat.check(rc, "ria_attn_prefill")
     return out

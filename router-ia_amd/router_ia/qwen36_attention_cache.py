@@ -10,10 +10,14 @@ moved into the HIP library (include/ria_hybrid_attn.h):
   _rope / _apply_rope        :137-162        ria_rope_table / ria_rope_apply
   _l2norm                    :169-173        ria_l2norm
   _causal_conv1d_step        :176-221        ria_conv1d_step (4-slot conv ring)
-  _linear_stateful           :224-282        ria_gdn_decode (conv + gating +
-                                             l2norm + recurrence + read-out)
-  _full_stateful             :285-324        ria_kv_append (RoPE k) +
-                                             ria_attn_decode (RoPE q, gate)
+  _linear_stateful           :224-282        ria_rmsnorm (input norm) +
+                                             ria_gdn_decode (conv + gating +
+                                             l2norm + recurrence + read-out +
+                                             gated RMSNorm)
+  _full_stateful             :285-324        ria_rmsnorm (input norm) +
+                                             ria_kv_append (k_norm, RoPE k) +
+                                             ria_attn_decode (q_norm, RoPE q,
+                                             gate)
   _append_full_kv            :334-373        limits on the host, then
                                              ria_kv_append into 16-bit pages
   step_attention / stats     :376-404        same
@@ -33,9 +37,12 @@ Differences a caller can observe, all inside the stated tolerances:
     storage, because the reference's limit semantics are tested with CPU
     tensors and that path only stores.
 
-Projections, RMSNorms and weight loading are outside the accelerated path and
-use torch (``norms``, ``weights``), keeping the reference's dtype order
-(fp16 projections on the GPU).
+Projections and weight loading are outside the accelerated path and use
+torch (``weights``), keeping the reference's dtype order (fp16 projections on
+the GPU).  The norms run in the HIP library: the layer-input RMSNorm as its
+own launch, q_norm / k_norm and the DeltaNet gated RMSNorm fused into the
+attention launches.  ``rmsnorm`` / ``gated_rmsnorm`` remain module
+attributes (the torch forms, usable on any device) as in the reference.
 """
 
 from __future__ import annotations
@@ -354,14 +361,21 @@ def _linear_state(state: AttentionState, layer: int, device: torch.device) -> to
     return s
 
 
+def _input_norm(x0: torch.Tensor, weight: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    """rmsnorm(x0, input_layernorm) (:227, :291) cast to the layer's compute dtype, in one launch."""
+    x = x0.reshape(1, base.HIDDEN).contiguous()
+    out = torch.empty((1, base.HIDDEN), device=x.device, dtype=out_dtype)
+    return K.rmsnorm(x, weight.float().contiguous(), out=out)
+
+
 def _linear_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> torch.Tensor:
     state = active(root, device)
     prefix = base.layer_prefix(layer)
     if not is_cuda(device):
         raise RuntimeError("_linear_stateful: the attention arithmetic runs only on a ROCm GPU device")
     input_norm = base.load_layer_weight(root, layer, "input_layernorm.weight", device)
-    h = rmsnorm(x0, input_norm)
-    h_compute = h.to(dtype=torch.bfloat16)
+    # rmsnorm(x0) in fp32, then .to(bf16) (:227-229), in one launch
+    h_compute = _input_norm(x0, input_norm, torch.bfloat16)
 
     qkv_w = _projection(root, prefix + "linear_attn.in_proj_qkv", device)
     mixed = F.linear(h_compute.to(dtype=qkv_w.dtype), qkv_w).reshape(1, LINEAR_CONV_DIM)
@@ -375,33 +389,37 @@ def _linear_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> t
     a_raw = F.linear(h_compute.to(dtype=a_w.dtype), a_w).reshape(1, base.LINEAR_NUM_V_HEADS).float()
     b_raw = F.linear(h_compute.to(dtype=b_w.dtype), b_w).reshape(1, base.LINEAR_NUM_V_HEADS).float()
 
+    z_w = _projection(root, prefix + "linear_attn.in_proj_z", device)
+    z = F.linear(h_compute.to(dtype=z_w.dtype), z_w).reshape(1, base.LINEAR_NUM_V_HEADS, 128)
+    norm_w = base.load_layer_weight(root, layer, "linear_attn.norm.weight", device).float().contiguous()
+    out_w = _projection(root, prefix + "linear_attn.out_proj", device)
+
     dev = x0.device
     linear_state = _linear_state(state, layer, dev)
-    attn = torch.empty((1, base.LINEAR_NUM_V_HEADS, 128), device=dev, dtype=torch.float32)
+    # the read-out leaves the kernel through the gated RMSNorm (:268-271), cast
+    # to the out_proj dtype as the reference casts `gated` (:273-275)
+    gated = torch.empty((1, base.LINEAR_NUM_V_HEADS, 128), device=dev, dtype=out_w.dtype)
     conv_step = globals()["_causal_conv1d_step"]
     if conv_step is _ORIGINAL_CONV_STEP:
         if conv_w.dtype != torch.bfloat16:
             raise TypeError("_linear_stateful: the HIP conv computes in bf16 and needs a bf16 conv weight")
         ring = _conv_ring(state, layer, dev)
-        K.gdn_decode(mixed, linear_state, a_raw.contiguous(), b_raw.contiguous(), attn,
+        K.gdn_decode(mixed, linear_state, a_raw.contiguous(), b_raw.contiguous(), gated,
                      num_k_heads=base.LINEAR_NUM_K_HEADS, num_v_heads=base.LINEAR_NUM_V_HEADS, fuse_conv=True,
                      conv_weight=conv_w.contiguous(), conv_ring=ring, conv_pos=state.conv_steps[int(layer)],
-                     gate_mode=nat.RIA_GATE_RAW, A_log=a_log.contiguous(), dt_bias=dt_bias.contiguous())
+                     gate_mode=nat.RIA_GATE_RAW, A_log=a_log.contiguous(), dt_bias=dt_bias.contiguous(),
+                     z=z, norm_weight=norm_w)
         state.conv_steps[int(layer)] += 1
     else:
         # A replaced conv step (probes swap this module attribute): run it, then
         # the recurrence on its output.
         mixed = conv_step(state, layer, mixed, conv_w)
-        K.gdn_decode(mixed.contiguous(), linear_state, a_raw.contiguous(), b_raw.contiguous(), attn,
+        K.gdn_decode(mixed.contiguous(), linear_state, a_raw.contiguous(), b_raw.contiguous(), gated,
                      num_k_heads=base.LINEAR_NUM_K_HEADS, num_v_heads=base.LINEAR_NUM_V_HEADS, fuse_conv=False,
-                     gate_mode=nat.RIA_GATE_RAW, A_log=a_log.contiguous(), dt_bias=dt_bias.contiguous())
+                     gate_mode=nat.RIA_GATE_RAW, A_log=a_log.contiguous(), dt_bias=dt_bias.contiguous(),
+                     z=z, norm_weight=norm_w)
 
-    z_w = _projection(root, prefix + "linear_attn.in_proj_z", device)
-    z = F.linear(h_compute.to(dtype=z_w.dtype), z_w).reshape(1, base.LINEAR_NUM_V_HEADS, 128)
-    norm_w = base.load_layer_weight(root, layer, "linear_attn.norm.weight", device)
-    gated, _, _ = gated_rmsnorm(attn, z, norm_w)
-    out_w = _projection(root, prefix + "linear_attn.out_proj", device)
-    gated_compute = gated.reshape(1, base.LINEAR_VALUE_DIM).to(dtype=out_w.dtype)
+    gated_compute = gated.reshape(1, base.LINEAR_VALUE_DIM)
     attn_projected = F.linear(gated_compute, out_w).float()
     return x0.reshape(1, base.HIDDEN).float() + attn_projected
 
@@ -441,8 +459,9 @@ def _check_full_kv_limits(state: AttentionState, layer: int, append_bytes: int) 
 
 
 def _paged_append(state: AttentionState, layer: int, k_token: torch.Tensor, v_token: torch.Tensor,
-                  position: int | None, kv_dtype: torch.dtype) -> _LayerKV:
-    """Append [1, Hkv, 1, 256] k/v into the layer's pages (RoPE on k when position is given)."""
+                  position: int | None, kv_dtype: torch.dtype,
+                  k_norm_weight: torch.Tensor | None = None) -> _LayerKV:
+    """Append [1, Hkv, 1, 256] k/v into the layer's pages (k_norm, then RoPE on k, when position is given)."""
     store = _full_store(state, layer, k_token.device, kv_dtype)
     store.reserve(store.length + 1)
     k2 = k_token.reshape(1, base.FULL_NUM_KV_HEADS, K.ATTN_HEAD_DIM).contiguous()
@@ -452,7 +471,7 @@ def _paged_append(state: AttentionState, layer: int, k_token: torch.Tensor, v_to
     else:
         inv = _inv_freq(k_token.device)
     K.kv_append(k2, v2, store.k, store.v, store.page_table, positions=int(position or 0), slots=store.length,
-                inv_freq=inv)
+                inv_freq=inv, k_norm_weight=k_norm_weight)
     store.length += 1
     return store
 
@@ -466,9 +485,8 @@ def _full_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> tor
     # earlier entries stay resident.
     position = int(state.tokens_seen)
     input_norm = base.load_layer_weight(root, layer, "input_layernorm.weight", device)
-    h = rmsnorm(x0, input_norm)
     compute_dtype = torch.float16
-    h_compute = h.to(dtype=compute_dtype)
+    h_compute = _input_norm(x0, input_norm, compute_dtype)
     q_w = _projection(root, prefix + "self_attn.q_proj", device)
     k_w = _projection(root, prefix + "self_attn.k_proj", device)
     v_w = _projection(root, prefix + "self_attn.v_proj", device)
@@ -476,15 +494,17 @@ def _full_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> tor
     q, gate = torch.chunk(q_gate, 2, dim=-1)
     k = F.linear(h_compute.to(dtype=k_w.dtype), k_w).reshape(1, base.FULL_NUM_KV_HEADS, base.FULL_HEAD_DIM)
     v = F.linear(h_compute.to(dtype=v_w.dtype), v_w).reshape(1, base.FULL_NUM_KV_HEADS, base.FULL_HEAD_DIM)
-    q_norm_w = base.load_layer_weight(root, layer, "self_attn.q_norm.weight", device)
-    k_norm_w = base.load_layer_weight(root, layer, "self_attn.k_norm.weight", device)
-    q = rmsnorm(q, q_norm_w).float().contiguous()
-    k = rmsnorm(k, k_norm_w).float().contiguous()
+    # q_norm / k_norm (:302-305) run inside the append and attention launches:
+    # RMSNorm in fp32, cast back to the projection dtype, then RoPE
+    q_norm_w = base.load_layer_weight(root, layer, "self_attn.q_norm.weight", device).float().contiguous()
+    k_norm_w = base.load_layer_weight(root, layer, "self_attn.k_norm.weight", device).float().contiguous()
+    q = q.contiguous()
+    k = k.contiguous()
     v = v.float().contiguous()
 
     _check_full_kv_limits(state, layer, append_bytes=2 * base.FULL_NUM_KV_HEADS * base.FULL_HEAD_DIM * 2)
-    store = _paged_append(state, layer, k, v, position, torch.float16)
-    attn = _attend(store, q, gate.contiguous(), position)
+    store = _paged_append(state, layer, k, v, position, torch.float16, k_norm_weight=k_norm_w)
+    attn = _attend(store, q, gate.contiguous(), position, q_norm_weight=q_norm_w)
     if attn.shape != (1, base.FULL_NUM_HEADS, base.FULL_HEAD_DIM):
         raise RuntimeError(f"Unexpected full-attention output shape: {tuple(attn.shape)}")
     attn_flat = attn.reshape(1, base.FULL_Q_DIM).to(dtype=compute_dtype)
@@ -493,8 +513,9 @@ def _full_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> tor
     return x0.reshape(1, base.HIDDEN).float() + attn_projected
 
 
-def _attend(store: _LayerKV, q: torch.Tensor, gate: torch.Tensor, position: int) -> torch.Tensor:
-    """softmax(RoPE(q) K^T / 16) V * sigmoid(gate) over the store's resident tokens (fp32 out)."""
+def _attend(store: _LayerKV, q: torch.Tensor, gate: torch.Tensor, position: int,
+            q_norm_weight: torch.Tensor | None = None) -> torch.Tensor:
+    """softmax(RoPE(q_norm(q)) K^T / 16) V * sigmoid(gate) over the store's resident tokens (fp32 out)."""
     dev = q.device
     ctx = store.length
     pages_cap = int(store.page_table.shape[1]) * _PAGE
@@ -504,7 +525,7 @@ def _attend(store: _LayerKV, q: torch.Tensor, gate: torch.Tensor, position: int)
     out = torch.empty((1, base.FULL_NUM_HEADS, base.FULL_HEAD_DIM), dtype=torch.float32, device=dev)
     K.attn_decode(q, gate, store.k, store.v, store.page_table, out, positions=int(position), ctx_lens=ctx,
                   max_ctx=min(ctx, pages_cap), inv_freq=_inv_freq(dev), scale=base.FULL_HEAD_DIM ** -0.5,
-                  workspace=ws, split_tokens=split)
+                  workspace=ws, split_tokens=split, q_norm_weight=q_norm_weight)
     return out
 
 

@@ -71,3 +71,30 @@ def ragged_lengths(seed: int, batch: int, lo: int, hi: int) -> list[int]:
     g = torch.Generator()
     g.manual_seed(seed)
     return [int(x) for x in torch.randint(lo, hi + 1, (batch,), generator=g)]
+
+
+def norm_params(seed: int, device="cpu") -> dict[str, torch.Tensor]:
+    """Norm weights around the attention arithmetic, fp32 as the kernels take them.
+
+    q_norm / k_norm [256] and the layer input norm [2048] are (1 + w) RMSNorms
+    (zero-centred w ~ N(0, 0.1)); the DeltaNet gated norm [128] multiplies by
+    w directly (w ~ 1 + N(0, 0.1)).  Values are bf16-representable, like a
+    checkpoint's bf16 weights widened to fp32.
+    """
+    g = _gen(seed, device)
+
+    def bf(t):
+        return t.to(torch.bfloat16).float()
+
+    return {
+        "q_norm": bf(torch.randn((FULL_HEAD_DIM,), generator=g, device=device) * 0.1),
+        "k_norm": bf(torch.randn((FULL_HEAD_DIM,), generator=g, device=device) * 0.1),
+        "gated_norm": bf(1.0 + torch.randn((HEAD_DIM,), generator=g, device=device) * 0.1),
+        "input_norm": bf(torch.randn((2048,), generator=g, device=device) * 0.1),
+    }
+
+
+def gate_z_inputs(seed: int, steps: int, batch: int, device="cpu") -> torch.Tensor:
+    """Gated-norm gates z bf16 ~N(0,1) [steps, B, 32, 128] (the in_proj_z output)."""
+    g = _gen(seed, device)
+    return torch.randn((steps, batch, NUM_V_HEADS, HEAD_DIM), generator=g, device=device).to(torch.bfloat16)

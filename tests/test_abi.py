@@ -44,10 +44,10 @@ def test_abi_version_and_host_side_validation() -> None:
     lib = nat.load()
     assert lib.ria_abi_version() == nat.ABI_VERSION
     rc = lib.ria_gdn_decode(-1, 16, 32, None, 0, 0, 1, None, None, None, 0, None, None, None, None, 0, 0,
-                            None, None, None, 0, None)
+                            None, None, None, 0, None, 0, 0, None, None)
     assert rc == 1 and b"batch" in lib.ria_last_error()
     rc = lib.ria_attn_decode(1, 16, 2, None, 0, 4096, None, 0, 4096, None, None, 0, 1, None, 1, None, None, 0,
-                             None, 1, 1, None, 64, 0.0625, 0, None, 0, None, 0, None)
+                             None, 1, 1, None, 64, None, 0.0625, 0, None, 0, None, 0, None)
     assert rc == 1 and b"null" in lib.ria_last_error()
     assert lib.ria_attn_decode_workspace_bytes(0, 16, 2, 10, 0) == 0
     assert lib.ria_attn_decode_workspace_bytes(1, 16, 2, 64, 64) > 0
@@ -64,15 +64,41 @@ def test_prefill_attention_host_validation() -> None:
     lib = nat.load()
     # 16 query heads per KV head is beyond the kernel's group limit
     rc = lib.ria_attn_prefill(16, 32, 2, None, 8192, None, 512, None, 512, None, 8192, 0, None, None, 0, 4, None,
-                              4, 0, None, 64, 0.0625, None, None)
+                              4, 0, None, 64, None, None, 0.0625, None, None)
     assert rc == 1 and b"at most 8" in lib.ria_last_error()
     # the prompt must fit in the row's pages: 60 + 10 tokens > 4 pages of 16
     fake = ctypes.c_void_p(256)
     rc = lib.ria_attn_prefill(10, 16, 2, fake, 4096, fake, 512, fake, 512, fake, 4096, 0, fake, fake, 0, 4, fake,
-                              4, 60, fake, 64, 0.0625, fake, None)
+                              4, 60, fake, 64, None, None, 0.0625, fake, None)
     assert rc == 1 and b"exceed" in lib.ria_last_error()
-    rc = lib.ria_kv_append_seq(10, 2, fake, 0, 512, fake, 0, 512, fake, fake, 0, 4, fake, 4, 60, fake, 64, None)
+    rc = lib.ria_kv_append_seq(10, 2, fake, 0, 512, fake, 0, 512, fake, fake, 0, 4, fake, 4, 60, fake, 64, None,
+                               None)
     assert rc == 1 and b"exceed" in lib.ria_last_error()
     # zero-length prompts are a no-op
     assert lib.ria_attn_prefill(0, 16, 2, fake, 4096, fake, 512, fake, 512, fake, 4096, 0, fake, fake, 0, 4, fake,
-                                4, 0, fake, 64, 0.0625, fake, None) == 0
+                                4, 0, fake, 64, None, None, 0.0625, fake, None) == 0
+    # the prefill kernel reads the q_norm weight in 16-byte vectors
+    rc = lib.ria_attn_prefill(10, 16, 2, fake, 4096, fake, 512, fake, 512, fake, 4096, 0, fake, fake, 0, 4, fake,
+                              4, 0, fake, 64, ctypes.c_void_p(260), None, 0.0625, fake, None)
+    assert rc == 1 and b"q_norm_weight" in lib.ria_last_error()
+
+
+def test_norm_entry_points_host_validation() -> None:
+    lib = nat.load()
+    fake = ctypes.c_void_p(256)
+    # zero tokens: nothing to do, even with null pointers
+    assert lib.ria_rmsnorm(0, 16, 256, None, 0, 4096, None, 1e-6, None, 0, 4096, None) == 0
+    assert lib.ria_gated_rmsnorm(0, 32, 128, None, 2, 4096, None, 0, 4096, None, 1e-6, None, 0, 4096, None) == 0
+    rc = lib.ria_rmsnorm(1, 16, 256, fake, 7, 4096, fake, 1e-6, fake, 0, 4096, None)
+    assert rc == 1 and b"dtype" in lib.ria_last_error()
+    rc = lib.ria_rmsnorm(2, 16, 256, fake, 0, 2048, fake, 1e-6, fake, 0, 4096, None)
+    assert rc == 1 and b"stride" in lib.ria_last_error()
+    rc = lib.ria_gated_rmsnorm(1, 32, 128, fake, 2, 4096, None, 0, 4096, fake, 1e-6, fake, 0, 4096, None)
+    assert rc == 1 and b"null" in lib.ria_last_error()
+    # a gated DeltaNet read-out needs the norm weight with its gate
+    rc = lib.ria_gdn_decode(1, 16, 32, fake, 0, 8192, 0, None, None, None, 0, fake, None, fake, fake, 32, 0,
+                            None, None, fake, 0, fake, 0, 4096, None, None)
+    assert rc == 1 and b"norm_weight" in lib.ria_last_error()
+    rc = lib.ria_gdn_prefill(64, 16, 32, fake, 0, 8192, fake, fake, 0, fake, fake, fake, 32, 0, None, None, fake, 0,
+                             fake, 0, 4096, None, fake, 1 << 30, None)
+    assert rc == 1 and b"norm_weight" in lib.ria_last_error()

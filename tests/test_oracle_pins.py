@@ -92,6 +92,43 @@ def test_l2norm_matches_fp64_and_unit_norm():
     assert torch.equal(z, torch.zeros(1, 4))
 
 
+def test_rmsnorm_matches_fp64_and_invariants():
+    g = _gen(21)
+    x = torch.randn((3, 16, 256), generator=g) * 3
+    w = torch.randn(256, generator=g) * 0.1
+    y = O.rmsnorm(x, w)
+    np.testing.assert_allclose(y.numpy(), fp64.rmsnorm(x.numpy(), w.numpy()), rtol=2e-6, atol=2e-6)
+    # the affine factor is (1 + w): w = 0 leaves rows of unit RMS (not zeros)
+    u = O.rmsnorm(x, torch.zeros(256))
+    torch.testing.assert_close(u.pow(2).mean(-1), torch.ones(3, 16), rtol=1e-5, atol=1e-5)
+    # positive rescaling of a row cancels (eps aside)
+    torch.testing.assert_close(O.rmsnorm(x * 7.5, w), y, rtol=1e-5, atol=1e-5)
+    # the result is cast back to the input dtype after the fp32 math
+    xh = x.to(torch.float16)
+    yh = O.rmsnorm(xh, w.to(torch.bfloat16))
+    assert yh.dtype == torch.float16
+    ref = fp64.rmsnorm(xh.float().numpy(), w.to(torch.bfloat16).float().numpy())
+    # within one fp16 ulp of the fp64 value rounded to fp16 (double rounding)
+    torch.testing.assert_close(yh, torch.from_numpy(ref).to(torch.float16), rtol=1e-3, atol=0)
+
+
+def test_gated_rmsnorm_matches_fp64_and_invariants():
+    g = _gen(22)
+    x = torch.randn((2, 32, 128), generator=g) * 0.3
+    z = torch.randn((2, 32, 128), generator=g) * 2
+    w = torch.randn(128, generator=g).to(torch.bfloat16)
+    y = O.gated_rmsnorm(x, z, w)
+    assert y.dtype == torch.float32
+    np.testing.assert_allclose(y.numpy(), fp64.gated_rmsnorm(x.numpy(), z.numpy(), w.float().numpy()),
+                               rtol=3e-6, atol=2e-6)
+    # the weight multiplies as w (no 1 +): w = 0 gives zeros; the gate is SiLU(z) per element
+    assert torch.equal(O.gated_rmsnorm(x, z, torch.zeros(128)), torch.zeros_like(x))
+    assert torch.equal(O.gated_rmsnorm(x, torch.zeros_like(z), w), torch.zeros_like(x))
+    big = torch.full_like(z, 30.0)
+    n = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
+    torch.testing.assert_close(O.gated_rmsnorm(x, big, w), w.float() * n * 30.0, rtol=1e-5, atol=1e-5)
+
+
 # ----------------------------------------------------------------------------- conv
 def _conv_case(seed, channels=64):
     g = _gen(seed)

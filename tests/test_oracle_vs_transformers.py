@@ -78,3 +78,21 @@ def test_l2norm_and_repeat_kv_match_transformers():
     assert torch.equal(O.l2norm(x), hf.l2norm(x, dim=-1, eps=1e-6))
     kv = torch.randn((1, 2, 5, 256), generator=torch.Generator().manual_seed(7))
     assert torch.equal(kv.repeat_interleave(8, dim=1), hf.repeat_kv(kv, 8))
+
+
+def test_rmsnorms_match_transformers():
+    g = torch.Generator().manual_seed(8)
+    norm = hf.Qwen3_5MoeRMSNorm(256, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(256, generator=g) * 0.1)
+    for dt in (torch.float32, torch.float16, torch.bfloat16):
+        x = (torch.randn((1, 16, 256), generator=g) * 4).to(dt)
+        with torch.no_grad():
+            assert torch.equal(O.rmsnorm(x, norm.weight), norm(x))
+    gated = hf.Qwen3_5MoeRMSNormGated(128, eps=1e-6)
+    with torch.no_grad():
+        gated.weight.copy_(torch.randn(128, generator=g))
+    x = torch.randn((1, 32, 128), generator=g) * 0.2
+    z = torch.randn((1, 32, 128), generator=g)
+    with torch.no_grad():
+        assert torch.equal(O.gated_rmsnorm(x, z, gated.weight), gated(x, gate=z))

@@ -46,6 +46,7 @@ CONV_DIM = 8192
 # Algorithmic bytes (state + KV + activations), per (sequence, layer, token).
 GDN_BYTES_PER_SEQ = 2 * 2_097_152 + 49_152 + 16_384 + 16_384 + 256 + 8_192  # 4,284,672
 GDN_BYTES_PER_LAYER = 65_536  # conv weight, shared by the batch
+GDN_NORM_BYTES_PER_SEQ = NUM_V_HEADS * 128 * 2  # the gated norm's z gate, bf16: 8,192
 ATTN_KV_BYTES_PER_TOKEN = 2 * NUM_KV_HEADS * HEAD_DIM_ATTN * 2  # 2048 B of K+V per context token
 ATTN_APPEND_BYTES = 2_048
 ATTN_ACT_BYTES = 3 * NUM_Q_HEADS * HEAD_DIM_ATTN * 2  # q, gate, out in bf16: 24,576
@@ -66,8 +67,14 @@ WORKLOADS = {
     "prefill16k": dict(batch=1, lo=PREFILL_LEN, hi=PREFILL_LEN, seed=3, prefill=True,
                        desc="prefill of one 16384-token prompt through 1 Gated DeltaNet layer (chunk 64) and "
                             "1 GQA full-attention layer (causal, fills 16-token KV pages, shuffled page table)"),
+    "prefill16k-norms": dict(batch=1, lo=PREFILL_LEN, hi=PREFILL_LEN, seed=3, prefill=True, norms=True,
+                             desc="prefill16k with q_norm/k_norm fused into the append and attention launches and "
+                                  "the gated RMSNorm applied to the DeltaNet read-out"),
     "ragged128": dict(batch=128, lo=1024, hi=32768, seed=4,
                       desc="40-layer stack, B=128, context U[1024,32768] (seed 4), 16-token pages, shuffled page table"),
+    "ragged128-norms": dict(batch=128, lo=1024, hi=32768, seed=4, norms=True,
+                            desc="40-layer stack as ragged128, with q_norm/k_norm fused into the append and attention "
+                                 "launches and the gated RMSNorm fused into the DeltaNet read-out"),
     "batch32": dict(batch=32, lo=8192, hi=8192, seed=2,
                     desc="40-layer stack, B=32, context 8192 (seed 2), 16-token pages, shuffled page table"),
 }
@@ -81,12 +88,13 @@ def is_full(layer: int) -> bool:
     return layer % 4 == 3
 
 
-def step_bytes(ctx: list[int]) -> int:
+def step_bytes(ctx: list[int], norms: bool = False) -> int:
     """Algorithmic bytes of one decode step; ctx[b] = context incl. the new token."""
     n_lin = sum(1 for layer in range(LAYERS) if not is_full(layer))
     n_full = LAYERS - n_lin
     b = len(ctx)
-    lin = n_lin * (b * GDN_BYTES_PER_SEQ + GDN_BYTES_PER_LAYER)
+    per_seq = GDN_BYTES_PER_SEQ + (GDN_NORM_BYTES_PER_SEQ if norms else 0)
+    lin = n_lin * (b * per_seq + GDN_BYTES_PER_LAYER)
     full = n_full * sum(ATTN_KV_BYTES_PER_TOKEN * t + ATTN_APPEND_BYTES + ATTN_ACT_BYTES for t in ctx)
     return lin + full
 
@@ -146,6 +154,14 @@ def run_gpu(args, wl) -> dict:
                      dtype=torch.bfloat16)
     kv_in = torch.randn((total_new, n_full, 2, batch, NUM_KV_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev,
                         dtype=torch.bfloat16)
+    norms = bool(wl.get("norms"))
+    if norms:
+        # gated-norm gates z per (step, layer) and fp32 norm weights per layer
+        z_in = torch.randn((total_new, n_lin, batch, NUM_V_HEADS, 128), generator=gen, device=dev,
+                           dtype=torch.bfloat16)
+        gnw = [1.0 + 0.1 * torch.randn((128,), generator=gen, device=dev) for _ in range(n_lin)]
+        qnw = [0.1 * torch.randn((HEAD_DIM_ATTN,), generator=gen, device=dev) for _ in range(n_full)]
+        knw = [0.1 * torch.randn((HEAD_DIM_ATTN,), generator=gen, device=dev) for _ in range(n_full)]
     gdn_out = torch.empty((batch, NUM_V_HEADS, 128), device=dev, dtype=torch.bfloat16)
     attn_out = torch.empty((batch, NUM_Q_HEADS, HEAD_DIM_ATTN), device=dev, dtype=torch.bfloat16)
     torch.cuda.synchronize()
@@ -162,9 +178,9 @@ def run_gpu(args, wl) -> dict:
                 fi = layer // 4
                 kc, vc = st.kv.layer(fi)
                 K.kv_append(kv_in[s, fi, 0], kv_in[s, fi, 1], kc, vc, st.kv.page_table, positions=st.tokens_seen,
-                            slots=st.tokens_seen, inv_freq=st.inv_freq)
+                            slots=st.tokens_seen, inv_freq=st.inv_freq, k_norm_weight=knw[fi] if norms else None)
                 kw = dict(positions=st.tokens_seen, ctx_lens=st.ctx_lens, max_ctx=max_ctx, inv_freq=st.inv_freq,
-                          scale=st.scale, workspace=st.workspace)
+                          scale=st.scale, workspace=st.workspace, q_norm_weight=qnw[fi] if norms else None)
                 if timed:
                     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                     e0.record()
@@ -185,7 +201,8 @@ def run_gpu(args, wl) -> dict:
                 K.gdn_decode(mixed[s, li], st.linear_states[li], gate_ab[s, li, 0], gate_ab[s, li, 1], gdn_out,
                              num_k_heads=st.num_k_heads, num_v_heads=st.num_v_heads, conv_weight=conv_w[li],
                              conv_ring=st.conv_rings[li], conv_pos=st.tokens_seen, gate_mode=nat.RIA_GATE_RAW,
-                             A_log=a_log[li], dt_bias=dt_bias[li])
+                             A_log=a_log[li], dt_bias=dt_bias[li], z=z_in[s, li] if norms else None,
+                             norm_weight=gnw[li] if norms else None)
                 if timed:
                     e1.record()
                     gdn_events.append((e0, e1))
@@ -195,7 +212,7 @@ def run_gpu(args, wl) -> dict:
         one_step(s, False)
     torch.cuda.synchronize()
     ctx_at_start = [n + 1 for n in st._host_seen]
-    algo_bytes = sum(step_bytes([c + i for c in ctx_at_start]) for i in range(args.steps))
+    algo_bytes = sum(step_bytes([c + i for c in ctx_at_start], norms) for i in range(args.steps))
     log(f"[bench] warmup {args.warmup} steps done; timing {args.steps} steps")
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
@@ -216,7 +233,7 @@ def run_gpu(args, wl) -> dict:
     attn_avg_s = sum(attn_ms) / len(attn_ms) / 1e3
     attn_bytes_avg = sum(attn_bytes) / len(attn_bytes)
     gdn_avg_s = sum(gdn_ms) / len(gdn_ms) / 1e3
-    gdn_bytes = batch * GDN_BYTES_PER_SEQ + GDN_BYTES_PER_LAYER
+    gdn_bytes = batch * (GDN_BYTES_PER_SEQ + (GDN_NORM_BYTES_PER_SEQ if norms else 0)) + GDN_BYTES_PER_LAYER
     achieved = attn_bytes_avg / attn_avg_s / 1e9
     step_gbps = algo_bytes / elapsed_s / 1e9
     return {
@@ -346,16 +363,21 @@ def run_prefill_gpu(args, wl) -> dict:
     kv.ensure(0, L)
     inv_freq = rope_inv_freq(1e7, 64).to(dev)
     attn_out = torch.empty((L, NUM_Q_HEADS, HEAD_DIM_ATTN), device=dev, dtype=torch.bfloat16)
+    norms = bool(wl.get("norms"))
+    z = torch.randn((L, NUM_V_HEADS, 128), generator=gen, device=dev).to(torch.bfloat16) if norms else None
+    gnw = 1.0 + 0.1 * torch.randn((128,), generator=gen, device=dev) if norms else None
+    qnw = 0.1 * torch.randn((HEAD_DIM_ATTN,), generator=gen, device=dev) if norms else None
+    knw = 0.1 * torch.randn((HEAD_DIM_ATTN,), generator=gen, device=dev) if norms else None
     log(f"[bench] {wl['desc']}")
 
     def gdn():
         K.gdn_prefill(mixed, state, a_raw, b_raw, gdn_out, num_k_heads=16, num_v_heads=NUM_V_HEADS,
                       conv_weight=conv_w, conv_ring=ring, conv_pos=0, workspace=ws, gate_mode=nat.RIA_GATE_RAW,
-                      A_log=a_log, dt_bias=dt_bias)
+                      A_log=a_log, dt_bias=dt_bias, z=z, norm_weight=gnw)
 
     def attn(phase):
         K.attn_prefill(q, k, v, gate, kv.k[0], kv.v[0], kv.page_table[0], attn_out, start=0, inv_freq=inv_freq,
-                       scale=HEAD_DIM_ATTN ** -0.5, phase=phase)
+                       scale=HEAD_DIM_ATTN ** -0.5, phase=phase, q_norm_weight=qnw, k_norm_weight=knw)
 
     for _ in range(args.warmup):
         gdn()

@@ -107,7 +107,7 @@ const char* ria_last_error(void);
  *            qwen36_gated_norm_probe.py:19-36):
  *            out = norm_weight * o / sqrt(mean(o^2) + 1e-6) * SiLU(z) per head.
  * z          NULL, or the gate [batch, Hv, 128] of z_dtype with row stride
- *            z_row_stride; norm_weight [128] f32.
+ *            z_row_stride (even, z 4-byte aligned); norm_weight [128] f32.
  * conv_dim = 2 * num_k_heads * 128 + num_v_heads * 128.
  */
 int ria_gdn_decode(int batch, int num_k_heads, int num_v_heads,

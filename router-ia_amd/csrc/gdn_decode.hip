@@ -113,6 +113,8 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
   __shared__ float v_s[COLS];
   __shared__ float red_s[NW][2][COLS];
   __shared__ float scal_s[8];
+  __shared__ float zg_s[NORM ? COLS : 1];  // gated norm: SiLU input z and weight w per column
+  __shared__ float wg_s[NORM ? COLS : 1];
 
   // Conv / projection inputs first, so their latency overlaps the state loads.
   const bool qk_writer = FUSE && (h % group == 0) && cb == 0;
@@ -120,6 +122,15 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
   float qk_raw = conv_channel<XT, FUSE>(a, b, row, n, qk_c, qk_writer);
   float v_raw = 0.f;
   if (tid < COLS) v_raw = conv_channel<XT, FUSE>(a, b, row, n, 2 * kdim + h * kGdnHeadDim + col0 + tid, FUSE);
+  // The gated norm's z (as the raw 32-bit word holding it; every thread loads
+  // one, threads past COLS a repeat, so no branch makes the wait early) and w.
+  ActWord z_word{};
+  float w_raw = 0.f;
+  if constexpr (NORM) {
+    const int tc = tid % COLS;
+    z_word = load_act_word(a.z, (int64_t)b * a.z_stride + h * kGdnHeadDim + tc, a.z_dtype);
+    w_raw = a.norm_w[tc];
+  }
 
   float* S = a.state + ((int64_t)row * a.num_v_heads + h) * (kGdnHeadDim * kGdnHeadDim);
   f32x4 s[RPT];
@@ -127,6 +138,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
   for (int r = 0; r < RPT; ++r) {
     s[r] = ld_stream(reinterpret_cast<const f32x4*>(S + (rg + RG * r) * kGdnHeadDim + col0 + jl));
   }
+
 
   // Gating (every thread computes the same two scalars).
   const float ga = a.gate_a[(int64_t)b * a.gate_stride + h];
@@ -145,6 +157,12 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
   const float ss = wave_sum(mul_rn(qk_raw, qk_raw));
   if (lane == 0) scal_s[wave] = ss;
   if (tid < COLS) v_s[tid] = v_raw;
+  if constexpr (NORM) {
+    if (tid < COLS) {
+      zg_s[tid] = act_from_word(z_word, a.z_dtype);
+      wg_s[tid] = w_raw;
+    }
+  }
   __syncthreads();
   const float inv = 1.0f / sqrtf((tid < 128 ? scal_s[0] + scal_s[1] : scal_s[2] + scal_s[3]) + 1e-6f);
   float qk_n = mul_rn(qk_raw, inv);
@@ -223,12 +241,8 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) ss = add_rn(ss, mul_rn(oo[c], oo[c]));
       const float r = rms_scale(half_wave_sum(ss), kGdnHeadDim);
-      {
-        const int64_t zo = (int64_t)b * a.z_stride + h * kGdnHeadDim + jl;
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          oo[c] = gated_norm_elem<RIA_DT_F32>(oo[c], r, a.norm_w[jl + c], load_act_dt(a.z, zo + c, a.z_dtype));
-      }
+      for (int c = 0; c < 4; ++c) oo[c] = gated_norm_elem<RIA_DT_F32>(oo[c], r, wg_s[jl + c], zg_s[jl + c]);
     }
   }
   if (rg == 0) {
@@ -337,6 +351,8 @@ extern "C" int ria_gdn_decode(int batch, int num_k_heads, int num_v_heads, const
   if (gate_row_stride < num_v_heads) return set_error(RIA_ERR_INVALID, "ria_gdn_decode: gate_row_stride < Hv");
   if (z && (!norm_weight || !valid_dtype(z_dtype) || z_row_stride < (int64_t)num_v_heads * kGdnHeadDim))
     return set_error(RIA_ERR_INVALID, "ria_gdn_decode: a gate z needs norm_weight, a dtype code and row stride >= Hv*128");
+  if (z && (reinterpret_cast<uintptr_t>(z) % 4 || z_row_stride % 2))
+    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: z must be 4-byte aligned with an even row stride");
 
   GdnDecodeArgs a{};
   a.x = mixed_qkv;

@@ -75,6 +75,28 @@ __device__ __forceinline__ float load_act_dt(const void* p, int64_t i, int dt) {
   return load_act<RIA_DT_F32>(p, i);
 }
 
+// Element i of a tensor with a run-time dtype code, loaded without branches
+// (a branch around a load makes the compiler wait for it at the join): the
+// aligned 32-bit word holding the element is loaded, and act_from_word picks
+// the element out later, so that the wait for the load can come late too.
+// A 16-bit tensor must start on a 4-byte boundary with an even row stride.
+struct ActWord {
+  uint32_t w;
+  bool high;  // 16-bit element in the upper half
+};
+
+__device__ __forceinline__ ActWord load_act_word(const void* p, int64_t i, int dt) {
+  const int64_t byte = dt == RIA_DT_F32 ? i * 4 : i * 2;
+  return ActWord{*reinterpret_cast<const uint32_t*>(static_cast<const char*>(p) + (byte & ~int64_t(3))),
+                 (byte & 2) != 0};
+}
+
+__device__ __forceinline__ float act_from_word(ActWord a, int dt) {
+  const uint16_t h = static_cast<uint16_t>(a.high ? (a.w >> 16) : (a.w & 0xffffu));
+  const float narrow = dt == RIA_DT_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+  return dt == RIA_DT_F32 ? __uint_as_float(a.w) : narrow;
+}
+
 template <int DT>
 __device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
   if constexpr (DT == RIA_DT_BF16) {
@@ -137,6 +159,16 @@ __device__ __forceinline__ void load_act4(const void* p, int64_t i, float (&x)[4
   }
 }
 
+// load_act4 with the dtype code known only at run time.
+__device__ __forceinline__ void load_act4_dt(const void* p, int64_t i, int dt, float (&x)[4]) {
+  if (dt == RIA_DT_BF16)
+    load_act4<RIA_DT_BF16>(p, i, x);
+  else if (dt == RIA_DT_F16)
+    load_act4<RIA_DT_F16>(p, i, x);
+  else
+    load_act4<RIA_DT_F32>(p, i, x);
+}
+
 template <int DT>
 __device__ __forceinline__ void store_act4(void* p, int64_t i, const float (&x)[4]) {
   if constexpr (DT == RIA_DT_F32) {
@@ -165,8 +197,19 @@ __device__ __forceinline__ float through_dtype(float v) {
   }
 }
 
-__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+// A rounded product / sum that is never fused with a neighbouring add or
+// multiply into an FMA.  hipcc contracts by default (-ffp-contract=fast-
+// honor-pragmas) and HIP's __fmul_rn / __fadd_rn are plain `*` / `+`, so the
+// pragma is what keeps torch's separate roundings: it clears the contract
+// flag on these operations, which survives inlining.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
 
 // torch.sigmoid / F.softplus(beta=1, threshold=20) / F.silu on fp32.
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }

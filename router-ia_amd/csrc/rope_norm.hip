@@ -106,14 +106,89 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
   }
 }
 
-template <int XT, bool GATED>
-static void launch_norm_ot(const NormArgs& a, int out_dtype, dim3 grid, hipStream_t st) {
-  if (out_dtype == RIA_DT_BF16)
-    hipLaunchKernelGGL((rmsnorm_kernel<XT, RIA_DT_BF16, GATED>), grid, dim3(256), 0, st, a);
-  else if (out_dtype == RIA_DT_F16)
-    hipLaunchKernelGGL((rmsnorm_kernel<XT, RIA_DT_F16, GATED>), grid, dim3(256), 0, st, a);
+// Vector form for rows whose elements can move four at a time (dim, strides
+// and head offsets multiples of 4, bases aligned to 4 elements): a group of
+// RL lanes owns each row, every lane loads and stores 4 contiguous elements
+// per access, and the group reduces its sum of squares with xor shuffles.
+template <int XT, int OT, bool GATED, int RL>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
+  constexpr int kRowsPerWave = 64 / RL;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kRowsPerWave + lane / RL;
+  const int li = lane % RL;
+  const bool ok = r < a.rows;  // rows past the end still take part in the shuffles
+  const int64_t t = ok ? r / a.heads : 0;
+  const int64_t hoff = ok ? (r - t * a.heads) * a.dim : 0;
+  const int64_t xo = t * a.x_stride + hoff;
+  float ss = 0.f;
+  if (ok) {
+    for (int c = 4 * li; c < a.dim; c += 4 * RL) {
+      float v[4];
+      load_act4<XT>(a.x, xo + c, v);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ss = add_rn(ss, mul_rn(v[j], v[j]));
+    }
+  }
+#pragma unroll
+  for (int off = RL / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if (!ok) return;
+  const float rs = rms_scale(ss, a.dim, a.eps);
+  const int64_t oo = t * a.out_stride + hoff;
+  const int64_t zo = t * a.z_stride + hoff;
+  for (int c = 4 * li; c < a.dim; c += 4 * RL) {
+    float v[4], y[4];
+    load_act4<XT>(a.x, xo + c, v);
+    const f32x4 w = *reinterpret_cast<const f32x4*>(a.weight + c);
+    if constexpr (GATED) {
+      float z[4];
+      load_act4_dt(a.z, zo + c, a.z_dtype, z);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[j] = gated_norm_elem<XT>(v[j], rs, w[j], z[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[j] = rmsnorm_elem<XT>(v[j], rs, w[j]);
+    }
+    store_act4<OT>(a.out, oo + c, y);
+  }
+}
+
+template <int XT, int OT, bool GATED>
+static void launch_norm_rl(const NormArgs& a, bool vec, hipStream_t st) {
+  if (!vec) {  // one row per wavefront, four per workgroup
+    hipLaunchKernelGGL((rmsnorm_kernel<XT, OT, GATED>), dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, st, a);
+    return;
+  }
+  // lanes per row: one 4-element chunk per lane for dims up to 256
+  const int rl = a.dim >= 256 ? 64 : (a.dim >= 128 ? 32 : 16);
+  const int64_t rows_per_block = 4 * (64 / rl);
+  const dim3 grid((unsigned)((a.rows + rows_per_block - 1) / rows_per_block));
+  if (rl == 64)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<XT, OT, GATED, 64>), grid, dim3(256), 0, st, a);
+  else if (rl == 32)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<XT, OT, GATED, 32>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((rmsnorm_kernel<XT, RIA_DT_F32, GATED>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<XT, OT, GATED, 16>), grid, dim3(256), 0, st, a);
+}
+
+template <int XT, bool GATED>
+static void launch_norm_ot(const NormArgs& a, int out_dtype, bool vec, hipStream_t st) {
+  if (out_dtype == RIA_DT_BF16)
+    launch_norm_rl<XT, RIA_DT_BF16, GATED>(a, vec, st);
+  else if (out_dtype == RIA_DT_F16)
+    launch_norm_rl<XT, RIA_DT_F16, GATED>(a, vec, st);
+  else
+    launch_norm_rl<XT, RIA_DT_F32, GATED>(a, vec, st);
+}
+
+static int dt_bytes(int dt) { return dt == RIA_DT_F32 ? 4 : 2; }
+
+// Whether every row of this launch can move in aligned 4-element vectors.
+static bool norm_vectorizable(const NormArgs& a, int x_dtype, int out_dtype, bool gated) {
+  auto aligned = [](const void* p, int dt, int64_t stride) {
+    return reinterpret_cast<uintptr_t>(p) % (4 * dt_bytes(dt)) == 0 && stride % 4 == 0;
+  };
+  return a.dim % 4 == 0 && reinterpret_cast<uintptr_t>(a.weight) % 16 == 0 && aligned(a.x, x_dtype, a.x_stride) &&
+         aligned(a.out, out_dtype, a.out_stride) && (!gated || aligned(a.z, a.z_dtype, a.z_stride));
 }
 
 static bool norm_dtype_ok(int dt) { return dt == RIA_DT_BF16 || dt == RIA_DT_F16 || dt == RIA_DT_F32; }
@@ -132,8 +207,7 @@ static int launch_norm(const char* who, int64_t tokens, int heads, int dim, cons
   if (tokens == 0) return RIA_OK;
   if (!x || !weight || !out || (GATED && !z)) return set_error(RIA_ERR_INVALID, "%s: null pointer", who);
   const int64_t rows = tokens * heads;
-  const int64_t blocks = (rows + 3) / 4;
-  if (blocks > 0x7fffffff) return set_error(RIA_ERR_INVALID, "%s: too many rows", who);
+  if ((rows + 3) / 4 > 0x7fffffff) return set_error(RIA_ERR_INVALID, "%s: too many rows", who);
   NormArgs a{};
   a.x = x;
   a.x_stride = x_stride;
@@ -147,14 +221,14 @@ static int launch_norm(const char* who, int64_t tokens, int heads, int dim, cons
   a.rows = rows;
   a.heads = heads;
   a.dim = dim;
-  const dim3 grid(static_cast<unsigned>(blocks));
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec = norm_vectorizable(a, x_dtype, out_dtype, GATED);
   if (x_dtype == RIA_DT_BF16)
-    launch_norm_ot<RIA_DT_BF16, GATED>(a, out_dtype, grid, st);
+    launch_norm_ot<RIA_DT_BF16, GATED>(a, out_dtype, vec, st);
   else if (x_dtype == RIA_DT_F16)
-    launch_norm_ot<RIA_DT_F16, GATED>(a, out_dtype, grid, st);
+    launch_norm_ot<RIA_DT_F16, GATED>(a, out_dtype, vec, st);
   else
-    launch_norm_ot<RIA_DT_F32, GATED>(a, out_dtype, grid, st);
+    launch_norm_ot<RIA_DT_F32, GATED>(a, out_dtype, vec, st);
   return check_launch(who);
 }
 

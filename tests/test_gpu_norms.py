@@ -57,6 +57,14 @@ def test_rmsnorm_matches_oracle(gpu, dtype):
     out = torch.empty((7, 16, 256), dtype=torch.float32, device=gpu)
     K.rmsnorm(q.to(gpu), w["q_norm"].to(gpu), out=out)
     assert torch.equal(out.cpu(), got.cpu().float())
+    # rows one element off 4-element alignment take the scalar form
+    odd = wide.to(gpu)[:, 1:2049]
+    _ulp_close(K.rmsnorm(odd, w["input_norm"].to(gpu)), O.rmsnorm(wide[:, 1:2049], w["input_norm"]), dtype,
+               "unaligned rows")
+    # 96-element rows: 16 lanes per row, some lanes take two 4-element chunks
+    x96 = (torch.randn((9, 3, 96), generator=g) * 2).to(dtype)
+    w96 = torch.randn(96, generator=g).to(torch.bfloat16).float() * 0.1
+    _ulp_close(K.rmsnorm(x96.to(gpu), w96.to(gpu)), O.rmsnorm(x96, w96), dtype, "96-element rows")
 
 
 @pytest.mark.parametrize("z_dtype", [torch.bfloat16, torch.float16, torch.float32])

@@ -75,6 +75,10 @@ WORKLOADS = {
     "ragged128-norms": dict(batch=128, lo=1024, hi=32768, seed=4, norms=True,
                             desc="40-layer stack as ragged128, with q_norm/k_norm fused into the append and attention "
                                  "launches and the gated RMSNorm fused into the DeltaNet read-out"),
+    "snapshot128": dict(batch=128, lo=1024, hi=32768, seed=4, snapshot=True,
+                        desc="save + restore of every sequence of the ragged128 stack (40 layers, B=128, "
+                             "context U[1024,32768]): DeltaNet states, conv rings and KV pages to one payload "
+                             "per sequence and back"),
     "batch32": dict(batch=32, lo=8192, hi=8192, seed=2,
                     desc="40-layer stack, B=32, context 8192 (seed 2), 16-token pages, shuffled page table"),
 }
@@ -332,6 +336,96 @@ def run_cpu_baseline(wl, lengths: list[int], n_seqs: int, n_steps: int) -> dict:
     }
 
 
+def run_snapshot_gpu(args, wl) -> dict:
+    """Save every row of the ragged stack into a payload and restore it, `steps` times."""
+    from router_ia import kernels as K
+    from router_ia import workloads as W
+    from router_ia.batched_state import BatchedAttentionState
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    batch = wl["batch"]
+    lengths = W.ragged_lengths(wl["seed"], batch, wl["lo"], wl["hi"])
+    num_pages = sum((n + 16) // 16 for n in lengths) + batch
+    st = BatchedAttentionState(batch, max(lengths) + 16, num_pages=num_pages, device=dev,
+                               page_shuffle_seed=wl["seed"])
+    st.set_positions(lengths)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(wl["seed"])
+    st.linear_states.normal_(0.0, 0.02, generator=gen)
+    st.conv_rings.normal_(0.0, 1.0, generator=gen)
+    st.kv.k.normal_(0.0, 1.0, generator=gen)
+    st.kv.v.normal_(0.0, 1.0, generator=gen)
+    sizes = [K.seq_state_bytes(st.num_linear_layers, st.num_v_heads, st.conv_dim, st.num_full_layers,
+                               st.num_kv_heads, n) for n in lengths]
+    payload = torch.empty(max(sizes), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    log(f"[bench] {wl['desc']}: payload {sum(sizes) / 2**30:.1f} GiB over {batch} sequences")
+    pools = (st.linear_states, st.conv_rings, st.kv.k, st.kv.v, st.kv.page_table)
+
+    def one_pass(ev):
+        for r, n in enumerate(lengths):
+            e0 = torch.cuda.Event(enable_timing=True) if ev is not None else None
+            if e0 is not None:
+                e0.record()
+            K.seq_state_save(*pools, row=r, tokens=n, payload=payload)
+            K.seq_state_restore(*pools, row=r, tokens=n, payload=payload)
+            if e0 is not None:
+                e1 = torch.cuda.Event(enable_timing=True)
+                e1.record()
+                ev.append((e0, e1, 4 * sizes[r]))
+
+    for _ in range(args.warmup):
+        one_pass(None)
+    torch.cuda.synchronize()
+    ev: list = []
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        one_pass(ev)
+    t1.record()
+    torch.cuda.synchronize()
+    elapsed = t0.elapsed_time(t1) / 1e3
+    moved = 4 * sum(sizes) * args.steps  # save reads + writes the payload's bytes, restore the same again
+    per_row_s = sum(a.elapsed_time(b) for a, b, _ in ev) / 1e3
+    achieved = sum(nb for _, _, nb in ev) / per_row_s / 1e9
+    return {
+        "batch": batch, "lengths": lengths, "elapsed_s": elapsed,
+        "seq_per_s": batch * args.steps / elapsed,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "payload_bytes": sum(sizes),
+        "roofline": {"bound": "hbm", "kernel": "ria_seq_state_save + ria_seq_state_restore (dense + tile copies)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_pass": moved // args.steps},
+        "step_GBps": round(moved / elapsed / 1e9, 1),
+    }
+
+
+def snapshot_main(args, wl) -> int:
+    gpu = run_snapshot_gpu(args, wl)
+    result = {
+        "metric": "sequence snapshot save+restore GB/s (40 layers, B=128 ragged 1k-32k); % of HBM peak",
+        "value": gpu["step_GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bytes (fp32 state, bf16 conv ring and KV)",
+        "data": "synthetic (seeded random state and KV)",
+        "config": {"workload": wl["desc"], "batch": gpu["batch"], "payload_GiB": round(gpu["payload_bytes"] / 2**30, 2),
+                   "sequences_per_s": round(gpu["seq_per_s"], 1), "parallelism": "single GPU"},
+        "roofline": gpu["roofline"],
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def run_prefill_gpu(args, wl) -> dict:
     """One 16384-token prompt through one DeltaNet layer and one attention layer, `steps` times."""
     from router_ia import _native as nat
@@ -509,6 +603,8 @@ def main() -> int:
     wl = WORKLOADS[args.workload]
     if wl.get("prefill"):
         return prefill_main(args, wl)
+    if wl.get("snapshot"):
+        return snapshot_main(args, wl)
     gpu = run_gpu(args, wl)
     prof = profiled_traffic("attn_splitk_kernel") if args.workload == "ragged128" else None
     if prof:

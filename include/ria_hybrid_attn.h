@@ -386,6 +386,43 @@ int ria_kv_gather(int batch, int num_kv_heads,
                   const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
                   int32_t start, int32_t count, void* k_out, void* v_out, void* stream);
 
+/*
+ * Sequence snapshots: one row's DeltaNet states, conv ring and KV pages as a
+ * contiguous device payload, to be restored into any row (of this pool or
+ * another with the same shapes) that has pages for `tokens` tokens; decoding
+ * then continues exactly as in the original row.  The reference keeps this
+ * state in AttentionState's per-layer tensors (qwen36_attention_cache.py:27-92)
+ * and cannot save or reload it.
+ *
+ * Payload sections, each starting on a 256-byte boundary:
+ *   DeltaNet states f32  [L_lin, Hv, 128, 128]
+ *   conv rings      bf16 [L_lin, 4, conv_dim]           (token t in slot t mod 4)
+ *   K tiles         kv   [L_full, pages, Hkv, K tile]   (the cache's tile order)
+ *   V tiles         kv   [L_full, pages, Hkv, V tile]
+ * with pages = ceil(tokens / 16) in logical page order; token slots past
+ * `tokens` are saved as zeros.  Pools are the batched layouts: states
+ * [L_lin, pool_rows, Hv, 128, 128], conv rings [L_lin, pool_rows, 4, conv_dim],
+ * K/V caches [L_full, num_pages, Hkv, tile] with page_table [pool_rows,
+ * page_table_stride].  The position (tokens) travels with the payload on the
+ * host side.  Pools and payload 16-byte aligned.
+ */
+int64_t ria_seq_state_bytes(int num_linear_layers, int num_v_heads, int conv_dim, int num_full_layers,
+                            int num_kv_heads, int tokens);
+
+int ria_seq_state_save(int row, int pool_rows, int num_linear_layers, int num_v_heads,
+                       const float* linear_states, const void* conv_rings, int conv_dim,
+                       int num_full_layers, int num_kv_heads, int num_pages,
+                       const void* k_cache, const void* v_cache,
+                       const int32_t* page_table, int64_t page_table_stride, int tokens,
+                       void* payload, int64_t payload_bytes, void* stream);
+
+int ria_seq_state_restore(int row, int pool_rows, int num_linear_layers, int num_v_heads,
+                          float* linear_states, void* conv_rings, int conv_dim,
+                          int num_full_layers, int num_kv_heads, int num_pages,
+                          void* k_cache, void* v_cache,
+                          const int32_t* page_table, int64_t page_table_stride, int tokens,
+                          const void* payload, int64_t payload_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

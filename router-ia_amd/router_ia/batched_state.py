@@ -18,6 +18,10 @@ A prompt enters one row at a time through ``begin_prefill`` /
 ``linear_prefill`` / ``full_prefill`` / ``end_prefill`` (chunked DeltaNet and
 causal attention prefill), equal to decoding it token by token.
 
+``save_row`` / ``restore_row`` move one row's whole state (DeltaNet states,
+conv ring, KV pages) to and from a ``SequenceSnapshot``, e.g. to preempt a
+sequence and resume it later in any row.
+
 The norms on either side of the attention arithmetic run inside the same
 launches when their fp32 weights are passed: the gated RMSNorm of the
 DeltaNet read-out (``z``, ``norm_weight``; :268-271) and the q_norm / k_norm
@@ -31,6 +35,7 @@ import torch
 from . import _native as nat
 from . import kernels as K
 from .paged_kv import PagedKVCache
+from .snapshot import SequenceSnapshot
 
 
 def rope_inv_freq(theta: float, rope_dim: int) -> torch.Tensor:
@@ -267,6 +272,40 @@ class BatchedAttentionState:
         self._host_seen[row] += length
         self.tokens_seen[row] += length
         self.ctx_lens[row] += length
+        self._min_headroom = min(self.kv.alloc.capacity_tokens(r) - self._host_seen[r] for r in range(self.max_seqs))
+
+    # ---------------------------------------------------------------- snapshots
+    def save_row(self, row: int, out: torch.Tensor | None = None) -> SequenceSnapshot:
+        """Copy row `row`'s DeltaNet states, conv rings and KV pages into a snapshot (ria_seq_state_save)."""
+        tokens = self._host_seen[row]
+        n = SequenceSnapshot.nbytes(self.num_linear_layers, self.num_v_heads, self.conv_dim, self.num_full_layers,
+                                    self.num_kv_heads, tokens)
+        if out is None:
+            out = torch.empty(n, dtype=torch.uint8, device=self.device)
+        elif out.numel() < n:
+            raise ValueError(f"snapshot buffer holds {out.numel()} bytes, {n} needed")
+        K.seq_state_save(self.linear_states, self.conv_rings, self.kv.k, self.kv.v, self.kv.page_table, row=row,
+                         tokens=tokens, payload=out)
+        return SequenceSnapshot(out[:n], tokens, self.num_linear_layers, self.num_full_layers, self.num_v_heads,
+                                self.num_kv_heads, self.conv_dim, self.kv.dtype)
+
+    def restore_row(self, row: int, snap: SequenceSnapshot) -> None:
+        """Make row `row` continue the snapshot's sequence: new pages, then ria_seq_state_restore."""
+        shape = (snap.num_linear_layers, snap.num_full_layers, snap.num_v_heads, snap.num_kv_heads, snap.conv_dim,
+                 snap.kv_dtype)
+        mine = (self.num_linear_layers, self.num_full_layers, self.num_v_heads, self.num_kv_heads, self.conv_dim,
+                self.kv.dtype)
+        if shape != mine:
+            raise ValueError(f"snapshot shapes {shape} do not match this state's {mine}")
+        if snap.tokens + 1 > self.max_context:
+            raise RuntimeError(f"snapshot of {snap.tokens} tokens exceeds max_context={self.max_context}")
+        self.kv.release(row)
+        self.kv.ensure(row, snap.tokens + 1)
+        K.seq_state_restore(self.linear_states, self.conv_rings, self.kv.k, self.kv.v, self.kv.page_table, row=row,
+                            tokens=snap.tokens, payload=snap.payload)
+        self._host_seen[row] = snap.tokens
+        self.tokens_seen[row] = snap.tokens
+        self.ctx_lens[row] = snap.tokens + 1
         self._min_headroom = min(self.kv.alloc.capacity_tokens(r) - self._host_seen[r] for r in range(self.max_seqs))
 
     # ---------------------------------------------------------------- inspection

@@ -480,6 +480,57 @@ def kv_gather(
     return k_out, v_out
 
 
+def seq_state_bytes(num_linear_layers: int, num_v_heads: int, conv_dim: int, num_full_layers: int,
+                    num_kv_heads: int, tokens: int) -> int:
+    """Payload bytes of one sequence's snapshot (ria_seq_state_bytes)."""
+    return int(nat.load().ria_seq_state_bytes(num_linear_layers, num_v_heads, conv_dim, num_full_layers,
+                                               num_kv_heads, tokens))
+
+
+def _seq_state_args(states, rings, k_all, v_all, page_table, payload):
+    for name, t in (("linear_states", states), ("conv_rings", rings), ("k_cache", k_all), ("v_cache", v_all),
+                    ("page_table", page_table), ("payload", payload)):
+        _require_gpu(name, t, payload.device)
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if states.dtype != torch.float32 or states.dim() != 5 or tuple(states.shape[3:]) != (GDN_HEAD_DIM, GDN_HEAD_DIM):
+        raise ValueError("linear_states must be fp32 [L_lin, rows, Hv, 128, 128]")
+    if rings.dtype != torch.bfloat16 or rings.dim() != 4 or tuple(rings.shape[:2]) != tuple(states.shape[:2]) \
+            or rings.shape[2] != CONV_RING:
+        raise ValueError("conv_rings must be bf16 [L_lin, rows, 4, conv_dim] matching linear_states")
+    if k_all.dim() != 7 or v_all.dim() != 5 or k_all.shape[:3] != v_all.shape[:3] or k_all.dtype != v_all.dtype \
+            or k_all.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("k/v caches must be 16-bit [L_full, pages, Hkv, tile] of one dtype")
+    if page_table.dtype != torch.int32 or page_table.dim() != 2:
+        raise ValueError("page_table must be int32 [rows, pages per row]")
+    if payload.dtype != torch.uint8 or payload.dim() != 1:
+        raise ValueError("payload must be a 1-D uint8 tensor")
+    return (int(states.shape[1]), int(states.shape[0]), int(states.shape[2]), int(rings.shape[3]),
+            int(k_all.shape[0]), int(k_all.shape[2]), int(k_all.shape[1]))
+
+
+def seq_state_save(states: torch.Tensor, rings: torch.Tensor, k_all: torch.Tensor, v_all: torch.Tensor,
+                   page_table: torch.Tensor, *, row: int, tokens: int, payload: torch.Tensor) -> torch.Tensor:
+    """Copy row `row` (tokens seen `tokens`) of the pools into `payload` (ria_seq_state_save)."""
+    rows, n_lin, hv, cdim, n_full, hkv, pages = _seq_state_args(states, rings, k_all, v_all, page_table, payload)
+    rc = nat.load().ria_seq_state_save(int(row), rows, n_lin, hv, _ptr(states), _ptr(rings), cdim, n_full, hkv, pages,
+                                       _ptr(k_all), _ptr(v_all), _ptr(page_table), int(page_table.shape[1]),
+                                       int(tokens), _ptr(payload), payload.numel(), _stream(payload.device))
+    nat.check(rc, "ria_seq_state_save")
+    return payload
+
+
+def seq_state_restore(states: torch.Tensor, rings: torch.Tensor, k_all: torch.Tensor, v_all: torch.Tensor,
+                      page_table: torch.Tensor, *, row: int, tokens: int, payload: torch.Tensor) -> None:
+    """Copy a snapshot payload into row `row` of the pools, whose pages must be allocated (ria_seq_state_restore)."""
+    rows, n_lin, hv, cdim, n_full, hkv, pages = _seq_state_args(states, rings, k_all, v_all, page_table, payload)
+    rc = nat.load().ria_seq_state_restore(int(row), rows, n_lin, hv, _ptr(states), _ptr(rings), cdim, n_full, hkv,
+                                          pages, _ptr(k_all), _ptr(v_all), _ptr(page_table),
+                                          int(page_table.shape[1]), int(tokens), _ptr(payload), payload.numel(),
+                                          _stream(payload.device))
+    nat.check(rc, "ria_seq_state_restore")
+
+
 def gdn_prefill_workspace_bytes(num_k_heads: int, num_v_heads: int, segment_tokens: int) -> int:
     return int(nat.load().ria_gdn_prefill_workspace_bytes(num_k_heads, num_v_heads, segment_tokens))
 

@@ -387,6 +387,32 @@ int ria_kv_gather(int batch, int num_kv_heads,
                   int32_t start, int32_t count, void* k_out, void* v_out, void* stream);
 
 /*
+ * Projections with FP8 block-scaled weights.  The reference's checkpoint
+ * weights are float8_e4m3fn [N, K] with one fp32 `weight_scale_inv` per
+ * 128x128 block ([ceil(N/128), ceil(K/128)]); it dequantises them once to
+ * fp16(w * s) (qwen36_dequant.py:35-58, qwen36_cached_loop.py:537-542) and
+ * runs fp16 F.linear (qwen36_attention_cache.py:232-247, 268-276, 295-301,
+ * 318-320).
+ *
+ * ria_dequant_fp8: out[r][c] = float(w[r][c]) * s[r/128][c/128], rounded once
+ * to out_dtype (RIA_DT_F16 gives the reference's fp16 weight).  cols a
+ * multiple of 16; weight and out 16-byte aligned.
+ *
+ * ria_linear_fp8: y = fp16(x) W^T with W = fp16(w * s) dequantised in
+ * registers (the weight stays FP8 in memory), fp32 accumulation, the result
+ * rounded to fp16 (F.linear's fp16 output) and stored as y_dtype.  x [m, k]
+ * of x_dtype (converted to fp16 like `.to(float16)`), y [m, n].  n a multiple
+ * of 16, k of 128; x and weight 16-byte aligned, x row stride a multiple of 8.
+ * Built for decode-sized m (one weight pass per 128 rows of x).
+ */
+int ria_dequant_fp8(int64_t rows, int cols, const void* weight, const float* scale_inv,
+                    void* out, int out_dtype, void* stream);
+
+int ria_linear_fp8(int m, int n, int k, const void* x, int x_dtype, int64_t x_row_stride,
+                   const void* weight, const float* scale_inv,
+                   void* y, int y_dtype, int64_t y_row_stride, void* stream);
+
+/*
  * Sequence snapshots: one row's DeltaNet states, conv ring and KV pages as a
  * contiguous device payload, to be restored into any row (of this pool or
  * another with the same shapes) that has pages for `tokens` tokens; decoding

@@ -117,3 +117,24 @@ def gated_rmsnorm(x: np.ndarray, z: np.ndarray, w: np.ndarray, eps: float = 1e-6
             zd = zf[r, d]
             out[r, d] = float(w[d]) * flat[r, d] * scale * zd / (1.0 + math.exp(-zd))
     return out.reshape(x.shape)
+
+
+def e4m3fn_value(byte: int) -> float:
+    """OCP float8 e4m3fn: sign, 4 exponent bits (bias 7), 3 mantissa bits; subnormals; NaN at S.1111.111; no inf."""
+    sign = -1.0 if byte & 0x80 else 1.0
+    e, m = (byte >> 3) & 0xF, byte & 0x7
+    if e == 0xF and m == 0x7:
+        return math.nan
+    if e == 0:
+        return sign * (m / 8.0) * 2.0 ** -6
+    return sign * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+
+
+def dequant_fp8(w_bytes: np.ndarray, scale: np.ndarray, block: int = 128) -> np.ndarray:
+    """w[r][c] * scale[r // block][c // block], element by element in float64."""
+    rows, cols = w_bytes.shape
+    out = np.empty((rows, cols), dtype=np.float64)
+    for r in range(rows):
+        for c in range(cols):
+            out[r, c] = e4m3fn_value(int(w_bytes[r, c])) * float(scale[r // block, c // block])
+    return out

@@ -310,3 +310,30 @@ def full_layer_step(w: dict[str, torch.Tensor], st: SequenceState, layer: int, x
     o_w = proj(w["self_attn.o_proj.weight"])
     a_c = attn.reshape(1, -1).to(o_w.dtype if gpu_dtypes else torch.float32)
     return x0.reshape(1, -1).float() + F.linear(a_c, o_w).float()
+
+
+# ----------------------------------------------------------------------------- FP8 projections
+FP8_BLOCK = 128  # qwen36_dequant.py:13
+
+
+def dequantize_fp8_blockwise(weight: torch.Tensor, scale_inv: torch.Tensor) -> torch.Tensor:
+    """v2/src/router_ia/qwen36_dequant.py:35-58: fp32 weight times its 128x128 block's scale.
+
+    (The reference reshapes when both dims divide by 128 and expands the
+    scale grid otherwise; both give weight.float() * scale elementwise.)
+    """
+    out_f, in_f = weight.shape
+    expanded = scale_inv.float().repeat_interleave(FP8_BLOCK, dim=0).repeat_interleave(FP8_BLOCK, dim=1)
+    return weight.float() * expanded[:out_f, :in_f]
+
+
+def projection_fp8(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor) -> torch.Tensor:
+    """A projection as the reference's GPU path computes it.
+
+    The FP8 weight is dequantised once and cast to fp16
+    (qwen36_cached_loop.py:537-542); F.linear then multiplies the fp16
+    activation by it (qwen36_attention_cache.py:232-247) with fp32
+    accumulation, returning fp16.
+    """
+    w16 = dequantize_fp8_blockwise(weight, scale_inv).to(torch.float16)
+    return F.linear(x.to(torch.float16).float(), w16.float()).to(torch.float16)

@@ -480,6 +480,57 @@ def kv_gather(
     return k_out, v_out
 
 
+FP8_BLOCK = 128
+
+
+def _fp8_weight(name: str, w: torch.Tensor, scale_inv: torch.Tensor, dev: torch.device) -> tuple[int, int]:
+    _require_gpu(name, w, dev)
+    _require_gpu(name + " scale_inv", scale_inv, dev)
+    if w.dtype not in (torch.float8_e4m3fn, torch.uint8) or w.dim() != 2 or not w.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float8_e4m3fn (or its uint8 bytes) [N, K] tensor")
+    n, k = int(w.shape[0]), int(w.shape[1])
+    grid = ((n + FP8_BLOCK - 1) // FP8_BLOCK, (k + FP8_BLOCK - 1) // FP8_BLOCK)
+    if scale_inv.dtype != torch.float32 or tuple(scale_inv.shape) != grid or not scale_inv.is_contiguous():
+        raise ValueError(f"{name} scale_inv must be contiguous fp32 {grid}, got {tuple(scale_inv.shape)}")
+    return n, k
+
+
+def dequant_fp8(weight: torch.Tensor, scale_inv: torch.Tensor, out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """float(w) * s per 128x128 block, rounded once to out_dtype (ria_dequant_fp8)."""
+    dev = weight.device
+    n, k = _fp8_weight("weight", weight, scale_inv, dev)
+    out = torch.empty((n, k), dtype=out_dtype, device=dev)
+    rc = nat.load().ria_dequant_fp8(n, k, _ptr(weight), _ptr(scale_inv), _ptr(out), dtype_code(out), _stream(dev))
+    nat.check(rc, "ria_dequant_fp8")
+    return out
+
+
+def linear_fp8(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor, *, out: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """fp16(x) @ fp16(w * s)^T with fp32 accumulation, rounded to fp16 (ria_linear_fp8).
+
+    x [M, K] (rows may be strided); weight [N, K] float8_e4m3fn; scale_inv the
+    fp32 per-128x128-block scales; returns / fills y [M, N].
+    """
+    dev = x.device
+    _require_gpu("x", x, dev)
+    n, k = _fp8_weight("weight", weight, scale_inv, dev)
+    if x.dim() != 2 or x.shape[1] != k or (x.shape[1] > 1 and x.stride(1) != 1):
+        raise ValueError(f"x must be [M, {k}] with contiguous rows, got {tuple(x.shape)}")
+    m = int(x.shape[0])
+    xs = int(x.stride(0)) if m > 1 else k
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    _require_gpu("out", out, dev)
+    if out.dim() != 2 or tuple(out.shape) != (m, n) or (n > 1 and out.stride(1) != 1):
+        raise ValueError(f"out must be [{m}, {n}] with contiguous rows")
+    ys = int(out.stride(0)) if m > 1 else n
+    rc = nat.load().ria_linear_fp8(m, n, k, _ptr(x), dtype_code(x), xs, _ptr(weight), _ptr(scale_inv), _ptr(out),
+                                   dtype_code(out), ys, _stream(dev))
+    nat.check(rc, "ria_linear_fp8")
+    return out
+
+
 def seq_state_bytes(num_linear_layers: int, num_v_heads: int, conv_dim: int, num_full_layers: int,
                     num_kv_heads: int, tokens: int) -> int:
     """Payload bytes of one sequence's snapshot (ria_seq_state_bytes)."""

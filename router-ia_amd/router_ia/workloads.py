@@ -98,3 +98,24 @@ def gate_z_inputs(seed: int, steps: int, batch: int, device="cpu") -> torch.Tens
     """Gated-norm gates z bf16 ~N(0,1) [steps, B, 32, 128] (the in_proj_z output)."""
     g = _gen(seed, device)
     return torch.randn((steps, batch, NUM_V_HEADS, HEAD_DIM), generator=g, device=device).to(torch.bfloat16)
+
+
+FP8_MAX = 448.0  # largest finite float8_e4m3fn
+
+
+def fp8_block_weight(seed: int, n: int, k: int, std: float = 0.02,
+                     device="cpu") -> tuple[torch.Tensor, torch.Tensor]:
+    """A synthetic block-FP8 projection weight: float8_e4m3fn [n, k] and fp32 scale_inv [ceil(n/128), ceil(k/128)].
+
+    Quantised the way block-FP8 checkpoints are: per 128x128 block,
+    scale_inv = max|w| / 448 and w8 = e4m3(w / scale_inv).
+    """
+    g = _gen(seed, "cpu")
+    w = torch.randn((n, k), generator=g) * std
+    nb, kb = (n + 127) // 128, (k + 127) // 128
+    pad = torch.zeros((nb * 128, kb * 128))
+    pad[:n, :k] = w
+    amax = pad.reshape(nb, 128, kb, 128).abs().amax(dim=(1, 3))
+    scale_inv = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
+    q = (w / scale_inv.repeat_interleave(128, 0).repeat_interleave(128, 1)[:n, :k]).clamp(-FP8_MAX, FP8_MAX)
+    return q.to(torch.float8_e4m3fn).to(device), scale_inv.float().to(device)

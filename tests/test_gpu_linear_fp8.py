@@ -1,0 +1,79 @@
+"""GPU parity: projections with FP8 block-scaled weights (ria_dequant_fp8, ria_linear_fp8).
+
+The reference dequantises its float8_e4m3fn checkpoint weights once to fp16
+(qwen36_dequant.py:35-58, qwen36_cached_loop.py:537-542) and runs fp16
+F.linear.  The oracle (oracle.qwen36_cpu.projection_fp8, pinned against
+fp64, torch's e4m3fn decoding and transformers' Fp8Dequantize) restates
+that; the kernels must give the same dequantised weights bit for bit and
+the same fp16 projection up to the order of the fp32 accumulation.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import announce
+from helpers import assert_act_close
+from oracle import qwen36_cpu as O
+from router_ia import kernels as K
+from router_ia import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_dequant_all_byte_values_bit_exact(gpu, out_dtype):
+    announce(f"dequant_fp8: all 256 e4m3 bytes x 4 scale blocks -> {out_dtype}")
+    w8 = torch.arange(256, dtype=torch.uint8).repeat(130, 1)  # [130, 256]: every byte in every block
+    w8[:, :128] = w8[:, :128].roll(7, dims=1)
+    s = torch.tensor([[1.0, 0.5], [3.0e-3, 117.25]])
+    got = K.dequant_fp8(w8.to(gpu), s.to(gpu), out_dtype).cpu()
+    want = O.dequantize_fp8_blockwise(w8.view(torch.float8_e4m3fn), s).to(out_dtype)
+    torch.testing.assert_close(got, want, rtol=0, atol=0, equal_nan=True)
+
+
+CASES = [  # (m, n, k, x dtype): decode batches, one and two 128-row blocks, 16- and 32-wide tiles
+    (1, 8192, 2048, torch.bfloat16),
+    (7, 4096, 2048, torch.float16),
+    (32, 2048, 4096, torch.float32),
+    (128, 512, 2048, torch.bfloat16),
+    (128, 8192, 2048, torch.float16),
+    (200, 32, 2048, torch.float16),
+]
+
+
+@pytest.mark.parametrize("m,n,k,xdt", CASES)
+def test_linear_fp8_matches_oracle(gpu, m, n, k, xdt):
+    announce(f"linear_fp8: M={m} N={n} K={k} x {xdt}")
+    w8, s = W.fp8_block_weight(200 + m, n, k)
+    g = torch.Generator().manual_seed(300 + m)
+    # x rows inside a wider buffer (a strided view, as a fused projection output would be)
+    wide = torch.randn((m, k + 64), generator=g).to(xdt)
+    x = wide[:, :k]
+    got = K.linear_fp8(x.to(gpu), w8.to(gpu), s.to(gpu)).cpu()
+    want = O.projection_fp8(x, w8, s)
+    assert got.dtype == torch.float16
+    assert_act_close(got, want, f"M={m} N={n} K={k}")
+    # Against the exact product of the same fp16 operands, the kernel is as
+    # accurate as the oracle's fp32-accumulated F.linear: both err by the fp16
+    # rounding of the result plus an fp32 summation error that depends on the
+    # order (about 1e-4 here, where the K terms sum to ~26 in magnitude).
+    w16 = O.dequantize_fp8_blockwise(w8, s).to(torch.float16)
+    exact = x.to(torch.float16).double() @ w16.double().T
+    e_got = (got.double() - exact).abs().max().item()
+    e_ref = (want.double() - exact).abs().max().item()
+    assert e_got <= 1.5 * e_ref + 1e-6, (e_got, e_ref)
+
+
+def test_linear_fp8_output_dtypes_round_through_fp16(gpu):
+    announce("linear_fp8: fp32 and bf16 outputs carry the fp16 result")
+    w8, s = W.fp8_block_weight(400, 512, 2048)
+    x = torch.randn((9, 2048), generator=torch.Generator().manual_seed(401)).to(torch.bfloat16).to(gpu)
+    w8, s = w8.to(gpu), s.to(gpu)
+    y16 = K.linear_fp8(x, w8, s)
+    y32 = K.linear_fp8(x, w8, s, out_dtype=torch.float32)
+    yb = K.linear_fp8(x, w8, s, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(y32.cpu(), y16.cpu().float())
+    assert torch.equal(yb.cpu(), y16.cpu().to(torch.bfloat16))

@@ -277,3 +277,47 @@ def test_full_decode_gate_is_per_head_and_dim():
     out2, _, _ = O.full_decode_step(fk, fv, q, k, v, gate2, 5)
     diff = (out2 - base_out).abs() > 0
     assert diff[0, 3, 17] and diff.sum() == 1
+
+
+# ----------------------------------------------------------------------------- FP8 projections
+def test_e4m3fn_decoding_known_values_and_library_conversion():
+    known = {0x00: 0.0, 0x38: 1.0, 0xB8: -1.0, 0x7E: 448.0, 0x01: 2.0 ** -9, 0x08: 2.0 ** -6, 0x3C: 1.5,
+             0x30: 0.5, 0x77: 240.0}
+    for b, v in known.items():
+        assert fp64.e4m3fn_value(b) == v, hex(b)
+    assert np.isnan(fp64.e4m3fn_value(0x7F)) and np.isnan(fp64.e4m3fn_value(0xFF))
+    # torch's float8_e4m3fn conversion (the reference's weight.float()) agrees on all 256 bytes
+    allb = torch.arange(256, dtype=torch.uint8)
+    lib = allb.view(torch.float8_e4m3fn).float().double().numpy()
+    mine = np.array([fp64.e4m3fn_value(b) for b in range(256)])
+    np.testing.assert_array_equal(lib, mine)
+
+
+def _fp8_weight(seed, n, k):
+    g = _gen(seed)
+    w = (torch.randn((n, k), generator=g) * 0.05).float()
+    grid = (-(-n // 128), -(-k // 128))
+    s = torch.rand(grid, generator=g) * 1e-3 + 1e-4
+    q = (w / s.repeat_interleave(128, 0).repeat_interleave(128, 1)[:n, :k]).clamp(-448, 448)
+    return q.to(torch.float8_e4m3fn), s
+
+
+def test_dequantize_fp8_matches_fp64_including_ragged_blocks():
+    w8, s = _fp8_weight(31, 130, 200)
+    got = O.dequantize_fp8_blockwise(w8, s)
+    want = fp64.dequant_fp8(w8.view(torch.uint8).numpy(), s.double().numpy())
+    # one fp32 rounding of an exact product
+    np.testing.assert_allclose(got.double().numpy(), want, rtol=2 ** -24, atol=0)
+    # the scale of block (1, 1) reaches row 128 / col 128 and not before
+    assert torch.equal(got[128:, 128:], w8[128:, 128:].float() * s[1, 1])
+    assert torch.equal(got[:128, :128], w8[:128, :128].float() * s[0, 0])
+
+
+def test_projection_fp8_rounds_like_an_fp16_linear():
+    w8, s = _fp8_weight(32, 64, 256)
+    x = torch.randn((5, 256), generator=_gen(33))
+    y = O.projection_fp8(x, w8, s)
+    assert y.dtype == torch.float16
+    w16 = (w8.float().double() * torch.from_numpy(np.kron(s.double().numpy(), np.ones((128, 128))))[:64, :256])
+    ref = x.to(torch.float16).double() @ w16.to(torch.float16).double().T
+    torch.testing.assert_close(y.double(), ref.to(torch.float16).double(), rtol=1e-3, atol=1e-4)

@@ -96,3 +96,15 @@ def test_rmsnorms_match_transformers():
     z = torch.randn((1, 32, 128), generator=g)
     with torch.no_grad():
         assert torch.equal(O.gated_rmsnorm(x, z, gated.weight), gated(x, gate=z))
+
+
+def test_fp8_dequant_matches_transformers():
+    from transformers.integrations.finegrained_fp8 import Fp8Dequantize
+
+    g = torch.Generator().manual_seed(9)
+    w8 = (torch.randn((256, 384), generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    s = torch.rand((2, 3), generator=g) + 0.01
+    hf_w = Fp8Dequantize(None)._dequantize_one(w8, s, output_dtype=torch.float32)
+    assert torch.equal(O.dequantize_fp8_blockwise(w8, s), hf_w)
+    hf16 = Fp8Dequantize(None)._dequantize_one(w8, s, output_dtype=torch.float16)
+    assert torch.equal(O.dequantize_fp8_blockwise(w8, s).to(torch.float16), hf16)

@@ -79,6 +79,13 @@ WORKLOADS = {
                         desc="save + restore of every sequence of the ragged128 stack (40 layers, B=128, "
                              "context U[1024,32768]): DeltaNet states, conv rings and KV pages to one payload "
                              "per sequence and back"),
+    "proj128": dict(batch=128, seed=5, proj=True,
+                    desc="every projection of the 40-layer stack for one decode step of B=128 tokens, FP8 "
+                         "block-scaled weights (DeltaNet in_proj_qkv/z/a/b + out_proj, attention q/k/v/o_proj), "
+                         "fp16 outputs"),
+    "proj1": dict(batch=1, seed=5, proj=True,
+                  desc="every projection of the 40-layer stack for one decode step of B=1 token, FP8 block-scaled "
+                       "weights, fp16 outputs"),
     "batch32": dict(batch=32, lo=8192, hi=8192, seed=2,
                     desc="40-layer stack, B=32, context 8192 (seed 2), 16-token pages, shuffled page table"),
 }
@@ -334,6 +341,102 @@ def run_cpu_baseline(wl, lengths: list[int], n_seqs: int, n_steps: int) -> dict:
                    f"{n_steps} decode steps, torch-CPU restatement of the reference (fp32 state and KV, "
                    f"torch.cat KV append); {dt:.1f} s"),
     }
+
+
+# Projection launches of one layer, each a list of the (N, K) projections that
+# read the same x: DeltaNet in_proj_qkv, in_proj_z, in_proj_a, in_proj_b on the
+# normed hidden state, then out_proj (qwen36_attention_cache.py:232-247,
+# 268-276); attention q (with gate), k, v, then o (:295-301, 318-320); hidden
+# 2048 (qwen36_40layer_loop.py:36-50).
+GDN_PROJ = [[(8192, 2048), (4096, 2048), (32, 2048), (32, 2048)], [(2048, 4096)]]
+ATTN_PROJ = [[(8192, 2048), (512, 2048), (512, 2048)], [(2048, 4096)]]
+
+
+def run_proj_gpu(args, wl) -> dict:
+    """All projections of one decode step (40 layers) with FP8 weights, `steps` times."""
+    from router_ia import kernels as K
+    from router_ia import workloads as W
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    b = wl["batch"]
+    launches = [grp for layer in range(LAYERS) for grp in (ATTN_PROJ if is_full(layer) else GDN_PROJ)]
+    shapes = [s for grp in launches for s in grp]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(wl["seed"])
+
+    def weight(n, k):  # distinct weights per layer, so nothing stays in L2 between steps
+        w8 = (torch.randn((n, k), generator=gen, device=dev) * 8.0).clamp(-448, 448).to(torch.float8_e4m3fn)
+        s = torch.rand(((n + 127) // 128, (k + 127) // 128), generator=gen, device=dev) * 1e-3 + 1e-4
+        return w8, s
+
+    weights = [[weight(n, k) for n, k in grp] for grp in launches]
+    xs = {k: torch.randn((b, k), generator=gen, device=dev).to(torch.float16) for k in (2048, 4096)}
+    ys = [[torch.empty((b, n), device=dev, dtype=torch.float16) for n, _ in grp] for grp in launches]
+    wbytes = sum(n * k for n, k in shapes)
+    io_bytes = sum(2 * b * n for n, _ in shapes) + sum(2 * b * grp[0][1] for grp in launches)
+    flop = sum(2 * b * n * k for n, k in shapes)
+    log(f"[bench] {wl['desc']}: {len(shapes)} projections in {len(launches)} launches, "
+        f"{wbytes / 1e9:.3f} GB of FP8 weights per step")
+
+    def one_step():
+        for grp, w, y in zip(launches, weights, ys):
+            K.linear_fp8_group(xs[grp[0][1]], w, out=y)
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    # The step is 80 short launches; replaying it as one captured HIP graph
+    # keeps the host's per-call work out of the GPU timeline.
+    graph = torch.cuda.CUDAGraph()
+    capture = torch.cuda.Stream()
+    capture.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(capture):
+        with torch.cuda.graph(graph, stream=capture):
+            one_step()
+    torch.cuda.current_stream().wait_stream(capture)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    elapsed = t0.elapsed_time(t1) / 1e3
+    step_s = elapsed / args.steps
+    achieved = (wbytes + io_bytes) / step_s / 1e9
+    return {"batch": b, "elapsed_s": elapsed, "ms_per_step": step_s * 1e3, "tok_s": b / step_s,
+            "weight_bytes": wbytes, "flop": flop, "achieved_GBps": achieved,
+            "TFLOPs": flop / step_s / 1e12}
+
+
+def proj_main(args, wl) -> int:
+    gpu = run_proj_gpu(args, wl)
+    result = {
+        "metric": "projection pass tok/s (all 40 layers' FP8 projections for one decode step); weight GB/s % of HBM peak",
+        "value": round(gpu["tok_s"], 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8 e4m3 weights (128x128 block scales), fp16 activations and MFMA, fp32 accumulation",
+        "data": "synthetic (random FP8 weights and scales, random activations)",
+        "config": {"workload": wl["desc"], "batch": gpu["batch"], "fp8_weight_GB": round(gpu["weight_bytes"] / 1e9, 3),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "linear_fp8_kernel (ria_linear_fp8_group), all launches of the step",
+                     "achieved": round(gpu["achieved_GBps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gpu["achieved_GBps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "mfma_TFLOPs": round(gpu["TFLOPs"], 1),
+                     "mfma_frac": round(gpu["TFLOPs"] / MFMA_PEAK_TFLOPS, 4)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
 
 
 def run_snapshot_gpu(args, wl) -> dict:
@@ -605,6 +708,8 @@ def main() -> int:
         return prefill_main(args, wl)
     if wl.get("snapshot"):
         return snapshot_main(args, wl)
+    if wl.get("proj"):
+        return proj_main(args, wl)
     gpu = run_gpu(args, wl)
     prof = profiled_traffic("attn_splitk_kernel") if args.workload == "ragged128" else None
     if prof:

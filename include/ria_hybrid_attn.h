@@ -403,14 +403,32 @@ int ria_kv_gather(int batch, int num_kv_heads,
  * rounded to fp16 (F.linear's fp16 output) and stored as y_dtype.  x [m, k]
  * of x_dtype (converted to fp16 like `.to(float16)`), y [m, n].  n a multiple
  * of 16, k of 128; x and weight 16-byte aligned, x row stride a multiple of 8.
- * Built for decode-sized m (one weight pass per 128 rows of x).
+ * Built for decode-sized m (one weight pass per 128 rows of x); k up to 32768.
+ *
+ * ria_linear_fp8_group: 1 to 4 such projections of the same x in one launch,
+ * each with its own n, weight, scales and y (all y of y_dtype).  It replaces
+ * the reference's run of F.linear calls on one normed hidden state: DeltaNet
+ * in_proj_qkv / in_proj_z / in_proj_a / in_proj_b (qwen36_attention_cache.py:
+ * 232-247, 268) and attention q_proj / k_proj / v_proj (:295-301); results
+ * equal separate ria_linear_fp8 calls.
  */
+typedef struct ria_fp8_proj {
+  const void* weight;      /* [n, k] float8_e4m3fn */
+  const float* scale_inv;  /* [ceil(n / 128), k / 128] */
+  void* y;                 /* [m, n], rows y_row_stride elements apart */
+  int64_t y_row_stride;
+  int n;
+} ria_fp8_proj;
+
 int ria_dequant_fp8(int64_t rows, int cols, const void* weight, const float* scale_inv,
                     void* out, int out_dtype, void* stream);
 
 int ria_linear_fp8(int m, int n, int k, const void* x, int x_dtype, int64_t x_row_stride,
                    const void* weight, const float* scale_inv,
                    void* y, int y_dtype, int64_t y_row_stride, void* stream);
+
+int ria_linear_fp8_group(int m, int k, const void* x, int x_dtype, int64_t x_row_stride,
+                         int count, const ria_fp8_proj* projs, int y_dtype, void* stream);
 
 /*
  * Sequence snapshots: one row's DeltaNet states, conv ring and KV pages as a

@@ -16,21 +16,25 @@
 //                        dequantised weight; also feeds a library GEMM for
 //                        long prompts)
 //   linear_fp8_kernel    one workgroup per (16 or 32 output features,
-//                        128-row block of x); 4 waves, 32 rows of x each.
-//                        Weight chunks (the tile's rows x 128 K = one scale
-//                        block) stream through an 8-deep register ring, are
-//                        dequantised into an fp16 B-operand buffer in LDS
-//                        (double-buffered), and every wave runs 16x16x32 f16
-//                        MFMAs over its rows with x operands loaded one chunk
-//                        ahead.  Decode-sized M is bound by the weight stream.
+//                        128-row block of x).  Weight chunks (the tile's rows
+//                        x 128 K = one scale block) stream through an 8-deep
+//                        register ring in four producer waves, are dequantised
+//                        into an fp16 B-operand buffer in LDS (double-
+//                        buffered), and four consumer waves (32 rows of x
+//                        each) run 16x16x32 f16 MFMAs with x operands loaded
+//                        one chunk ahead.  Decode-sized M is bound by the
+//                        weight stream.
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 #include "ria_common.h"
 
 namespace ria {
 
 constexpr int kFp8Block = 128;  // scale block edge (qwen36_dequant.py:13)
-constexpr int kLinRing = 8;     // weight chunks in flight per workgroup
+constexpr int kLinRing = 12;    // weight chunks in flight per workgroup
+constexpr int kXAhead = 2;      // chunks of x loaded ahead of the MFMAs
 constexpr int kLinRows = 128;   // rows of x per workgroup (4 waves x 32)
 
 // Two fp8 e4m3 (OCP, float8_e4m3fn) bytes of `w` (low pair or high pair) to fp32.
@@ -41,13 +45,15 @@ __device__ __forceinline__ f32x2 fp8x2_to_f32(uint32_t w) {
 }
 
 // fp16 bits of (fp32(w8) * s): the reference's `weight.float() * scale` rounded by `.to(float16)`.
+// (two fp32 products, then one packed round-to-nearest conversion to fp16)
 template <bool HIGH>
 __device__ __forceinline__ uint32_t dequant_pair(uint32_t w, float s) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const f32x2 f = fp8x2_to_f32<HIGH>(w);
-  const _Float16 a = static_cast<_Float16>(mul_rn(f[0], s));
-  const _Float16 b = static_cast<_Float16>(mul_rn(f[1], s));
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+  h2 r;
+  r[0] = static_cast<_Float16>(mul_rn(f[0], s));
+  r[1] = static_cast<_Float16>(mul_rn(f[1], s));
+  return __builtin_bit_cast(uint32_t, r);
 }
 
 // One thread per 16 weight bytes of a row (K a multiple of 16).
@@ -79,15 +85,26 @@ __global__ __launch_bounds__(256) void dequant_fp8_kernel(const uint8_t* __restr
   }
 }
 
+// Up to kLinGroup projections of the same x in one launch (a layer's input
+// projections read the same normed hidden state); column tiles of projection
+// j are blockIdx.x = tile0[j] .. tile0[j + 1] - 1.
+constexpr int kLinGroup = 4;
+constexpr int kLinMaxChunks = 256;  // K <= 32768: the tile's scale row is staged in LDS
+
+struct Fp8Proj {
+  const uint8_t* w;     // [n, K] e4m3
+  const float* scale;   // [ceil(n / 128), K / 128]
+  void* y;              // [m, n], rows y_stride elements apart
+  int64_t y_stride;
+  int n;
+  int tile0;            // first column tile of this projection
+};
+
 struct LinearArgs {
   const void* x;
   int64_t x_stride;
-  const uint8_t* w;     // [N, K] e4m3
-  const float* scale;   // [ceil(N / 128), scale_cols]
-  int scale_cols;
-  void* y;
-  int64_t y_stride;
-  int m, n, k;
+  int m, k, count;
+  Fp8Proj p[kLinGroup];
 };
 
 // x operand of one 16x16x32 MFMA: 8 consecutive K values of one row as fp16.
@@ -105,111 +122,365 @@ __device__ __forceinline__ u32x4 load_x8(const void* x, int64_t i) {
   }
 }
 
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>): a loop the
+// compiler must unroll, so register arrays indexed by the counter stay in
+// registers (a rolled loop would move them to scratch memory).
+template <typename F, int... U>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, U...>) {
+  (f(std::integral_constant<int, U>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// One producer thread's weight bytes of a chunk: 8 (CT 1), 16 (CT 2) or 32 (CT 4).
+template <int CT>
+struct WeightSlot {
+  u32x4 v[CT / 2];
+  __device__ __forceinline__ void load(const uint8_t* p) {
+#pragma unroll
+    for (int q = 0; q < CT / 2; ++q) v[q] = *reinterpret_cast<const u32x4*>(p + 16 * q);
+  }
+  __device__ __forceinline__ uint32_t word(int i) const { return v[i >> 2][i & 3]; }
+};
+template <>
+struct WeightSlot<1> {
+  u32x2 v;
+  __device__ __forceinline__ void load(const uint8_t* p) { v = *reinterpret_cast<const u32x2*>(p); }
+  __device__ __forceinline__ uint32_t word(int i) const { return v[i]; }
+};
+
+// Producer / consumer waves.  A wave's vector-memory counter retires loads in
+// issue order, so a wave that both streamed weights far ahead and loaded x
+// for the next chunk would have to wait for every weight load issued before
+// that x.  Here waves 4-7 only stream weights (an 8-chunk register ring,
+// dequantised into the B buffer) and waves 0-3 only load x and run the MFMAs;
+// one LDS-only barrier per chunk hands each B buffer over.
+//
+// Both loops run whole groups of kLinRing chunks with no exit inside (the
+// ring slot u is a compile-time index), then the K % (128 kLinRing) tail:
+// an exit inside the ring loop makes the compiler join the ring registers
+// at each exit, which waits for every weight load in flight.
 template <int XT, int OT, int CT>
-__global__ __launch_bounds__(256) void linear_fp8_kernel(LinearArgs a) {
+__global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
   using F16 = Kv16<RIA_DT_F16>;
-  constexpr int kCols = 16 * CT;          // output features per workgroup
-  constexpr int kLoaders = kCols * 8;     // threads holding 16 weight bytes of a chunk
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kCols = 16 * CT;             // output features per workgroup
+  constexpr int kBytes = CT * 8;             // weight bytes per producer thread per chunk
+  constexpr int kWords = CT * 2;             // .. as 32-bit words
+  using Ring = WeightSlot<CT>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, so role branches are scalar
   const int n16 = lane & 15, g4 = lane >> 4;
-  const int n0 = blockIdx.x * kCols;
+  const int bx = blockIdx.x;
+  // this workgroup's projection: scalar selects over the group
+  const uint8_t* w = a.p[0].w;
+  const float* scale = a.p[0].scale;
+  void* y = a.p[0].y;
+  int64_t y_stride = a.p[0].y_stride;
+  int n = a.p[0].n, tile0 = 0;
+#pragma unroll
+  for (int j = 1; j < kLinGroup; ++j)
+    if (j < a.count && bx >= a.p[j].tile0) {
+      w = a.p[j].w;
+      scale = a.p[j].scale;
+      y = a.p[j].y;
+      y_stride = a.p[j].y_stride;
+      n = a.p[j].n;
+      tile0 = a.p[j].tile0;
+    }
+  const int n0 = (bx - tile0) * kCols;
   const int m0 = blockIdx.y * kLinRows;
   const int rows = min(kLinRows, a.m - m0);
   const int chunks = a.k / kFp8Block;
-  const int nb = n0 / kFp8Block;  // the tile lies in one scale block of rows
+  const int groups = chunks / kLinRing, tail = chunks - groups * kLinRing;
 
   // fp16 B operands of one chunk: [k-step 4][col tile CT][lane 64] x 16 bytes, double-buffered
   __shared__ u32x4 bop[2][4 * CT * 64];
+  __shared__ float sc_s[kLinMaxChunks];  // scale of each chunk (the tile lies in one block of 128 rows)
 
-  // weight bytes of this thread in every chunk: row n0 + wr, bytes 16 wk .. + 15 of the chunk
-  const int wr = tid >> 3, wk = tid & 7;
-  const bool loader = tid < kLoaders;
-  const uint8_t* wrow = a.w + (int64_t)(n0 + (loader ? wr : 0)) * a.k + 16 * wk;
-  // where its 16 values land: k-step wk / 2, k groups 2 (wk % 2) and + 1, column tile wr / 16
-  const int s_of = wk >> 1, g_of = 2 * (wk & 1), c_of = wr >> 4, lane0 = (wr & 15) + 16 * g_of;
-
-  u32x4 ring[kLinRing];
+  // the ring slot u also picks the B buffer (u % 2) and the x buffer
+  // (u % (kXAhead + 1)); both must repeat with each group of kLinRing chunks
+  static_assert(kLinRing % 2 == 0 && kLinRing % (kXAhead + 1) == 0, "buffers must follow the ring slot");
+  if (wave >= 4) {
+    // ---- producers: bytes kBytes * pk .. of row n0 + pr in every chunk
+    const int p = tid - 256;
+    const int pr = p / (128 / kBytes), pk = p % (128 / kBytes);
+    // (features past n, in the last tile of a projection narrower than the
+    // tile, repeat row n - 1: their columns are computed and not stored)
+    const uint8_t* wrow = w + (int64_t)min(n0 + pr, n - 1) * a.k + kBytes * pk;
+    // those values are 16 B (CT 2) or 8 B (CT 1) of K at k-step s, k groups g ..
+    const int kofs = kBytes * pk, s_of = kofs >> 5, g_of = (kofs & 31) >> 3;
+    const int slot = (s_of * CT + (pr >> 4)) * 64 + (pr & 15) + 16 * g_of;
+    // the tile's scale row (threads past the row repeat its last entry): loaded
+    // before the weight ring, so the wait for it does not wait for the ring
+    const int sp = min(p, chunks - 1);
+    const float sc0 = scale[(n0 / kFp8Block) * chunks + sp];
+    __builtin_amdgcn_sched_barrier(0);
+    Ring ring[kLinRing];
+    static_for<kLinRing>([&](auto u) { ring[u].load(wrow + (int64_t)min(int(u), chunks - 1) * kFp8Block); });
+    sc_s[sp] = sc0;
+    lds_barrier();  // sc_s is written
+    auto produce = [&](auto u, int c) {
+      const float sc = sc_s[c];
+      // the thread's bytes are k groups g_of .. g_of + CT - 1 of k-step s_of: 8 fp16 values each
 #pragma unroll
-  for (int u = 0; u < kLinRing; ++u)
-    if (loader) ring[u] = *reinterpret_cast<const u32x4*>(wrow + (int64_t)min(u, chunks - 1) * kFp8Block);
+      for (int q = 0; q < kWords / 2; ++q) {
+        const uint32_t w0 = ring[u].word(2 * q), w1 = ring[u].word(2 * q + 1);
+        bop[u & 1][slot + 16 * q] = u32x4{dequant_pair<false>(w0, sc), dequant_pair<true>(w0, sc),
+                                          dequant_pair<false>(w1, sc), dequant_pair<true>(w1, sc)};
+      }
+    };
+    for (int gi = 0; gi < groups; ++gi) {
+      static_for<kLinRing>([&](auto u) {
+        const int c = gi * kLinRing + u;
+        produce(u, c);
+        // keep the reload after the dequantisation, so it refills ring[u]'s own registers
+        __builtin_amdgcn_sched_barrier(0);
+        ring[u].load(wrow + (int64_t)min(c + kLinRing, chunks - 1) * kFp8Block);
+        lds_barrier();
+      });
+    }
+    static_for<kLinRing>([&](auto u) {
+      if (u < tail) {
+        produce(u, groups * kLinRing + u);
+        lds_barrier();
+      }
+    });
+    return;
+  }
 
-  // this wave's rows: 32 wave .. + 31 (two row tiles); rows past the end repeat the last one
-  const bool has_rows0 = 32 * wave < rows, has_rows1 = 32 * wave + 16 < rows;
+  // ---- consumers: rows 32 wave .. + 31 (two row tiles); rows past the end repeat the last one
   const int r0 = min(32 * wave + n16, rows - 1), r1 = min(32 * wave + 16 + n16, rows - 1);
   const int64_t xo0 = (int64_t)(m0 + r0) * a.x_stride + 8 * g4, xo1 = (int64_t)(m0 + r1) * a.x_stride + 8 * g4;
-  u32x4 ax[2][4][2];  // x operands of two chunks: [buffer][k-step][row tile]
-  auto load_x = [&](int c, u32x4 (&dst)[4][2]) {
+  // The number of row tiles this wave computes is fixed outside the chunk
+  // loop (one loop copy per count), so the loop body has no branch: a branch
+  // around the MFMAs would make the compiler wait for the next chunk's x too.
+  auto consume = [&](auto tiles) {
+    constexpr int NT = decltype(tiles)::value;
+    u32x4 ax[kXAhead + 1][4][2];  // x operands of the chunks in flight: [buffer][k-step][row tile]
+    auto load_x = [&](int c, u32x4 (&dst)[4][2]) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      dst[s][0] = load_x8<XT>(a.x, xo0 + c * kFp8Block + 32 * s);
-      dst[s][1] = load_x8<XT>(a.x, xo1 + c * kFp8Block + 32 * s);
-    }
-  };
-  load_x(0, ax[0]);
-
-  f32x4 acc[2][CT];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int c = 0; c < CT; ++c) acc[rt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // chunks run in groups of kLinRing so the ring index is static (and, the
-  // group size being even, so is the parity of c that picks the buffers)
-  static_assert(kLinRing % 2 == 0, "buffer parity must follow the ring index");
-  for (int c0 = 0; c0 < chunks; c0 += kLinRing) {
-#pragma unroll
-    for (int u = 0; u < kLinRing; ++u) {
-      const int c = c0 + u;
-      if (c >= chunks) break;
-      const int buf = u & 1;
-      // dequantise this thread's 16 bytes into the B operands of chunk c
-      if (loader) {
-        const float sc = a.scale[nb * a.scale_cols + c];
-        const u32x4 v = ring[u];
-        const u32x4 lo{dequant_pair<false>(v[0], sc), dequant_pair<true>(v[0], sc), dequant_pair<false>(v[1], sc),
-                       dequant_pair<true>(v[1], sc)};
-        const u32x4 hi{dequant_pair<false>(v[2], sc), dequant_pair<true>(v[2], sc), dequant_pair<false>(v[3], sc),
-                       dequant_pair<true>(v[3], sc)};
-        bop[buf][(s_of * CT + c_of) * 64 + lane0] = lo;
-        bop[buf][(s_of * CT + c_of) * 64 + lane0 + 16] = hi;
-        ring[u] = *reinterpret_cast<const u32x4*>(wrow + (int64_t)min(c + kLinRing, chunks - 1) * kFp8Block);
+      for (int s = 0; s < 4; ++s) {
+        if constexpr (NT >= 1) dst[s][0] = load_x8<XT>(a.x, xo0 + c * kFp8Block + 32 * s);
+        if constexpr (NT >= 2) dst[s][1] = load_x8<XT>(a.x, xo1 + c * kFp8Block + 32 * s);
       }
-      if (c + 1 < chunks) load_x(c + 1, ax[(u + 1) & 1]);
-      __syncthreads();
+    };
+#pragma unroll
+    for (int j = 0; j < kXAhead; ++j) load_x(min(j, chunks - 1), ax[j]);
+    f32x4 acc[2][CT];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    lds_barrier();  // the producers' sc_s
+    auto step = [&](auto u, int c) {
+      load_x(min(c + kXAhead, chunks - 1), ax[(u + kXAhead) % (kXAhead + 1)]);  // past the end: reloads
+      lds_barrier();  // B operands of chunk c are in bop[u & 1]
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         u32x4 b[CT];
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) b[ct] = bop[buf][(s * CT + ct) * 64 + lane];
+        for (int ct = 0; ct < CT; ++ct) b[ct] = bop[u & 1][(s * CT + ct) * 64 + lane];
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          if (has_rows0) acc[0][ct] = F16::mfma_k32(ax[buf][s][0], b[ct], acc[0][ct]);
-          if (has_rows1) acc[1][ct] = F16::mfma_k32(ax[buf][s][1], b[ct], acc[1][ct]);
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int rt = 0; rt < NT; ++rt)
+            acc[rt][ct] = F16::mfma_k32(ax[u % (kXAhead + 1)][s][rt], b[ct], acc[rt][ct]);
+      }
+    };
+    for (int gi = 0; gi < groups; ++gi) static_for<kLinRing>([&](auto u) { step(u, gi * kLinRing + u); });
+    static_for<kLinRing>([&](auto u) {
+      if (u < tail) step(u, groups * kLinRing + u);
+    });
+    // D tile rows 4 g4 + i, column n16; F.linear's fp16 result, stored as OT
+#pragma unroll
+    for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 32 * wave + 16 * rt + 4 * g4 + i;
+          if (r < rows && n0 + 16 * ct + n16 < n)
+            store_act<OT>(y, (int64_t)(m0 + r) * y_stride + n0 + 16 * ct + n16,
+                          through_dtype<RIA_DT_F16>(acc[rt][ct][i]));
+        }
+  };
+  if (32 * wave + 16 < rows)
+    consume(std::integral_constant<int, 2>{});
+  else if (32 * wave < rows)
+    consume(std::integral_constant<int, 1>{});
+  else
+    consume(std::integral_constant<int, 0>{});  // no rows: only keeps the barriers in step
+}
+
+// Decode-sized M (up to 16 rows): one workgroup per 16 output features and
+// 16 rows of x, one wave per 512 K.  A wave issues every load it needs at once
+// (its x operands, then 16 rows x 512 bytes of weight: 8 loads of 16 bytes a
+// lane), so the whole weight matrix is in flight with no ring and no LDS
+// handoff; it then dequantises in registers and runs 16 MFMAs (x as the A
+// operand, rows = tokens; weights as B, columns = features).  A lane's 16
+// weight bytes at K = 64 j + 16 g .. + 15 feed two MFMAs (low 8 bytes to step
+// 2 j, high 8 to 2 j + 1, k group g of each); x uses the same K order, so each
+// MFMA sums 32 matching products.  The waves' partial sums are added in wave
+// order through LDS.
+constexpr int kGemvSlice = 512;  // K per wave
+constexpr int kGemvRows = 16;    // rows of x per workgroup
+constexpr int kGemvMaxWaves = 8; // K <= 4096
+constexpr int kGemvStageRows = 4; // x rows staged through LDS
+
+template <int XT, int OT>
+__global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const LinearArgs a) {
+  using F16 = Kv16<RIA_DT_F16>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int waves = a.k / kGemvSlice;
+  const int c16 = lane & 15, g4 = lane >> 4;
+  const int bx = blockIdx.x;
+  const uint8_t* w = a.p[0].w;
+  const float* scale = a.p[0].scale;
+  void* y = a.p[0].y;
+  int64_t y_stride = a.p[0].y_stride;
+  int tile0 = 0;
+#pragma unroll
+  for (int j = 1; j < kLinGroup; ++j)
+    if (j < a.count && bx >= a.p[j].tile0) {
+      w = a.p[j].w;
+      scale = a.p[j].scale;
+      y = a.p[j].y;
+      y_stride = a.p[j].y_stride;
+      tile0 = a.p[j].tile0;
+    }
+  const int n0 = (bx - tile0) * 16;
+  const int m0 = blockIdx.y * kGemvRows;
+  const int rows = min(kGemvRows, a.m - m0);
+  const int k0 = wave * kGemvSlice;
+
+  const uint8_t* wp = w + (int64_t)(n0 + c16) * a.k + k0 + 16 * g4;
+  const float* sp = scale + (n0 / kFp8Block) * (a.k / kFp8Block) + k0 / kFp8Block;
+  // The loads of x go first, so that waiting for them leaves the weight loads
+  // in flight.  Up to kGemvStageRows rows, a lane loads 16 bytes of one row
+  // (one instruction per row for the wave's 1 KB slice) and the slice goes
+  // through the wave's own LDS region into the MFMA layout: far fewer load
+  // instructions than the layout's 16 per wave, whose issue time (not their
+  // bytes) would otherwise delay the weight stream.  Lanes of rows past the
+  // end hold zeros.
+  // LDS (sized at launch): per wave max(staged rows, 1) x 1 KB; the first
+  // KB of a wave's region later holds its partial sums
+  extern __shared__ u32x4 gemv_lds[];
+  const int region = 64 * (rows <= kGemvStageRows ? rows : 1);
+  u32x4* own = gemv_lds + wave * region;
+  u32x4 ax[8][2];
+  u32x4 wv[8];
+  float sc[4];
+  auto load_w = [&] {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wv[j] = *reinterpret_cast<const u32x4*>(wp + 64 * j);
+    // the slice's four scales (one per 128 K; the 16 features lie in one block of 128)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) sc[b] = sp[b];
+  };
+  // NR rows staged (NR = rows, 1 .. kGemvStageRows; the count is a template
+  // constant so the loads are straight-line code), or NR = 0: direct loads
+  auto load_operands = [&](auto nr) {
+    constexpr int NR = decltype(nr)::value;
+    if constexpr (NR > 0) {
+      u32x4 xs[NR];
+#pragma unroll
+      for (int r = 0; r < NR; ++r) xs[r] = load_x8<XT>(a.x, (int64_t)(m0 + r) * a.x_stride + k0 + 8 * lane);
+      load_w();
+      __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
+#pragma unroll
+      for (int r = 0; r < NR; ++r) own[64 * r + lane] = xs[r];
+      __builtin_amdgcn_wave_barrier();  // the region is this wave's: LDS keeps its order
+      const int r = min(c16, NR - 1);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const u32x4 v = own[64 * r + 8 * j + 2 * g4 + h];  // K = 64 j + 16 g4 + 8 h
+          ax[j][h] = c16 < NR ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+    } else {
+      const int64_t xo = (int64_t)(m0 + min(c16, rows - 1)) * a.x_stride + k0 + 16 * g4;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ax[j][0] = ax[j][1] = u32x4{0u, 0u, 0u, 0u};
+      if (c16 < rows) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          ax[j][0] = load_x8<XT>(a.x, xo + 64 * j);
+          ax[j][1] = load_x8<XT>(a.x, xo + 64 * j + 8);
         }
       }
+      load_w();
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  static_assert(kGemvStageRows == 4, "one case per staged row count");
+  switch (rows) {
+    case 1: load_operands(std::integral_constant<int, 1>{}); break;
+    case 2: load_operands(std::integral_constant<int, 2>{}); break;
+    case 3: load_operands(std::integral_constant<int, 3>{}); break;
+    case 4: load_operands(std::integral_constant<int, 4>{}); break;
+    default: load_operands(std::integral_constant<int, 0>{}); break;
   }
 
-  // D tile rows 4 g4 + i, column n16; F.linear's fp16 result, stored as OT
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int j = 0; j < 8; ++j) {
+    const float s = sc[j >> 1];
+    const u32x4 v = wv[j];
+    const u32x4 b0{dequant_pair<false>(v[0], s), dequant_pair<true>(v[0], s), dequant_pair<false>(v[1], s),
+                   dequant_pair<true>(v[1], s)};
+    const u32x4 b1{dequant_pair<false>(v[2], s), dequant_pair<true>(v[2], s), dequant_pair<false>(v[3], s),
+                   dequant_pair<true>(v[3], s)};
+    acc[0] = F16::mfma_k32(ax[j][0], b0, acc[0]);
+    acc[1] = F16::mfma_k32(ax[j][1], b1, acc[1]);
+  }
+  f32x4 part;
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
+  for (int i = 0; i < 4; ++i) part[i] = acc[0][i] + acc[1][i];
+
+  // (the MFMAs consumed this wave's staged x before its partial sums overwrite it)
+  reinterpret_cast<f32x4*>(own)[lane] = part;
+  lds_barrier();
+  if (wave == 0) {
+    f32x4 t = reinterpret_cast<const f32x4*>(gemv_lds)[lane];
+    for (int q = 1; q < waves; ++q) {
+      const f32x4 u = reinterpret_cast<const f32x4*>(gemv_lds + q * region)[lane];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 32 * wave + 16 * rt + 4 * g4 + i;
-        if (r < rows)
-          store_act<OT>(a.y, (int64_t)(m0 + r) * a.y_stride + n0 + 16 * ct + n16,
-                        through_dtype<RIA_DT_F16>(acc[rt][ct][i]));
-      }
+      for (int i = 0; i < 4; ++i) t[i] += u[i];
+    }
+    // D rows (tokens) 4 g4 + i, column (feature) c16; F.linear's fp16 result, stored as OT
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * g4 + i;
+      if (r < rows) store_act<OT>(y, (int64_t)(m0 + r) * y_stride + n0 + c16, through_dtype<RIA_DT_F16>(t[i]));
+    }
+  }
+}
+
+template <int XT>
+static void launch_gemv(const LinearArgs& a, int out_dtype, dim3 grid, hipStream_t st) {
+  const int waves = a.k / kGemvSlice;
+  const dim3 block(64 * waves);
+  const size_t lds = static_cast<size_t>(waves) * (a.m <= kGemvStageRows ? a.m : 1) * 64 * sizeof(u32x4);
+  if (out_dtype == RIA_DT_BF16)
+    hipLaunchKernelGGL((gemv_fp8_kernel<XT, RIA_DT_BF16>), grid, block, lds, st, a);
+  else if (out_dtype == RIA_DT_F16)
+    hipLaunchKernelGGL((gemv_fp8_kernel<XT, RIA_DT_F16>), grid, block, lds, st, a);
+  else
+    hipLaunchKernelGGL((gemv_fp8_kernel<XT, RIA_DT_F32>), grid, block, lds, st, a);
 }
 
 template <int XT, int OT>
 static void launch_linear_ct(const LinearArgs& a, int ct, dim3 grid, hipStream_t st) {
-  if (ct == 2)
-    hipLaunchKernelGGL((linear_fp8_kernel<XT, OT, 2>), grid, dim3(256), 0, st, a);
+  if (ct == 4)
+    hipLaunchKernelGGL((linear_fp8_kernel<XT, OT, 4>), grid, dim3(512), 0, st, a);
+  else if (ct == 2)
+    hipLaunchKernelGGL((linear_fp8_kernel<XT, OT, 2>), grid, dim3(512), 0, st, a);
   else
-    hipLaunchKernelGGL((linear_fp8_kernel<XT, OT, 1>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((linear_fp8_kernel<XT, OT, 1>), grid, dim3(512), 0, st, a);
 }
 
 template <int XT>
@@ -252,41 +523,96 @@ extern "C" int ria_dequant_fp8(int64_t rows, int cols, const void* weight, const
   return check_launch("ria_dequant_fp8");
 }
 
-extern "C" int ria_linear_fp8(int m, int n, int k, const void* x, int x_dtype, int64_t x_row_stride,
-                              const void* weight, const float* scale_inv, void* y, int y_dtype, int64_t y_row_stride,
-                              void* stream) {
-  if (m < 0 || n <= 0 || k <= 0) return set_error(RIA_ERR_INVALID, "ria_linear_fp8: bad sizes");
-  if (n % 16 || k % kFp8Block)
-    return set_error(RIA_ERR_INVALID, "ria_linear_fp8: N must be a multiple of 16 and K of 128 (got %d, %d)", n, k);
-  if (!lin_dtype_ok(x_dtype) || !lin_dtype_ok(y_dtype)) return set_error(RIA_ERR_INVALID, "ria_linear_fp8: unknown dtype code");
+// Validates and launches one group of projections of the same x (shared by
+// ria_linear_fp8 and ria_linear_fp8_group; `who` names the entry point in errors).
+static int linear_group(const char* who, int m, int k, const void* x, int x_dtype, int64_t x_row_stride, int count,
+                        const ria_fp8_proj* projs, int y_dtype, void* stream) {
+  if (count < 1 || count > kLinGroup) return set_error(RIA_ERR_INVALID, "%s: 1 to %d projections per call", who, kLinGroup);
+  if (m < 0 || k <= 0) return set_error(RIA_ERR_INVALID, "%s: bad sizes", who);
+  if (k % kFp8Block || k / kFp8Block > kLinMaxChunks)
+    return set_error(RIA_ERR_INVALID, "%s: K must be a multiple of 128 up to %d (got %d)", who,
+                     kFp8Block * kLinMaxChunks, k);
+  if (!lin_dtype_ok(x_dtype) || !lin_dtype_ok(y_dtype)) return set_error(RIA_ERR_INVALID, "%s: unknown dtype code", who);
+  if (!projs) return set_error(RIA_ERR_INVALID, "%s: null projection list", who);
+  for (int j = 0; j < count; ++j) {
+    const ria_fp8_proj& q = projs[j];
+    if (q.n <= 0 || q.n % 16)
+      return set_error(RIA_ERR_INVALID, "%s: N must be a positive multiple of 16 (projection %d: %d)", who, j, q.n);
+    if (q.y_row_stride < q.n) return set_error(RIA_ERR_INVALID, "%s: y row stride too small (projection %d)", who, j);
+  }
   if (m == 0) return RIA_OK;
-  if (!x || !weight || !scale_inv || !y) return set_error(RIA_ERR_INVALID, "ria_linear_fp8: null pointer");
-  if (x_row_stride < k || y_row_stride < n) return set_error(RIA_ERR_INVALID, "ria_linear_fp8: row stride too small");
+  if (!x) return set_error(RIA_ERR_INVALID, "%s: null x", who);
+  if (x_row_stride < k) return set_error(RIA_ERR_INVALID, "%s: x row stride too small", who);
   // x moves in 16-byte (fp16/bf16) or 32-byte (fp32) vectors of 8 elements
-  if (reinterpret_cast<uintptr_t>(x) % 16 || x_row_stride % 8 || reinterpret_cast<uintptr_t>(weight) % 16)
-    return set_error(RIA_ERR_INVALID, "ria_linear_fp8: x and weight 16-byte aligned, x row stride a multiple of 8");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || x_row_stride % 8)
+    return set_error(RIA_ERR_INVALID, "%s: x must be 16-byte aligned with a row stride a multiple of 8", who);
+  for (int j = 0; j < count; ++j) {
+    const ria_fp8_proj& q = projs[j];
+    if (!q.weight || !q.scale_inv || !q.y) return set_error(RIA_ERR_INVALID, "%s: null pointer (projection %d)", who, j);
+    if (reinterpret_cast<uintptr_t>(q.weight) % 16)
+      return set_error(RIA_ERR_INVALID, "%s: weight must be 16-byte aligned (projection %d)", who, j);
+  }
+  const bool gemv = m <= kGemvRows && k % kGemvSlice == 0 && k / kGemvSlice <= kGemvMaxWaves;
+  // Streaming kernel: 16 CT output features per workgroup.  Every workgroup
+  // reads all of its 128 rows of x (from L2), which costs more than its
+  // weights, so the width is the one that needs the fewest rounds of
+  // workgroups over the CUs, and the narrowest of those (more of the CUs busy).
+  int ct = 1;
+  if (!gemv) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    auto tiles = [&](int c) {
+      int64_t t = 0;
+      for (int j = 0; j < count; ++j) t += (projs[j].n + 16 * c - 1) / (16 * c);
+      return t;
+    };
+    auto rounds = [&](int c) { return (tiles(c) + cus - 1) / cus; };
+    if (rounds(2) < rounds(ct)) ct = 2;
+    if (rounds(4) < rounds(ct)) ct = 4;
+  }
   LinearArgs a{};
   a.x = x;
   a.x_stride = x_row_stride;
-  a.w = static_cast<const uint8_t*>(weight);
-  a.scale = scale_inv;
-  a.scale_cols = k / kFp8Block;
-  a.y = y;
-  a.y_stride = y_row_stride;
   a.m = m;
-  a.n = n;
   a.k = k;
-  // 32 output features per workgroup when that still gives a workgroup per CU, else 16
-  const int ct = (n % 32 == 0 && n / 32 >= 256) ? 2 : 1;
-  const int64_t mblocks = (m + kLinRows - 1) / kLinRows;
-  if (mblocks > 65535) return set_error(RIA_ERR_INVALID, "ria_linear_fp8: too many rows");
-  const dim3 grid(static_cast<unsigned>(n / (16 * ct)), static_cast<unsigned>(mblocks));
+  a.count = count;
+  int tile = 0;
+  for (int j = 0; j < count; ++j) {
+    const ria_fp8_proj& q = projs[j];
+    a.p[j] = Fp8Proj{static_cast<const uint8_t*>(q.weight), q.scale_inv, q.y, q.y_row_stride, q.n, tile};
+    tile += (q.n + 16 * ct - 1) / (16 * ct);
+  }
+  const int64_t mblocks = gemv ? 1 : (m + kLinRows - 1) / kLinRows;
+  if (mblocks > 65535) return set_error(RIA_ERR_INVALID, "%s: too many rows", who);
+  const dim3 grid(static_cast<unsigned>(tile), static_cast<unsigned>(mblocks));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (x_dtype == RIA_DT_F16)
+  if (gemv) {
+    if (x_dtype == RIA_DT_F16)
+      launch_gemv<RIA_DT_F16>(a, y_dtype, grid, st);
+    else if (x_dtype == RIA_DT_BF16)
+      launch_gemv<RIA_DT_BF16>(a, y_dtype, grid, st);
+    else
+      launch_gemv<RIA_DT_F32>(a, y_dtype, grid, st);
+  } else if (x_dtype == RIA_DT_F16) {
     launch_linear_ot<RIA_DT_F16>(a, y_dtype, ct, grid, st);
-  else if (x_dtype == RIA_DT_BF16)
+  } else if (x_dtype == RIA_DT_BF16) {
     launch_linear_ot<RIA_DT_BF16>(a, y_dtype, ct, grid, st);
-  else
+  } else {
     launch_linear_ot<RIA_DT_F32>(a, y_dtype, ct, grid, st);
-  return check_launch("ria_linear_fp8");
+  }
+  return check_launch(who);
+}
+
+extern "C" int ria_linear_fp8(int m, int n, int k, const void* x, int x_dtype, int64_t x_row_stride,
+                              const void* weight, const float* scale_inv, void* y, int y_dtype, int64_t y_row_stride,
+                              void* stream) {
+  const ria_fp8_proj p{weight, scale_inv, y, y_row_stride, n};
+  return linear_group("ria_linear_fp8", m, k, x, x_dtype, x_row_stride, 1, &p, y_dtype, stream);
+}
+
+extern "C" int ria_linear_fp8_group(int m, int k, const void* x, int x_dtype, int64_t x_row_stride, int count,
+                                    const ria_fp8_proj* projs, int y_dtype, void* stream) {
+  return linear_group("ria_linear_fp8_group", m, k, x, x_dtype, x_row_stride, count, projs, y_dtype, stream);
 }

@@ -83,6 +83,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "ria_dequant_fp8": (_c_int, [_c_i64, _c_int, _vp, _vp, _vp, _c_int, _vp]),
     "ria_linear_fp8": (_c_int, [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _vp, _c_int, _c_i64, _vp]),
+    "ria_linear_fp8_group": (_c_int, [_c_int, _c_int, _vp, _c_int, _c_i64, _c_int, _vp, _c_int, _vp]),
     "ria_seq_state_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "ria_seq_state_save": (
         _c_int,
@@ -114,6 +115,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_int, _c_int, _vp, _c_i64, _c_i32, _vp, _c_int, _vp, _vp, _c_f32, _vp, _c_int, _vp],
     ),
 }
+
+
+
+class Fp8Proj(ctypes.Structure):
+    """struct ria_fp8_proj: one projection of a ria_linear_fp8_group call."""
+    _fields_ = [("weight", _vp), ("scale_inv", _vp), ("y", _vp), ("y_row_stride", _c_i64), ("n", _c_int)]
+
+
+LINEAR_GROUP_MAX = 4  # projections per ria_linear_fp8_group call
 
 _LIB: ctypes.CDLL | None = None
 

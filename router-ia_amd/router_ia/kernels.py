@@ -531,6 +531,42 @@ def linear_fp8(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor, *
     return out
 
 
+def linear_fp8_group(x: torch.Tensor, projections: list[tuple[torch.Tensor, torch.Tensor]], *,
+                     out: list[torch.Tensor] | None = None,
+                     out_dtype: torch.dtype = torch.float16) -> list[torch.Tensor]:
+    """Up to 4 FP8 projections of the same x in one launch (ria_linear_fp8_group).
+
+    projections: (weight [N_j, K] float8_e4m3fn, scale_inv) pairs; returns /
+    fills y_j [M, N_j] of one dtype, each equal to linear_fp8(x, w_j, s_j).
+    """
+    dev = x.device
+    _require_gpu("x", x, dev)
+    if not 1 <= len(projections) <= nat.LINEAR_GROUP_MAX:
+        raise ValueError(f"1 to {nat.LINEAR_GROUP_MAX} projections per call, got {len(projections)}")
+    shapes = [_fp8_weight(f"weight {j}", w, s, dev) for j, (w, s) in enumerate(projections)]
+    k = shapes[0][1]
+    if any(kk != k for _, kk in shapes):
+        raise ValueError(f"all projections must share K, got {[kk for _, kk in shapes]}")
+    if x.dim() != 2 or x.shape[1] != k or (x.shape[1] > 1 and x.stride(1) != 1):
+        raise ValueError(f"x must be [M, {k}] with contiguous rows, got {tuple(x.shape)}")
+    m = int(x.shape[0])
+    xs = int(x.stride(0)) if m > 1 else k
+    if out is None:
+        out = [torch.empty((m, n), dtype=out_dtype, device=dev) for n, _ in shapes]
+    if len(out) != len(projections) or len({o.dtype for o in out}) != 1:
+        raise ValueError("out must hold one tensor per projection, all of one dtype")
+    arr = (nat.Fp8Proj * len(projections))()
+    for j, ((w, s), (n, _), y) in enumerate(zip(projections, shapes, out)):
+        _require_gpu(f"out {j}", y, dev)
+        if y.dim() != 2 or tuple(y.shape) != (m, n) or (n > 1 and y.stride(1) != 1):
+            raise ValueError(f"out {j} must be [{m}, {n}] with contiguous rows")
+        arr[j] = nat.Fp8Proj(_ptr(w), _ptr(s), _ptr(y), int(y.stride(0)) if m > 1 else n, n)
+    rc = nat.load().ria_linear_fp8_group(m, k, _ptr(x), dtype_code(x), xs, len(projections), ctypes.addressof(arr),
+                                         dtype_code(out[0]), _stream(dev))
+    nat.check(rc, "ria_linear_fp8_group")
+    return out
+
+
 def seq_state_bytes(num_linear_layers: int, num_v_heads: int, conv_dim: int, num_full_layers: int,
                     num_kv_heads: int, tokens: int) -> int:
     """Payload bytes of one sequence's snapshot (ria_seq_state_bytes)."""

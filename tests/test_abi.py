@@ -102,3 +102,34 @@ def test_norm_entry_points_host_validation() -> None:
     rc = lib.ria_gdn_prefill(64, 16, 32, fake, 0, 8192, fake, fake, 0, fake, fake, fake, 32, 0, None, None, fake, 0,
                              fake, 0, 4096, None, fake, 1 << 30, None)
     assert rc == 1 and b"norm_weight" in lib.ria_last_error()
+
+
+def test_fp8_projection_host_validation() -> None:
+    lib = nat.load()
+    fake = ctypes.c_void_p(256)
+    rc = lib.ria_dequant_fp8(4, 40, fake, fake, fake, 1, None)
+    assert rc == 1 and b"multiple of 16" in lib.ria_last_error()
+    rc = lib.ria_linear_fp8(1, 40, 2048, fake, 1, 2048, fake, fake, fake, 1, 40, None)
+    assert rc == 1 and b"multiple of 16" in lib.ria_last_error()
+    rc = lib.ria_linear_fp8(1, 32, 200, fake, 1, 256, fake, fake, fake, 1, 32, None)
+    assert rc == 1 and b"multiple of 128" in lib.ria_last_error()
+    rc = lib.ria_linear_fp8(1, 32, 128 * 257, fake, 1, 128 * 257, fake, fake, fake, 1, 32, None)
+    assert rc == 1 and b"32768" in lib.ria_last_error()
+    rc = lib.ria_linear_fp8(1, 32, 2048, ctypes.c_void_p(8), 1, 2048, fake, fake, fake, 1, 32, None)
+    assert rc == 1 and b"aligned" in lib.ria_last_error()
+    # zero rows: nothing to launch, even with null pointers
+    assert lib.ria_linear_fp8(0, 32, 2048, None, 1, 2048, None, None, None, 1, 32, None) == 0
+
+    def group(*ns, m=1, stride=None):
+        arr = (nat.Fp8Proj * max(1, len(ns)))()
+        for j, n in enumerate(ns):
+            arr[j] = nat.Fp8Proj(256, 256, 256, n if stride is None else stride, n)
+        return lib.ria_linear_fp8_group(m, 2048, fake, 1, 2048, len(ns), ctypes.addressof(arr), 1, None)
+
+    assert group(m=0) == 1 and b"1 to 4" in lib.ria_last_error()
+    assert group(32, 32, 32, 32, 32) == 1 and b"1 to 4" in lib.ria_last_error()
+    assert group(8192, 4096, 40) == 1 and b"projection 2" in lib.ria_last_error()
+    assert group(512, 512, stride=256) == 1 and b"stride" in lib.ria_last_error()
+    assert group(8192, 4096, 32, 32, m=0) == 0
+    rc = lib.ria_linear_fp8_group(1, 2048, fake, 1, 2048, 2, None, 1, None)
+    assert rc == 1 and b"null" in lib.ria_last_error()

@@ -1,4 +1,4 @@
-"""GPU parity: projections with FP8 block-scaled weights (ria_dequant_fp8, ria_linear_fp8).
+"""GPU parity: projections with FP8 block-scaled weights (ria_dequant_fp8, ria_linear_fp8[_group]).
 
 The reference dequantises its float8_e4m3fn checkpoint weights once to fp16
 (qwen36_dequant.py:35-58, qwen36_cached_loop.py:537-542) and runs fp16
@@ -34,12 +34,18 @@ def test_dequant_all_byte_values_bit_exact(gpu, out_dtype):
 
 
 CASES = [  # (m, n, k, x dtype): decode batches, one and two 128-row blocks, 16- and 32-wide tiles
-    (1, 8192, 2048, torch.bfloat16),
+    (1, 8192, 2048, torch.bfloat16),   # up to 16 rows and K a multiple of 512: the one-pass decode kernel
     (7, 4096, 2048, torch.float16),
+    (16, 2048, 4096, torch.float32),
+    (9, 256, 512, torch.bfloat16),     # one wave of K
+    (17, 512, 2048, torch.float16),    # one row past the decode kernel: the streaming kernel
     (32, 2048, 4096, torch.float32),
     (128, 512, 2048, torch.bfloat16),
     (128, 8192, 2048, torch.float16),
     (200, 32, 2048, torch.float16),
+    (5, 1024, 1408, torch.bfloat16),   # 11 chunks: one ring group and a 3-chunk tail
+    (3, 512, 384, torch.float16),      # 3 chunks: the tail alone
+    (1, 64, 128, torch.bfloat16),      # one chunk
 ]
 
 
@@ -66,10 +72,11 @@ def test_linear_fp8_matches_oracle(gpu, m, n, k, xdt):
     assert e_got <= 1.5 * e_ref + 1e-6, (e_got, e_ref)
 
 
-def test_linear_fp8_output_dtypes_round_through_fp16(gpu):
-    announce("linear_fp8: fp32 and bf16 outputs carry the fp16 result")
+@pytest.mark.parametrize("m", [9, 100])
+def test_linear_fp8_output_dtypes_round_through_fp16(gpu, m):
+    announce(f"linear_fp8: M={m} fp32 and bf16 outputs carry the fp16 result")
     w8, s = W.fp8_block_weight(400, 512, 2048)
-    x = torch.randn((9, 2048), generator=torch.Generator().manual_seed(401)).to(torch.bfloat16).to(gpu)
+    x = torch.randn((m, 2048), generator=torch.Generator().manual_seed(401)).to(torch.bfloat16).to(gpu)
     w8, s = w8.to(gpu), s.to(gpu)
     y16 = K.linear_fp8(x, w8, s)
     y32 = K.linear_fp8(x, w8, s, out_dtype=torch.float32)
@@ -77,3 +84,29 @@ def test_linear_fp8_output_dtypes_round_through_fp16(gpu):
     torch.cuda.synchronize()
     assert torch.equal(y32.cpu(), y16.cpu().float())
     assert torch.equal(yb.cpu(), y16.cpu().to(torch.bfloat16))
+
+
+GROUPS = [  # (m, [n_j], k): a DeltaNet layer's input projections, attention q/k/v, 16-wide tiles
+    (1, [8192, 4096, 32, 32], 2048),
+    (128, [8192, 4096, 32, 32], 2048),
+    (37, [8192, 512, 512], 2048),
+    (130, [48, 256], 1408),
+    (40, [8192, 48], 2048),   # 64-wide tiles: the 48-wide projection fills part of one
+]
+
+
+@pytest.mark.parametrize("m,ns,k", GROUPS)
+def test_linear_fp8_group_equals_separate_calls(gpu, m, ns, k):
+    announce(f"linear_fp8_group: M={m} N={ns} K={k}")
+    proj = [W.fp8_block_weight(500 + j, n, k) for j, n in enumerate(ns)]
+    x = torch.randn((m, k), generator=torch.Generator().manual_seed(510 + m)).to(torch.bfloat16).to(gpu)
+    proj_d = [(w.to(gpu), s.to(gpu)) for w, s in proj]
+    ys = K.linear_fp8_group(x, proj_d, out_dtype=torch.bfloat16)
+    for j, (w, s) in enumerate(proj_d):
+        sep = K.linear_fp8(x, w, s, out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        assert torch.equal(ys[j].cpu(), sep.cpu()), f"projection {j}"
+    # and each against the oracle
+    for j, (w, s) in enumerate(proj):
+        want = O.projection_fp8(x.cpu(), w, s).to(torch.bfloat16)
+        assert_act_close(ys[j].cpu(), want, f"projection {j}")

@@ -35,7 +35,7 @@ namespace ria {
 constexpr int kFp8Block = 128;  // scale block edge (qwen36_dequant.py:13)
 constexpr int kLinRing = 12;    // weight chunks in flight per workgroup
 constexpr int kXAhead = 2;      // chunks of x loaded ahead of the MFMAs
-constexpr int kLinRows = 128;   // rows of x per workgroup (4 waves x 32)
+constexpr int kLinRows = 128;   // most rows of x per workgroup (4 consumer waves x 32)
 
 // Two fp8 e4m3 (OCP, float8_e4m3fn) bytes of `w` (low pair or high pair) to fp32.
 template <bool HIGH>
@@ -104,6 +104,7 @@ struct LinearArgs {
   const void* x;
   int64_t x_stride;
   int m, k, count;
+  int mt;               // rows of x per workgroup (streaming kernel): 64 or 128
   Fp8Proj p[kLinGroup];
 };
 
@@ -190,8 +191,8 @@ __global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
       tile0 = a.p[j].tile0;
     }
   const int n0 = (bx - tile0) * kCols;
-  const int m0 = blockIdx.y * kLinRows;
-  const int rows = min(kLinRows, a.m - m0);
+  const int m0 = blockIdx.y * a.mt;
+  const int rows = min(a.mt, a.m - m0);
   const int chunks = a.k / kFp8Block;
   const int groups = chunks / kLinRing, tail = chunks - groups * kLinRing;
 
@@ -553,24 +554,31 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
       return set_error(RIA_ERR_INVALID, "%s: weight must be 16-byte aligned (projection %d)", who, j);
   }
   const bool gemv = m <= kGemvRows && k % kGemvSlice == 0 && k / kGemvSlice <= kGemvMaxWaves;
-  // Streaming kernel: 16 CT output features per workgroup.  Every workgroup
-  // reads all of its 128 rows of x (from L2), which costs more than its
-  // weights, so the width is the one that needs the fewest rounds of
-  // workgroups over the CUs, and the narrowest of those (more of the CUs busy).
-  int ct = 1;
+  // Streaming kernel: workgroups of mt rows x 16 ct output features.  A
+  // workgroup reads its mt rows of x (from L2) and its weights through the
+  // CU's L1, whose misses in flight bound the rate, so the shape is the one
+  // whose busiest CU moves the fewest bytes: (workgroups per CU) x (x bytes
+  // + weight bytes of one workgroup); ties go to more workgroups.
+  int ct = 1, mt = kLinRows;
   if (!gemv) {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
       cus = 256;
-    auto tiles = [&](int c) {
-      int64_t t = 0;
-      for (int j = 0; j < count; ++j) t += (projs[j].n + 16 * c - 1) / (16 * c);
-      return t;
-    };
-    auto rounds = [&](int c) { return (tiles(c) + cus - 1) / cus; };
-    if (rounds(2) < rounds(ct)) ct = 2;
-    if (rounds(4) < rounds(ct)) ct = 4;
+    int64_t best = -1, best_wgs = 0;
+    for (const int r : {kLinRows, kLinRows / 2})
+      for (const int c : {1, 2, 4}) {
+        int64_t wgs = 0;
+        for (int j = 0; j < count; ++j) wgs += (projs[j].n + 16 * c - 1) / (16 * c);
+        wgs *= (m + r - 1) / r;
+        const int64_t per_cu = (wgs + cus - 1) / cus * ((int64_t)std::min(r, m) * k * 2 + (int64_t)16 * c * k);
+        if (best < 0 || per_cu < best || (per_cu == best && wgs > best_wgs)) {
+          best = per_cu;
+          best_wgs = wgs;
+          ct = c;
+          mt = r;
+        }
+      }
   }
   LinearArgs a{};
   a.x = x;
@@ -578,13 +586,14 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
   a.m = m;
   a.k = k;
   a.count = count;
+  a.mt = mt;
   int tile = 0;
   for (int j = 0; j < count; ++j) {
     const ria_fp8_proj& q = projs[j];
     a.p[j] = Fp8Proj{static_cast<const uint8_t*>(q.weight), q.scale_inv, q.y, q.y_row_stride, q.n, tile};
     tile += (q.n + 16 * ct - 1) / (16 * ct);
   }
-  const int64_t mblocks = gemv ? 1 : (m + kLinRows - 1) / kLinRows;
+  const int64_t mblocks = gemv ? 1 : (m + mt - 1) / mt;
   if (mblocks > 65535) return set_error(RIA_ERR_INVALID, "%s: too many rows", who);
   const dim3 grid(static_cast<unsigned>(tile), static_cast<unsigned>(mblocks));
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -40,6 +40,8 @@ CASES = [  # (m, n, k, x dtype): decode batches, one and two 128-row blocks, 16-
     (9, 256, 512, torch.bfloat16),     # one wave of K
     (17, 512, 2048, torch.float16),    # one row past the decode kernel: the streaming kernel
     (32, 2048, 4096, torch.float32),
+    (128, 2048, 4096, torch.float16),  # 64-row workgroups: two per 16 features
+    (70, 2048, 4096, torch.bfloat16),  # .. the second one with 6 rows
     (128, 512, 2048, torch.bfloat16),
     (128, 8192, 2048, torch.float16),
     (200, 32, 2048, torch.float16),

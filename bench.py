@@ -428,7 +428,9 @@ def proj_main(args, wl) -> int:
         "data": "synthetic (random FP8 weights and scales, random activations)",
         "config": {"workload": wl["desc"], "batch": gpu["batch"], "fp8_weight_GB": round(gpu["weight_bytes"] / 1e9, 3),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "linear_fp8_kernel (ria_linear_fp8_group), all launches of the step",
+        "roofline": {"bound": "hbm",
+                     "kernel": ("gemv_fp8_kernel" if gpu["batch"] <= 16 else "linear_fp8_kernel")
+                     + " (ria_linear_fp8_group), all launches of the step",
                      "achieved": round(gpu["achieved_GBps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gpu["achieved_GBps"] / HBM_PEAK_GBPS, 4), "traffic": None,
                      "mfma_TFLOPs": round(gpu["TFLOPs"], 1),

@@ -83,6 +83,13 @@ WORKLOADS = {
                     desc="every projection of the 40-layer stack for one decode step of B=128 tokens, FP8 "
                          "block-scaled weights (DeltaNet in_proj_qkv/z/a/b + out_proj, attention q/k/v/o_proj), "
                          "fp16 outputs"),
+    "forward128": dict(batch=128, lo=1024, hi=32768, seed=4, forward=True,
+                       desc="attention side of the 40-layer stack for one decode step of B=128 sequences (context "
+                            "U[1024,32768], seed 4): input RMSNorm, FP8 block-scaled projections, conv + DeltaNet + "
+                            "gated RMSNorm / q,k norms + RoPE + paged GQA attention + gate, output projection and "
+                            "residual add per layer (router_ia.batched_forward; the MoE block is the caller's)"),
+    "forward1": dict(batch=1, lo=16384, hi=16384, seed=4, forward=True,
+                     desc="the forward128 loop for one sequence at context 16384 (the reference's batch-1 decode)"),
     "proj1": dict(batch=1, seed=5, proj=True,
                   desc="every projection of the 40-layer stack for one decode step of B=1 token, FP8 block-scaled "
                        "weights, fp16 outputs"),
@@ -411,6 +418,86 @@ def run_proj_gpu(args, wl) -> dict:
             "TFLOPs": flop / step_s / 1e12}
 
 
+def run_forward_gpu(args, wl) -> dict:
+    """BatchedForward.step over the 40-layer stack with synthetic FP8 weights, `steps` times."""
+    from router_ia import batched_forward as BF
+    from router_ia import workloads as W
+    from router_ia.batched_state import BatchedAttentionState
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    batch = wl["batch"]
+    lengths = W.ragged_lengths(wl["seed"], batch, wl["lo"], wl["hi"])
+    total_new = args.warmup + args.steps
+    max_context = max(lengths) + total_new + 16
+    num_pages = sum((n + total_new + 15) // 16 for n in lengths) + batch
+    st = BatchedAttentionState(batch, max_context, num_pages=num_pages, device=dev, page_shuffle_seed=wl["seed"])
+    st.set_positions(lengths)
+    st.reserve(total_new)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(wl["seed"])
+    for li in range(st.num_linear_layers):
+        st.linear_states[li].normal_(0.0, 0.02, generator=gen)
+        st.conv_rings[li].normal_(0.0, 1.0, generator=gen)
+    for fi in range(st.num_full_layers):
+        st.kv.k[fi].normal_(0.0, 1.0, generator=gen)
+        st.kv.v[fi].normal_(0.0, 1.0, generator=gen)
+    layers = [BF.layer_weights(W.synthetic_layer(100 * wl["seed"] + m, m, device=dev, on_device=True), m)
+              for m in range(LAYERS)]
+    fwd = BF.BatchedForward(st, layers)
+    xs = torch.randn((total_new, batch, BF.HIDDEN), generator=gen, device=dev)
+    wbytes = sum(p.weight.numel() + 4 * p.scale_inv.numel() for w in layers for p in vars(w).values()
+                 if isinstance(p, BF.Fp8Projection))
+    torch.cuda.synchronize()
+    log(f"[bench] {wl['desc']}: B={batch}, mean context {sum(lengths) / batch:.0f}, "
+        f"{wbytes / 1e9:.3f} GB of FP8 weights, {torch.cuda.memory_allocated(dev) / 2**30:.1f} GiB allocated")
+    for s in range(args.warmup):
+        fwd.step(xs[s])
+    torch.cuda.synchronize()
+    ctx = [n + 1 for n in st._host_seen]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for s in range(args.warmup, total_new):
+        fwd.step(xs[s])
+    t1.record()
+    torch.cuda.synchronize()
+    elapsed = t0.elapsed_time(t1) / 1e3
+    step_s = elapsed / args.steps
+    # bytes of one step: the state path (states, conv rings, KV, norm inputs), the
+    # projection weights, and the residual stream in and out of every layer
+    nbytes = step_bytes(ctx, norms=True) + wbytes + LAYERS * batch * BF.HIDDEN * 4 * 2
+    return {"batch": batch, "elapsed_s": elapsed, "ms_per_step": step_s * 1e3, "tok_s": batch / step_s,
+            "weight_bytes": wbytes, "step_bytes": nbytes, "achieved_GBps": nbytes / step_s / 1e9,
+            "mean_ctx": sum(lengths) / batch}
+
+
+def forward_main(args, wl) -> int:
+    gpu = run_forward_gpu(args, wl)
+    result = {
+        "metric": "decode tok/s through the attention side of the 40-layer stack (norms, FP8 projections, state "
+                  "path, output projections, residual)",
+        "value": round(gpu["tok_s"], 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 state and residual, bf16 KV, fp8 e4m3 weights with fp16 MFMA",
+        "data": "synthetic (seeded random state, KV, FP8 weights and residual-stream inputs)",
+        "config": {"workload": wl["desc"], "batch": gpu["batch"], "mean_context": round(gpu["mean_ctx"]),
+                   "fp8_weight_GB": round(gpu["weight_bytes"] / 1e9, 3), "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "whole step (all launches)", "achieved": round(gpu["achieved_GBps"], 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gpu["achieved_GBps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "bytes_per_step": gpu["step_bytes"]},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def proj_main(args, wl) -> int:
     gpu = run_proj_gpu(args, wl)
     result = {
@@ -712,6 +799,8 @@ def main() -> int:
         return snapshot_main(args, wl)
     if wl.get("proj"):
         return proj_main(args, wl)
+    if wl.get("forward"):
+        return forward_main(args, wl)
     gpu = run_gpu(args, wl)
     prof = profiled_traffic("attn_splitk_kernel") if args.workload == "ragged128" else None
     if prof:

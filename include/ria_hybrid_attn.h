@@ -406,7 +406,7 @@ int ria_kv_gather(int batch, int num_kv_heads,
  * Built for decode-sized m (one weight pass per 128 rows of x); k up to 32768.
  *
  * ria_linear_fp8_group: 1 to 4 such projections of the same x in one launch,
- * each with its own n, weight, scales and y (all y of y_dtype).  It replaces
+ * each with its own n, weight, scales, y and y dtype.  It replaces
  * the reference's run of F.linear calls on one normed hidden state: DeltaNet
  * in_proj_qkv / in_proj_z / in_proj_a / in_proj_b (qwen36_attention_cache.py:
  * 232-247, 268) and attention q_proj / k_proj / v_proj (:295-301); results
@@ -418,6 +418,7 @@ typedef struct ria_fp8_proj {
   void* y;                 /* [m, n], rows y_row_stride elements apart */
   int64_t y_row_stride;
   int n;
+  int y_dtype;             /* RIA_DT_*: the fp16 result stored in this dtype */
 } ria_fp8_proj;
 
 int ria_dequant_fp8(int64_t rows, int cols, const void* weight, const float* scale_inv,
@@ -428,7 +429,7 @@ int ria_linear_fp8(int m, int n, int k, const void* x, int x_dtype, int64_t x_ro
                    void* y, int y_dtype, int64_t y_row_stride, void* stream);
 
 int ria_linear_fp8_group(int m, int k, const void* x, int x_dtype, int64_t x_row_stride,
-                         int count, const ria_fp8_proj* projs, int y_dtype, void* stream);
+                         int count, const ria_fp8_proj* projs, void* stream);
 
 /*
  * Sequence snapshots: one row's DeltaNet states, conv ring and KV pages as a

@@ -97,6 +97,7 @@ struct Fp8Proj {
   void* y;              // [m, n], rows y_stride elements apart
   int64_t y_stride;
   int n;
+  int y_dtype;          // RIA_DT_*: y holds the fp16 result in this dtype
   int tile0;            // first column tile of this projection
 };
 
@@ -163,7 +164,7 @@ struct WeightSlot<1> {
 // ring slot u is a compile-time index), then the K % (128 kLinRing) tail:
 // an exit inside the ring loop makes the compiler join the ring registers
 // at each exit, which waits for every weight load in flight.
-template <int XT, int OT, int CT>
+template <int XT, int CT>
 __global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
   using F16 = Kv16<RIA_DT_F16>;
   constexpr int kCols = 16 * CT;             // output features per workgroup
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
   const float* scale = a.p[0].scale;
   void* y = a.p[0].y;
   int64_t y_stride = a.p[0].y_stride;
-  int n = a.p[0].n, tile0 = 0;
+  int n = a.p[0].n, y_dtype = a.p[0].y_dtype, tile0 = 0;
 #pragma unroll
   for (int j = 1; j < kLinGroup; ++j)
     if (j < a.count && bx >= a.p[j].tile0) {
@@ -188,6 +189,7 @@ __global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
       y = a.p[j].y;
       y_stride = a.p[j].y_stride;
       n = a.p[j].n;
+      y_dtype = a.p[j].y_dtype;
       tile0 = a.p[j].tile0;
     }
   const int n0 = (bx - tile0) * kCols;
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
     static_for<kLinRing>([&](auto u) {
       if (u < tail) step(u, groups * kLinRing + u);
     });
-    // D tile rows 4 g4 + i, column n16; F.linear's fp16 result, stored as OT
+    // D tile rows 4 g4 + i, column n16; F.linear's fp16 result, stored as y_dtype
 #pragma unroll
     for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
@@ -303,8 +305,8 @@ __global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
         for (int i = 0; i < 4; ++i) {
           const int r = 32 * wave + 16 * rt + 4 * g4 + i;
           if (r < rows && n0 + 16 * ct + n16 < n)
-            store_act<OT>(y, (int64_t)(m0 + r) * y_stride + n0 + 16 * ct + n16,
-                          through_dtype<RIA_DT_F16>(acc[rt][ct][i]));
+            store_act_dt(y, (int64_t)(m0 + r) * y_stride + n0 + 16 * ct + n16,
+                         through_dtype<RIA_DT_F16>(acc[rt][ct][i]), y_dtype);
         }
   };
   if (32 * wave + 16 < rows)
@@ -330,7 +332,7 @@ constexpr int kGemvRows = 16;    // rows of x per workgroup
 constexpr int kGemvMaxWaves = 8; // K <= 4096
 constexpr int kGemvStageRows = 4; // x rows staged through LDS
 
-template <int XT, int OT>
+template <int XT>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const LinearArgs a) {
   using F16 = Kv16<RIA_DT_F16>;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -342,7 +344,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
   const float* scale = a.p[0].scale;
   void* y = a.p[0].y;
   int64_t y_stride = a.p[0].y_stride;
-  int tile0 = 0;
+  int y_dtype = a.p[0].y_dtype, tile0 = 0;
 #pragma unroll
   for (int j = 1; j < kLinGroup; ++j)
     if (j < a.count && bx >= a.p[j].tile0) {
@@ -350,6 +352,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
       scale = a.p[j].scale;
       y = a.p[j].y;
       y_stride = a.p[j].y_stride;
+      y_dtype = a.p[j].y_dtype;
       tile0 = a.p[j].tile0;
     }
   const int n0 = (bx - tile0) * 16;
@@ -452,46 +455,31 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
 #pragma unroll
       for (int i = 0; i < 4; ++i) t[i] += u[i];
     }
-    // D rows (tokens) 4 g4 + i, column (feature) c16; F.linear's fp16 result, stored as OT
+    // D rows (tokens) 4 g4 + i, column (feature) c16; F.linear's fp16 result, stored as y_dtype
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * g4 + i;
-      if (r < rows) store_act<OT>(y, (int64_t)(m0 + r) * y_stride + n0 + c16, through_dtype<RIA_DT_F16>(t[i]));
+      if (r < rows)
+        store_act_dt(y, (int64_t)(m0 + r) * y_stride + n0 + c16, through_dtype<RIA_DT_F16>(t[i]), y_dtype);
     }
   }
 }
 
 template <int XT>
-static void launch_gemv(const LinearArgs& a, int out_dtype, dim3 grid, hipStream_t st) {
+static void launch_gemv(const LinearArgs& a, dim3 grid, hipStream_t st) {
   const int waves = a.k / kGemvSlice;
-  const dim3 block(64 * waves);
   const size_t lds = static_cast<size_t>(waves) * (a.m <= kGemvStageRows ? a.m : 1) * 64 * sizeof(u32x4);
-  if (out_dtype == RIA_DT_BF16)
-    hipLaunchKernelGGL((gemv_fp8_kernel<XT, RIA_DT_BF16>), grid, block, lds, st, a);
-  else if (out_dtype == RIA_DT_F16)
-    hipLaunchKernelGGL((gemv_fp8_kernel<XT, RIA_DT_F16>), grid, block, lds, st, a);
-  else
-    hipLaunchKernelGGL((gemv_fp8_kernel<XT, RIA_DT_F32>), grid, block, lds, st, a);
-}
-
-template <int XT, int OT>
-static void launch_linear_ct(const LinearArgs& a, int ct, dim3 grid, hipStream_t st) {
-  if (ct == 4)
-    hipLaunchKernelGGL((linear_fp8_kernel<XT, OT, 4>), grid, dim3(512), 0, st, a);
-  else if (ct == 2)
-    hipLaunchKernelGGL((linear_fp8_kernel<XT, OT, 2>), grid, dim3(512), 0, st, a);
-  else
-    hipLaunchKernelGGL((linear_fp8_kernel<XT, OT, 1>), grid, dim3(512), 0, st, a);
+  hipLaunchKernelGGL((gemv_fp8_kernel<XT>), grid, dim3(64 * waves), lds, st, a);
 }
 
 template <int XT>
-static void launch_linear_ot(const LinearArgs& a, int out_dtype, int ct, dim3 grid, hipStream_t st) {
-  if (out_dtype == RIA_DT_BF16)
-    launch_linear_ct<XT, RIA_DT_BF16>(a, ct, grid, st);
-  else if (out_dtype == RIA_DT_F16)
-    launch_linear_ct<XT, RIA_DT_F16>(a, ct, grid, st);
+static void launch_linear(const LinearArgs& a, int ct, dim3 grid, hipStream_t st) {
+  if (ct == 4)
+    hipLaunchKernelGGL((linear_fp8_kernel<XT, 4>), grid, dim3(512), 0, st, a);
+  else if (ct == 2)
+    hipLaunchKernelGGL((linear_fp8_kernel<XT, 2>), grid, dim3(512), 0, st, a);
   else
-    launch_linear_ct<XT, RIA_DT_F32>(a, ct, grid, st);
+    hipLaunchKernelGGL((linear_fp8_kernel<XT, 1>), grid, dim3(512), 0, st, a);
 }
 
 static bool lin_dtype_ok(int dt) { return dt == RIA_DT_BF16 || dt == RIA_DT_F16 || dt == RIA_DT_F32; }
@@ -527,19 +515,20 @@ extern "C" int ria_dequant_fp8(int64_t rows, int cols, const void* weight, const
 // Validates and launches one group of projections of the same x (shared by
 // ria_linear_fp8 and ria_linear_fp8_group; `who` names the entry point in errors).
 static int linear_group(const char* who, int m, int k, const void* x, int x_dtype, int64_t x_row_stride, int count,
-                        const ria_fp8_proj* projs, int y_dtype, void* stream) {
+                        const ria_fp8_proj* projs, void* stream) {
   if (count < 1 || count > kLinGroup) return set_error(RIA_ERR_INVALID, "%s: 1 to %d projections per call", who, kLinGroup);
   if (m < 0 || k <= 0) return set_error(RIA_ERR_INVALID, "%s: bad sizes", who);
   if (k % kFp8Block || k / kFp8Block > kLinMaxChunks)
     return set_error(RIA_ERR_INVALID, "%s: K must be a multiple of 128 up to %d (got %d)", who,
                      kFp8Block * kLinMaxChunks, k);
-  if (!lin_dtype_ok(x_dtype) || !lin_dtype_ok(y_dtype)) return set_error(RIA_ERR_INVALID, "%s: unknown dtype code", who);
+  if (!lin_dtype_ok(x_dtype)) return set_error(RIA_ERR_INVALID, "%s: unknown dtype code", who);
   if (!projs) return set_error(RIA_ERR_INVALID, "%s: null projection list", who);
   for (int j = 0; j < count; ++j) {
     const ria_fp8_proj& q = projs[j];
     if (q.n <= 0 || q.n % 16)
       return set_error(RIA_ERR_INVALID, "%s: N must be a positive multiple of 16 (projection %d: %d)", who, j, q.n);
     if (q.y_row_stride < q.n) return set_error(RIA_ERR_INVALID, "%s: y row stride too small (projection %d)", who, j);
+    if (!lin_dtype_ok(q.y_dtype)) return set_error(RIA_ERR_INVALID, "%s: unknown dtype code (projection %d)", who, j);
   }
   if (m == 0) return RIA_OK;
   if (!x) return set_error(RIA_ERR_INVALID, "%s: null x", who);
@@ -590,7 +579,7 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
   int tile = 0;
   for (int j = 0; j < count; ++j) {
     const ria_fp8_proj& q = projs[j];
-    a.p[j] = Fp8Proj{static_cast<const uint8_t*>(q.weight), q.scale_inv, q.y, q.y_row_stride, q.n, tile};
+    a.p[j] = Fp8Proj{static_cast<const uint8_t*>(q.weight), q.scale_inv, q.y, q.y_row_stride, q.n, q.y_dtype, tile};
     tile += (q.n + 16 * ct - 1) / (16 * ct);
   }
   const int64_t mblocks = gemv ? 1 : (m + mt - 1) / mt;
@@ -599,17 +588,17 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (gemv) {
     if (x_dtype == RIA_DT_F16)
-      launch_gemv<RIA_DT_F16>(a, y_dtype, grid, st);
+      launch_gemv<RIA_DT_F16>(a, grid, st);
     else if (x_dtype == RIA_DT_BF16)
-      launch_gemv<RIA_DT_BF16>(a, y_dtype, grid, st);
+      launch_gemv<RIA_DT_BF16>(a, grid, st);
     else
-      launch_gemv<RIA_DT_F32>(a, y_dtype, grid, st);
+      launch_gemv<RIA_DT_F32>(a, grid, st);
   } else if (x_dtype == RIA_DT_F16) {
-    launch_linear_ot<RIA_DT_F16>(a, y_dtype, ct, grid, st);
+    launch_linear<RIA_DT_F16>(a, ct, grid, st);
   } else if (x_dtype == RIA_DT_BF16) {
-    launch_linear_ot<RIA_DT_BF16>(a, y_dtype, ct, grid, st);
+    launch_linear<RIA_DT_BF16>(a, ct, grid, st);
   } else {
-    launch_linear_ot<RIA_DT_F32>(a, y_dtype, ct, grid, st);
+    launch_linear<RIA_DT_F32>(a, ct, grid, st);
   }
   return check_launch(who);
 }
@@ -617,11 +606,11 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
 extern "C" int ria_linear_fp8(int m, int n, int k, const void* x, int x_dtype, int64_t x_row_stride,
                               const void* weight, const float* scale_inv, void* y, int y_dtype, int64_t y_row_stride,
                               void* stream) {
-  const ria_fp8_proj p{weight, scale_inv, y, y_row_stride, n};
-  return linear_group("ria_linear_fp8", m, k, x, x_dtype, x_row_stride, 1, &p, y_dtype, stream);
+  const ria_fp8_proj p{weight, scale_inv, y, y_row_stride, n, y_dtype};
+  return linear_group("ria_linear_fp8", m, k, x, x_dtype, x_row_stride, 1, &p, stream);
 }
 
 extern "C" int ria_linear_fp8_group(int m, int k, const void* x, int x_dtype, int64_t x_row_stride, int count,
-                                    const ria_fp8_proj* projs, int y_dtype, void* stream) {
-  return linear_group("ria_linear_fp8_group", m, k, x, x_dtype, x_row_stride, count, projs, y_dtype, stream);
+                                    const ria_fp8_proj* projs, void* stream) {
+  return linear_group("ria_linear_fp8_group", m, k, x, x_dtype, x_row_stride, count, projs, stream);
 }

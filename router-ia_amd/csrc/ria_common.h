@@ -108,6 +108,16 @@ __device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
   }
 }
 
+// store_act with the dtype as a run-time value.
+__device__ __forceinline__ void store_act_dt(void* p, int64_t i, float v, int dt) {
+  if (dt == RIA_DT_BF16)
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
+  else if (dt == RIA_DT_F16)
+    static_cast<uint16_t*>(p)[i] = f32_to_f16_bits(v);
+  else
+    static_cast<float*>(p)[i] = v;
+}
+
 // Eight consecutive activation elements starting at element i (i a multiple
 // of 8, base pointer 16-byte aligned), widened to fp32.
 template <int DT>

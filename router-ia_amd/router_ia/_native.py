@@ -83,7 +83,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "ria_dequant_fp8": (_c_int, [_c_i64, _c_int, _vp, _vp, _vp, _c_int, _vp]),
     "ria_linear_fp8": (_c_int, [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _vp, _c_int, _c_i64, _vp]),
-    "ria_linear_fp8_group": (_c_int, [_c_int, _c_int, _vp, _c_int, _c_i64, _c_int, _vp, _c_int, _vp]),
+    "ria_linear_fp8_group": (_c_int, [_c_int, _c_int, _vp, _c_int, _c_i64, _c_int, _vp, _vp]),
     "ria_seq_state_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "ria_seq_state_save": (
         _c_int,
@@ -120,7 +120,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
 
 class Fp8Proj(ctypes.Structure):
     """struct ria_fp8_proj: one projection of a ria_linear_fp8_group call."""
-    _fields_ = [("weight", _vp), ("scale_inv", _vp), ("y", _vp), ("y_row_stride", _c_i64), ("n", _c_int)]
+    _fields_ = [("weight", _vp), ("scale_inv", _vp), ("y", _vp), ("y_row_stride", _c_i64), ("n", _c_int),
+                ("y_dtype", _c_int)]
 
 
 LINEAR_GROUP_MAX = 4  # projections per ria_linear_fp8_group call

@@ -533,11 +533,11 @@ def linear_fp8(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor, *
 
 def linear_fp8_group(x: torch.Tensor, projections: list[tuple[torch.Tensor, torch.Tensor]], *,
                      out: list[torch.Tensor] | None = None,
-                     out_dtype: torch.dtype = torch.float16) -> list[torch.Tensor]:
+                     out_dtype: torch.dtype | list[torch.dtype] = torch.float16) -> list[torch.Tensor]:
     """Up to 4 FP8 projections of the same x in one launch (ria_linear_fp8_group).
 
     projections: (weight [N_j, K] float8_e4m3fn, scale_inv) pairs; returns /
-    fills y_j [M, N_j] of one dtype, each equal to linear_fp8(x, w_j, s_j).
+    fills y_j [M, N_j] (each in its own dtype), each equal to linear_fp8(x, w_j, s_j).
     """
     dev = x.device
     _require_gpu("x", x, dev)
@@ -552,17 +552,18 @@ def linear_fp8_group(x: torch.Tensor, projections: list[tuple[torch.Tensor, torc
     m = int(x.shape[0])
     xs = int(x.stride(0)) if m > 1 else k
     if out is None:
-        out = [torch.empty((m, n), dtype=out_dtype, device=dev) for n, _ in shapes]
-    if len(out) != len(projections) or len({o.dtype for o in out}) != 1:
-        raise ValueError("out must hold one tensor per projection, all of one dtype")
+        dts = out_dtype if isinstance(out_dtype, (list, tuple)) else [out_dtype] * len(shapes)
+        out = [torch.empty((m, n), dtype=dt, device=dev) for (n, _), dt in zip(shapes, dts)]
+    if len(out) != len(projections):
+        raise ValueError("out must hold one tensor per projection")
     arr = (nat.Fp8Proj * len(projections))()
     for j, ((w, s), (n, _), y) in enumerate(zip(projections, shapes, out)):
         _require_gpu(f"out {j}", y, dev)
         if y.dim() != 2 or tuple(y.shape) != (m, n) or (n > 1 and y.stride(1) != 1):
             raise ValueError(f"out {j} must be [{m}, {n}] with contiguous rows")
-        arr[j] = nat.Fp8Proj(_ptr(w), _ptr(s), _ptr(y), int(y.stride(0)) if m > 1 else n, n)
+        arr[j] = nat.Fp8Proj(_ptr(w), _ptr(s), _ptr(y), int(y.stride(0)) if m > 1 else n, n, dtype_code(y))
     rc = nat.load().ria_linear_fp8_group(m, k, _ptr(x), dtype_code(x), xs, len(projections), ctypes.addressof(arr),
-                                         dtype_code(out[0]), _stream(dev))
+                                         _stream(dev))
     nat.check(rc, "ria_linear_fp8_group")
     return out
 

@@ -1,8 +1,10 @@
 """Seeded synthetic inputs for the hybrid-attention workloads.
 
 Shapes are the model family's (16 QK heads x 128, 32 V heads x 128, conv over
-8192 channels; full attention 16 Q / 2 KV heads x 256).  Projections are
-excluded: each layer step gets its q/k/v, gate and decay inputs directly.
+8192 channels; full attention 16 Q / 2 KV heads x 256).  The layer-step
+workloads exclude the projections (each step gets its q/k/v, gate and decay
+inputs directly); ``synthetic_layer`` gives whole layers, FP8 projections
+included, for the batched forward loop.
 
 Gating inputs are drawn so that the raw-gate formula of the reference
 (qwen36_attention_cache.py:242-250) reproduces the requested distributions:
@@ -104,18 +106,58 @@ FP8_MAX = 448.0  # largest finite float8_e4m3fn
 
 
 def fp8_block_weight(seed: int, n: int, k: int, std: float = 0.02,
-                     device="cpu") -> tuple[torch.Tensor, torch.Tensor]:
+                     device="cpu", on_device: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
     """A synthetic block-FP8 projection weight: float8_e4m3fn [n, k] and fp32 scale_inv [ceil(n/128), ceil(k/128)].
 
     Quantised the way block-FP8 checkpoints are: per 128x128 block,
-    scale_inv = max|w| / 448 and w8 = e4m3(w / scale_inv).
+    scale_inv = max|w| / 448 and w8 = e4m3(w / scale_inv).  Drawn on the CPU
+    (the values of a seed do not depend on the device) unless on_device.
     """
-    g = _gen(seed, "cpu")
-    w = torch.randn((n, k), generator=g) * std
+    gen_dev = device if on_device else "cpu"
+    g = _gen(seed, gen_dev)
+    w = torch.randn((n, k), generator=g, device=gen_dev) * std
     nb, kb = (n + 127) // 128, (k + 127) // 128
-    pad = torch.zeros((nb * 128, kb * 128))
+    pad = torch.zeros((nb * 128, kb * 128), device=gen_dev)
     pad[:n, :k] = w
     amax = pad.reshape(nb, 128, kb, 128).abs().amax(dim=(1, 3))
+    del pad
     scale_inv = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
     q = (w / scale_inv.repeat_interleave(128, 0).repeat_interleave(128, 1)[:n, :k]).clamp(-FP8_MAX, FP8_MAX)
     return q.to(torch.float8_e4m3fn).to(device), scale_inv.float().to(device)
+
+
+# (N, K) of each FP8 projection of a layer, by checkpoint name (hidden 2048;
+# qwen36_attention_cache.py:232-247, 268, 295-301, 318-320)
+LINEAR_PROJECTIONS = {"in_proj_qkv": (CONV_DIM, 2048), "in_proj_z": (NUM_V_HEADS * HEAD_DIM, 2048),
+                      "in_proj_a": (NUM_V_HEADS, 2048), "in_proj_b": (NUM_V_HEADS, 2048),
+                      "out_proj": (2048, NUM_V_HEADS * HEAD_DIM)}
+FULL_PROJECTIONS = {"q_proj": (2 * FULL_Q_HEADS * FULL_HEAD_DIM, 2048), "k_proj": (FULL_KV_HEADS * FULL_HEAD_DIM, 2048),
+                    "v_proj": (FULL_KV_HEADS * FULL_HEAD_DIM, 2048), "o_proj": (2048, FULL_Q_HEADS * FULL_HEAD_DIM)}
+
+
+def synthetic_layer(seed: int, model_layer: int, device="cpu", on_device: bool = False) -> dict[str, torch.Tensor]:
+    """One layer's weights as a checkpoint holds them, keyed by the checkpoint's suffixes.
+
+    Model layer 4i + 3 is full attention, the others Gated DeltaNet
+    (qwen36_40layer_loop.py:68-78).  Projections are block-FP8 (``<name>.weight``
+    e4m3 and ``<name>.weight_scale_inv``); norm weights are fp32 holding bf16
+    values; the conv weight is bf16.
+    """
+    norms = norm_params(seed, device)
+    out = {"input_layernorm.weight": norms["input_norm"]}
+    if model_layer % 4 == 3:
+        for j, (name, (n, k)) in enumerate(FULL_PROJECTIONS.items()):
+            w8, s = fp8_block_weight(seed * 16 + j, n, k, 0.02, device=device, on_device=on_device)
+            out[f"self_attn.{name}.weight"], out[f"self_attn.{name}.weight_scale_inv"] = w8, s
+        out["self_attn.q_norm.weight"] = norms["q_norm"]
+        out["self_attn.k_norm.weight"] = norms["k_norm"]
+    else:
+        for j, (name, (n, k)) in enumerate(LINEAR_PROJECTIONS.items()):
+            w8, s = fp8_block_weight(seed * 16 + j, n, k, 0.02, device=device, on_device=on_device)
+            out[f"linear_attn.{name}.weight"], out[f"linear_attn.{name}.weight_scale_inv"] = w8, s
+        p = gdn_layer_params(seed, device)
+        out["linear_attn.conv1d.weight"] = p["conv_weight"]
+        out["linear_attn.A_log"] = p["A_log"]
+        out["linear_attn.dt_bias"] = p["dt_bias"]
+        out["linear_attn.norm.weight"] = norms["gated_norm"]
+    return out

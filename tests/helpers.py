@@ -19,6 +19,21 @@ def assert_act_close(got: torch.Tensor, want: torch.Tensor, what: str = "") -> N
     torch.testing.assert_close(got, want, rtol=ACT_RTOL, atol=ACT_ATOL, msg=lambda m: f"{what}: {m}")
 
 
+def assert_residual_close(got: torch.Tensor, want: torch.Tensor, layers: int, what: str = "") -> None:
+    """An fp32 residual stream after `layers` layers that each add an fp16-rounded projection.
+
+    Two correct implementations may round each layer's fp16 projection output
+    one unit in the last place apart (their fp32 accumulation orders differ),
+    so besides the activation rtol the absolute bound is one fp16 ulp
+    (2^-10 relative) of the stream's largest magnitude per layer.
+    """
+    got = got.detach().float().cpu()
+    want = want.detach().float().cpu()
+    assert got.shape == want.shape, f"{what}: shape {tuple(got.shape)} != {tuple(want.shape)}"
+    atol = max(ACT_ATOL, layers * 2.0 ** -10 * want.abs().max().item())
+    torch.testing.assert_close(got, want, rtol=ACT_RTOL, atol=atol, msg=lambda m: f"{what} (atol {atol:.3g}): {m}")
+
+
 def state_rel_err(got: torch.Tensor, want: torch.Tensor) -> float:
     got = got.detach().double().cpu()
     want = want.detach().double().cpu()

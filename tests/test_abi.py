@@ -123,13 +123,17 @@ def test_fp8_projection_host_validation() -> None:
     def group(*ns, m=1, stride=None):
         arr = (nat.Fp8Proj * max(1, len(ns)))()
         for j, n in enumerate(ns):
-            arr[j] = nat.Fp8Proj(256, 256, 256, n if stride is None else stride, n)
-        return lib.ria_linear_fp8_group(m, 2048, fake, 1, 2048, len(ns), ctypes.addressof(arr), 1, None)
+            arr[j] = nat.Fp8Proj(256, 256, 256, n if stride is None else stride, n, 1)
+        return lib.ria_linear_fp8_group(m, 2048, fake, 1, 2048, len(ns), ctypes.addressof(arr), None)
 
     assert group(m=0) == 1 and b"1 to 4" in lib.ria_last_error()
     assert group(32, 32, 32, 32, 32) == 1 and b"1 to 4" in lib.ria_last_error()
     assert group(8192, 4096, 40) == 1 and b"projection 2" in lib.ria_last_error()
     assert group(512, 512, stride=256) == 1 and b"stride" in lib.ria_last_error()
     assert group(8192, 4096, 32, 32, m=0) == 0
-    rc = lib.ria_linear_fp8_group(1, 2048, fake, 1, 2048, 2, None, 1, None)
+    rc = lib.ria_linear_fp8_group(1, 2048, fake, 1, 2048, 2, None, None)
     assert rc == 1 and b"null" in lib.ria_last_error()
+    arr = (nat.Fp8Proj * 1)()
+    arr[0] = nat.Fp8Proj(256, 256, 256, 64, 64, 9)
+    rc = lib.ria_linear_fp8_group(1, 2048, fake, 1, 2048, 1, ctypes.addressof(arr), None)
+    assert rc == 1 and b"dtype" in lib.ria_last_error()

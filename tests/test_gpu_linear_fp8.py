@@ -103,12 +103,13 @@ def test_linear_fp8_group_equals_separate_calls(gpu, m, ns, k):
     proj = [W.fp8_block_weight(500 + j, n, k) for j, n in enumerate(ns)]
     x = torch.randn((m, k), generator=torch.Generator().manual_seed(510 + m)).to(torch.bfloat16).to(gpu)
     proj_d = [(w.to(gpu), s.to(gpu)) for w, s in proj]
-    ys = K.linear_fp8_group(x, proj_d, out_dtype=torch.bfloat16)
+    dts = [torch.bfloat16, torch.float32, torch.float16, torch.float32][:len(ns)]  # each projection its own dtype
+    ys = K.linear_fp8_group(x, proj_d, out_dtype=dts)
     for j, (w, s) in enumerate(proj_d):
-        sep = K.linear_fp8(x, w, s, out_dtype=torch.bfloat16)
+        sep = K.linear_fp8(x, w, s, out_dtype=dts[j])
         torch.cuda.synchronize()
-        assert torch.equal(ys[j].cpu(), sep.cpu()), f"projection {j}"
+        assert ys[j].dtype == dts[j] and torch.equal(ys[j].cpu(), sep.cpu()), f"projection {j}"
     # and each against the oracle
     for j, (w, s) in enumerate(proj):
-        want = O.projection_fp8(x.cpu(), w, s).to(torch.bfloat16)
+        want = O.projection_fp8(x.cpu(), w, s).to(dts[j])
         assert_act_close(ys[j].cpu(), want, f"projection {j}")

@@ -88,8 +88,11 @@ WORKLOADS = {
                             "U[1024,32768], seed 4): input RMSNorm, FP8 block-scaled projections, conv + DeltaNet + "
                             "gated RMSNorm / q,k norms + RoPE + paged GQA attention + gate, output projection and "
                             "residual add per layer (router_ia.batched_forward; the MoE block is the caller's)"),
-    "forward1": dict(batch=1, lo=16384, hi=16384, seed=4, forward=True,
-                     desc="the forward128 loop for one sequence at context 16384 (the reference's batch-1 decode)"),
+    "forward1": dict(batch=1, lo=16384, hi=16384, seed=4, forward=True, graph=True,
+                     desc="the forward128 loop for one sequence at context 16384 (the reference's batch-1 decode), "
+                          "each step replayed as one captured HIP graph"),
+    "forward1-eager": dict(batch=1, lo=16384, hi=16384, seed=4, forward=True,
+                           desc="forward1 with every launch issued from Python (no graph)"),
     "proj1": dict(batch=1, seed=5, proj=True,
                   desc="every projection of the 40-layer stack for one decode step of B=1 token, FP8 block-scaled "
                        "weights, fp16 outputs"),
@@ -428,7 +431,7 @@ def run_forward_gpu(args, wl) -> dict:
     torch.cuda.set_device(dev)
     batch = wl["batch"]
     lengths = W.ragged_lengths(wl["seed"], batch, wl["lo"], wl["hi"])
-    total_new = args.warmup + args.steps
+    total_new = max(args.warmup, 1) + args.steps
     max_context = max(lengths) + total_new + 16
     num_pages = sum((n + total_new + 15) // 16 for n in lengths) + batch
     st = BatchedAttentionState(batch, max_context, num_pages=num_pages, device=dev, page_shuffle_seed=wl["seed"])
@@ -451,14 +454,20 @@ def run_forward_gpu(args, wl) -> dict:
     torch.cuda.synchronize()
     log(f"[bench] {wl['desc']}: B={batch}, mean context {sum(lengths) / batch:.0f}, "
         f"{wbytes / 1e9:.3f} GB of FP8 weights, {torch.cuda.memory_allocated(dev) / 2**30:.1f} GiB allocated")
-    for s in range(args.warmup):
+    warm = max(args.warmup, 1)  # at least one eager step: it loads every kernel before a capture
+    for s in range(warm):
         fwd.step(xs[s])
+    graph = fwd.capture(args.steps) if wl.get("graph") else None
     torch.cuda.synchronize()
     ctx = [n + 1 for n in st._host_seen]
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
-    for s in range(args.warmup, total_new):
-        fwd.step(xs[s])
+    for s in range(warm, total_new):
+        if graph is None:
+            fwd.step(xs[s])
+        else:
+            graph.x.copy_(xs[s])
+            graph.replay()
     t1.record()
     torch.cuda.synchronize()
     elapsed = t0.elapsed_time(t1) / 1e3

@@ -174,6 +174,7 @@ class BatchedForward:
         self.v = buf(b, hkv, 256)
         self.attn = buf(b, hq, 256)
         self.proj_out = buf(b, HIDDEN, dtype=torch.float32)  # out_proj / o_proj: fp16 values as fp32
+        self._stepped = False
 
     def layer(self, model_layer: int, x: torch.Tensor) -> torch.Tensor:
         """x [B, 2048] fp32 += this layer's attention output (in place); returns x."""
@@ -199,6 +200,26 @@ class BatchedForward:
             K.linear_fp8(self.attn.view(b, -1), *w.o_proj.pair(), out=self.proj_out)
         return x.add_(self.proj_out)
 
+    def capture(self, steps: int,
+                mlp: Callable[[int, torch.Tensor], torch.Tensor] | None = None) -> "ForwardGraph":
+        """Record one ``step`` as a HIP graph that can be replayed for the next `steps` tokens.
+
+        KV pages for `steps` more tokens of every row are reserved first, so a
+        replay does no host work beyond the launch.  Every launch of a step reads
+        positions and context lengths from device memory (the balanced split-K
+        attention schedules itself from them on the device), so one recording
+        serves every position.  Run one eager ``step`` before the first capture,
+        so that every kernel has been loaded.
+        """
+        st = self.state
+        if not self._stepped:
+            raise RuntimeError("run one eager step() before capture(), so every kernel is loaded")
+        if st.split_tokens != 0:
+            raise RuntimeError("capture needs the balanced attention schedule (split_tokens=0): a fixed split "
+                               "sizes its grid from the host-side context length")
+        st.reserve(steps)
+        return ForwardGraph(self, steps, mlp)
+
     def step(self, x: torch.Tensor,
              mlp: Callable[[int, torch.Tensor], torch.Tensor] | None = None) -> torch.Tensor:
         """One token per sequence through all layers (qwen36_chat_batch.py:181-187), then advance the positions.
@@ -214,4 +235,40 @@ class BatchedForward:
             if mlp is not None:
                 x = mlp(m, x)
         self.state.advance()
+        self._stepped = True
         return x
+
+
+class ForwardGraph:
+    """A recorded ``BatchedForward.step``: write the inputs into ``x``, call ``replay()``, read ``x``."""
+
+    def __init__(self, fwd: BatchedForward, steps: int, mlp: Callable[[int, torch.Tensor], torch.Tensor] | None):
+        st = fwd.state
+        self.fwd = fwd
+        self.remaining = int(steps)
+        self.x = torch.zeros((st.max_seqs, HIDDEN), dtype=torch.float32, device=st.device)
+        host_seen, headroom = list(st._host_seen), st._min_headroom
+        self.graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream(device=st.device)
+        stream.wait_stream(torch.cuda.current_stream(st.device))
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(self.graph, stream=stream):
+                out = fwd.step(self.x, mlp)
+        torch.cuda.current_stream(st.device).wait_stream(stream)
+        if out.data_ptr() != self.x.data_ptr():
+            self.x = out  # the mlp returned a new tensor: the step's output lives there
+        # recording ran the host side of advance(); nothing ran on the device yet
+        st._host_seen, st._min_headroom = host_seen, headroom
+
+    def replay(self) -> torch.Tensor:
+        """One token per sequence; the state's positions advance as with step()."""
+        if self.remaining <= 0:
+            raise RuntimeError("the graph's reserved steps are used up: capture again")
+        st = self.fwd.state
+        if max(st._host_seen) + 1 >= st.max_context:
+            raise RuntimeError(f"context reaches max_context={st.max_context}")
+        self.graph.replay()
+        st._host_seen = [n + 1 for n in st._host_seen]
+        st._min_headroom -= 1
+        self.remaining -= 1
+        return self.x

@@ -27,10 +27,10 @@ LAYERS = 4  # model layers 0, 1, 2 (DeltaNet) and 3 (full attention)
 LENGTHS = [37, 200, 515]
 
 
-def _setup(dev):
+def _setup(dev, split_tokens=64):
     ckpts = [W.synthetic_layer(700 + m, m) for m in range(LAYERS)]
     st = BatchedAttentionState(len(LENGTHS), 1100, num_linear_layers=3, num_full_layers=1, device=dev,
-                               page_shuffle_seed=5, split_tokens=64)
+                               page_shuffle_seed=5, split_tokens=split_tokens)
     st.set_positions(LENGTHS)
     g = torch.Generator(device=dev)
     g.manual_seed(71)
@@ -99,6 +99,13 @@ def test_batched_forward_matches_the_reference_composites(gpu):
                                rel=1e-3 if m == 0 else 2e-2)
 
 
+def test_capture_refuses_a_fixed_split(gpu):
+    _, st, fwd = _setup(gpu)
+    fwd.step(torch.zeros((len(LENGTHS), 2048), device=gpu))
+    with pytest.raises(RuntimeError, match="balanced"):
+        fwd.capture(2)
+
+
 def test_step_runs_every_layer_and_the_mlp_between(gpu):
     announce("batched forward: step() == layer() loop + advance, mlp called per layer")
     _, st, fwd = _setup(gpu)
@@ -122,3 +129,26 @@ def test_step_runs_every_layer_and_the_mlp_between(gpu):
         x.mul_(0.5)
     torch.cuda.synchronize()
     assert torch.equal(got.cpu(), x.cpu())
+
+
+def test_graph_replays_equal_eager_steps(gpu):
+    announce("batched forward: captured step replayed 3 times == 3 eager steps (bit for bit)")
+    _, st, fwd = _setup(gpu, split_tokens=0)  # the balanced attention schedule, which a graph can replay
+    xs = torch.randn((4, len(LENGTHS), 2048), generator=torch.Generator().manual_seed(91)).to(gpu)
+    fwd.step(xs[0].clone())  # one eager step loads every kernel
+    snaps = [st.save_row(r) for r in range(len(LENGTHS))]
+    graph = fwd.capture(3)
+    replayed = []
+    for s in range(1, 4):
+        graph.x.copy_(xs[s])
+        replayed.append(graph.replay().clone())
+        torch.cuda.synchronize()  # eager work and a sync between replays
+        assert st.max_seen == max(LENGTHS) + 1 + s
+    with pytest.raises(RuntimeError, match="used up"):
+        graph.replay()
+    for r, snap in enumerate(snaps):
+        st.restore_row(r, snap)
+    for s in range(1, 4):
+        got = fwd.step(xs[s].clone())
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), replayed[s - 1].cpu()), f"replay {s}"

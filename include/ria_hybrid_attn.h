@@ -410,7 +410,8 @@ int ria_kv_gather(int batch, int num_kv_heads,
  * the reference's run of F.linear calls on one normed hidden state: DeltaNet
  * in_proj_qkv / in_proj_z / in_proj_a / in_proj_b (qwen36_attention_cache.py:
  * 232-247, 268) and attention q_proj / k_proj / v_proj (:295-301); results
- * equal separate ria_linear_fp8 calls.
+ * equal separate ria_linear_fp8 calls.  With y_add, y += the fp16 result in
+ * fp32 (the residual add `x0.float() + F.linear(...).float()` of :281, :324).
  */
 typedef struct ria_fp8_proj {
   const void* weight;      /* [n, k] float8_e4m3fn */
@@ -419,6 +420,7 @@ typedef struct ria_fp8_proj {
   int64_t y_row_stride;
   int n;
   int y_dtype;             /* RIA_DT_*: the fp16 result stored in this dtype */
+  int y_add;               /* nonzero: y (RIA_DT_F32) += the result instead (a residual add) */
 } ria_fp8_proj;
 
 int ria_dequant_fp8(int64_t rows, int cols, const void* weight, const float* scale_inv,

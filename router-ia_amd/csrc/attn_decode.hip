@@ -494,15 +494,40 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     first = ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits;
     count = min((ctx + a.split_tokens - 1) / a.split_tokens, a.max_splits);
   }
+  // Partials are read kCombineBatch at a time (independent loads in flight)
+  // and added in split order, so the result does not depend on the batching.
+  constexpr int kCombineBatch = 16;
   float M = -INFINITY;
-  for (int64_t s = 0; s < count; ++s) M = fmaxf(M, a.ws_stats[((first + s) * a.group + hi) * 2]);
+  int64_t s = 0;
+  for (; s + kCombineBatch <= count; s += kCombineBatch) {
+    float mv[kCombineBatch];
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) mv[j] = a.ws_stats[((first + s + j) * a.group + hi) * 2];
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) M = fmaxf(M, mv[j]);
+  }
+  for (; s < count; ++s) M = fmaxf(M, a.ws_stats[((first + s) * a.group + hi) * 2]);
   float num = 0.f, den = 0.f;
-  for (int64_t s = 0; s < count; ++s) {
-    const int64_t ph = (first + s) * a.group + hi;
-    const float mv = a.ws_stats[ph * 2];
+  auto add = [&](float mv, float acc, float sum) {
     const float wt = mv == -INFINITY ? 0.f : exp2f(mv - M);  // stats are in log2 units
-    num = fmaf(wt, a.ws_acc[ph * kAttnHeadDim + d], num);
-    den = fmaf(wt, a.ws_stats[ph * 2 + 1], den);
+    num = fmaf(wt, acc, num);
+    den = fmaf(wt, sum, den);
+  };
+  for (s = 0; s + kCombineBatch <= count; s += kCombineBatch) {
+    float mv[kCombineBatch], acc[kCombineBatch], sum[kCombineBatch];
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) {
+      const int64_t ph = (first + s + j) * a.group + hi;
+      mv[j] = a.ws_stats[ph * 2];
+      sum[j] = a.ws_stats[ph * 2 + 1];
+      acc[j] = a.ws_acc[ph * kAttnHeadDim + d];
+    }
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) add(mv[j], acc[j], sum[j]);
+  }
+  for (; s < count; ++s) {
+    const int64_t ph = (first + s) * a.group + hi;
+    add(a.ws_stats[ph * 2], a.ws_acc[ph * kAttnHeadDim + d], a.ws_stats[ph * 2 + 1]);
   }
   const float attn = num / den;
   const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + d;

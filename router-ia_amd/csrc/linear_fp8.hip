@@ -98,6 +98,7 @@ struct Fp8Proj {
   int64_t y_stride;
   int n;
   int y_dtype;          // RIA_DT_*: y holds the fp16 result in this dtype
+  int y_add;            // nonzero: y (fp32) += the result, the residual add of a layer output
   int tile0;            // first column tile of this projection
 };
 
@@ -134,6 +135,15 @@ __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int
 template <int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// The fp16 result v stored as y_dtype, or (y_add) added to the fp32 y in
+// one rounding: the reference's `x0.float() + F.linear(...).float()`.
+__device__ __forceinline__ void store_result(void* y, int64_t i, float v, int y_dtype, int y_add) {
+  if (y_add)
+    static_cast<float*>(y)[i] = add_rn(static_cast<const float*>(y)[i], v);
+  else
+    store_act_dt(y, i, v, y_dtype);
 }
 
 // One producer thread's weight bytes of a chunk: 8 (CT 1), 16 (CT 2) or 32 (CT 4).
@@ -180,7 +190,7 @@ __global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
   const float* scale = a.p[0].scale;
   void* y = a.p[0].y;
   int64_t y_stride = a.p[0].y_stride;
-  int n = a.p[0].n, y_dtype = a.p[0].y_dtype, tile0 = 0;
+  int n = a.p[0].n, y_dtype = a.p[0].y_dtype, y_add = a.p[0].y_add, tile0 = 0;
 #pragma unroll
   for (int j = 1; j < kLinGroup; ++j)
     if (j < a.count && bx >= a.p[j].tile0) {
@@ -190,6 +200,7 @@ __global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
       y_stride = a.p[j].y_stride;
       n = a.p[j].n;
       y_dtype = a.p[j].y_dtype;
+      y_add = a.p[j].y_add;
       tile0 = a.p[j].tile0;
     }
   const int n0 = (bx - tile0) * kCols;
@@ -305,8 +316,8 @@ __global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
         for (int i = 0; i < 4; ++i) {
           const int r = 32 * wave + 16 * rt + 4 * g4 + i;
           if (r < rows && n0 + 16 * ct + n16 < n)
-            store_act_dt(y, (int64_t)(m0 + r) * y_stride + n0 + 16 * ct + n16,
-                         through_dtype<RIA_DT_F16>(acc[rt][ct][i]), y_dtype);
+            store_result(y, (int64_t)(m0 + r) * y_stride + n0 + 16 * ct + n16,
+                         through_dtype<RIA_DT_F16>(acc[rt][ct][i]), y_dtype, y_add);
         }
   };
   if (32 * wave + 16 < rows)
@@ -344,7 +355,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
   const float* scale = a.p[0].scale;
   void* y = a.p[0].y;
   int64_t y_stride = a.p[0].y_stride;
-  int y_dtype = a.p[0].y_dtype, tile0 = 0;
+  int y_dtype = a.p[0].y_dtype, y_add = a.p[0].y_add, tile0 = 0;
 #pragma unroll
   for (int j = 1; j < kLinGroup; ++j)
     if (j < a.count && bx >= a.p[j].tile0) {
@@ -353,6 +364,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
       y = a.p[j].y;
       y_stride = a.p[j].y_stride;
       y_dtype = a.p[j].y_dtype;
+      y_add = a.p[j].y_add;
       tile0 = a.p[j].tile0;
     }
   const int n0 = (bx - tile0) * 16;
@@ -460,7 +472,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * g4 + i;
       if (r < rows)
-        store_act_dt(y, (int64_t)(m0 + r) * y_stride + n0 + c16, through_dtype<RIA_DT_F16>(t[i]), y_dtype);
+        store_result(y, (int64_t)(m0 + r) * y_stride + n0 + c16, through_dtype<RIA_DT_F16>(t[i]), y_dtype, y_add);
     }
   }
 }
@@ -529,6 +541,8 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
       return set_error(RIA_ERR_INVALID, "%s: N must be a positive multiple of 16 (projection %d: %d)", who, j, q.n);
     if (q.y_row_stride < q.n) return set_error(RIA_ERR_INVALID, "%s: y row stride too small (projection %d)", who, j);
     if (!lin_dtype_ok(q.y_dtype)) return set_error(RIA_ERR_INVALID, "%s: unknown dtype code (projection %d)", who, j);
+    if (q.y_add && q.y_dtype != RIA_DT_F32)
+      return set_error(RIA_ERR_INVALID, "%s: y_add needs an fp32 y (projection %d)", who, j);
   }
   if (m == 0) return RIA_OK;
   if (!x) return set_error(RIA_ERR_INVALID, "%s: null x", who);
@@ -579,7 +593,8 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
   int tile = 0;
   for (int j = 0; j < count; ++j) {
     const ria_fp8_proj& q = projs[j];
-    a.p[j] = Fp8Proj{static_cast<const uint8_t*>(q.weight), q.scale_inv, q.y, q.y_row_stride, q.n, q.y_dtype, tile};
+    a.p[j] = Fp8Proj{static_cast<const uint8_t*>(q.weight), q.scale_inv, q.y, q.y_row_stride, q.n, q.y_dtype, q.y_add,
+                     tile};
     tile += (q.n + 16 * ct - 1) / (16 * ct);
   }
   const int64_t mblocks = gemv ? 1 : (m + mt - 1) / mt;
@@ -606,7 +621,7 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
 extern "C" int ria_linear_fp8(int m, int n, int k, const void* x, int x_dtype, int64_t x_row_stride,
                               const void* weight, const float* scale_inv, void* y, int y_dtype, int64_t y_row_stride,
                               void* stream) {
-  const ria_fp8_proj p{weight, scale_inv, y, y_row_stride, n, y_dtype};
+  const ria_fp8_proj p{weight, scale_inv, y, y_row_stride, n, y_dtype, 0};
   return linear_group("ria_linear_fp8", m, k, x, x_dtype, x_row_stride, 1, &p, stream);
 }
 

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
 // and head offsets multiples of 4, bases aligned to 4 elements): a group of
 // RL lanes owns each row, every lane loads and stores 4 contiguous elements
 // per access, and the group reduces its sum of squares with xor shuffles.
-template <int XT, int OT, bool GATED, int RL>
+template <int XT, int OT, bool GATED, int RL, int NCH>
 __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
   constexpr int kRowsPerWave = 64 / RL;
   const int lane = threadIdx.x & 63;
@@ -120,24 +120,10 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
   const int64_t t = ok ? r / a.heads : 0;
   const int64_t hoff = ok ? (r - t * a.heads) * a.dim : 0;
   const int64_t xo = t * a.x_stride + hoff;
-  float ss = 0.f;
-  if (ok) {
-    for (int c = 4 * li; c < a.dim; c += 4 * RL) {
-      float v[4];
-      load_act4<XT>(a.x, xo + c, v);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) ss = add_rn(ss, mul_rn(v[j], v[j]));
-    }
-  }
-#pragma unroll
-  for (int off = RL / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-  if (!ok) return;
-  const float rs = rms_scale(ss, a.dim, a.eps);
   const int64_t oo = t * a.out_stride + hoff;
   const int64_t zo = t * a.z_stride + hoff;
-  for (int c = 4 * li; c < a.dim; c += 4 * RL) {
-    float v[4], y[4];
-    load_act4<XT>(a.x, xo + c, v);
+  auto finish = [&](int c, const float (&v)[4], float rs) {
+    float y[4];
     const f32x4 w = *reinterpret_cast<const f32x4*>(a.weight + c);
     if constexpr (GATED) {
       float z[4];
@@ -149,6 +135,45 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
       for (int j = 0; j < 4; ++j) y[j] = rmsnorm_elem<XT>(v[j], rs, w[j]);
     }
     store_act4<OT>(a.out, oo + c, y);
+  };
+  float ss = 0.f;
+  if constexpr (NCH > 0) {
+    // dim == 4 RL NCH: the lane's NCH chunks are loaded at once and kept in
+    // registers for the second pass (the squares are summed in the same order
+    // as the loop below, so both give the same bits)
+    float v[NCH][4];
+    if (ok) {
+#pragma unroll
+      for (int q = 0; q < NCH; ++q) load_act4<XT>(a.x, xo + 4 * li + 4 * RL * q, v[q]);
+#pragma unroll
+      for (int q = 0; q < NCH; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ss = add_rn(ss, mul_rn(v[q][j], v[q][j]));
+    }
+#pragma unroll
+    for (int off = RL / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (!ok) return;
+    const float rs = rms_scale(ss, a.dim, a.eps);
+#pragma unroll
+    for (int q = 0; q < NCH; ++q) finish(4 * li + 4 * RL * q, v[q], rs);
+  } else {
+    if (ok) {
+      for (int c = 4 * li; c < a.dim; c += 4 * RL) {
+        float v[4];
+        load_act4<XT>(a.x, xo + c, v);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ss = add_rn(ss, mul_rn(v[j], v[j]));
+      }
+    }
+#pragma unroll
+    for (int off = RL / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (!ok) return;
+    const float rs = rms_scale(ss, a.dim, a.eps);
+    for (int c = 4 * li; c < a.dim; c += 4 * RL) {
+      float v[4];
+      load_act4<XT>(a.x, xo + c, v);
+      finish(c, v, rs);
+    }
   }
 }
 
@@ -162,12 +187,29 @@ static void launch_norm_rl(const NormArgs& a, bool vec, hipStream_t st) {
   const int rl = a.dim >= 256 ? 64 : (a.dim >= 128 ? 32 : 16);
   const int64_t rows_per_block = 4 * (64 / rl);
   const dim3 grid((unsigned)((a.rows + rows_per_block - 1) / rows_per_block));
-  if (rl == 64)
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<XT, OT, GATED, 64>), grid, dim3(256), 0, st, a);
-  else if (rl == 32)
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<XT, OT, GATED, 32>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<XT, OT, GATED, 16>), grid, dim3(256), 0, st, a);
+  // chunks of 4 per lane: held in registers when the row is 1, 2, 4 or 8 of them
+  const int nch = a.dim % (4 * rl) == 0 ? a.dim / (4 * rl) : 0;
+#define RIA_NORM_VEC(RL_, NCH_) hipLaunchKernelGGL((rmsnorm_vec_kernel<XT, OT, GATED, RL_, NCH_>), grid, dim3(256), 0, st, a)
+  if (rl == 64) {
+    if (nch == 8)
+      RIA_NORM_VEC(64, 8);
+    else if (nch == 4)
+      RIA_NORM_VEC(64, 4);
+    else if (nch == 2)
+      RIA_NORM_VEC(64, 2);
+    else if (nch == 1)
+      RIA_NORM_VEC(64, 1);
+    else
+      RIA_NORM_VEC(64, 0);
+  } else if (rl == 32) {
+    if (nch == 1)
+      RIA_NORM_VEC(32, 1);
+    else
+      RIA_NORM_VEC(32, 0);
+  } else {
+    RIA_NORM_VEC(16, 0);
+  }
+#undef RIA_NORM_VEC
 }
 
 template <int XT, bool GATED>

@@ -121,7 +121,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
 class Fp8Proj(ctypes.Structure):
     """struct ria_fp8_proj: one projection of a ria_linear_fp8_group call."""
     _fields_ = [("weight", _vp), ("scale_inv", _vp), ("y", _vp), ("y_row_stride", _c_i64), ("n", _c_int),
-                ("y_dtype", _c_int)]
+                ("y_dtype", _c_int), ("y_add", _c_int)]
 
 
 LINEAR_GROUP_MAX = 4  # projections per ria_linear_fp8_group call

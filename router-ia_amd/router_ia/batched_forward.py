@@ -21,7 +21,7 @@ Per layer (B rows, hidden 2048, the reference's CUDA dtypes):
                                    FP8 launch                            FP8 launch
     conv, gates, delta rule,       ria_gdn_decode  k_norm + RoPE + append, q_norm +
     read-out, gated RMSNorm (fp16)                 RoPE + attention + gate (fp16)
-    x += out_proj(.) (fp16 -> fp32)                x += o_proj(.)
+    x += out_proj(.) in the projection launch      x += o_proj(.) likewise
 
 q_proj's rows interleave each head's query and gate (:295-299); they are split
 once, when the weights are prepared, into two projections whose outputs are
@@ -173,7 +173,6 @@ class BatchedForward:
         self.k = buf(b, hkv, 256)
         self.v = buf(b, hkv, 256)
         self.attn = buf(b, hq, 256)
-        self.proj_out = buf(b, HIDDEN, dtype=torch.float32)  # out_proj / o_proj: fp16 values as fp32
         self._stepped = False
 
     def layer(self, model_layer: int, x: torch.Tensor) -> torch.Tensor:
@@ -189,7 +188,7 @@ class BatchedForward:
                                out=[self.mixed, self.z, self.gate_a, self.gate_b])
             st.linear_step(i, self.mixed, w.conv_weight, self.gate_a, self.gate_b, gate_mode=nat.RIA_GATE_RAW,
                            A_log=w.A_log, dt_bias=w.dt_bias, out=self.gated, z=self.z, norm_weight=w.norm_weight)
-            K.linear_fp8(self.gated.view(b, -1), *w.out_proj.pair(), out=self.proj_out)
+            K.linear_fp8_group(self.gated.view(b, -1), [w.out_proj.pair()], out=[x], accumulate=[True])
         else:
             K.rmsnorm(x, w.input_norm, out=self.h_f16)
             K.linear_fp8_group(self.h_f16, [w.query.pair(), w.gate.pair(), w.k_proj.pair(), w.v_proj.pair()],
@@ -197,8 +196,8 @@ class BatchedForward:
                                     self.v.view(b, -1)])
             st.full_step(i, self.q, self.k, self.v, self.gate, out=self.attn, q_norm_weight=w.q_norm,
                          k_norm_weight=w.k_norm)
-            K.linear_fp8(self.attn.view(b, -1), *w.o_proj.pair(), out=self.proj_out)
-        return x.add_(self.proj_out)
+            K.linear_fp8_group(self.attn.view(b, -1), [w.o_proj.pair()], out=[x], accumulate=[True])
+        return x
 
     def capture(self, steps: int,
                 mlp: Callable[[int, torch.Tensor], torch.Tensor] | None = None) -> "ForwardGraph":

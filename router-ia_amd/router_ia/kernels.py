@@ -533,11 +533,13 @@ def linear_fp8(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor, *
 
 def linear_fp8_group(x: torch.Tensor, projections: list[tuple[torch.Tensor, torch.Tensor]], *,
                      out: list[torch.Tensor] | None = None,
-                     out_dtype: torch.dtype | list[torch.dtype] = torch.float16) -> list[torch.Tensor]:
+                     out_dtype: torch.dtype | list[torch.dtype] = torch.float16,
+                     accumulate: list[bool] | None = None) -> list[torch.Tensor]:
     """Up to 4 FP8 projections of the same x in one launch (ria_linear_fp8_group).
 
     projections: (weight [N_j, K] float8_e4m3fn, scale_inv) pairs; returns /
     fills y_j [M, N_j] (each in its own dtype), each equal to linear_fp8(x, w_j, s_j).
+    With accumulate[j], the fp32 out[j] receives out[j] + y_j (a residual add).
     """
     dev = x.device
     _require_gpu("x", x, dev)
@@ -561,7 +563,10 @@ def linear_fp8_group(x: torch.Tensor, projections: list[tuple[torch.Tensor, torc
         _require_gpu(f"out {j}", y, dev)
         if y.dim() != 2 or tuple(y.shape) != (m, n) or (n > 1 and y.stride(1) != 1):
             raise ValueError(f"out {j} must be [{m}, {n}] with contiguous rows")
-        arr[j] = nat.Fp8Proj(_ptr(w), _ptr(s), _ptr(y), int(y.stride(0)) if m > 1 else n, n, dtype_code(y))
+        add = bool(accumulate[j]) if accumulate is not None else False
+        if add and y.dtype != torch.float32:
+            raise ValueError(f"out {j}: accumulating needs fp32")
+        arr[j] = nat.Fp8Proj(_ptr(w), _ptr(s), _ptr(y), int(y.stride(0)) if m > 1 else n, n, dtype_code(y), int(add))
     rc = nat.load().ria_linear_fp8_group(m, k, _ptr(x), dtype_code(x), xs, len(projections), ctypes.addressof(arr),
                                          _stream(dev))
     nat.check(rc, "ria_linear_fp8_group")

@@ -123,7 +123,7 @@ def test_fp8_projection_host_validation() -> None:
     def group(*ns, m=1, stride=None):
         arr = (nat.Fp8Proj * max(1, len(ns)))()
         for j, n in enumerate(ns):
-            arr[j] = nat.Fp8Proj(256, 256, 256, n if stride is None else stride, n, 1)
+            arr[j] = nat.Fp8Proj(256, 256, 256, n if stride is None else stride, n, 1, 0)
         return lib.ria_linear_fp8_group(m, 2048, fake, 1, 2048, len(ns), ctypes.addressof(arr), None)
 
     assert group(m=0) == 1 and b"1 to 4" in lib.ria_last_error()
@@ -134,6 +134,9 @@ def test_fp8_projection_host_validation() -> None:
     rc = lib.ria_linear_fp8_group(1, 2048, fake, 1, 2048, 2, None, None)
     assert rc == 1 and b"null" in lib.ria_last_error()
     arr = (nat.Fp8Proj * 1)()
-    arr[0] = nat.Fp8Proj(256, 256, 256, 64, 64, 9)
+    arr[0] = nat.Fp8Proj(256, 256, 256, 64, 64, 9, 0)
     rc = lib.ria_linear_fp8_group(1, 2048, fake, 1, 2048, 1, ctypes.addressof(arr), None)
     assert rc == 1 and b"dtype" in lib.ria_last_error()
+    arr[0] = nat.Fp8Proj(256, 256, 256, 64, 64, 1, 1)  # accumulating into fp16
+    rc = lib.ria_linear_fp8_group(1, 2048, fake, 1, 2048, 1, ctypes.addressof(arr), None)
+    assert rc == 1 and b"y_add" in lib.ria_last_error()

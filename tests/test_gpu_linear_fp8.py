@@ -113,3 +113,17 @@ def test_linear_fp8_group_equals_separate_calls(gpu, m, ns, k):
     for j, (w, s) in enumerate(proj):
         want = O.projection_fp8(x.cpu(), w, s).to(dts[j])
         assert_act_close(ys[j].cpu(), want, f"projection {j}")
+
+
+@pytest.mark.parametrize("m", [3, 100])
+def test_linear_fp8_group_accumulates_into_fp32(gpu, m):
+    announce(f"linear_fp8_group: M={m} y += fp16 result (residual add)")
+    w8, s = W.fp8_block_weight(600, 2048, 4096)
+    g = torch.Generator().manual_seed(601)
+    x = torch.randn((m, 4096), generator=g).to(torch.float16).to(gpu)
+    base = torch.randn((m, 2048), generator=g).to(gpu)
+    y = base.clone()
+    K.linear_fp8_group(x, [(w8.to(gpu), s.to(gpu))], out=[y], accumulate=[True])
+    sep = K.linear_fp8(x, w8.to(gpu), s.to(gpu), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), base.cpu() + sep.cpu())

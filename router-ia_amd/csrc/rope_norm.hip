@@ -122,9 +122,8 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
   const int64_t xo = t * a.x_stride + hoff;
   const int64_t oo = t * a.out_stride + hoff;
   const int64_t zo = t * a.z_stride + hoff;
-  auto finish = [&](int c, const float (&v)[4], float rs) {
+  auto finish = [&](int c, const float (&v)[4], float rs, f32x4 w) {
     float y[4];
-    const f32x4 w = *reinterpret_cast<const f32x4*>(a.weight + c);
     if constexpr (GATED) {
       float z[4];
       load_act4_dt(a.z, zo + c, a.z_dtype, z);
@@ -142,9 +141,12 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
     // registers for the second pass (the squares are summed in the same order
     // as the loop below, so both give the same bits)
     float v[NCH][4];
+    f32x4 w[NCH];  // the weights too, so their loads overlap the reduction
     if (ok) {
 #pragma unroll
       for (int q = 0; q < NCH; ++q) load_act4<XT>(a.x, xo + 4 * li + 4 * RL * q, v[q]);
+#pragma unroll
+      for (int q = 0; q < NCH; ++q) w[q] = *reinterpret_cast<const f32x4*>(a.weight + 4 * li + 4 * RL * q);
 #pragma unroll
       for (int q = 0; q < NCH; ++q)
 #pragma unroll
@@ -155,7 +157,7 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
     if (!ok) return;
     const float rs = rms_scale(ss, a.dim, a.eps);
 #pragma unroll
-    for (int q = 0; q < NCH; ++q) finish(4 * li + 4 * RL * q, v[q], rs);
+    for (int q = 0; q < NCH; ++q) finish(4 * li + 4 * RL * q, v[q], rs, w[q]);
   } else {
     if (ok) {
       for (int c = 4 * li; c < a.dim; c += 4 * RL) {
@@ -172,7 +174,7 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
     for (int c = 4 * li; c < a.dim; c += 4 * RL) {
       float v[4];
       load_act4<XT>(a.x, xo + c, v);
-      finish(c, v, rs);
+      finish(c, v, rs, *reinterpret_cast<const f32x4*>(a.weight + c));
     }
   }
 }

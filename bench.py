@@ -98,6 +98,9 @@ WORKLOADS = {
                        "weights, fp16 outputs"),
     "batch32": dict(batch=32, lo=8192, hi=8192, seed=2,
                     desc="40-layer stack, B=32, context 8192 (seed 2), 16-token pages, shuffled page table"),
+    "batch1": dict(batch=1, lo=8192, hi=8192, seed=2, graph=True,
+                   desc="40-layer stack, B=1, context 8192 (seed 2), 16-token pages, shuffled page table; each "
+                        "step (fresh inputs copied in, 40 layers, advance) replayed as one captured HIP graph"),
 }
 
 
@@ -480,6 +483,121 @@ def run_forward_gpu(args, wl) -> dict:
             "mean_ctx": sum(lengths) / batch}
 
 
+def run_stack_graph(args, wl) -> dict:
+    """The 40-layer state stack (projections excluded) with each decode step replayed as one HIP graph."""
+    from router_ia import _native as nat
+    from router_ia import workloads as W
+    from router_ia.batched_state import BatchedAttentionState
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    batch = wl["batch"]
+    lengths = W.ragged_lengths(wl["seed"], batch, wl["lo"], wl["hi"])
+    warm = max(args.warmup, 1)
+    total_new = warm + args.steps
+    max_context = max(lengths) + total_new + 16
+    num_pages = sum((n + total_new + 15) // 16 for n in lengths) + batch
+    st = BatchedAttentionState(batch, max_context, num_pages=num_pages, device=dev, page_shuffle_seed=wl["seed"])
+    st.set_positions(lengths)
+    st.reserve(total_new)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(wl["seed"])
+    for li in range(st.num_linear_layers):
+        st.linear_states[li].normal_(0.0, 0.02, generator=gen)
+        st.conv_rings[li].normal_(0.0, 1.0, generator=gen)
+    for fi in range(st.num_full_layers):
+        st.kv.k[fi].normal_(0.0, 1.0, generator=gen)
+        st.kv.v[fi].normal_(0.0, 1.0, generator=gen)
+    n_lin, n_full = st.num_linear_layers, st.num_full_layers
+    conv_w = [(torch.randn((CONV_DIM, 1, 4), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+              for _ in range(n_lin)]
+    a_log = [torch.rand((NUM_V_HEADS,), generator=gen, device=dev) * 4.0 - 4.0 for _ in range(n_lin)]
+    dt_bias = [torch.zeros((NUM_V_HEADS,), device=dev) for _ in range(n_lin)]
+    # fresh per-step inputs (pool) and the fixed buffers the graph reads
+    pool = {
+        "mixed": torch.randn((total_new, n_lin, batch, CONV_DIM), generator=gen, device=dev, dtype=torch.bfloat16),
+        "gate_ab": torch.randn((total_new, n_lin, 2, batch, NUM_V_HEADS), generator=gen, device=dev),
+        "qg": torch.randn((total_new, n_full, 2, batch, NUM_Q_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev,
+                          dtype=torch.bfloat16),
+        "kv": torch.randn((total_new, n_full, 2, batch, NUM_KV_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev,
+                          dtype=torch.bfloat16),
+    }
+    inp = {k: torch.empty_like(v[0]) for k, v in pool.items()}
+    gdn_out = torch.empty((batch, NUM_V_HEADS, 128), device=dev, dtype=torch.bfloat16)
+    attn_out = torch.empty((batch, NUM_Q_HEADS, HEAD_DIM_ATTN), device=dev, dtype=torch.bfloat16)
+
+    def step():
+        for layer in range(LAYERS):
+            if is_full(layer):
+                fi = layer // 4
+                st.full_step(fi, inp["qg"][fi, 0], inp["kv"][fi, 0], inp["kv"][fi, 1], inp["qg"][fi, 1], out=attn_out)
+            else:
+                li = layer - layer // 4
+                st.linear_step(li, inp["mixed"][li], conv_w[li], inp["gate_ab"][li, 0], inp["gate_ab"][li, 1],
+                               gate_mode=nat.RIA_GATE_RAW, A_log=a_log[li], dt_bias=dt_bias[li], out=gdn_out)
+        st.advance()
+
+    def feed(s):
+        for k in inp:
+            inp[k].copy_(pool[k][s])
+
+    for s in range(warm):
+        feed(s)
+        step()
+    torch.cuda.synchronize()
+    # record one step; recording runs the host side of advance(), which the replays redo
+    host_seen, headroom = list(st._host_seen), st._min_headroom
+    graph = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        with torch.cuda.graph(graph, stream=cs):
+            step()
+    torch.cuda.current_stream().wait_stream(cs)
+    st._host_seen, st._min_headroom = host_seen, headroom
+    torch.cuda.synchronize()
+    ctx = [n + 1 for n in st._host_seen]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for s in range(warm, total_new):
+        feed(s)
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    elapsed = t0.elapsed_time(t1) / 1e3
+    step_s = elapsed / args.steps
+    nbytes = step_bytes(ctx)
+    return {"batch": batch, "ms_per_step": step_s * 1e3, "tok_s": batch / step_s, "step_bytes": nbytes,
+            "achieved_GBps": nbytes / step_s / 1e9, "mean_ctx": sum(lengths) / batch}
+
+
+def stack_graph_main(args, wl) -> int:
+    gpu = run_stack_graph(args, wl)
+    result = {
+        "metric": "attn-stack decode tok/s (40 layers, B=1..128); state+KV HBM GB/s % of peak",
+        "value": round(gpu["tok_s"], 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 state, bf16 KV and activations",
+        "data": "synthetic (seeded random state, KV and per-layer inputs; projections excluded)",
+        "config": {"workload": wl["desc"], "batch": gpu["batch"], "mean_context": round(gpu["mean_ctx"]),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "whole step (all launches, one graph)",
+                     "achieved": round(gpu["achieved_GBps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gpu["achieved_GBps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_step": gpu["step_bytes"]},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def forward_main(args, wl) -> int:
     gpu = run_forward_gpu(args, wl)
     result = {
@@ -810,6 +928,8 @@ def main() -> int:
         return proj_main(args, wl)
     if wl.get("forward"):
         return forward_main(args, wl)
+    if wl.get("graph"):
+        return stack_graph_main(args, wl)
     gpu = run_gpu(args, wl)
     prof = profiled_traffic("attn_splitk_kernel") if args.workload == "ragged128" else None
     if prof:

@@ -155,7 +155,7 @@ __device__ __forceinline__ int row_ctx(const AttnArgs& a, int b) {
 // index w + u, which is unique because the (w, u) pairs that meet form a
 // monotone staircase.
 constexpr int kMaxBalancedUnits = 4096;
-constexpr int kMinChunkPages = 16;
+constexpr int kMinChunkPages = 4;  // 64 tokens: small batches still spread over the CUs
 
 // Inclusive block scan of up to 256 per-thread values through LDS; returns
 // the exclusive prefix of this thread's value.
@@ -535,6 +535,101 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   store_act<OT>(a.out, ((int64_t)b * a.num_q_heads + h) * kAttnHeadDim + d, mul_rn(attn, gv));
 }
 
+// attn_combine_kernel for long partial lists (a few units share all the
+// workgroups, as at small batches).  Wave p of the STREAMS waves takes partials p, p + STREAMS, ... (kBatch of
+// them in flight), lane dg its dims 4 dg .. 4 dg + 3 (16-byte loads); the
+// streams are added in order through LDS.
+template <int GT, int OT, bool BALANCED, int STREAMS>
+__global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArgs a) {
+  constexpr int kBatch = 8;
+  const int b = blockIdx.x / a.num_q_heads;
+  const int h = blockIdx.x % a.num_q_heads;
+  const int dg = threadIdx.x & 63;
+  const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kvh = h / a.group;
+  const int hi = h % a.group;
+  int64_t first, count;
+  if constexpr (BALANCED) {
+    // partials of unit u come from workgroups off[u] / chunk .. (off[u + 1] - 1) / chunk, at index w + u
+    const int u = b * a.num_kv_heads + kvh;
+    const int chunk = a.ws_units[1];
+    const int o0 = a.ws_units[2 + u], o1 = a.ws_units[3 + u];
+    const int w0 = o0 / chunk, w1 = (o1 - 1) / chunk;
+    first = (int64_t)w0 + u;
+    count = o1 > o0 ? w1 - w0 + 1 : 0;
+  } else {
+    const int ctx = row_ctx(a, b);
+    first = ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits;
+    count = min((ctx + a.split_tokens - 1) / a.split_tokens, a.max_splits);
+  }
+  const float* stats = a.ws_stats + (first * a.group + hi) * 2;  // partial s: stats[s * group * 2 + {0, 1}]
+  const float* accs = a.ws_acc + (first * a.group + hi) * kAttnHeadDim + 4 * dg;
+  const int64_t sstep = (int64_t)a.group * 2, astep = (int64_t)a.group * kAttnHeadDim;
+  // the largest partial max (stats are in log2 units)
+  float M = -INFINITY;
+  for (int64_t s0 = p; s0 < count; s0 += STREAMS * kBatch) {
+    float mv[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t s = s0 + j * STREAMS;  // past the end: the last partial, loaded and ignored
+      const float v = stats[min(s, count - 1) * sstep];
+      mv[j] = s < count ? v : -INFINITY;
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) M = fmaxf(M, mv[j]);
+  }
+  __shared__ float m_s[STREAMS];
+  __shared__ f32x4 num_s[STREAMS][64];
+  __shared__ float den_s[STREAMS];
+  if (dg == 0) m_s[p] = M;
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < STREAMS; ++q) M = fmaxf(M, m_s[q]);
+  f32x4 num = {0.f, 0.f, 0.f, 0.f};
+  float den = 0.f;
+  for (int64_t s0 = p; s0 < count; s0 += STREAMS * kBatch) {
+    float mv[kBatch], sum[kBatch];
+    f32x4 acc[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t s = s0 + j * STREAMS, sc = min(s, count - 1);
+      const bool in = s < count;
+      const float v = stats[sc * sstep], w = stats[sc * sstep + 1];
+      const f32x4 x = *reinterpret_cast<const f32x4*>(accs + sc * astep);
+      mv[j] = in ? v : -INFINITY;
+      sum[j] = in ? w : 0.f;
+      acc[j] = in ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const float wt = mv[j] == -INFINITY ? 0.f : exp2f(mv[j] - M);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) num[i] = fmaf(wt, acc[j][i], num[i]);
+      den = fmaf(wt, sum[j], den);
+    }
+  }
+  num_s[p][dg] = num;
+  if (dg == 0) den_s[p] = den;
+  __syncthreads();
+  if (p != 0) return;
+  f32x4 tn = num_s[0][dg];
+  float td = den_s[0];
+#pragma unroll
+  for (int q = 1; q < STREAMS; ++q) {
+    const f32x4 u = num_s[q][dg];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tn[i] += u[i];
+    td += den_s[q];
+  }
+  const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + 4 * dg;
+  const int64_t oi = ((int64_t)b * a.num_q_heads + h) * kAttnHeadDim + 4 * dg;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float gv = sigmoid_f(load_act<GT>(a.gate, gi + i));
+    store_act<OT>(a.out, oi + i, mul_rn(tn[i] / td, gv));
+  }
+}
+
 __global__ __launch_bounds__(256) void kv_gather_kernel(const uint16_t* k_cache, const uint16_t* v_cache,
                                                         int num_pages, const int32_t* page_table,
                                                         int64_t pt_stride, const int32_t* seq_slot,
@@ -852,10 +947,16 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
   if (!(phase & RIA_ATTN_COMBINE)) return RIA_OK;
 
   dim3 cgrid(batch * num_q_heads);
-#define RIA_COMB_LAUNCH(GT_, OT_)                                                               \
-  if (balanced)                                                                                 \
-    hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_, true>), cgrid, dim3(256), 0, st, a);      \
-  else                                                                                          \
+  // a few (sequence, KV head) units share all the splits: long partial lists, merged by 16 waves
+  const bool long_lists = (int64_t)batch * num_kv_heads <= 32;
+#define RIA_COMB_LAUNCH(GT_, OT_)                                                                          \
+  if (balanced && long_lists)                                                                              \
+    hipLaunchKernelGGL((attn_combine_long_kernel<GT_, OT_, true, 16>), cgrid, dim3(1024), 0, st, a);       \
+  else if (balanced)                                                                                       \
+    hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_, true>), cgrid, dim3(256), 0, st, a);                 \
+  else if (long_lists)                                                                                     \
+    hipLaunchKernelGGL((attn_combine_long_kernel<GT_, OT_, false, 16>), cgrid, dim3(1024), 0, st, a);      \
+  else                                                                                                     \
     hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_, false>), cgrid, dim3(256), 0, st, a)
 #define RIA_COMB_OT(GT_)                     \
   if (out_dtype == RIA_DT_BF16) {            \

@@ -183,8 +183,13 @@ class BatchedForward:
         b = st.max_seqs
         if isinstance(w, LinearLayerWeights):
             K.rmsnorm(x, w.input_norm, out=self.h_bf16)
-            K.linear_fp8_group(self.h_bf16, [w.in_proj_qkv.pair(), w.in_proj_z.pair(), w.in_proj_a.pair(),
-                                             w.in_proj_b.pair()],
+            h = self.h_bf16
+            if b > 16:
+                # bf16(h) -> fp16 once here (exact in fp16's range, as the projection
+                # would convert it), rather than in every workgroup of the streaming kernel
+                h = self.h_f16.copy_(self.h_bf16)
+            K.linear_fp8_group(h, [w.in_proj_qkv.pair(), w.in_proj_z.pair(), w.in_proj_a.pair(),
+                                   w.in_proj_b.pair()],
                                out=[self.mixed, self.z, self.gate_a, self.gate_b])
             st.linear_step(i, self.mixed, w.conv_weight, self.gate_a, self.gate_b, gate_mode=nat.RIA_GATE_RAW,
                            A_log=w.A_log, dt_bias=w.dt_bias, out=self.gated, z=self.z, norm_weight=w.norm_weight)

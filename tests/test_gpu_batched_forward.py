@@ -25,13 +25,16 @@ pytestmark = pytest.mark.gpu
 
 LAYERS = 4  # model layers 0, 1, 2 (DeltaNet) and 3 (full attention)
 LENGTHS = [37, 200, 515]
+# 20 rows: more than the 16 of the one-pass projection kernel, so the
+# projections take the streaming kernel (and the fp16 copy of the normed input)
+LENGTHS_20 = LENGTHS + [1, 2, 15, 16, 17, 31, 64, 99, 128, 250, 300, 333, 401, 480, 512, 550, 600]
 
 
-def _setup(dev, split_tokens=64):
+def _setup(dev, split_tokens=64, lengths=LENGTHS):
     ckpts = [W.synthetic_layer(700 + m, m) for m in range(LAYERS)]
-    st = BatchedAttentionState(len(LENGTHS), 1100, num_linear_layers=3, num_full_layers=1, device=dev,
+    st = BatchedAttentionState(len(lengths), 1100, num_linear_layers=3, num_full_layers=1, device=dev,
                                page_shuffle_seed=5, split_tokens=split_tokens)
-    st.set_positions(LENGTHS)
+    st.set_positions(lengths)
     g = torch.Generator(device=dev)
     g.manual_seed(71)
     st.linear_states.normal_(0.0, 0.02, generator=g)
@@ -55,7 +58,7 @@ def _oracle_weights(ck):
 
 def _oracle_states(st):
     states = []
-    for row in range(len(LENGTHS)):
+    for row in range(st.max_seqs):
         ref = st.save_row(row).to_reference()
         s = O.SequenceState()
         s.conv = {m: t.cpu() for m, t in ref["linear_conv_states"].items()}
@@ -72,15 +75,16 @@ def _oracle_layer(w, s, m, x):
     return step(w, s, m, x, gpu_dtypes=True)
 
 
-def test_batched_forward_matches_the_reference_composites(gpu):
-    announce(f"batched forward: {LAYERS} layers, rows at {LENGTHS}, 2 steps, FP8 projections")
-    ckpts, st, fwd = _setup(gpu)
+@pytest.mark.parametrize("lengths", [LENGTHS, LENGTHS_20], ids=["3rows", "20rows"])
+def test_batched_forward_matches_the_reference_composites(gpu, lengths):
+    announce(f"batched forward: {LAYERS} layers, rows at {lengths}, 2 steps, FP8 projections")
+    ckpts, st, fwd = _setup(gpu, lengths=lengths)
     ws = [_oracle_weights(ck) for ck in ckpts]
     ref = _oracle_states(st)
     for step in range(2):
-        x0 = torch.randn((len(LENGTHS), 2048), generator=torch.Generator().manual_seed(80 + step))
+        x0 = torch.randn((len(lengths), 2048), generator=torch.Generator().manual_seed(80 + step))
         x = x0.to(gpu).contiguous()
-        want = [x0[row:row + 1] for row in range(len(LENGTHS))]
+        want = [x0[row:row + 1] for row in range(len(lengths))]
         for m in range(LAYERS):  # layer by layer, so a mismatch names its layer
             fwd.layer(m, x)
             got = x.cpu()
@@ -90,13 +94,16 @@ def test_batched_forward_matches_the_reference_composites(gpu):
         st.advance()
         for s in ref:
             s.tokens_seen += 1
-    # Layer 0 sees the same input on both sides: its state meets the bar of
-    # the drop-in test.  Later layers take the previous layer's output, equal
-    # only to the activation tolerance, so their states are held to that.
+    # The states take k, v and the gates from fp16 projections whose two
+    # implementations may round an element one fp16 ulp apart (different fp32
+    # accumulation orders), so even layer 0, which sees the same input on both
+    # sides, is held to 5e-3 (an ulp of a unit-size v moves the state by about
+    # 1e-3 of its largest entry); later layers take the previous layer's output,
+    # equal to the activation tolerance, and are held to that.
     for i, m in enumerate((0, 1, 2)):
         for row, s in enumerate(ref):
             assert_state_close(st.linear_states[i, row].cpu(), s.linear[m][0], f"state layer {m} row {row}",
-                               rel=1e-3 if m == 0 else 2e-2)
+                               rel=5e-3 if m == 0 else 2e-2)
 
 
 def test_capture_refuses_a_fixed_split(gpu):

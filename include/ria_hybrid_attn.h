@@ -434,6 +434,19 @@ int ria_linear_fp8_group(int m, int k, const void* x, int x_dtype, int64_t x_row
                          int count, const ria_fp8_proj* projs, void* stream);
 
 /*
+ * ria_linear_fp8_group_normed: ria_linear_fp8_group on h = the layer's input
+ * RMSNorm of the fp32 residual stream x, in the same launch:
+ * h = (x * rsqrt(mean(x^2) + eps)) * (1 + norm_weight) in fp32, rounded to
+ * h_dtype (RIA_DT_BF16 for a DeltaNet layer, RIA_DT_F16 for attention) and then
+ * to fp16 (qwen36_attention_cache.py:227-233, 291-293).  Decode sizes only:
+ * m <= 4, k a multiple of 512 up to 4096; norm_weight fp32 [k], 16-byte
+ * aligned; x row stride a multiple of 4.
+ */
+int ria_linear_fp8_group_normed(int m, int k, const float* x, int64_t x_row_stride,
+                                const float* norm_weight, float eps, int h_dtype, int count,
+                                const ria_fp8_proj* projs, void* stream);
+
+/*
  * Sequence snapshots: one row's DeltaNet states, conv ring and KV pages as a
  * contiguous device payload, to be restored into any row (of this pool or
  * another with the same shapes) that has pages for `tokens` tokens; decoding

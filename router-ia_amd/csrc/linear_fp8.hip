@@ -107,6 +107,9 @@ struct LinearArgs {
   int64_t x_stride;
   int m, k, count;
   int mt;               // rows of x per workgroup (streaming kernel): 64 or 128
+  const float* norm_w;  // fused input RMSNorm (one-pass kernel, up to 4 rows of fp32 x), or null
+  float norm_eps;
+  int norm_dtype;       // the normed rows are rounded to this dtype, then to fp16
   Fp8Proj p[kLinGroup];
 };
 
@@ -343,8 +346,9 @@ constexpr int kGemvRows = 16;    // rows of x per workgroup
 constexpr int kGemvMaxWaves = 8; // K <= 4096
 constexpr int kGemvStageRows = 4; // x rows staged through LDS
 
-template <int XT>
+template <int XT, bool NORM>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const LinearArgs a) {
+  static_assert(!NORM || XT == RIA_DT_F32, "the fused norm reads the fp32 residual stream");
   using F16 = Kv16<RIA_DT_F16>;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -402,10 +406,59 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
     constexpr int NR = decltype(nr)::value;
     if constexpr (NR > 0) {
       u32x4 xs[NR];
+      if constexpr (NORM) {
+        // h = rmsnorm(x) (1 + w) over the whole row, rounded to norm_dtype, then
+        // to fp16 (qwen36_attention_cache.py:227-233, 291-293): each wave sums
+        // the squares of its 512 K, the waves' sums meet in LDS (added in wave
+        // order), and every wave normalises its own slice.
+        f32x4 xf[NR][2];
+        const f32x4* xp = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) + k0 + 8 * lane);
 #pragma unroll
-      for (int r = 0; r < NR; ++r) xs[r] = load_x8<XT>(a.x, (int64_t)(m0 + r) * a.x_stride + k0 + 8 * lane);
-      load_w();
-      __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
+        for (int r = 0; r < NR; ++r) {
+          xf[r][0] = xp[(m0 + r) * a.x_stride / 4];
+          xf[r][1] = xp[(m0 + r) * a.x_stride / 4 + 1];
+        }
+        const f32x4* wn = reinterpret_cast<const f32x4*>(a.norm_w + k0 + 8 * lane);
+        const f32x4 nw0 = wn[0], nw1 = wn[1];
+        load_w();
+        __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
+        __shared__ float norm_ss[kGemvMaxWaves][kGemvStageRows];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          float ss = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ss = add_rn(ss, mul_rn(xf[r][0][i], xf[r][0][i]));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ss = add_rn(ss, mul_rn(xf[r][1][i], xf[r][1][i]));
+          ss = wave_sum(ss);
+          if (lane == 0) norm_ss[wave][r] = ss;
+        }
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          float tot = 0.f;
+          for (int q = 0; q < waves; ++q) tot += norm_ss[q][r];
+          const float rs = rms_scale(tot, a.k, a.norm_eps);
+          float hv[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            hv[i] = rmsnorm_elem<RIA_DT_F32>(xf[r][0][i], rs, nw0[i]);
+            hv[4 + i] = rmsnorm_elem<RIA_DT_F32>(xf[r][1][i], rs, nw1[i]);
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            hv[i] = a.norm_dtype == RIA_DT_BF16 ? through_dtype<RIA_DT_BF16>(hv[i]) : hv[i];
+          uint32_t pk[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pk[j] = F16::pack2(hv[2 * j], hv[2 * j + 1]);
+          xs[r] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) xs[r] = load_x8<XT>(a.x, (int64_t)(m0 + r) * a.x_stride + k0 + 8 * lane);
+        load_w();
+        __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait
+      }
 #pragma unroll
       for (int r = 0; r < NR; ++r) own[64 * r + lane] = xs[r];
       __builtin_amdgcn_wave_barrier();  // the region is this wave's: LDS keeps its order
@@ -438,7 +491,9 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
     case 2: load_operands(std::integral_constant<int, 2>{}); break;
     case 3: load_operands(std::integral_constant<int, 3>{}); break;
     case 4: load_operands(std::integral_constant<int, 4>{}); break;
-    default: load_operands(std::integral_constant<int, 0>{}); break;
+    default:
+      if constexpr (!NORM) load_operands(std::integral_constant<int, 0>{});  // the host keeps NORM to 4 rows
+      break;
   }
 
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -477,11 +532,11 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
   }
 }
 
-template <int XT>
+template <int XT, bool NORM = false>
 static void launch_gemv(const LinearArgs& a, dim3 grid, hipStream_t st) {
   const int waves = a.k / kGemvSlice;
   const size_t lds = static_cast<size_t>(waves) * (a.m <= kGemvStageRows ? a.m : 1) * 64 * sizeof(u32x4);
-  hipLaunchKernelGGL((gemv_fp8_kernel<XT>), grid, dim3(64 * waves), lds, st, a);
+  hipLaunchKernelGGL((gemv_fp8_kernel<XT, NORM>), grid, dim3(64 * waves), lds, st, a);
 }
 
 template <int XT>
@@ -527,7 +582,8 @@ extern "C" int ria_dequant_fp8(int64_t rows, int cols, const void* weight, const
 // Validates and launches one group of projections of the same x (shared by
 // ria_linear_fp8 and ria_linear_fp8_group; `who` names the entry point in errors).
 static int linear_group(const char* who, int m, int k, const void* x, int x_dtype, int64_t x_row_stride, int count,
-                        const ria_fp8_proj* projs, void* stream) {
+                        const ria_fp8_proj* projs, void* stream, const float* norm_w = nullptr, float norm_eps = 0.f,
+                        int norm_dtype = RIA_DT_F16) {
   if (count < 1 || count > kLinGroup) return set_error(RIA_ERR_INVALID, "%s: 1 to %d projections per call", who, kLinGroup);
   if (m < 0 || k <= 0) return set_error(RIA_ERR_INVALID, "%s: bad sizes", who);
   if (k % kFp8Block || k / kFp8Block > kLinMaxChunks)
@@ -557,6 +613,16 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
       return set_error(RIA_ERR_INVALID, "%s: weight must be 16-byte aligned (projection %d)", who, j);
   }
   const bool gemv = m <= kGemvRows && k % kGemvSlice == 0 && k / kGemvSlice <= kGemvMaxWaves;
+  if (norm_w) {
+    if (!gemv || m > kGemvStageRows)
+      return set_error(RIA_ERR_INVALID, "%s: the fused input norm takes up to %d rows and K a multiple of %d up to %d",
+                       who, kGemvStageRows, kGemvSlice, kGemvSlice * kGemvMaxWaves);
+    if (x_dtype != RIA_DT_F32 || x_row_stride % 4 || reinterpret_cast<uintptr_t>(norm_w) % 16)
+      return set_error(RIA_ERR_INVALID, "%s: fused norm: fp32 x with a row stride a multiple of 4, 16-byte aligned "
+                       "norm weight", who);
+    if (norm_dtype != RIA_DT_BF16 && norm_dtype != RIA_DT_F16)
+      return set_error(RIA_ERR_INVALID, "%s: fused norm rounds to bf16 or fp16", who);
+  }
   // Streaming kernel: workgroups of mt rows x 16 ct output features.  A
   // workgroup reads its mt rows of x (from L2) and its weights through the
   // CU's L1, whose misses in flight bound the rate, so the shape is the one
@@ -590,6 +656,9 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
   a.k = k;
   a.count = count;
   a.mt = mt;
+  a.norm_w = norm_w;
+  a.norm_eps = norm_eps;
+  a.norm_dtype = norm_dtype;
   int tile = 0;
   for (int j = 0; j < count; ++j) {
     const ria_fp8_proj& q = projs[j];
@@ -601,7 +670,9 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
   if (mblocks > 65535) return set_error(RIA_ERR_INVALID, "%s: too many rows", who);
   const dim3 grid(static_cast<unsigned>(tile), static_cast<unsigned>(mblocks));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (gemv) {
+  if (norm_w) {
+    launch_gemv<RIA_DT_F32, true>(a, grid, st);
+  } else if (gemv) {
     if (x_dtype == RIA_DT_F16)
       launch_gemv<RIA_DT_F16>(a, grid, st);
     else if (x_dtype == RIA_DT_BF16)
@@ -628,4 +699,12 @@ extern "C" int ria_linear_fp8(int m, int n, int k, const void* x, int x_dtype, i
 extern "C" int ria_linear_fp8_group(int m, int k, const void* x, int x_dtype, int64_t x_row_stride, int count,
                                     const ria_fp8_proj* projs, void* stream) {
   return linear_group("ria_linear_fp8_group", m, k, x, x_dtype, x_row_stride, count, projs, stream);
+}
+
+extern "C" int ria_linear_fp8_group_normed(int m, int k, const float* x, int64_t x_row_stride,
+                                           const float* norm_weight, float eps, int h_dtype, int count,
+                                           const ria_fp8_proj* projs, void* stream) {
+  if (!norm_weight) return set_error(RIA_ERR_INVALID, "ria_linear_fp8_group_normed: null norm_weight");
+  return linear_group("ria_linear_fp8_group_normed", m, k, x, RIA_DT_F32, x_row_stride, count, projs, stream,
+                      norm_weight, eps, h_dtype);
 }

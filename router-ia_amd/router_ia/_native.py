@@ -84,6 +84,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ria_dequant_fp8": (_c_int, [_c_i64, _c_int, _vp, _vp, _vp, _c_int, _vp]),
     "ria_linear_fp8": (_c_int, [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _vp, _c_int, _c_i64, _vp]),
     "ria_linear_fp8_group": (_c_int, [_c_int, _c_int, _vp, _c_int, _c_i64, _c_int, _vp, _vp]),
+    "ria_linear_fp8_group_normed": (_c_int, [_c_int, _c_int, _vp, _c_i64, _vp, _c_f32, _c_int, _c_int, _vp, _vp]),
     "ria_seq_state_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "ria_seq_state_save": (
         _c_int,

@@ -17,6 +17,7 @@ Per layer (B rows, hidden 2048, the reference's CUDA dtypes):
 
     DeltaNet (model layer 4i, 4i+1, 4i+2)        full attention (model layer 4i+3)
     h = bf16(rmsnorm(x))           ria_rmsnorm     h = fp16(rmsnorm(x))
+                                   (inside the projection launch up to 4 rows)
     qkv, z (fp16), a, b (fp32)     one grouped     q, gate, k, v (fp16)  one grouped
                                    FP8 launch                            FP8 launch
     conv, gates, delta rule,       ria_gdn_decode  k_norm + RoPE + append, q_norm +
@@ -40,6 +41,7 @@ from . import kernels as K
 from .batched_state import BatchedAttentionState
 
 HIDDEN = 2048
+FUSED_NORM_ROWS = 4  # up to this many rows the input RMSNorm runs inside the projection launch
 
 
 @dataclass
@@ -181,24 +183,31 @@ class BatchedForward:
         i = self.index[model_layer]
         st = self.state
         b = st.max_seqs
+        fused = b <= FUSED_NORM_ROWS  # the input norm inside the projection launch
         if isinstance(w, LinearLayerWeights):
-            K.rmsnorm(x, w.input_norm, out=self.h_bf16)
-            h = self.h_bf16
-            if b > 16:
-                # bf16(h) -> fp16 once here (exact in fp16's range, as the projection
-                # would convert it), rather than in every workgroup of the streaming kernel
-                h = self.h_f16.copy_(self.h_bf16)
-            K.linear_fp8_group(h, [w.in_proj_qkv.pair(), w.in_proj_z.pair(), w.in_proj_a.pair(),
-                                   w.in_proj_b.pair()],
-                               out=[self.mixed, self.z, self.gate_a, self.gate_b])
+            projs = [w.in_proj_qkv.pair(), w.in_proj_z.pair(), w.in_proj_a.pair(), w.in_proj_b.pair()]
+            outs = [self.mixed, self.z, self.gate_a, self.gate_b]
+            if fused:
+                K.linear_fp8_group(x, projs, out=outs, norm_weight=w.input_norm, norm_dtype=torch.bfloat16)
+            else:
+                K.rmsnorm(x, w.input_norm, out=self.h_bf16)
+                h = self.h_bf16
+                if b > 16:
+                    # bf16(h) -> fp16 once here (exact in fp16's range, as the projection
+                    # would convert it), rather than in every workgroup of the streaming kernel
+                    h = self.h_f16.copy_(self.h_bf16)
+                K.linear_fp8_group(h, projs, out=outs)
             st.linear_step(i, self.mixed, w.conv_weight, self.gate_a, self.gate_b, gate_mode=nat.RIA_GATE_RAW,
                            A_log=w.A_log, dt_bias=w.dt_bias, out=self.gated, z=self.z, norm_weight=w.norm_weight)
             K.linear_fp8_group(self.gated.view(b, -1), [w.out_proj.pair()], out=[x], accumulate=[True])
         else:
-            K.rmsnorm(x, w.input_norm, out=self.h_f16)
-            K.linear_fp8_group(self.h_f16, [w.query.pair(), w.gate.pair(), w.k_proj.pair(), w.v_proj.pair()],
-                               out=[self.q.view(b, -1), self.gate.view(b, -1), self.k.view(b, -1),
-                                    self.v.view(b, -1)])
+            projs = [w.query.pair(), w.gate.pair(), w.k_proj.pair(), w.v_proj.pair()]
+            outs = [self.q.view(b, -1), self.gate.view(b, -1), self.k.view(b, -1), self.v.view(b, -1)]
+            if fused:
+                K.linear_fp8_group(x, projs, out=outs, norm_weight=w.input_norm, norm_dtype=torch.float16)
+            else:
+                K.rmsnorm(x, w.input_norm, out=self.h_f16)
+                K.linear_fp8_group(self.h_f16, projs, out=outs)
             st.full_step(i, self.q, self.k, self.v, self.gate, out=self.attn, q_norm_weight=w.q_norm,
                          k_norm_weight=w.k_norm)
             K.linear_fp8_group(self.attn.view(b, -1), [w.o_proj.pair()], out=[x], accumulate=[True])

@@ -534,12 +534,16 @@ def linear_fp8(x: torch.Tensor, weight: torch.Tensor, scale_inv: torch.Tensor, *
 def linear_fp8_group(x: torch.Tensor, projections: list[tuple[torch.Tensor, torch.Tensor]], *,
                      out: list[torch.Tensor] | None = None,
                      out_dtype: torch.dtype | list[torch.dtype] = torch.float16,
-                     accumulate: list[bool] | None = None) -> list[torch.Tensor]:
+                     accumulate: list[bool] | None = None, norm_weight: torch.Tensor | None = None,
+                     norm_dtype: torch.dtype = torch.bfloat16, eps: float = 1e-6) -> list[torch.Tensor]:
     """Up to 4 FP8 projections of the same x in one launch (ria_linear_fp8_group).
 
     projections: (weight [N_j, K] float8_e4m3fn, scale_inv) pairs; returns /
     fills y_j [M, N_j] (each in its own dtype), each equal to linear_fp8(x, w_j, s_j).
     With accumulate[j], the fp32 out[j] receives out[j] + y_j (a residual add).
+    With the fp32 ``norm_weight`` [K], x is the fp32 residual stream and the
+    projections read its (1 + w) RMSNorm rounded to norm_dtype
+    (ria_linear_fp8_group_normed; up to 4 rows).
     """
     dev = x.device
     _require_gpu("x", x, dev)
@@ -567,9 +571,20 @@ def linear_fp8_group(x: torch.Tensor, projections: list[tuple[torch.Tensor, torc
         if add and y.dtype != torch.float32:
             raise ValueError(f"out {j}: accumulating needs fp32")
         arr[j] = nat.Fp8Proj(_ptr(w), _ptr(s), _ptr(y), int(y.stride(0)) if m > 1 else n, n, dtype_code(y), int(add))
-    rc = nat.load().ria_linear_fp8_group(m, k, _ptr(x), dtype_code(x), xs, len(projections), ctypes.addressof(arr),
-                                         _stream(dev))
-    nat.check(rc, "ria_linear_fp8_group")
+    if norm_weight is None:
+        rc = nat.load().ria_linear_fp8_group(m, k, _ptr(x), dtype_code(x), xs, len(projections),
+                                             ctypes.addressof(arr), _stream(dev))
+        nat.check(rc, "ria_linear_fp8_group")
+        return out
+    if x.dtype != torch.float32:
+        raise ValueError("the fused input norm reads fp32 x")
+    if norm_dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("norm_dtype must be bf16 or fp16")
+    rc = nat.load().ria_linear_fp8_group_normed(m, k, _ptr(x), xs, _norm_weight("norm_weight", norm_weight, k, dev),
+                                                float(eps), nat.RIA_DT_BF16 if norm_dtype == torch.bfloat16
+                                                else nat.RIA_DT_F16, len(projections), ctypes.addressof(arr),
+                                                _stream(dev))
+    nat.check(rc, "ria_linear_fp8_group_normed")
     return out
 
 

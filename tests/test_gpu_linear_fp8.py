@@ -127,3 +127,30 @@ def test_linear_fp8_group_accumulates_into_fp32(gpu, m):
     sep = K.linear_fp8(x, w8.to(gpu), s.to(gpu), out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(y.cpu(), base.cpu() + sep.cpu())
+
+
+@pytest.mark.parametrize("m,k,hdt", [(1, 2048, torch.bfloat16), (3, 2048, torch.float16), (4, 4096, torch.bfloat16)])
+def test_linear_fp8_group_with_fused_input_norm(gpu, m, k, hdt):
+    announce(f"linear_fp8_group_normed: M={m} K={k} h {hdt}")
+    ns = [8192, 4096, 32, 32] if k == 2048 else [2048]
+    proj = [W.fp8_block_weight(700 + j, n, k) for j, n in enumerate(ns)]
+    g = torch.Generator().manual_seed(710 + m)
+    x = (torch.randn((m, k), generator=g) * 3.0).to(gpu)
+    wn = (torch.randn((k,), generator=g) * 0.1).to(torch.bfloat16).float().to(gpu)
+    proj_d = [(w.to(gpu), s.to(gpu)) for w, s in proj]
+    fused = K.linear_fp8_group(x, proj_d, norm_weight=wn, norm_dtype=hdt)
+    h = K.rmsnorm(x, wn, out=torch.empty((m, k), dtype=hdt, device=gpu))
+    separate = K.linear_fp8_group(h, proj_d)
+    for j, (w, s) in enumerate(proj):
+        # both against the oracle's rmsnorm -> dtype -> fp16 projection
+        want = O.projection_fp8(O.rmsnorm(x.cpu(), wn.cpu()).to(hdt), w, s)
+        assert_act_close(fused[j].cpu(), want, f"fused projection {j}")
+        assert_act_close(separate[j].cpu(), want, f"separate projection {j}")
+
+
+def test_linear_fp8_group_normed_host_checks(gpu):
+    w8, s = W.fp8_block_weight(720, 64, 2048)
+    x = torch.randn((5, 2048)).to(gpu)
+    wn = torch.zeros((2048,), device=gpu)
+    with pytest.raises(RuntimeError, match="up to 4 rows"):
+        K.linear_fp8_group(x, [(w8.to(gpu), s.to(gpu))], norm_weight=wn)

@@ -32,6 +32,8 @@
 //     combine kernel merges the splits and applies the sigmoid gate.
 #include <math.h>
 
+#include <algorithm>
+
 #include "ria_common.h"
 
 namespace ria {
@@ -144,6 +146,13 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   a.v_cache[(tile * kAttnHeadDim + d) * kPageTokens + off] = Kv16<KVT>::from_f32(vv);
 }
 
+// Scalar (SMEM) load of a wave-uniform index from a buffer this kernel never
+// writes (positions, context lengths, rows, page tables): it is counted apart
+// from the vector loads, so waiting for it does not wait for K/V in flight.
+__device__ __forceinline__ int32_t ld_uniform(const int32_t* p, int64_t i) {
+  return ((const __attribute__((address_space(4))) int32_t*)p)[i];
+}
+
 // Pages of the context of batch row b (never past the row's page-table entries).
 __device__ __forceinline__ int row_ctx(const AttnArgs& a, int b) {
   return min(a.ctx_lens ? a.ctx_lens[b] : a.ctx_scalar, (int)min<int64_t>(a.pt_stride * kPageTokens, 1 << 30));
@@ -154,12 +163,20 @@ __device__ __forceinline__ int row_ctx(const AttnArgs& a, int b) {
 // [w * chunk, (w + 1) * chunk).  Workgroup w's partial for unit u lives at
 // index w + u, which is unique because the (w, u) pairs that meet form a
 // monotone staircase.
+//
+// When few units share the grid (units * kPadUnitsRatio <= workgroups), each
+// unit's range is padded to whole chunks, so no workgroup straddles two
+// units: a straddling workgroup runs the q prologue and the merge twice, and
+// at small batches, where every workgroup streams only a few pages, it ends
+// last.  The chunk is then sized over workgroups - units, which leaves room
+// for the padding (at most one partial chunk per unit).
 constexpr int kMaxBalancedUnits = 4096;
 constexpr int kMinChunkPages = 4;  // 64 tokens: small batches still spread over the CUs
+constexpr int kPadUnitsRatio = 32;
 
 // Inclusive block scan of up to 256 per-thread values through LDS; returns
-// the exclusive prefix of this thread's value.
-__device__ int block_exclusive_scan(int v, int* scratch) {
+// the exclusive prefix of this thread's value and the block total.
+__device__ int block_exclusive_scan(int v, int* scratch, int* total) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int x = v;
 #pragma unroll
@@ -168,10 +185,11 @@ __device__ int block_exclusive_scan(int v, int* scratch) {
     if (lane >= off) x += y;
   }
   if (lane == 63) scratch[wave] = x;
-  __syncthreads();
+  lds_barrier();
   int base = 0;
   for (int w = 0; w < wave; ++w) base += scratch[w];
-  __syncthreads();
+  *total = scratch[0] + scratch[1] + scratch[2] + scratch[3];
+  lds_barrier();
   return base + x - v;
 }
 
@@ -194,34 +212,84 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
   float (*q_lds)[kAttnHeadDim] = sm_o[0];
   // Scores are kept in log2 units: s2 = (q . k) * scale * log2(e).
   const float sl2 = a.scale * 1.4426950408889634f;
+  // Per-launch constants: the RoPE frequency of this thread's rotary dim and
+  // the q_norm weights of its dim and RoPE partner.
+  const float ifreq = a.rope_dim == 64 ? a.inv_freq[tid & 31] : 0.f;
+  float w_self = 0.f, w_partner = 0.f;
+  if constexpr (QNORM) {
+    w_self = a.q_norm_w[tid];
+    w_partner = a.q_norm_w[tid ^ 32];
+  }
 
-  // One (batch row, KV head, token range) -> partial `part`.
-  auto process = [&](int b, int kvh, int tok0, int tok1, int64_t part) {
-    const int row = a.seq_slot ? a.seq_slot[b] : b;
-    const float pos = static_cast<float>(a.positions ? a.positions[b] : a.pos_scalar);
-    __syncthreads();  // the previous range's merge has been read out of sm_o
+  // One (batch row, KV head, token range [tok0, min(context, tok_hi))) -> partial `part`.
+  auto process = [&](int b, int kvh, int tok0, int tok_hi, int64_t part) {
+    // Every load that depends only on the unit is issued at once: the
+    // group's q rows (heads unrolled to the largest group, 8; heads past the
+    // group re-read the last one, so no load waits inside a branch for its
+    // own conversion), the position, the row, the context and this wave's
+    // first page-table entry.  The first page's K/V loads follow, so they are
+    // in flight while q is normalised, rotated and packed (at small batches a
+    // wave streams only a page or two).
+    // (an opaque copy of the thread index keeps the prologue's addresses from
+    // being hoisted out of the unit loop and held across the page loop)
+    int t = tid;
+    asm volatile("" : "+v"(t));
+    const bool rope = a.rope_dim == 64;
+    float qx[8], qp[8];
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      const int64_t base = (int64_t)b * a.q_stride + (int64_t)(kvh * G + min(h, G - 1)) * kAttnHeadDim;
+      qx[h] = load_act<QT>(a.q, base + t);
+      qp[h] = QNORM ? 0.f : load_act<QT>(a.q, base + (t ^ 32));
+    }
+    const int page0 = tok0 / kPageTokens;
+    const int64_t pfirst = min<int64_t>(page0 + __builtin_amdgcn_readfirstlane(wave), a.pt_stride - 1);
+    int row = b, phys_first;  // phys_first is used only if the wave has a page
+    if (a.seq_slot) {         // indirected rows: the table row is known only after this load
+      row = ld_uniform(a.seq_slot, b);
+      phys_first = ld_uniform(a.page_table + (int64_t)row * a.pt_stride, pfirst);
+    } else {
+      phys_first = ld_uniform(a.page_table + (int64_t)b * a.pt_stride, pfirst);
+    }
+    const int posi = a.positions ? ld_uniform(a.positions, b) : a.pos_scalar;
+    const int ctx = min(a.ctx_lens ? ld_uniform(a.ctx_lens, b) : a.ctx_scalar,
+                        static_cast<int>(min<int64_t>(a.pt_stride * kPageTokens, 1 << 30)));
+    const int32_t* pt = a.page_table + (int64_t)row * a.pt_stride;
+    const int tok1 = min(ctx, tok_hi);
+    const int page_end = (tok1 + kPageTokens - 1) / kPageTokens;
+
+    auto load_tile = [&](int phys, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
+      phys = (phys < 0 || phys >= a.num_pages) ? 0 : phys;  // unallocated entries never fault
+      const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
+      const u32x4* kp = reinterpret_cast<const u32x4*>(a.k_cache + tile * kTileElems) + lane;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) kr[kk] = ld_stream(kp + kk * 64);
+      const uint16_t* vp = a.v_cache + tile * kTileElems + n * kPageTokens + 4 * g4;
+#pragma unroll
+      for (int db = 0; db < 16; ++db) vr[db] = ld_stream(reinterpret_cast<const u32x2*>(vp + db * 16 * kPageTokens));
+    };
+    auto load_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) { load_tile(pt[p], kr, vr); };
+
+    u32x4 kA[8], kB[8];
+    u32x2 vA[16], vB[16];
+    int p = page0 + wave;
+    if (p < page_end) load_tile(phys_first, kA, vA);
+    lds_barrier();  // the previous range's merge has been read out of sm_o
 
     // ---- Q: rotate the group's query heads into LDS (one thread per dim).
     float rc = 1.f, rs = 0.f;
-    if (a.rope_dim == 64 && tid < 64) {
-      const float ang = mul_rn(pos, a.inv_freq[tid & 31]);
-      rc = cosf(ang);
-      rs = sinf(ang);
-    }
+    if (rope && t < 64) sincosf(mul_rn(static_cast<float>(posi), ifreq), &rs, &rc);
     if constexpr (QNORM) {
       // q_norm (qwen36_attention_cache.py:302-304) before RoPE: raw rows into
       // the second merge slice (free until this range's merge), one wave per
       // head for the sum of squares, then each thread normalises its dim (and
       // its RoPE partner) and rotates.
-      // (an opaque copy of the thread index keeps this branch's addresses
-      // from being hoisted out of the unit loop and held across the page loop)
-      int t = tid;
-      asm volatile("" : "+v"(t));
       const int tl = t & 63, tw = t >> 6;
       float (*raw)[kAttnHeadDim] = sm_o[1];
-      for (int h = 0; h < G; ++h)
-        raw[h][t] = load_act<QT>(a.q, (int64_t)b * a.q_stride + (int64_t)(kvh * G + h) * kAttnHeadDim + t);
-      __syncthreads();
+#pragma unroll
+      for (int h = 0; h < 8; ++h)
+        if (h < G) raw[h][t] = qx[h];
+      lds_barrier();
       for (int h = tw; h < G; h += 4) {
         float ss = 0.f;
 #pragma unroll
@@ -229,28 +297,29 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
         ss = wave_sum(ss);
         if (tl == 0) qn_s[h] = rms_scale(ss, kAttnHeadDim);
       }
-      __syncthreads();
-      const float w_self = a.q_norm_w[t], w_partner = a.q_norm_w[t ^ 32];
-      for (int h = 0; h < G; ++h) {
-        float x = rmsnorm_elem<QT>(raw[h][t], qn_s[h], w_self);
-        if (a.rope_dim == 64 && t < 64) {
-          const float partner = rmsnorm_elem<QT>(raw[h][t ^ 32], qn_s[h], w_partner);
-          x = add_rn(mul_rn(x, rc), mul_rn(t < 32 ? -partner : partner, rs));
+      lds_barrier();
+#pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        if (h < G) {
+          float x = rmsnorm_elem<QT>(qx[h], qn_s[h], w_self);
+          if (rope && t < 64) {
+            const float partner = rmsnorm_elem<QT>(raw[h][t ^ 32], qn_s[h], w_partner);
+            x = add_rn(mul_rn(x, rc), mul_rn(t < 32 ? -partner : partner, rs));
+          }
+          q_lds[h][t] = x;
         }
-        q_lds[h][t] = x;
       }
     } else {
-      for (int h = 0; h < G; ++h) {
-        const int64_t base = (int64_t)b * a.q_stride + (int64_t)(kvh * G + h) * kAttnHeadDim;
-        float x = load_act<QT>(a.q, base + tid);
-        if (a.rope_dim == 64 && tid < 64) {
-          const float partner = load_act<QT>(a.q, base + (tid ^ 32));
-          x = add_rn(mul_rn(x, rc), mul_rn(tid < 32 ? -partner : partner, rs));
+#pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        if (h < G) {
+          float x = qx[h];
+          if (rope && t < 64) x = add_rn(mul_rn(x, rc), mul_rn(t < 32 ? -qp[h] : qp[h], rs));
+          q_lds[h][t] = x;
         }
-        q_lds[h][tid] = x;
       }
     }
-    __syncthreads();
+    lds_barrier();
     // Pack the B operand: lane (head n, group g4) holds dims 64*g4 + 8*kk + j,
     // as a bf16 hi part and a bf16 remainder.
     {
@@ -272,28 +341,12 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
         q_pk[1][kk0 + k2][lane] = uint4{wl[0], wl[1], wl[2], wl[3]};
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     f32x4 o[16];
 #pragma unroll
     for (int db = 0; db < 16; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;
-
-    const int page0 = tok0 / kPageTokens;
-    const int page_end = (tok1 + kPageTokens - 1) / kPageTokens;
-    const int32_t* pt = a.page_table + (int64_t)row * a.pt_stride;
-
-    auto load_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
-      int phys = pt[p];
-      phys = (phys < 0 || phys >= a.num_pages) ? 0 : phys;  // unallocated entries never fault
-      const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
-      const u32x4* kp = reinterpret_cast<const u32x4*>(a.k_cache + tile * kTileElems) + lane;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) kr[kk] = ld_stream(kp + kk * 64);
-      const uint16_t* vp = a.v_cache + tile * kTileElems + n * kPageTokens + 4 * g4;
-#pragma unroll
-      for (int db = 0; db < 16; ++db) vr[db] = ld_stream(reinterpret_cast<const u32x2*>(vp + db * 16 * kPageTokens));
-    };
 
     auto compute_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
       // Re-read the Q operand from LDS every page (an opaque offset keeps the
@@ -359,11 +412,7 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
 
     // Pages wave, wave+4, ...: the next page's loads are issued before the
     // current page is consumed (two register buffers, loop unrolled by two).
-    int p = page0 + wave;
     if (p < page_end) {
-      u32x4 kA[8], kB[8];
-      u32x2 vA[16], vB[16];
-      load_page(p, kA, vA);
       while (true) {
         int pn = p + 4;
         if (pn < page_end) load_page(pn, kB, vB);
@@ -392,8 +441,11 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
         for (int i = 0; i < 4; ++i) sm_o[wave][n & 7][db * 16 + 4 * g4 + i] = o[db][i];
       }
     }
-    __syncthreads();
-    for (int h = 0; h < G; ++h) {
+    lds_barrier();
+    // Unrolled over the (at most 8) heads so every head's LDS reads issue at
+    // once; heads past the group read unused LDS and store nothing.
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
       float M = -INFINITY;
 #pragma unroll
       for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w][h]);
@@ -404,10 +456,12 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
         acc = fmaf(wt, sm_o[w][h][tid], acc);
         L = fmaf(wt, sm_l[w][h], L);
       }
-      a.ws_acc[(part * G + h) * kAttnHeadDim + tid] = acc;
-      if (tid == 0) {
-        a.ws_stats[(part * G + h) * 2 + 0] = M;
-        a.ws_stats[(part * G + h) * 2 + 1] = L;
+      if (h < G) {
+        a.ws_acc[(part * G + h) * kAttnHeadDim + tid] = acc;
+        if (tid == 0) {
+          a.ws_stats[(part * G + h) * 2 + 0] = M;
+          a.ws_stats[(part * G + h) * 2 + 1] = L;
+        }
       }
     }
   };
@@ -419,31 +473,53 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
     const int ctx = row_ctx(a, b);
     const int tok0 = split * a.split_tokens;
     if (tok0 >= ctx) return;
-    process(b, kvh, tok0, min(ctx, tok0 + a.split_tokens), ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits + split);
+    process(b, kvh, tok0, tok0 + a.split_tokens, ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits + split);
   } else {
     // ---- page offsets of every unit (u = b * Hkv + kvh) in LDS
     __shared__ int off[kMaxBalancedUnits + 1];
     __shared__ int scan_scratch[4];
     const int units = a.batch * a.num_kv_heads;
     const int per = (units + 255) / 256;  // units per thread (<= 16)
-    int mine = 0;
-    for (int i = 0; i < per; ++i) {
-      const int u = tid * per + i;
-      if (u < units) mine += (row_ctx(a, u / a.num_kv_heads) + kPageTokens - 1) / kPageTokens;
+    const int nwg = static_cast<int>(gridDim.x);
+    int upages[16];
+    if (a.ctx_lens) {  // unconditional loads (clamped unit), masked below
+#pragma unroll
+      for (int i = 0; i < 16; ++i) upages[i] = a.ctx_lens[min(tid * per + i, units - 1) / a.num_kv_heads];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) upages[i] = a.ctx_scalar;
     }
-    int run = block_exclusive_scan(mine, scan_scratch);
-    for (int i = 0; i < per; ++i) {
+    const int ctx_cap = static_cast<int>(min<int64_t>(a.pt_stride * kPageTokens, 1 << 30));
+    int mine = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
       const int u = tid * per + i;
-      if (u < units) {
+      upages[i] = (i < per && u < units) ? (min(upages[i], ctx_cap) + kPageTokens - 1) / kPageTokens : 0;
+      mine += upages[i];
+    }
+    int total = 0;
+    int run = block_exclusive_scan(mine, scan_scratch, &total);
+    const bool padded = units * kPadUnitsRatio <= nwg;
+    const int chunk = max((total + (padded ? nwg - units : nwg) - 1) / (padded ? nwg - units : nwg), kMinChunkPages);
+    if (padded) {  // each unit rounded up to whole chunks
+      mine = 0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        upages[i] = (upages[i] + chunk - 1) / chunk * chunk;
+        mine += upages[i];
+      }
+      run = block_exclusive_scan(mine, scan_scratch, &total);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int u = tid * per + i;
+      if (i < per && u < units) {
         off[u] = run;
-        run += (row_ctx(a, u / a.num_kv_heads) + kPageTokens - 1) / kPageTokens;
+        run += upages[i];
       }
     }
     if (tid == (units - 1) / per) off[units] = run;  // the thread that holds the last unit
-    __syncthreads();
-    const int total = off[units];
-    const int nwg = static_cast<int>(gridDim.x);
-    const int chunk = max((total + nwg - 1) / nwg, kMinChunkPages);
+    lds_barrier();
     if (blockIdx.x == 0) {
       // publish the partition for the combine kernel
       for (int u = tid; u <= units; u += 256) a.ws_units[2 + u] = off[u];
@@ -462,12 +538,16 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
       const int mid = (lo + hi + 1) >> 1;
       if (off[mid] <= p0) lo = mid; else hi = mid - 1;
     }
-    for (int u = lo; u < units && off[u] < p1; ++u) {
-      const int a0 = max(off[u], p0) - off[u], a1 = min(off[u + 1], p1) - off[u];  // unit-local pages
+    // (the unit and its page range come from LDS, which the compiler treats
+    // as per-lane: readfirstlane makes them scalar, so the unit's own loads
+    // in process() are scalar loads)
+    for (int u = __builtin_amdgcn_readfirstlane(lo); u < units; ++u) {
+      const int ou = __builtin_amdgcn_readfirstlane(off[u]);
+      if (ou >= p1) break;
+      const int a0 = max(ou, p0) - ou, a1 = min(__builtin_amdgcn_readfirstlane(off[u + 1]), p1) - ou;  // unit-local pages
       if (a1 <= a0) continue;
       const int b = u / a.num_kv_heads, kvh = u % a.num_kv_heads;
-      const int ctx = row_ctx(a, b);
-      process(b, kvh, a0 * kPageTokens, min(ctx, a1 * kPageTokens), (int64_t)w + u);
+      process(b, kvh, a0 * kPageTokens, a1 * kPageTokens, (int64_t)w + u);
     }
   }
 }
@@ -536,9 +616,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 }
 
 // attn_combine_kernel for long partial lists (a few units share all the
-// workgroups, as at small batches).  Wave p of the STREAMS waves takes partials p, p + STREAMS, ... (kBatch of
-// them in flight), lane dg its dims 4 dg .. 4 dg + 3 (16-byte loads); the
-// streams are added in order through LDS.
+// workgroups, as at small batches).  Wave p of the STREAMS waves takes
+// partials p, p + STREAMS, ... (kBatch of them in flight), lane dg its dims
+// 4 dg .. 4 dg + 3 (16-byte loads), in one pass with a running max; the
+// streams are merged in order through LDS.
 template <int GT, int OT, bool BALANCED, int STREAMS>
 __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArgs a) {
   constexpr int kBatch = 8;
@@ -565,40 +646,32 @@ __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArg
   const float* stats = a.ws_stats + (first * a.group + hi) * 2;  // partial s: stats[s * group * 2 + {0, 1}]
   const float* accs = a.ws_acc + (first * a.group + hi) * kAttnHeadDim + 4 * dg;
   const int64_t sstep = (int64_t)a.group * 2, astep = (int64_t)a.group * kAttnHeadDim;
-  // the largest partial max (stats are in log2 units)
-  float M = -INFINITY;
-  for (int64_t s0 = p; s0 < count; s0 += STREAMS * kBatch) {
-    float mv[kBatch];
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int64_t s = s0 + j * STREAMS;  // past the end: the last partial, loaded and ignored
-      const float v = stats[min(s, count - 1) * sstep];
-      mv[j] = s < count ? v : -INFINITY;
-    }
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) M = fmaxf(M, mv[j]);
-  }
-  __shared__ float m_s[STREAMS];
-  __shared__ f32x4 num_s[STREAMS][64];
-  __shared__ float den_s[STREAMS];
-  if (dg == 0) m_s[p] = M;
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < STREAMS; ++q) M = fmaxf(M, m_s[q]);
+  // One pass with a running max (stats are in log2 units): each wave keeps
+  // (max, num, den) over its partials, rescaled when a batch raises the max.
+  float M = -INFINITY, den = 0.f;
   f32x4 num = {0.f, 0.f, 0.f, 0.f};
-  float den = 0.f;
   for (int64_t s0 = p; s0 < count; s0 += STREAMS * kBatch) {
     float mv[kBatch], sum[kBatch];
     f32x4 acc[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
-      const int64_t s = s0 + j * STREAMS, sc = min(s, count - 1);
+      const int64_t s = s0 + j * STREAMS, sc = min(s, count - 1);  // past the end: the last partial, ignored
       const bool in = s < count;
       const float v = stats[sc * sstep], w = stats[sc * sstep + 1];
       const f32x4 x = *reinterpret_cast<const f32x4*>(accs + sc * astep);
       mv[j] = in ? v : -INFINITY;
       sum[j] = in ? w : 0.f;
       acc[j] = in ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float mb = M;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, mv[j]);
+    if (mb > M) {  // uniform: every lane of the wave reads the same stats
+      const float r = exp2f(M - mb);
+      den *= r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) num[i] *= r;
+      M = mb;
     }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
@@ -608,18 +681,28 @@ __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArg
       den = fmaf(wt, sum[j], den);
     }
   }
+  __shared__ float m_s[STREAMS];
+  __shared__ f32x4 num_s[STREAMS][64];
+  __shared__ float den_s[STREAMS];
   num_s[p][dg] = num;
-  if (dg == 0) den_s[p] = den;
+  if (dg == 0) {
+    m_s[p] = M;
+    den_s[p] = den;
+  }
   __syncthreads();
   if (p != 0) return;
-  f32x4 tn = num_s[0][dg];
-  float td = den_s[0];
+  float Mt = -INFINITY;
 #pragma unroll
-  for (int q = 1; q < STREAMS; ++q) {
+  for (int q = 0; q < STREAMS; ++q) Mt = fmaxf(Mt, m_s[q]);
+  f32x4 tn = {0.f, 0.f, 0.f, 0.f};
+  float td = 0.f;
+#pragma unroll
+  for (int q = 0; q < STREAMS; ++q) {
+    const float wq = m_s[q] == -INFINITY ? 0.f : exp2f(m_s[q] - Mt);
     const f32x4 u = num_s[q][dg];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) tn[i] += u[i];
-    td += den_s[q];
+    for (int i = 0; i < 4; ++i) tn[i] = fmaf(wq, u[i], tn[i]);
+    td = fmaf(wq, den_s[q], td);
   }
   const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + 4 * dg;
   const int64_t oi = ((int64_t)b * a.num_q_heads + h) * kAttnHeadDim + 4 * dg;
@@ -913,7 +996,12 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (phase & RIA_ATTN_SPLITK) {
-  dim3 grid = balanced ? dim3(balanced_workgroups()) : dim3(a.max_splits, num_kv_heads, batch);
+  // A balanced launch needs no more workgroups than the largest possible page
+  // stream fills at the minimum chunk (a small batch leaves the rest idle).
+  const int64_t max_stream = (int64_t)batch * num_kv_heads * ((max_ctx + kPageTokens - 1) / kPageTokens);
+  const int bal_wgs = static_cast<int>(std::min<int64_t>(
+      balanced_workgroups(), (max_stream + kMinChunkPages - 1) / kMinChunkPages + (int64_t)batch * num_kv_heads));
+  dim3 grid = balanced ? dim3(bal_wgs) : dim3(a.max_splits, num_kv_heads, batch);
 #define RIA_SPLITK_KV(QT_, BAL_, QN_)                                                                  \
   if (kv_dtype == RIA_DT_F16)                                                                          \
     hipLaunchKernelGGL((attn_splitk_kernel<QT_, RIA_DT_F16, BAL_, QN_>), grid, dim3(256), 0, st, a);   \

@@ -183,6 +183,46 @@ __global__ __launch_bounds__(256) void conv_ring_tail_kernel(PrefillArgs a) {
         f32_to_bf16_bits(load_act<XT>(a.x, (int64_t)t * a.x_stride + c));
 }
 
+
+// Step 3 of phase A for two 16-row tiles RA > RB: A rows (q or k, hi/lo bf16
+// rows of stride 136) times k^T over tiles tj <= RA (resp. RB), each tile
+// with the same MFMA sequence as one tile alone; the epilogue applies the
+// decay mask and writes (q k^T) o D (IS_Q) or L = strict_lower(beta k k^T o D).
+template <int RA, int RB, bool IS_Q>
+__device__ __forceinline__ void qk_tile_rows(const uint16_t* A, const uint16_t* khl, const float* G_s,
+                                             const float* beta_s, float* outm, int n, int g4) {
+  f32x4 acc[RA + 1 + RB + 1];
+#pragma unroll
+  for (int t = 0; t < RA + RB + 2; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int d = 32 * s + 8 * g4;
+    const u32x4 aah = lds16(A + (16 * RA + n) * 136 + d), aal = lds16(A + 64 * 136 + (16 * RA + n) * 136 + d);
+    const u32x4 abh = lds16(A + (16 * RB + n) * 136 + d), abl = lds16(A + 64 * 136 + (16 * RB + n) * 136 + d);
+    u32x4 bh[RA + 1], bl[RA + 1];
+#pragma unroll
+    for (int tj = 0; tj <= RA; ++tj) {
+      bh[tj] = lds16(khl + (16 * tj + n) * 136 + d);
+      bl[tj] = lds16(khl + 64 * 136 + (16 * tj + n) * 136 + d);
+    }
+#pragma unroll
+    for (int tj = 0; tj <= RA; ++tj) acc[tj] = mfma3(aah, aal, bh[tj], bl[tj], acc[tj]);
+#pragma unroll
+    for (int tj = 0; tj <= RB; ++tj) acc[RA + 1 + tj] = mfma3(abh, abl, bh[tj], bl[tj], acc[RA + 1 + tj]);
+  }
+#pragma unroll
+  for (int t = 0; t < RA + RB + 2; ++t) {
+    const int ti = t <= RA ? RA : RB, tj = t <= RA ? t : t - RA - 1;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int i = 16 * ti + 4 * g4 + i4, j = 16 * tj + n;
+      const float dec = j <= i ? expf(G_s[i] - G_s[j]) : 0.f;
+      if (IS_Q) outm[i * 68 + j] = j <= i ? acc[t][i4] * dec : 0.f;
+      else outm[i * 68 + j] = j < i ? beta_s[i] * acc[t][i4] * dec : 0.f;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- phase A
 // LDS regions (bytes) and what they hold over the kernel's steps.
 constexpr int kR1 = 0;                   // q hi/lo [64][136] bf16 -> (beta v)^T hi/lo [128][68] bf16
@@ -269,13 +309,18 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     G_s[lane] = g;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_wave_barrier();
-    if (lane == 0) {
-      float acc = 0.f;
-      for (int i = 0; i < kChunk; ++i) {
-        acc += G_s[i];
-        G_s[i] = acc;
-      }
+    // Lane t adds g_0 .. g_t one at a time, the order of a sequential
+    // cumsum (the masked terms add +0, which leaves the sum unchanged).
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kChunk; i += 4) {
+      const float4 gv = *reinterpret_cast<const float4*>(G_s + i);
+      acc += i + 0 <= lane ? gv.x : 0.f;
+      acc += i + 1 <= lane ? gv.y : 0.f;
+      acc += i + 2 <= lane ? gv.z : 0.f;
+      acc += i + 3 <= lane ? gv.w : 0.f;
     }
+    G_s[lane] = acc;
   }
   // Step 2: l2norm of the q and k rows (a row is spread over the 4 lane groups).
   float sq = 0.f, sk = 0.f;
@@ -339,30 +384,13 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
       kt_rec[((dt * 2 + s) * 2 + 1) * 64 + lane] = lo;
     }
   }
-  for (int job = wave; job < 20; job += 4) {
-    const bool is_q = job >= 10;
-    int idx = job % 10, ti = 0;
-    while (idx > ti) {
-      idx -= ti + 1;
-      ++ti;
-    }
-    const int tj = idx;
-    const uint16_t* A = is_q ? qhl : khl;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int d = 32 * s + 8 * g4;
-      acc = mfma3(lds16(A + (16 * ti + n) * 136 + d), lds16(A + 64 * 136 + (16 * ti + n) * 136 + d),
-                  lds16(khl + (16 * tj + n) * 136 + d), lds16(khl + 64 * 136 + (16 * tj + n) * 136 + d), acc);
-    }
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const int i = 16 * ti + 4 * g4 + i4, j = 16 * tj + n;
-      const float dec = j <= i ? expf(G_s[i] - G_s[j]) : 0.f;
-      if (is_q) QKs[i * 68 + j] = j <= i ? acc[i4] * dec : 0.f;
-      else Lm[i * 68 + j] = j < i ? beta_s[i] * acc[i4] * dec : 0.f;
-    }
-  }
+  // Wave 0: K K^T rows 3 and 0, wave 1: rows 2 and 1, waves 2 and 3 the same
+  // rows of Q K^T (5 tiles each); a wave's tiles share their A rows and the
+  // k rows as B operands, so all their operand reads issue together.
+  if (wave == 0) qk_tile_rows<3, 0, false>(khl, khl, G_s, beta_s, Lm, n, g4);
+  else if (wave == 1) qk_tile_rows<2, 1, false>(khl, khl, G_s, beta_s, Lm, n, g4);
+  else if (wave == 2) qk_tile_rows<3, 0, true>(qhl, khl, G_s, beta_s, QKs, n, g4);
+  else qk_tile_rows<2, 1, true>(qhl, khl, G_s, beta_s, QKs, n, g4);
   for (int e = tid; e < kChunk * kChunk; e += 256) {  // upper tiles of (q k^T) o D are zero
     const int i = e >> 6, j = e & 63;
     if ((j >> 4) > (i >> 4)) QKs[i * 68 + j] = 0.f;
@@ -396,30 +424,31 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     for (int i = 0; i < 16; ++i) Tm[(b0 + i) * 68 + b0 + lane] = col[i];
   }
   lds_barrier();
-  for (int dist = 1; dist < 4; ++dist) {  // T_ij = -T_ii sum_{m=j}^{i-1} L_im T_mj
+  // T_ij = -T_ii sum_{m=j}^{i-1} L_im T_mj, block distance by distance, on
+  // fp32 MFMA 16x16x4: lane l supplies A (row l % 16, k l / 16) and B
+  // (k l / 16, column l % 16) and receives C rows 4 (l / 16) .. + 3 of
+  // column l % 16.
+  for (int dist = 1; dist < 4; ++dist) {
     const int bi = wave + dist, bj = wave;
     if (bi < 4) {
       float* X = Xs + wave * 16 * 17;
+      f32x4 x = {0.f, 0.f, 0.f, 0.f};
+      for (int bm = bj; bm < bi; ++bm)
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int e = lane * 4 + q4, r = e >> 4, c = e & 15;
-        float sacc = 0.f;
-        for (int bm = bj; bm < bi; ++bm)
+        for (int kk = 0; kk < 4; ++kk)
+          x = __builtin_amdgcn_mfma_f32_16x16x4f32(Lm[(16 * bi + n) * 68 + 16 * bm + 4 * kk + g4],
+                                                   Tm[(16 * bm + 4 * kk + g4) * 68 + 16 * bj + n], x, 0, 0, 0);
 #pragma unroll
-          for (int m = 0; m < 16; ++m)
-            sacc = fmaf(Lm[(16 * bi + r) * 68 + 16 * bm + m], Tm[(16 * bm + m) * 68 + 16 * bj + c], sacc);
-        X[r * 17 + c] = sacc;
-      }
+      for (int r = 0; r < 4; ++r) X[(4 * g4 + r) * 17 + n] = x[r];
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       __builtin_amdgcn_wave_barrier();
+      f32x4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int e = lane * 4 + q4, r = e >> 4, c = e & 15;
-        float sacc = 0.f;
+      for (int kk = 0; kk < 4; ++kk)
+        y = __builtin_amdgcn_mfma_f32_16x16x4f32(Tm[(16 * bi + n) * 68 + 16 * bi + 4 * kk + g4],
+                                                 X[(4 * kk + g4) * 17 + n], y, 0, 0, 0);
 #pragma unroll
-        for (int m = 0; m < 16; ++m) sacc = fmaf(Tm[(16 * bi + r) * 68 + 16 * bi + m], X[m * 17 + c], sacc);
-        Tm[(16 * bi + r) * 68 + 16 * bj + c] = -sacc;
-      }
+      for (int r = 0; r < 4; ++r) Tm[(16 * bi + 4 * g4 + r) * 68 + 16 * bj + n] = -y[r];
     }
     lds_barrier();
   }
@@ -454,22 +483,36 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
   // Step 6: U = T (beta v) and W = T (beta e^G k), 32 + 32 tiles of 16x16.
   float* Wst = QKs;  // -W staging [64][132] over R4 + R5 (QK and T fp32 are dead)
   f32x4* u_rec = reinterpret_cast<f32x4*>(rec + kRecU);
-  for (int job = wave; job < 64; job += 4) {
-    const bool is_w = job >= 32;
-    const int tt = (job & 31) >> 3, td = job & 7;
-    const uint16_t* B = is_w ? kbT : vbT;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    const int nsteps = (16 * tt + 15) / 32 + 1;  // T is lower triangular
-    for (int s = 0; s < nsteps; ++s) {
-      const int kofs = 32 * s + 8 * g4;
-      acc = mfma3(lds16(Thl + (16 * tt + n) * 68 + kofs), lds16(Thl + 64 * 68 + (16 * tt + n) * 68 + kofs),
-                  lds16(B + (16 * td + n) * 68 + kofs), lds16(B + 128 * 68 + (16 * td + n) * 68 + kofs), acc);
-    }
-    if (is_w) {
+  // Wave w: column tiles td = w and w + 4 of U and of W for every token tile,
+  // the four tiles of a token tile sharing the T operand reads.
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) Wst[(16 * tt + 4 * g4 + i4) * 132 + 16 * td + n] = -acc[i4];
-    } else {
-      u_rec[(tt * 8 + td) * 64 + lane] = acc;
+  for (int tt = 0; tt < 4; ++tt) {
+    constexpr int kSteps[4] = {1, 1, 2, 2};  // T is lower triangular: k-steps of 32 up to column 16 tt + 15
+    f32x4 acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int s = 0; s < kSteps[tt]; ++s) {
+      const int kofs = 32 * s + 8 * g4;
+      const u32x4 ah = lds16(Thl + (16 * tt + n) * 68 + kofs), al = lds16(Thl + 64 * 68 + (16 * tt + n) * 68 + kofs);
+      u32x4 bh[4], bl[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint16_t* B = q < 2 ? vbT : kbT;
+        const int td = wave + 4 * (q & 1);
+        bh[q] = lds16(B + (16 * td + n) * 68 + kofs);
+        bl[q] = lds16(B + 128 * 68 + (16 * td + n) * 68 + kofs);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = mfma3(ah, al, bh[q], bl[q], acc[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int td = wave + 4 * (q & 1);
+      if (q < 2) {
+        u_rec[(tt * 8 + td) * 64 + lane] = acc[q];
+      } else {
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) Wst[(16 * tt + 4 * g4 + i4) * 132 + 16 * td + n] = -acc[q][i4];
+      }
     }
   }
   lds_barrier();

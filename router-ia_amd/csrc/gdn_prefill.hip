@@ -184,57 +184,70 @@ __global__ __launch_bounds__(256) void conv_ring_tail_kernel(PrefillArgs a) {
 }
 
 
-// Step 3 of phase A for two 16-row tiles RA > RB: A rows (q or k, hi/lo bf16
-// rows of stride 136) times k^T over tiles tj <= RA (resp. RB), each tile
-// with the same MFMA sequence as one tile alone; the epilogue applies the
-// decay mask and writes (q k^T) o D (IS_Q) or L = strict_lower(beta k k^T o D).
-template <int RA, int RB, bool IS_Q>
-__device__ __forceinline__ void qk_tile_rows(const uint16_t* A, const uint16_t* khl, const float* G_s,
-                                             const float* beta_s, float* outm, int n, int g4) {
-  f32x4 acc[RA + 1 + RB + 1];
+// Step 3 of phase A for wave W: row tile W of Q K^T (A operand = the wave's
+// own q rows, split on the fly) and row tile 3 - W of K K^T (A operand from
+// the k rows in LDS), 5 tiles in all; B operands are the k rows of tiles tj.
+// Each tile runs the MFMA sequence of one tile alone; the epilogue applies the
+// decay mask and writes (q k^T) o D and L = strict_lower(beta k k^T o D).
+template <int W>
+__device__ __forceinline__ void prep_qk_kk_tiles(const float (&qv)[4][8], const uint16_t* khl, const float* G_s,
+                                                 const float* beta_s, float* Lm, float* QKs, int n, int g4) {
+  constexpr int RQ = W, RK = 3 - W;
+  constexpr int NB = (RQ > RK ? RQ : RK) + 1;
+  f32x4 aq[RQ + 1], ak[RK + 1];
 #pragma unroll
-  for (int t = 0; t < RA + RB + 2; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t <= RQ; ++t) aq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t <= RK; ++t) ak[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int d = 32 * s + 8 * g4;
-    const u32x4 aah = lds16(A + (16 * RA + n) * 136 + d), aal = lds16(A + 64 * 136 + (16 * RA + n) * 136 + d);
-    const u32x4 abh = lds16(A + (16 * RB + n) * 136 + d), abl = lds16(A + 64 * 136 + (16 * RB + n) * 136 + d);
-    u32x4 bh[RA + 1], bl[RA + 1];
+    u32x4 qh, ql;
+    split8(qv[s], qh, ql);
+    const u32x4 kh = lds16(khl + (16 * RK + n) * 136 + d), kl = lds16(khl + 64 * 136 + (16 * RK + n) * 136 + d);
+    u32x4 bh[NB], bl[NB];
 #pragma unroll
-    for (int tj = 0; tj <= RA; ++tj) {
+    for (int tj = 0; tj < NB; ++tj) {
       bh[tj] = lds16(khl + (16 * tj + n) * 136 + d);
       bl[tj] = lds16(khl + 64 * 136 + (16 * tj + n) * 136 + d);
     }
 #pragma unroll
-    for (int tj = 0; tj <= RA; ++tj) acc[tj] = mfma3(aah, aal, bh[tj], bl[tj], acc[tj]);
+    for (int tj = 0; tj <= RQ; ++tj) aq[tj] = mfma3(qh, ql, bh[tj], bl[tj], aq[tj]);
 #pragma unroll
-    for (int tj = 0; tj <= RB; ++tj) acc[RA + 1 + tj] = mfma3(abh, abl, bh[tj], bl[tj], acc[RA + 1 + tj]);
+    for (int tj = 0; tj <= RK; ++tj) ak[tj] = mfma3(kh, kl, bh[tj], bl[tj], ak[tj]);
   }
 #pragma unroll
-  for (int t = 0; t < RA + RB + 2; ++t) {
-    const int ti = t <= RA ? RA : RB, tj = t <= RA ? t : t - RA - 1;
+  for (int tj = 0; tj <= RQ; ++tj)
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
-      const int i = 16 * ti + 4 * g4 + i4, j = 16 * tj + n;
-      const float dec = j <= i ? expf(G_s[i] - G_s[j]) : 0.f;
-      if (IS_Q) outm[i * 68 + j] = j <= i ? acc[t][i4] * dec : 0.f;
-      else outm[i * 68 + j] = j < i ? beta_s[i] * acc[t][i4] * dec : 0.f;
+      const int i = 16 * RQ + 4 * g4 + i4, j = 16 * tj + n;
+      QKs[i * 68 + j] = j <= i ? aq[tj][i4] * expf(G_s[i] - G_s[j]) : 0.f;
     }
-  }
+#pragma unroll
+  for (int tj = 0; tj <= RK; ++tj)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int i = 16 * RK + 4 * g4 + i4, j = 16 * tj + n;
+      Lm[i * 68 + j] = j < i ? beta_s[i] * ak[tj][i4] * expf(G_s[i] - G_s[j]) : 0.f;
+    }
 }
 
 // ---------------------------------------------------------------- phase A
-// LDS regions (bytes) and what they hold over the kernel's steps.
-constexpr int kR1 = 0;                   // q hi/lo [64][136] bf16 -> (beta v)^T hi/lo [128][68] bf16
-constexpr int kR2 = kR1 + 34816;         // k hi/lo [64][136] bf16 -> (beta e^G k)^T hi/lo [128][68]
-constexpr int kR3 = kR2 + 34816;         // L fp32 [64][68]       -> T hi/lo [64][68] bf16
-constexpr int kR4 = kR3 + 17408;         // (q k^T) o D fp32 [64][68] -> -W fp32 [64][132] (with R5)
-constexpr int kR5 = kR4 + 17408;         // (e^{G_C-G} k)^T fp32 [128][68] -> T fp32 [64][68]
-constexpr int kRScal = kR5 + 34816;      // beta, G, scratch
+// LDS regions (bytes) and what they hold over the kernel's steps; 74.5 KB in
+// all, so two workgroups share a CU and one's loads and barriers overlap the
+// other's arithmetic.
+//   RA: k hi/lo rows [2][64][136] bf16 (steps 2-3) -> T fp32 [64][68] (4-5)
+//       -> (beta v)^T hi/lo [2][128][68] bf16 (6U) -> (beta e^G k)^T hi/lo (6W)
+//       -> -W fp32 [64][132] (7)
+//   RB: (e^{G_C-G} k)^T fp32 [128][68] (2) -> L fp32 [64][68] | (q k^T) o D
+//       fp32 [64][68] (3-4) -> T hi/lo [2][64][68] bf16 | - (5-6)
+constexpr int kRA = 0;
+constexpr int kRB = kRA + 34816;
+constexpr int kRScal = kRB + 34816;  // beta, G, inverse scratch
 constexpr int kPrepLdsBytes = kRScal + 4 * 64 * 2 + 4 * 4 * 16 * 17;
 
 template <int XT, int GM>
-__global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   const int cl = blockIdx.x;  // chunk within the segment
   const int h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -245,11 +258,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
   const int kdim = a.num_k_heads * kDim;
 
   __shared__ __attribute__((aligned(16))) unsigned char lds[kPrepLdsBytes];
-  uint16_t* qhl = reinterpret_cast<uint16_t*>(lds + kR1);  // hi at [0, 64*136), lo after
-  uint16_t* khl = reinterpret_cast<uint16_t*>(lds + kR2);
-  float* Lm = reinterpret_cast<float*>(lds + kR3);
-  float* QKs = reinterpret_cast<float*>(lds + kR4);
-  float* KtS = reinterpret_cast<float*>(lds + kR5);
+  uint16_t* khl = reinterpret_cast<uint16_t*>(lds + kRA);  // hi at [0, 64*136), lo after
+  float* KtS = reinterpret_cast<float*>(lds + kRB);
+  float* Lm = reinterpret_cast<float*>(lds + kRB);
+  float* QKs = Lm + 64 * 68;
   float* beta_s = reinterpret_cast<float*>(lds + kRScal);
   float* G_s = beta_s + 64;
   float* Xs = G_s + 64;  // [4][16][17]
@@ -290,7 +302,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
       unpack(rv[s], vv[s]);
     }
   }
-  // Gates and the cumulative decay (sequential, like torch.cumsum).
+  // Gates and the cumulative decay.
   if (wave == 0) {
     const int tt = t0 + lane;
     float beta = 0.f, g = 0.f;
@@ -347,16 +359,14 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
   const float eg = expf(G_s[row]);                    // e^{G_t}
   const float ekl = expf(G_s[kChunk - 1] - G_s[row]);  // e^{G_C - G_t}
   const float bt = beta_s[row];
-  // q, k hi/lo rows into LDS; exp(G) q straight to the record (A-operand order).
+  // k hi/lo rows into RA; exp(G) q straight to the record (A-operand order);
+  // (e^{G_C-G} k)^T into RB.
   {
     u32x4* qt_rec = reinterpret_cast<u32x4*>(rec + kRecQt);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int d = 32 * s + 8 * g4;
       u32x4 hi, lo;
-      split8(qv[s], hi, lo);
-      *reinterpret_cast<u32x4*>(qhl + row * 136 + d) = hi;
-      *reinterpret_cast<u32x4*>(qhl + 64 * 136 + row * 136 + d) = lo;
       split8(kv[s], hi, lo);
       *reinterpret_cast<u32x4*>(khl + row * 136 + d) = hi;
       *reinterpret_cast<u32x4*>(khl + 64 * 136 + row * 136 + d) = lo;
@@ -371,7 +381,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     }
   }
   lds_barrier();
-  // Step 3: Kt operand to the record; K K^T -> L and Q K^T -> (q k^T) o D.
+  // Kt operand to the record.
   {
     u32x4* kt_rec = reinterpret_cast<u32x4*>(rec + kRecKt);
     for (int job = wave; job < 16; job += 4) {
@@ -384,20 +394,19 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
       kt_rec[((dt * 2 + s) * 2 + 1) * 64 + lane] = lo;
     }
   }
-  // Wave 0: K K^T rows 3 and 0, wave 1: rows 2 and 1, waves 2 and 3 the same
-  // rows of Q K^T (5 tiles each); a wave's tiles share their A rows and the
-  // k rows as B operands, so all their operand reads issue together.
-  if (wave == 0) qk_tile_rows<3, 0, false>(khl, khl, G_s, beta_s, Lm, n, g4);
-  else if (wave == 1) qk_tile_rows<2, 1, false>(khl, khl, G_s, beta_s, Lm, n, g4);
-  else if (wave == 2) qk_tile_rows<3, 0, true>(qhl, khl, G_s, beta_s, QKs, n, g4);
-  else qk_tile_rows<2, 1, true>(qhl, khl, G_s, beta_s, QKs, n, g4);
+  lds_barrier();  // RB free for L and (q k^T) o D
+  // Step 3: Q K^T -> (q k^T) o D and K K^T -> L, 5 tiles per wave.
+  if (wave == 0) prep_qk_kk_tiles<0>(qv, khl, G_s, beta_s, Lm, QKs, n, g4);
+  else if (wave == 1) prep_qk_kk_tiles<1>(qv, khl, G_s, beta_s, Lm, QKs, n, g4);
+  else if (wave == 2) prep_qk_kk_tiles<2>(qv, khl, G_s, beta_s, Lm, QKs, n, g4);
+  else prep_qk_kk_tiles<3>(qv, khl, G_s, beta_s, Lm, QKs, n, g4);
   for (int e = tid; e < kChunk * kChunk; e += 256) {  // upper tiles of (q k^T) o D are zero
     const int i = e >> 6, j = e & 63;
     if ((j >> 4) > (i >> 4)) QKs[i * 68 + j] = 0.f;
   }
-  lds_barrier();
-  // Step 4: QK operand to the record; T = (I + L)^-1 into R5 (blocked 4x4 of 16x16).
-  float* Tm = KtS;
+  lds_barrier();  // k rows dead: RA takes T
+  // Step 4: QK operand to the record; T = (I + L)^-1 into RA (blocked 4x4 of 16x16).
+  float* Tm = reinterpret_cast<float*>(lds + kRA);
   {
     u32x4* qk_rec = reinterpret_cast<u32x4*>(rec + kRecQK);
     for (int job = wave; job < 8; job += 4) {
@@ -452,9 +461,9 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     }
     lds_barrier();
   }
-  // Step 5: T hi/lo into R3 (L is dead); (beta v)^T and (beta e^G k)^T hi/lo
-  // into R1 / R2 (q, k rows are dead), from the rows still in registers.
-  uint16_t* Thl = reinterpret_cast<uint16_t*>(lds + kR3);  // hi [64][68], lo after
+  // Step 5: T hi/lo into RB (L and (q k^T) o D are dead), then (beta v)^T
+  // hi/lo into RA (T fp32 is dead) from the rows still in registers.
+  uint16_t* Thl = reinterpret_cast<uint16_t*>(lds + kRB);  // hi [64][68], lo after
   for (int e = tid; e < kChunk * kChunk; e += 256) {
     const int i = e >> 6, j = e & 63;
     const float v = (j >> 4) > (i >> 4) ? 0.f : Tm[i * 68 + j];
@@ -462,59 +471,75 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(PrefillArgs a) {
     Thl[i * 68 + j] = hb;
     Thl[64 * 68 + i * 68 + j] = f32_to_bf16_bits(v - bf16_bits_to_f32(hb));
   }
-  uint16_t* vbT = qhl;  // hi [128][68], lo after
-  uint16_t* kbT = khl;
-  lds_barrier();  // q/k rows in R1/R2 no longer read
+  uint16_t* BT = reinterpret_cast<uint16_t*>(lds + kRA);  // (beta v)^T, then (beta e^G k)^T: hi [128][68], lo after
+  lds_barrier();
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int d = 32 * s + 8 * g4 + j;
       const float vb = vv[s][j] * bt;
-      const float kb = kv[s][j] * (bt * eg);
-      uint16_t hb = f32_to_bf16_bits(vb);
-      vbT[d * 68 + row] = hb;
-      vbT[128 * 68 + d * 68 + row] = f32_to_bf16_bits(vb - bf16_bits_to_f32(hb));
-      hb = f32_to_bf16_bits(kb);
-      kbT[d * 68 + row] = hb;
-      kbT[128 * 68 + d * 68 + row] = f32_to_bf16_bits(kb - bf16_bits_to_f32(hb));
+      const uint16_t hb = f32_to_bf16_bits(vb);
+      BT[d * 68 + row] = hb;
+      BT[128 * 68 + d * 68 + row] = f32_to_bf16_bits(vb - bf16_bits_to_f32(hb));
     }
   lds_barrier();
-  // Step 6: U = T (beta v) and W = T (beta e^G k), 32 + 32 tiles of 16x16.
-  float* Wst = QKs;  // -W staging [64][132] over R4 + R5 (QK and T fp32 are dead)
-  f32x4* u_rec = reinterpret_cast<f32x4*>(rec + kRecU);
-  // Wave w: column tiles td = w and w + 4 of U and of W for every token tile,
-  // the four tiles of a token tile sharing the T operand reads.
+  // Step 6: U = T (beta v), then W = T (beta e^G k).  Wave w takes column
+  // tiles td = w and w + 4 for every token tile; the tiles of a token tile
+  // share the T operand reads.
+  constexpr int kSteps[4] = {1, 1, 2, 2};  // T is lower triangular: k-steps of 32 up to column 16 tt + 15
+  auto t_times_bt = [&](int tt, f32x4 (&acc)[2]) {
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    constexpr int kSteps[4] = {1, 1, 2, 2};  // T is lower triangular: k-steps of 32 up to column 16 tt + 15
-    f32x4 acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    for (int q = 0; q < 2; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < kSteps[tt]; ++s) {
+    for (int s = 0; s < 2; ++s) {
+      if (s >= kSteps[tt]) break;
       const int kofs = 32 * s + 8 * g4;
       const u32x4 ah = lds16(Thl + (16 * tt + n) * 68 + kofs), al = lds16(Thl + 64 * 68 + (16 * tt + n) * 68 + kofs);
-      u32x4 bh[4], bl[4];
+      u32x4 bh[2], bl[2];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint16_t* B = q < 2 ? vbT : kbT;
-        const int td = wave + 4 * (q & 1);
-        bh[q] = lds16(B + (16 * td + n) * 68 + kofs);
-        bl[q] = lds16(B + 128 * 68 + (16 * td + n) * 68 + kofs);
+      for (int q = 0; q < 2; ++q) {
+        const int td = wave + 4 * q;
+        bh[q] = lds16(BT + (16 * td + n) * 68 + kofs);
+        bl[q] = lds16(BT + 128 * 68 + (16 * td + n) * 68 + kofs);
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = mfma3(ah, al, bh[q], bl[q], acc[q]);
+      for (int q = 0; q < 2; ++q) acc[q] = mfma3(ah, al, bh[q], bl[q], acc[q]);
     }
+  };
+  {
+    f32x4* u_rec = reinterpret_cast<f32x4*>(rec + kRecU);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int td = wave + 4 * (q & 1);
-      if (q < 2) {
-        u_rec[(tt * 8 + td) * 64 + lane] = acc[q];
-      } else {
+    for (int tt = 0; tt < 4; ++tt) {
+      f32x4 acc[2];
+      t_times_bt(tt, acc);
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) Wst[(16 * tt + 4 * g4 + i4) * 132 + 16 * td + n] = -acc[q][i4];
-      }
+      for (int q = 0; q < 2; ++q) u_rec[(tt * 8 + wave + 4 * q) * 64 + lane] = acc[q];
     }
   }
+  lds_barrier();  // (beta v)^T read: RA takes (beta e^G k)^T
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = 32 * s + 8 * g4 + j;
+      const float kb = kv[s][j] * (bt * eg);
+      const uint16_t hb = f32_to_bf16_bits(kb);
+      BT[d * 68 + row] = hb;
+      BT[128 * 68 + d * 68 + row] = f32_to_bf16_bits(kb - bf16_bits_to_f32(hb));
+    }
+  lds_barrier();
+  f32x4 wacc[4][2];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) t_times_bt(tt, wacc[tt]);
+  lds_barrier();  // (beta e^G k)^T read: RA takes the -W staging
+  float* Wst = reinterpret_cast<float*>(lds + kRA);  // -W [64][132]
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) Wst[(16 * tt + 4 * g4 + i4) * 132 + 16 * (wave + 4 * q) + n] = -wacc[tt][q][i4];
   lds_barrier();
   // Step 7: -W operand to the record.
   {

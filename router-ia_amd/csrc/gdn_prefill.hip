@@ -674,19 +674,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     lds_barrier();
   };
 
+  // Chunk cl + 2's record is pulled into L2 (one load per 128-byte line,
+  // spread over the workgroup) while chunk cl computes, so the operand loads
+  // of chunk cl + 1, issued at the same time, find their lines in L2: from
+  // HBM a chunk's 147 KB arrives in about the time a chunk computes, and the
+  // scan waited for it.  A touched value is consumed (an empty asm use) one
+  // chunk later, when it has long arrived, so no wait is spent on it.
+  // The 8 column-block workgroups of a head share an L2, so each touches
+  // every 8th line (its own eighth of the record).
+  constexpr int kRecLines = kRecBytes / 128;
+  constexpr int kTouch = (kRecLines + 8 * 256 - 1) / (8 * 256);
+  auto touch = [&](int cl, uint32_t (&tv)[kTouch]) {
+    const char* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecBytes;
+#pragma unroll
+    for (int i = 0; i < kTouch; ++i)
+      tv[i] = *reinterpret_cast<const uint32_t*>(rec + (int64_t)min(8 * (tid + 256 * i) + cb, kRecLines - 1) * 128);
+  };
+  auto consume = [](const uint32_t (&tv)[kTouch]) {
+#pragma unroll
+    for (int i = 0; i < kTouch; ++i) asm volatile("" ::"v"(tv[i]));
+  };
   // Chunk cl + 1's operands load while chunk cl computes (unrolled by two).
   // The prefetch is unconditional (the last chunk is simply loaded again):
   // a conditional one splits the loop into paths the compiler's wait
   // analysis merges conservatively, draining the prefetch every chunk.
   ChunkOps A, B;
+  uint32_t tX[kTouch], tY[kTouch];
+#pragma unroll
+  for (int i = 0; i < kTouch; ++i) tY[i] = 0u;
   load_ops(0, A);
   const int last = a.seg_chunks - 1;
   for (int cl = 0; cl < a.seg_chunks; cl += 2) {
     load_ops(min(cl + 1, last), B);
+    touch(min(cl + 2, last), tX);
     process(cl, A);
+    consume(tY);
     if (cl + 1 >= a.seg_chunks) break;
     load_ops(min(cl + 2, last), A);
+    touch(min(cl + 3, last), tY);
     process(cl + 1, B);
+    consume(tX);
   }
   for (int e = tid; e < kDim * 16; e += 256) {
     const int r = e >> 4, c = e & 15;

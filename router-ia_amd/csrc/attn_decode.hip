@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
 
     u32x4 kA[8], kB[8];
     u32x2 vA[16], vB[16];
-    int p = page0 + wave;
+    int p = page0 + __builtin_amdgcn_readfirstlane(wave);  // wave-uniform: the page loop branches on scalars
     if (p < page_end) load_tile(phys_first, kA, vA);
     lds_barrier();  // the previous range's merge has been read out of sm_o
 
@@ -411,16 +411,27 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
     };
 
     // Pages wave, wave+4, ...: the next page's loads are issued before the
-    // current page is consumed (two register buffers, loop unrolled by two).
+    // current page is consumed (two register buffers, loop unrolled by two),
+    // and the page-table entry of the page after it one page earlier still,
+    // so issuing a page's loads never waits for the loads in flight.
     if (p < page_end) {
+      int phys_next = pt[min(p + 4, page_end - 1)];
       while (true) {
         int pn = p + 4;
-        if (pn < page_end) load_page(pn, kB, vB);
+        if (pn < page_end) {
+          const int ph = phys_next;
+          phys_next = pt[min(pn + 4, page_end - 1)];
+          load_tile(ph, kB, vB);
+        }
         compute_page(p, kA, vA);
         if (pn >= page_end) break;
         p = pn;
         pn = p + 4;
-        if (pn < page_end) load_page(pn, kA, vA);
+        if (pn < page_end) {
+          const int ph = phys_next;
+          phys_next = pt[min(pn + 4, page_end - 1)];
+          load_tile(ph, kA, vA);
+        }
         compute_page(p, kB, vB);
         if (pn >= page_end) break;
         p = pn;

@@ -50,7 +50,7 @@ GDN_NORM_BYTES_PER_SEQ = NUM_V_HEADS * 128 * 2  # the gated norm's z gate, bf16:
 ATTN_KV_BYTES_PER_TOKEN = 2 * NUM_KV_HEADS * HEAD_DIM_ATTN * 2  # 2048 B of K+V per context token
 ATTN_APPEND_BYTES = 2_048
 ATTN_ACT_BYTES = 3 * NUM_Q_HEADS * HEAD_DIM_ATTN * 2  # q, gate, out in bf16: 24,576
-SPLITK_Q_BYTES = NUM_Q_HEADS * HEAD_DIM_ATTN * 2  # the split-K launch reads q only
+SPLITK_Q_BYTES = NUM_Q_HEADS * HEAD_DIM_ATTN * 2  # the split-K launch reads q
 
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, AMD specification
 PREFILL_METRIC = "prefill tok/s (1 Gated DeltaNet + 1 full-attention layer, one 16384-token prompt); MFMA TFLOP/s % of peak"
@@ -201,22 +201,23 @@ def run_gpu(args, wl) -> dict:
             if is_full(layer):
                 fi = layer // 4
                 kc, vc = st.kv.layer(fi)
-                K.kv_append(kv_in[s, fi, 0], kv_in[s, fi, 1], kc, vc, st.kv.page_table, positions=st.tokens_seen,
-                            slots=st.tokens_seen, inv_freq=st.inv_freq, k_norm_weight=knw[fi] if norms else None)
                 kw = dict(positions=st.tokens_seen, ctx_lens=st.ctx_lens, max_ctx=max_ctx, inv_freq=st.inv_freq,
                           scale=st.scale, workspace=st.workspace, q_norm_weight=qnw[fi] if norms else None)
                 if timed:
                     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                     e0.record()
-                K.attn_decode(qg[s, fi, 0], qg[s, fi, 1], kc, vc, st.kv.page_table, attn_out,
-                              phase=nat.RIA_ATTN_SPLITK, **kw)
+                # split-K over each row's resident tokens; the combine launch appends the new token
+                # (k_norm, RoPE, into the page) and folds it into the row's softmax
+                app = dict(k_norm_weight=knw[fi] if norms else None)
+                K.attn_decode_append(qg[s, fi, 0], qg[s, fi, 1], kv_in[s, fi, 0], kv_in[s, fi, 1], kc, vc,
+                                     st.kv.page_table, attn_out, phase=nat.RIA_ATTN_SPLITK, **app, **kw)
                 if timed:
                     e1.record()
                     if ctx_bytes is None:
-                        ctx_bytes = sum(ATTN_KV_BYTES_PER_TOKEN * (n + 1) + SPLITK_Q_BYTES for n in st._host_seen)
+                        ctx_bytes = sum(ATTN_KV_BYTES_PER_TOKEN * n + SPLITK_Q_BYTES for n in st._host_seen)
                     attn_events.append((e0, e1, ctx_bytes))
-                K.attn_decode(qg[s, fi, 0], qg[s, fi, 1], kc, vc, st.kv.page_table, attn_out,
-                              phase=nat.RIA_ATTN_COMBINE, **kw)
+                K.attn_decode_append(qg[s, fi, 0], qg[s, fi, 1], kv_in[s, fi, 0], kv_in[s, fi, 1], kc, vc,
+                                     st.kv.page_table, attn_out, phase=nat.RIA_ATTN_COMBINE, **app, **kw)
             else:
                 li = layer - layer // 4
                 if timed:
@@ -269,7 +270,7 @@ def run_gpu(args, wl) -> dict:
         "ms_per_step": elapsed_s / args.steps * 1e3,
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_splitk_kernel (ria_attn_decode split-K phase)",
+            "kernel": "attn_splitk_kernel (ria_attn_decode_append split-K phase, over the resident tokens)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

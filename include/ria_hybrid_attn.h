@@ -60,7 +60,7 @@
 extern "C" {
 #endif
 
-#define RIA_ABI_VERSION 2
+#define RIA_ABI_VERSION 3
 
 enum ria_dtype { RIA_DT_BF16 = 0, RIA_DT_F16 = 1, RIA_DT_F32 = 2 };
 
@@ -338,6 +338,33 @@ int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads,
                           float scale, int split_tokens,
                           void* workspace, int64_t workspace_bytes,
                           void* out, int out_dtype, int phase, void* stream);
+
+/*
+ * ria_kv_append followed by ria_attn_decode_phase, with no launch of its own:
+ * replaces qwen36_attention_cache.py:302-317 (k_norm and RoPE of the new k,
+ * _append_full_kv at :327-373, then the decode attention over the grown
+ * context).  Each row's new token goes into slot ctx_lens[b] - 1 (its
+ * position is positions[b]).  The split-K phase leaves that token out; the
+ * combine phase computes it from k and v with the arithmetic of
+ * ria_kv_append (the page gets the same bits), writes it into the page and
+ * folds its score and value into the row's softmax.  q, gate, k and v share
+ * one dtype; k and v are [batch, Hkv, 256]; k_norm_weight as in
+ * ria_kv_append.  The page of slot ctx_lens[b] - 1 must be allocated.  Both
+ * phases take the same arguments (phase as in ria_attn_decode_phase).
+ */
+int ria_attn_decode_append(int batch, int num_q_heads, int num_kv_heads,
+                           const void* q, int q_dtype, int64_t q_row_stride,
+                           const void* gate, int gate_dtype, int64_t gate_row_stride,
+                           const void* k, int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                           const float* k_norm_weight,
+                           void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                           const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                           const int32_t* positions, int32_t position_scalar,
+                           const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
+                           const float* inv_freq, int rope_dim, const float* q_norm_weight,
+                           float scale, int split_tokens,
+                           void* workspace, int64_t workspace_bytes,
+                           void* out, int out_dtype, int phase, void* stream);
 
 /*
  * Workspace bytes ria_gdn_prefill needs to process `segment_tokens` tokens

@@ -76,6 +76,16 @@ struct AttnArgs {
   int num_kv_heads;
   int group;
   void* out;
+  // fused append (ria_attn_decode_append): this token's k and v rows, in q's
+  // dtype, go into slot ctx - 1 of each row (k_norm, RoPE at the row's
+  // position) before the row attends
+  const void* k_new;
+  int64_t kn_stride;
+  const void* v_new;
+  int64_t vn_stride;
+  const float* k_norm_w;  // k_norm weight [256] f32, or null
+  int exclude_last;       // split-K: stop before each row's last token (the combine adds it)
+  int kv_dtype;           // RIA_DT_* of the pages (the fused append rounds k and v to it)
 };
 
 struct AppendArgs {
@@ -255,7 +265,9 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
     const int ctx = min(a.ctx_lens ? ld_uniform(a.ctx_lens, b) : a.ctx_scalar,
                         static_cast<int>(min<int64_t>(a.pt_stride * kPageTokens, 1 << 30)));
     const int32_t* pt = a.page_table + (int64_t)row * a.pt_stride;
-    const int tok1 = min(ctx, tok_hi);
+    // fused append: the row's last token (slot ctx - 1, appended by this
+    // step) is left to the combine launch, which computes it from the inputs
+    const int tok1 = min(a.exclude_last ? ctx - 1 : ctx, tok_hi);
     const int page_end = (tok1 + kPageTokens - 1) / kPageTokens;
 
     auto load_tile = [&](int phys, u32x4 (&kr)[8], u32x2 (&vr)[16]) {
@@ -563,8 +575,84 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
   }
 }
 
+// Fused append, in the combine launch of (row b, query head h): the row's new
+// token at slot ctx - 1 (the split-K launch stopped before it).  Every thread
+// of the workgroup calls this (it holds barriers); threads tid < 256 own dim
+// tid.  k goes through kv_append_kernel's arithmetic (k_norm, RoPE, rounding
+// to the page dtype), so the page gets the same bits as a separate append;
+// q through the split-K prologue's (q_norm, RoPE).  Returns the token's score
+// with head h in log2 units (every thread) and leaves its rounded v in v_s;
+// with write_cache the token's k and v go into the page.
+template <int QT>
+__device__ float fused_new_token(const AttnArgs& a, int b, int h, bool write_cache, float* x_s, float* red_s,
+                                 float* v_s) {
+  const int tid = threadIdx.x;
+  const bool own = tid < kAttnHeadDim;
+  const int d = own ? tid : 0;
+  const int w = tid >> 6;
+  const int kvh = h / a.group;
+  const int posi = a.positions ? a.positions[b] : a.pos_scalar;
+  const int ctx = row_ctx(a, b);
+  float qv = 0.f, kv = 0.f, vv = 0.f;
+  if (own) {
+    qv = load_act<QT>(a.q, (int64_t)b * a.q_stride + (int64_t)h * kAttnHeadDim + d);
+    kv = load_act<QT>(a.k_new, (int64_t)b * a.kn_stride + (int64_t)kvh * kAttnHeadDim + d);
+    vv = load_act<QT>(a.v_new, (int64_t)b * a.vn_stride + (int64_t)kvh * kAttnHeadDim + d);
+  }
+  // sums of squares: per wave, then the four waves in order (kv_append_kernel's order)
+  const float sq = wave_sum(mul_rn(qv, qv)), sk = wave_sum(mul_rn(kv, kv));
+  if ((tid & 63) == 0 && w < 4) {
+    red_s[w] = sq;
+    red_s[4 + w] = sk;
+  }
+  __syncthreads();
+  if (own) {
+    if (a.q_norm_w)
+      qv = rmsnorm_elem<QT>(qv, rms_scale(red_s[0] + red_s[1] + red_s[2] + red_s[3], kAttnHeadDim), a.q_norm_w[d]);
+    if (a.k_norm_w)
+      kv = rmsnorm_elem<QT>(kv, rms_scale(red_s[4] + red_s[5] + red_s[6] + red_s[7], kAttnHeadDim), a.k_norm_w[d]);
+    x_s[d] = qv;
+    x_s[kAttnHeadDim + d] = kv;
+  }
+  __syncthreads();
+  float dot = 0.f;
+  if (own) {
+    float qr = qv;
+    if (a.rope_dim == 64 && d < 64) {
+      float rs, rc;
+      sincosf(mul_rn(static_cast<float>(posi), a.inv_freq[d & 31]), &rs, &rc);
+      const float pq = x_s[d ^ 32];
+      qr = add_rn(mul_rn(qv, rc), mul_rn(d < 32 ? -pq : pq, rs));
+    }
+    const int half = a.rope_dim >> 1;
+    const float pk = d < a.rope_dim ? x_s[kAttnHeadDim + (d < half ? d + half : d - half)] : 0.f;
+    const float kr = rope_elem(kv, pk, d, a.rope_dim, static_cast<float>(posi), a.inv_freq);
+    const bool f16 = a.kv_dtype == RIA_DT_F16;
+    const uint16_t k16 = f16 ? Kv16<RIA_DT_F16>::from_f32(kr) : Kv16<RIA_DT_BF16>::from_f32(kr);
+    const uint16_t v16 = f16 ? Kv16<RIA_DT_F16>::from_f32(vv) : Kv16<RIA_DT_BF16>::from_f32(vv);
+    const float kq = f16 ? Kv16<RIA_DT_F16>::to_f32(k16) : Kv16<RIA_DT_BF16>::to_f32(k16);
+    v_s[d] = f16 ? Kv16<RIA_DT_F16>::to_f32(v16) : Kv16<RIA_DT_BF16>::to_f32(v16);
+    dot = qr * kq;
+    if (write_cache && ctx > 0) {
+      const int row = a.seq_slot ? a.seq_slot[b] : b;
+      const int slot = ctx - 1;
+      const int phys = a.page_table[(int64_t)row * a.pt_stride + slot / kPageTokens];
+      if (phys >= 0 && phys < a.num_pages) {  // the host allocates the page; never write outside the pool
+        const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
+        const int off = slot % kPageTokens;
+        const_cast<uint16_t*>(a.k_cache)[tile * kTileElems + k_tile_offset(off, d)] = k16;
+        const_cast<uint16_t*>(a.v_cache)[(tile * kAttnHeadDim + d) * kPageTokens + off] = v16;
+      }
+    }
+  }
+  dot = wave_sum(dot);
+  if ((tid & 63) == 0 && w < 4) red_s[8 + w] = dot;
+  __syncthreads();
+  return (red_s[8] + red_s[9] + red_s[10] + red_s[11]) * (a.scale * 1.4426950408889634f);
+}
+
 // Merge the partials of one (sequence, query head) and apply the sigmoid gate.
-template <int GT, int OT, bool BALANCED>
+template <int GT, int OT, bool BALANCED, bool APPEND>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const int b = blockIdx.x / a.num_q_heads;
   const int h = blockIdx.x % a.num_q_heads;
@@ -620,6 +708,14 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     const int64_t ph = (first + s) * a.group + hi;
     add(a.ws_stats[ph * 2], a.ws_acc[ph * kAttnHeadDim + d], a.ws_stats[ph * 2 + 1]);
   }
+  if constexpr (APPEND) {  // fold in the row's new token (q, k and v in the gate's dtype)
+    __shared__ float x_s[2 * kAttnHeadDim], red_s[12], v_s[kAttnHeadDim];
+    const float sn = fused_new_token<GT>(a, b, h, hi == 0, x_s, red_s, v_s);
+    const float Mn = fmaxf(M, sn);
+    const float r = M == -INFINITY ? 0.f : exp2f(M - Mn), pn = exp2f(sn - Mn);
+    num = fmaf(pn, v_s[d], num * r);
+    den = fmaf(pn, 1.f, den * r);
+  }
   const float attn = num / den;
   const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + d;
   const float gv = sigmoid_f(load_act<GT>(a.gate, gi));
@@ -631,7 +727,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 // partials p, p + STREAMS, ... (kBatch of them in flight), lane dg its dims
 // 4 dg .. 4 dg + 3 (16-byte loads), in one pass with a running max; the
 // streams are merged in order through LDS.
-template <int GT, int OT, bool BALANCED, int STREAMS>
+template <int GT, int OT, bool BALANCED, int STREAMS, bool APPEND>
 __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArgs a) {
   constexpr int kBatch = 8;
   const int b = blockIdx.x / a.num_q_heads;
@@ -700,9 +796,12 @@ __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArg
     m_s[p] = M;
     den_s[p] = den;
   }
+  float sn = -INFINITY;  // fused append: the new token's score (log2 units); its v in v_s
+  __shared__ float x_s[APPEND ? 2 * kAttnHeadDim : 1], red_s[12], v_s[APPEND ? kAttnHeadDim : 1];
+  if constexpr (APPEND) sn = fused_new_token<GT>(a, b, h, h % a.group == 0, x_s, red_s, v_s);
   __syncthreads();
   if (p != 0) return;
-  float Mt = -INFINITY;
+  float Mt = APPEND ? sn : -INFINITY;
 #pragma unroll
   for (int q = 0; q < STREAMS; ++q) Mt = fmaxf(Mt, m_s[q]);
   f32x4 tn = {0.f, 0.f, 0.f, 0.f};
@@ -714,6 +813,12 @@ __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArg
 #pragma unroll
     for (int i = 0; i < 4; ++i) tn[i] = fmaf(wq, u[i], tn[i]);
     td = fmaf(wq, den_s[q], td);
+  }
+  if constexpr (APPEND) {
+    const float pn = exp2f(sn - Mt);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tn[i] = fmaf(pn, v_s[4 * dg + i], tn[i]);
+    td = fmaf(pn, 1.f, td);
   }
   const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + 4 * dg;
   const int64_t oi = ((int64_t)b * a.num_q_heads + h) * kAttnHeadDim + 4 * dg;
@@ -931,16 +1036,33 @@ extern "C" int64_t ria_attn_decode_workspace_bytes(int batch, int num_q_heads, i
   return (unit_ints + stats_aligned + parts * group * kAttnHeadDim) * (int64_t)sizeof(float);
 }
 
-extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
-                                     int64_t q_row_stride, const void* gate, int gate_dtype, int64_t gate_row_stride,
-                                     const void* k_cache, const void* v_cache, int kv_dtype, int num_pages,
-                                     const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
-                                     const int32_t* positions, int32_t position_scalar, const int32_t* ctx_lens,
-                                     int32_t ctx_scalar, int max_ctx, const float* inv_freq, int rope_dim,
-                                     const float* q_norm_weight, float scale, int split_tokens, void* workspace,
-                                     int64_t workspace_bytes, void* out, int out_dtype, int phase, void* stream) {
+// The fused append's inputs (ria_attn_decode_append), or none.
+struct AppendIn {
+  const void* k;
+  int64_t k_stride;
+  const void* v;
+  int64_t v_stride;
+  const float* k_norm_w;
+};
+
+static int attn_decode_impl(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
+                            int64_t q_row_stride, const void* gate, int gate_dtype, int64_t gate_row_stride,
+                            const void* k_cache, const void* v_cache, int kv_dtype, int num_pages,
+                            const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                            const int32_t* positions, int32_t position_scalar, const int32_t* ctx_lens,
+                            int32_t ctx_scalar, int max_ctx, const float* inv_freq, int rope_dim,
+                            const float* q_norm_weight, float scale, int split_tokens, void* workspace,
+                            int64_t workspace_bytes, void* out, int out_dtype, int phase, const AppendIn* app,
+                            void* stream) {
   if (phase < RIA_ATTN_SPLITK || phase > RIA_ATTN_BOTH)
     return set_error(RIA_ERR_INVALID, "ria_attn_decode: unknown phase %d", phase);
+  if (app) {
+    if (!app->k || !app->v) return set_error(RIA_ERR_INVALID, "ria_attn_decode_append: null k or v");
+    if (gate_dtype != q_dtype)
+      return set_error(RIA_ERR_INVALID, "ria_attn_decode_append: q, gate, k and v must share one dtype");
+    if (app->k_stride < (int64_t)num_kv_heads * kAttnHeadDim || app->v_stride < (int64_t)num_kv_heads * kAttnHeadDim)
+      return set_error(RIA_ERR_INVALID, "ria_attn_decode_append: k/v row stride smaller than Hkv*256");
+  }
   if (batch < 0) return set_error(RIA_ERR_INVALID, "ria_attn_decode: batch must be >= 0");
   if (batch == 0) return RIA_OK;
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
@@ -1003,6 +1125,15 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
   a.num_kv_heads = num_kv_heads;
   a.group = group;
   a.out = out;
+  a.kv_dtype = kv_dtype;
+  if (app) {
+    a.k_new = app->k;
+    a.kn_stride = app->k_stride;
+    a.v_new = app->v;
+    a.vn_stride = app->v_stride;
+    a.k_norm_w = app->k_norm_w;
+    a.exclude_last = 1;
+  }
   if (a.max_splits > 65535 || batch > 65535) return set_error(RIA_ERR_INVALID, "ria_attn_decode: grid too large");
 
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1048,15 +1179,21 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
   dim3 cgrid(batch * num_q_heads);
   // a few (sequence, KV head) units share all the splits: long partial lists, merged by 16 waves
   const bool long_lists = (int64_t)batch * num_kv_heads <= 32;
-#define RIA_COMB_LAUNCH(GT_, OT_)                                                                          \
-  if (balanced && long_lists)                                                                              \
-    hipLaunchKernelGGL((attn_combine_long_kernel<GT_, OT_, true, 16>), cgrid, dim3(1024), 0, st, a);       \
-  else if (balanced)                                                                                       \
-    hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_, true>), cgrid, dim3(256), 0, st, a);                 \
-  else if (long_lists)                                                                                     \
-    hipLaunchKernelGGL((attn_combine_long_kernel<GT_, OT_, false, 16>), cgrid, dim3(1024), 0, st, a);      \
-  else                                                                                                     \
-    hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_, false>), cgrid, dim3(256), 0, st, a)
+#define RIA_COMB_AP(GT_, OT_, AP_)                                                                             \
+  if (balanced && long_lists)                                                                                  \
+    hipLaunchKernelGGL((attn_combine_long_kernel<GT_, OT_, true, 16, AP_>), cgrid, dim3(1024), 0, st, a);      \
+  else if (balanced)                                                                                           \
+    hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_, true, AP_>), cgrid, dim3(256), 0, st, a);                \
+  else if (long_lists)                                                                                         \
+    hipLaunchKernelGGL((attn_combine_long_kernel<GT_, OT_, false, 16, AP_>), cgrid, dim3(1024), 0, st, a);     \
+  else                                                                                                         \
+    hipLaunchKernelGGL((attn_combine_kernel<GT_, OT_, false, AP_>), cgrid, dim3(256), 0, st, a)
+#define RIA_COMB_LAUNCH(GT_, OT_)       \
+  if (app) {                            \
+    RIA_COMB_AP(GT_, OT_, true);        \
+  } else {                              \
+    RIA_COMB_AP(GT_, OT_, false);       \
+  }
 #define RIA_COMB_OT(GT_)                     \
   if (out_dtype == RIA_DT_BF16) {            \
     RIA_COMB_LAUNCH(GT_, RIA_DT_BF16);       \
@@ -1074,7 +1211,41 @@ extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_head
   }
 #undef RIA_COMB_OT
 #undef RIA_COMB_LAUNCH
+#undef RIA_COMB_AP
   return check_launch("ria_attn_decode (combine)");
+}
+
+extern "C" int ria_attn_decode_phase(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
+                                     int64_t q_row_stride, const void* gate, int gate_dtype, int64_t gate_row_stride,
+                                     const void* k_cache, const void* v_cache, int kv_dtype, int num_pages,
+                                     const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                                     const int32_t* positions, int32_t position_scalar, const int32_t* ctx_lens,
+                                     int32_t ctx_scalar, int max_ctx, const float* inv_freq, int rope_dim,
+                                     const float* q_norm_weight, float scale, int split_tokens, void* workspace,
+                                     int64_t workspace_bytes, void* out, int out_dtype, int phase, void* stream) {
+  return attn_decode_impl(batch, num_q_heads, num_kv_heads, q, q_dtype, q_row_stride, gate, gate_dtype,
+                          gate_row_stride, k_cache, v_cache, kv_dtype, num_pages, page_table, page_table_stride,
+                          seq_slot, positions, position_scalar, ctx_lens, ctx_scalar, max_ctx, inv_freq, rope_dim,
+                          q_norm_weight, scale, split_tokens, workspace, workspace_bytes, out, out_dtype, phase,
+                          nullptr, stream);
+}
+
+extern "C" int ria_attn_decode_append(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,
+                                      int64_t q_row_stride, const void* gate, int gate_dtype, int64_t gate_row_stride,
+                                      const void* k, int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                      const float* k_norm_weight, void* k_cache, void* v_cache, int kv_dtype,
+                                      int num_pages, const int32_t* page_table, int64_t page_table_stride,
+                                      const int32_t* seq_slot, const int32_t* positions, int32_t position_scalar,
+                                      const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx, const float* inv_freq,
+                                      int rope_dim, const float* q_norm_weight, float scale, int split_tokens,
+                                      void* workspace, int64_t workspace_bytes, void* out, int out_dtype, int phase,
+                                      void* stream) {
+  const AppendIn app{k, k_row_stride, v, v_row_stride, k_norm_weight};
+  return attn_decode_impl(batch, num_q_heads, num_kv_heads, q, q_dtype, q_row_stride, gate, gate_dtype,
+                          gate_row_stride, k_cache, v_cache, kv_dtype, num_pages, page_table, page_table_stride,
+                          seq_slot, positions, position_scalar, ctx_lens, ctx_scalar, max_ctx, inv_freq, rope_dim,
+                          q_norm_weight, scale, split_tokens, workspace, workspace_bytes, out, out_dtype, phase, &app,
+                          stream);
 }
 
 extern "C" int ria_attn_decode(int batch, int num_q_heads, int num_kv_heads, const void* q, int q_dtype,

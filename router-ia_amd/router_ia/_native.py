@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIB_ENV = "RIA_HIP_LIB"
 DEFAULT_LIB = Path(__file__).resolve().parent / "_lib" / "libria_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 RIA_DT_BF16 = 0
 RIA_DT_F16 = 1
@@ -74,6 +74,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp,
          _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _vp, _c_f32, _c_int, _vp, _c_i64,
          _vp, _c_int, _c_int, _vp],
+    ),
+    "ria_attn_decode_append": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp,
+         _vp, _vp, _c_int, _c_int, _vp, _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _vp,
+         _c_f32, _c_int, _vp, _c_i64, _vp, _c_int, _c_int, _vp],
     ),
     "ria_gdn_prefill_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int]),
     "ria_gdn_prefill": (

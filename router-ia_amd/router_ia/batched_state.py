@@ -65,8 +65,11 @@ class BatchedAttentionState:
         split_tokens: int = 0,
         kv_dtype: torch.dtype = torch.bfloat16,
         prefill_segment_tokens: int = 4096,
+        fused_append: bool = True,
     ):
         self.device = torch.device(device)
+        # decode steps append each row's k, v inside the attention's combine launch (ria_attn_decode_append)
+        self.fused_append = bool(fused_append)
         if self.device.type != "cuda":
             raise RuntimeError("BatchedAttentionState needs a ROCm GPU device; there is no CPU implementation")
         nat.load()
@@ -193,10 +196,17 @@ class BatchedAttentionState:
         if self._min_headroom < 1:
             self._ensure([n + 1 for n in self._host_seen])
         k_cache, v_cache = self.kv.layer(layer)
-        K.kv_append(k, v, k_cache, v_cache, self.kv.page_table, positions=self.tokens_seen,
-                    slots=self.tokens_seen, inv_freq=self.inv_freq, k_norm_weight=k_norm_weight)
         if out is None:
             out = torch.empty((self.max_seqs, self.num_q_heads, 256), dtype=out_dtype, device=self.device)
+        if self.fused_append and k.dtype == q.dtype and v.dtype == q.dtype and gate.dtype == q.dtype:
+            # no append launch: the attention's combine launch writes each row's token (slot tokens_seen = ctx - 1)
+            return K.attn_decode_append(q, gate, k, v, k_cache, v_cache, self.kv.page_table, out,
+                                        positions=self.tokens_seen, ctx_lens=self.ctx_lens, max_ctx=max_ctx,
+                                        inv_freq=self.inv_freq, scale=self.scale, workspace=self.workspace,
+                                        split_tokens=self.split_tokens, q_norm_weight=q_norm_weight,
+                                        k_norm_weight=k_norm_weight)
+        K.kv_append(k, v, k_cache, v_cache, self.kv.page_table, positions=self.tokens_seen,
+                    slots=self.tokens_seen, inv_freq=self.inv_freq, k_norm_weight=k_norm_weight)
         return K.attn_decode(q, gate, k_cache, v_cache, self.kv.page_table, out, positions=self.tokens_seen,
                              ctx_lens=self.ctx_lens, max_ctx=max_ctx, inv_freq=self.inv_freq, scale=self.scale,
                              workspace=self.workspace, split_tokens=self.split_tokens, q_norm_weight=q_norm_weight)

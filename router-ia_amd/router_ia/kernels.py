@@ -724,6 +724,76 @@ def _page_row(page_table: torch.Tensor, dev: torch.device) -> int:
     return int(page_table.numel())
 
 
+
+def attn_decode_append(
+    q: torch.Tensor,
+    gate: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    positions: torch.Tensor | int,
+    ctx_lens: torch.Tensor | int,
+    max_ctx: int,
+    inv_freq: torch.Tensor | None,
+    scale: float,
+    workspace: torch.Tensor,
+    seq_slot: torch.Tensor | None = None,
+    split_tokens: int = 0,
+    phase: int = nat.RIA_ATTN_BOTH,
+    q_norm_weight: torch.Tensor | None = None,
+    k_norm_weight: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """kv_append + attn_decode without a launch of its own (ria_attn_decode_append).
+
+    Row b's new token (k, v [batch, Hkv, 256] in q's dtype) goes into slot
+    ``ctx_lens[b] - 1`` at RoPE position ``positions[b]``: the split-K launch
+    stops before it, the combine launch computes it with kv_append's
+    arithmetic (the pages hold the same bits), writes it into the page and
+    folds it into the row's softmax.  Both phases take the same arguments.
+    """
+    batch = int(q.shape[0])
+    num_q_heads = int(q.shape[1])
+    num_kv_heads = int(k_cache.shape[1])
+    dev = q.device
+    for name, t in (("q", q), ("gate", gate), ("k", k), ("v", v), ("k_cache", k_cache), ("v_cache", v_cache),
+                    ("out", out), ("inv_freq", inv_freq), ("workspace", workspace), ("seq_slot", seq_slot)):
+        _require_gpu(name, t, dev)
+    if k.dtype != q.dtype or v.dtype != q.dtype or gate.dtype != q.dtype:
+        raise ValueError("attn_decode_append: q, gate, k and v must share one dtype")
+    qs = _row_stride("q", q, batch, num_q_heads * ATTN_HEAD_DIM)
+    gs = _row_stride("gate", gate, batch, num_q_heads * ATTN_HEAD_DIM)
+    ks = _row_stride("k", k, batch, num_kv_heads * ATTN_HEAD_DIM)
+    vs = _row_stride("v", v, batch, num_kv_heads * ATTN_HEAD_DIM)
+    pages = _check_kv_cache(k_cache, v_cache, num_kv_heads)
+    pts = _check_page_table(page_table, dev)
+    if max_ctx > page_table.shape[1] * PAGE_TOKENS:
+        raise ValueError(f"max_ctx {max_ctx} exceeds the page table capacity {page_table.shape[1] * PAGE_TOKENS}")
+    if seq_slot is None and page_table.shape[0] < batch:
+        raise ValueError("page table has fewer rows than batch")
+    if tuple(out.shape) != (batch, num_q_heads, ATTN_HEAD_DIM) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{batch}, {num_q_heads}, 256]")
+    if not workspace.is_contiguous():
+        raise ValueError("workspace must be contiguous")
+    pos_t, pos_s = _rows_i32("positions", positions, batch, dev)
+    ctx_t, ctx_s = _rows_i32("ctx_lens", ctx_lens, batch, dev)
+    if seq_slot is not None:
+        _rows_i32("seq_slot", seq_slot, batch, dev)
+    rope_dim = 0 if inv_freq is None else 2 * int(inv_freq.numel())
+    ws_bytes = workspace.numel() * workspace.element_size()
+    rc = nat.load().ria_attn_decode_append(
+        batch, num_q_heads, num_kv_heads, _ptr(q), dtype_code(q), qs, _ptr(gate), dtype_code(gate), gs,
+        _ptr(k), ks, _ptr(v), vs, _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev),
+        _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table), pts, _ptr(seq_slot),
+        _ptr(pos_t), pos_s, _ptr(ctx_t), ctx_s, int(max_ctx), _ptr(inv_freq), rope_dim,
+        _norm_weight("q_norm_weight", q_norm_weight, ATTN_HEAD_DIM, dev), float(scale), int(split_tokens),
+        _ptr(workspace), ws_bytes, _ptr(out), dtype_code(out), int(phase), _stream(dev))
+    nat.check(rc, "ria_attn_decode_append")
+    return out
+
 def kv_append_seq(
     k: torch.Tensor,
     v: torch.Tensor,

@@ -82,6 +82,34 @@ def test_attn_decode_ragged_shuffled_pages(gpu, split_tokens):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("lengths", [[1], [40], [5000, 17, 2049], [3000, 3001, 16, 1, 777]])
+def test_attn_decode_padded_partition_few_units(gpu, lengths):
+    """Few (sequence, KV head) units against a large grid: every unit's page range is
+    padded to whole chunks (units x 32 <= workgroups), so no workgroup straddles two
+    units; tiny, page-aligned and ragged contexts in one launch."""
+    announce(f"attn_decode: padded balanced partition, lengths {lengths}")
+    batch, steps = len(lengths), 3
+    kpre, vpre = W.prefilled_kv(27, batch, max(lengths))
+    x = W.attn_step_inputs(28, steps, batch)
+    st = _attn_state(gpu, batch, max(lengths) + steps + 32, shuffle_seed=11)
+    assert st.split_tokens == 0  # the balanced partition
+    _prefill(st, lengths, kpre, vpre)
+    states = []
+    for b, n in enumerate(lengths):
+        s = O.SequenceState()
+        s.keys[0], s.values[0], s.tokens_seen = kpre[b:b + 1, :, :n].float(), vpre[b:b + 1, :, :n].float(), n
+        states.append(s)
+    for t in range(steps):
+        out = st.full_step(0, x["q"][t].to(gpu), x["k"][t].to(gpu), x["v"][t].to(gpu), x["gate"][t].to(gpu),
+                           out_dtype=torch.float32)
+        want = O.full_step_batched(states, 0, x["q"][t], x["k"][t], x["v"][t], x["gate"][t])
+        st.advance()
+        for s in states:
+            s.tokens_seen += 1
+        assert_act_close(out, want, f"step {t}")
+
+
+@pytest.mark.gpu
 def test_attn_decode_balanced_partition_many_units(gpu):
     """Balanced (stream-K) decode: 48 ragged rows, ~9.6k pages over the grid, so
     workgroups cross unit boundaries and units span several workgroups."""

@@ -42,6 +42,7 @@ from .batched_state import BatchedAttentionState
 
 HIDDEN = 2048
 FUSED_NORM_ROWS = 4  # up to this many rows the input RMSNorm runs inside the projection launch
+FP8_KERNEL_ROWS = 16  # up to this many rows the projections read the FP8 weights (one-pass kernel)
 
 
 @dataclass
@@ -141,7 +142,11 @@ def layer_weights(ckpt: dict[str, torch.Tensor], model_layer: int,
 class BatchedForward:
     """The attention side of every layer for one token of each of B sequences (see the module docstring)."""
 
-    def __init__(self, state: BatchedAttentionState, layers: list[LinearLayerWeights | FullLayerWeights]):
+    def __init__(self, state: BatchedAttentionState, layers: list[LinearLayerWeights | FullLayerWeights],
+                 projections: str = "auto"):
+        """projections: "auto" runs batches of more than 16 rows on the library fp16 GEMM over weights
+        dequantised once (ria_dequant_fp8: the reference's fp16 weights, bit for bit) and smaller ones
+        on the FP8 kernels; "fp8" always reads the FP8 weights."""
         n_lin = sum(isinstance(w, LinearLayerWeights) for w in layers)
         n_full = sum(isinstance(w, FullLayerWeights) for w in layers)
         if n_lin + n_full != len(layers):
@@ -176,6 +181,22 @@ class BatchedForward:
         self.v = buf(b, hkv, 256)
         self.attn = buf(b, hq, 256)
         self._stepped = False
+        if projections not in ("auto", "fp8"):
+            raise ValueError(f"projections must be 'auto' or 'fp8', got {projections!r}")
+        # At batch sizes where a projection is a GEMM rather than a weight stream, the library's
+        # fp16 GEMM outruns the FP8 streaming kernel (M=128: 15.8 against 42 us for the DeltaNet
+        # input projections), at the cost of an fp16 copy of the weights (2.6 GB for the 40 layers).
+        self.gemm16 = projections == "auto" and b > FP8_KERNEL_ROWS
+        self.w16: list[tuple[torch.Tensor, torch.Tensor]] = []
+        if self.gemm16:
+            self.gate_ab = buf(b, 2 * hv, dtype=torch.float32)  # a | b of one row side by side
+            for w in layers:
+                if isinstance(w, LinearLayerWeights):
+                    parts, wo = [w.in_proj_qkv, w.in_proj_z, w.in_proj_a, w.in_proj_b], w.out_proj
+                else:
+                    parts, wo = [w.query, w.gate, w.k_proj, w.v_proj], w.o_proj
+                w_in = torch.cat([K.dequant_fp8(p.weight, p.scale_inv) for p in parts], 0)
+                self.w16.append((w_in, K.dequant_fp8(wo.weight, wo.scale_inv)))
 
     def layer(self, model_layer: int, x: torch.Tensor) -> torch.Tensor:
         """x [B, 2048] fp32 += this layer's attention output (in place); returns x."""
@@ -184,6 +205,8 @@ class BatchedForward:
         st = self.state
         b = st.max_seqs
         fused = b <= FUSED_NORM_ROWS  # the input norm inside the projection launch
+        if self.gemm16:
+            return self._layer_gemm16(w, i, model_layer, x)
         if isinstance(w, LinearLayerWeights):
             projs = [w.in_proj_qkv.pair(), w.in_proj_z.pair(), w.in_proj_a.pair(), w.in_proj_b.pair()]
             outs = [self.mixed, self.z, self.gate_a, self.gate_b]
@@ -211,6 +234,37 @@ class BatchedForward:
             st.full_step(i, self.q, self.k, self.v, self.gate, out=self.attn, q_norm_weight=w.q_norm,
                          k_norm_weight=w.k_norm)
             K.linear_fp8_group(self.attn.view(b, -1), [w.o_proj.pair()], out=[x], accumulate=[True])
+        return x
+
+    def _layer_gemm16(self, w, i: int, model_layer: int, x: torch.Tensor) -> torch.Tensor:
+        """``layer`` with the projections as fp16 GEMMs: F.linear(fp16(h), W16), the reference's
+        CUDA projection (qwen36_attention_cache.py:232-247, 268, 295-301, 318-320), one GEMM per
+        layer's input projections (their weights stacked) and one for the output projection."""
+        st = self.state
+        b = st.max_seqs
+        w_in, w_out = self.w16[model_layer]
+        if isinstance(w, LinearLayerWeights):
+            K.rmsnorm(x, w.input_norm, out=self.h_bf16)
+            h = self.h_f16.copy_(self.h_bf16)  # bf16(h) -> fp16, as F.linear on fp16 weights takes it
+            y = torch.nn.functional.linear(h, w_in)  # [B, qkv | z | a | b] fp16
+            nq, nz = self.mixed.shape[1], self.z.shape[1]
+            hv = st.num_v_heads
+            ab = self.gate_ab.copy_(y[:, nq + nz:nq + nz + 2 * hv])  # a, b .float() (:245-246), one launch
+            st.linear_step(i, y[:, :nq], w.conv_weight, ab[:, :hv], ab[:, hv:], gate_mode=nat.RIA_GATE_RAW,
+                           A_log=w.A_log, dt_bias=w.dt_bias, out=self.gated, z=y[:, nq:nq + nz],
+                           norm_weight=w.norm_weight)
+            x.add_(torch.nn.functional.linear(self.gated.view(b, -1), w_out))
+        else:
+            K.rmsnorm(x, w.input_norm, out=self.h_f16)
+            y = torch.nn.functional.linear(self.h_f16, w_in)  # [B, query | gate | k | v] fp16
+            hq, hkv = st.num_q_heads, st.num_kv_heads
+            nq, nk = hq * 256, hkv * 256
+            q = y[:, :nq].view(b, hq, 256)
+            gate = y[:, nq:2 * nq].view(b, hq, 256)
+            k = y[:, 2 * nq:2 * nq + nk].view(b, hkv, 256)
+            v = y[:, 2 * nq + nk:2 * nq + 2 * nk].view(b, hkv, 256)
+            st.full_step(i, q, k, v, gate, out=self.attn, q_norm_weight=w.q_norm, k_norm_weight=w.k_norm)
+            x.add_(torch.nn.functional.linear(self.attn.view(b, -1), w_out))
         return x
 
     def capture(self, steps: int,

@@ -26,11 +26,13 @@ pytestmark = pytest.mark.gpu
 LAYERS = 4  # model layers 0, 1, 2 (DeltaNet) and 3 (full attention)
 LENGTHS = [37, 200, 515]
 # 20 rows: more than the 16 of the one-pass projection kernel, so the
-# projections take the streaming kernel (and the fp16 copy of the normed input)
+# projections take the library fp16 GEMM over the dequantised weights (or,
+# with projections="fp8", the FP8 streaming kernel and the fp16 copy of the
+# normed input)
 LENGTHS_20 = LENGTHS + [1, 2, 15, 16, 17, 31, 64, 99, 128, 250, 300, 333, 401, 480, 512, 550, 600]
 
 
-def _setup(dev, split_tokens=64, lengths=LENGTHS):
+def _setup(dev, split_tokens=64, lengths=LENGTHS, projections="auto"):
     ckpts = [W.synthetic_layer(700 + m, m) for m in range(LAYERS)]
     st = BatchedAttentionState(len(lengths), 1100, num_linear_layers=3, num_full_layers=1, device=dev,
                                page_shuffle_seed=5, split_tokens=split_tokens)
@@ -41,7 +43,8 @@ def _setup(dev, split_tokens=64, lengths=LENGTHS):
     st.conv_rings.normal_(0.0, 1.0, generator=g)
     st.kv.k.normal_(0.0, 1.0, generator=g)
     st.kv.v.normal_(0.0, 1.0, generator=g)
-    fwd = BF.BatchedForward(st, [BF.layer_weights(ck, m, dev) for m, ck in enumerate(ckpts)])
+    fwd = BF.BatchedForward(st, [BF.layer_weights(ck, m, dev) for m, ck in enumerate(ckpts)],
+                            projections=projections)
     return ckpts, st, fwd
 
 
@@ -75,10 +78,11 @@ def _oracle_layer(w, s, m, x):
     return step(w, s, m, x, gpu_dtypes=True)
 
 
-@pytest.mark.parametrize("lengths", [LENGTHS, LENGTHS_20], ids=["3rows", "20rows"])
-def test_batched_forward_matches_the_reference_composites(gpu, lengths):
-    announce(f"batched forward: {LAYERS} layers, rows at {lengths}, 2 steps, FP8 projections")
-    ckpts, st, fwd = _setup(gpu, lengths=lengths)
+@pytest.mark.parametrize("lengths,projections", [(LENGTHS, "auto"), (LENGTHS_20, "auto"), (LENGTHS_20, "fp8")],
+                         ids=["3rows", "20rows-gemm16", "20rows-fp8"])
+def test_batched_forward_matches_the_reference_composites(gpu, lengths, projections):
+    announce(f"batched forward: {LAYERS} layers, rows at {lengths}, 2 steps, projections {projections}")
+    ckpts, st, fwd = _setup(gpu, lengths=lengths, projections=projections)
     ws = [_oracle_weights(ck) for ck in ckpts]
     ref = _oracle_states(st)
     for step in range(2):
@@ -138,19 +142,20 @@ def test_step_runs_every_layer_and_the_mlp_between(gpu):
     assert torch.equal(got.cpu(), x.cpu())
 
 
-def test_graph_replays_equal_eager_steps(gpu):
-    announce("batched forward: captured step replayed 3 times == 3 eager steps (bit for bit)")
-    _, st, fwd = _setup(gpu, split_tokens=0)  # the balanced attention schedule, which a graph can replay
-    xs = torch.randn((4, len(LENGTHS), 2048), generator=torch.Generator().manual_seed(91)).to(gpu)
+@pytest.mark.parametrize("lengths", [LENGTHS, LENGTHS_20], ids=["3rows-fp8", "20rows-gemm16"])
+def test_graph_replays_equal_eager_steps(gpu, lengths):
+    announce(f"batched forward: captured step replayed 3 times == 3 eager steps (bit for bit), {len(lengths)} rows")
+    _, st, fwd = _setup(gpu, split_tokens=0, lengths=lengths)  # the balanced attention schedule, which a graph can replay
+    xs = torch.randn((4, len(lengths), 2048), generator=torch.Generator().manual_seed(91)).to(gpu)
     fwd.step(xs[0].clone())  # one eager step loads every kernel
-    snaps = [st.save_row(r) for r in range(len(LENGTHS))]
+    snaps = [st.save_row(r) for r in range(len(lengths))]
     graph = fwd.capture(3)
     replayed = []
     for s in range(1, 4):
         graph.x.copy_(xs[s])
         replayed.append(graph.replay().clone())
         torch.cuda.synchronize()  # eager work and a sync between replays
-        assert st.max_seen == max(LENGTHS) + 1 + s
+        assert st.max_seen == max(lengths) + 1 + s
     with pytest.raises(RuntimeError, match="used up"):
         graph.replay()
     for r, snap in enumerate(snaps):

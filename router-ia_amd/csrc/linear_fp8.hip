@@ -384,7 +384,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
   // through the wave's own LDS region into the MFMA layout: far fewer load
   // instructions than the layout's 16 per wave, whose issue time (not their
   // bytes) would otherwise delay the weight stream.  Lanes of rows past the
-  // end hold zeros.
+  // last token repeat its x.
   // LDS (sized at launch): per wave max(staged rows, 1) x 1 KB; the first
   // KB of a wave's region later holds its partial sums
   extern __shared__ u32x4 gemv_lds[];
@@ -462,24 +462,20 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
 #pragma unroll
       for (int r = 0; r < NR; ++r) own[64 * r + lane] = xs[r];
       __builtin_amdgcn_wave_barrier();  // the region is this wave's: LDS keeps its order
+      // MFMA rows past the last token repeat its x: D row m depends on A row m
+      // alone, and only rows below NR are stored, so they need no zeroing
       const int r = min(c16, NR - 1);
 #pragma unroll
       for (int j = 0; j < 8; ++j)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const u32x4 v = own[64 * r + 8 * j + 2 * g4 + h];  // K = 64 j + 16 g4 + 8 h
-          ax[j][h] = c16 < NR ? v : u32x4{0u, 0u, 0u, 0u};
-        }
+        for (int h = 0; h < 2; ++h) ax[j][h] = own[64 * r + 8 * j + 2 * g4 + h];  // K = 64 j + 16 g4 + 8 h
     } else {
+      // rows past the last token re-read it (see above: their D rows are not stored)
       const int64_t xo = (int64_t)(m0 + min(c16, rows - 1)) * a.x_stride + k0 + 16 * g4;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ax[j][0] = ax[j][1] = u32x4{0u, 0u, 0u, 0u};
-      if (c16 < rows) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          ax[j][0] = load_x8<XT>(a.x, xo + 64 * j);
-          ax[j][1] = load_x8<XT>(a.x, xo + 64 * j + 8);
-        }
+      for (int j = 0; j < 8; ++j) {
+        ax[j][0] = load_x8<XT>(a.x, xo + 64 * j);
+        ax[j][1] = load_x8<XT>(a.x, xo + 64 * j + 8);
       }
       load_w();
       __builtin_amdgcn_sched_barrier(0);

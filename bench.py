@@ -96,8 +96,18 @@ WORKLOADS = {
     "proj1": dict(batch=1, seed=5, proj=True,
                   desc="every projection of the 40-layer stack for one decode step of B=1 token, FP8 block-scaled "
                        "weights, fp16 outputs"),
-    "batch32": dict(batch=32, lo=8192, hi=8192, seed=2,
-                    desc="40-layer stack, B=32, context 8192 (seed 2), 16-token pages, shuffled page table"),
+    "batch32": dict(batch=32, lo=8192, hi=8192, seed=2, graph=True,
+                    desc="40-layer stack, B=32, context 8192 (seed 2), 16-token pages, shuffled page table; each "
+                         "step replayed as one captured HIP graph"),
+    "batch8": dict(batch=8, lo=8192, hi=8192, seed=2, graph=True,
+                   desc="40-layer stack, B=8, context 8192 (seed 2), 16-token pages, shuffled page table; each "
+                        "step replayed as one captured HIP graph"),
+    "batch64": dict(batch=64, lo=8192, hi=8192, seed=2, graph=True,
+                    desc="40-layer stack, B=64, context 8192 (seed 2), 16-token pages, shuffled page table; each "
+                         "step replayed as one captured HIP graph"),
+    "batch128": dict(batch=128, lo=8192, hi=8192, seed=2, graph=True,
+                     desc="40-layer stack, B=128, context 8192 (seed 2), 16-token pages, shuffled page table; each "
+                          "step replayed as one captured HIP graph"),
     "batch1": dict(batch=1, lo=8192, hi=8192, seed=2, graph=True,
                    desc="40-layer stack, B=1, context 8192 (seed 2), 16-token pages, shuffled page table; each "
                         "step (fresh inputs copied in, 40 layers, advance) replayed as one captured HIP graph"),

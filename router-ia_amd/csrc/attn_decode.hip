@@ -280,7 +280,6 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
 #pragma unroll
       for (int db = 0; db < 16; ++db) vr[db] = ld_stream(reinterpret_cast<const u32x2*>(vp + db * 16 * kPageTokens));
     };
-    auto load_page = [&](int p, u32x4 (&kr)[8], u32x2 (&vr)[16]) { load_tile(pt[p], kr, vr); };
 
     u32x4 kA[8], kB[8];
     u32x2 vA[16], vB[16];

@@ -36,8 +36,6 @@ namespace ria {
 
 constexpr int kChunk = 64;
 constexpr int kDim = kGdnHeadDim;  // 128
-constexpr int kPadQ = 132;          // fp32 row stride of q / k / v tiles in LDS
-constexpr int kPadT = 68;           // fp32 row stride of the 64x64 matrices in LDS
 
 // Per (chunk, head) phase-A record, consumed by phase B.  Operands are stored
 // pre-split (bf16 hi, bf16 lo) in MFMA 16x16x32 operand order, one 16-byte

@@ -598,16 +598,26 @@ __device__ float fused_new_token(const AttnArgs& a, int b, int h, bool write_cac
     kv = load_act<QT>(a.k_new, (int64_t)b * a.kn_stride + (int64_t)kvh * kAttnHeadDim + d);
     vv = load_act<QT>(a.v_new, (int64_t)b * a.vn_stride + (int64_t)kvh * kAttnHeadDim + d);
   }
-  // sums of squares: per wave, then the four waves in order (kv_append_kernel's order)
-  const float sq = wave_sum(mul_rn(qv, qv)), sk = wave_sum(mul_rn(kv, kv));
-  if ((tid & 63) == 0 && w < 4) {
-    red_s[w] = sq;
-    red_s[4 + w] = sk;
+  // Sums of squares in the orders of the kernels whose results this token
+  // must reproduce.  k: per wave, then the four waves in order
+  // (kv_append_kernel).  q: lane l sums dims l, l + 64, l + 128, l + 192 in
+  // that order, then one wave sum (the split-K prologue), so the q this
+  // token's score uses is bit for bit the q of the resident tokens' scores.
+  // The raw q goes through v_s, which takes the token's v only later.
+  if (own) v_s[d] = qv;
+  const float sk = wave_sum(mul_rn(kv, kv));
+  if ((tid & 63) == 0 && w < 4) red_s[4 + w] = sk;
+  __syncthreads();
+  if (w == 0) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kAttnHeadDim; j += 64) ss = add_rn(ss, mul_rn(v_s[j + tid], v_s[j + tid]));
+    ss = wave_sum(ss);
+    if (tid == 0) red_s[0] = ss;
   }
   __syncthreads();
   if (own) {
-    if (a.q_norm_w)
-      qv = rmsnorm_elem<QT>(qv, rms_scale(red_s[0] + red_s[1] + red_s[2] + red_s[3], kAttnHeadDim), a.q_norm_w[d]);
+    if (a.q_norm_w) qv = rmsnorm_elem<QT>(qv, rms_scale(red_s[0], kAttnHeadDim), a.q_norm_w[d]);
     if (a.k_norm_w)
       kv = rmsnorm_elem<QT>(kv, rms_scale(red_s[4] + red_s[5] + red_s[6] + red_s[7], kAttnHeadDim), a.k_norm_w[d]);
     x_s[d] = qv;

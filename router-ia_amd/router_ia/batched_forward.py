@@ -307,7 +307,15 @@ class BatchedForward:
 
 
 class ForwardGraph:
-    """A recorded ``BatchedForward.step``: write the inputs into ``x``, call ``replay()``, read ``x``."""
+    """A recorded ``BatchedForward.step``: write the inputs into ``x``, call ``replay()``, read ``out``.
+
+    ``x`` is the buffer the recording reads its input from and ``out`` the one
+    it leaves the step's result in.  They are the same tensor when the mlp
+    updates the residual stream in place; an mlp that returns a new tensor
+    makes ``out`` a buffer of the graph's own pool.  Both stay referenced here
+    for the life of the graph, so neither is ever handed back to the allocator
+    while a replay can still write it.
+    """
 
     def __init__(self, fwd: BatchedForward, steps: int, mlp: Callable[[int, torch.Tensor], torch.Tensor] | None):
         st = fwd.state
@@ -322,13 +330,12 @@ class ForwardGraph:
             with torch.cuda.graph(self.graph, stream=stream):
                 out = fwd.step(self.x, mlp)
         torch.cuda.current_stream(st.device).wait_stream(stream)
-        if out.data_ptr() != self.x.data_ptr():
-            self.x = out  # the mlp returned a new tensor: the step's output lives there
+        self.out = out
         # recording ran the host side of advance(); nothing ran on the device yet
         st._host_seen, st._min_headroom = host_seen, headroom
 
     def replay(self) -> torch.Tensor:
-        """One token per sequence; the state's positions advance as with step()."""
+        """One token per sequence (input in ``x``); returns ``out``. Positions advance as with step()."""
         if self.remaining <= 0:
             raise RuntimeError("the graph's reserved steps are used up: capture again")
         st = self.fwd.state
@@ -338,4 +345,4 @@ class ForwardGraph:
         st._host_seen = [n + 1 for n in st._host_seen]
         st._min_headroom -= 1
         self.remaining -= 1
-        return self.x
+        return self.out

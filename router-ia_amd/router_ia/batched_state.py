@@ -309,6 +309,15 @@ class BatchedAttentionState:
             raise ValueError(f"snapshot shapes {shape} do not match this state's {mine}")
         if snap.tokens + 1 > self.max_context:
             raise RuntimeError(f"snapshot of {snap.tokens} tokens exceeds max_context={self.max_context}")
+        # room first: releasing the row's pages and then failing to find new
+        # ones would leave the row with neither its old state nor the new one
+        need = (snap.tokens + 1 + K.PAGE_TOKENS - 1) // K.PAGE_TOKENS
+        if need > self.kv.alloc.max_pages_per_seq:
+            raise RuntimeError(f"snapshot of {snap.tokens} tokens needs {need} pages, the page table holds "
+                               f"{self.kv.alloc.max_pages_per_seq}")
+        if need > self.kv.alloc.free_pages + len(self.kv.alloc.tables[row]):
+            raise RuntimeError(f"KV page pool exhausted: the snapshot needs {need} pages, "
+                               f"{self.kv.alloc.free_pages + len(self.kv.alloc.tables[row])} available to row {row}")
         self.kv.release(row)
         self.kv.ensure(row, snap.tokens + 1)
         K.seq_state_restore(self.linear_states, self.conv_rings, self.kv.k, self.kv.v, self.kv.page_table, row=row,

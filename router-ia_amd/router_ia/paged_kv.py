@@ -67,6 +67,18 @@ class PageAllocator:
             table.append(page)
         return added
 
+    def pages_needed(self, n_tokens: list[int]) -> int:
+        """Pages rows 0..len-1 must take to hold n_tokens[row] tokens; raises if a row's table is too narrow."""
+        total = 0
+        for row, n in enumerate(n_tokens):
+            need = (n + PAGE_TOKENS - 1) // PAGE_TOKENS
+            if need > self.max_pages_per_seq:
+                raise RuntimeError(
+                    f"sequence row {row} needs {need} pages, page table holds {self.max_pages_per_seq}"
+                )
+            total += max(0, need - len(self.tables[row]))
+        return total
+
     def release(self, row: int) -> None:
         table = self.tables[row]
         self._free.extend(reversed(table))
@@ -114,13 +126,23 @@ class PagedKVCache:
             self.page_table[row].copy_(host_row)
 
     def ensure_many(self, n_tokens: list[int]) -> None:
-        """ensure() for rows 0..len-1 with one table upload."""
+        """ensure() for rows 0..len-1 with one table upload, all or nothing.
+
+        Every row's need is checked against the page-table width and the free
+        list before any page is taken, so a request that cannot be met raises
+        with the host tables, the free list and the device table unchanged.
+        """
+        need = self.alloc.pages_needed(n_tokens)
+        if need > self.alloc.free_pages:
+            raise RuntimeError(f"KV page pool exhausted: {need} more pages needed, {self.alloc.free_pages} free")
         changed = False
-        for row, n in enumerate(n_tokens):
-            if self.alloc.ensure(row, n):
-                changed = True
-        if changed:
-            self.upload_tables()
+        try:
+            for row, n in enumerate(n_tokens):
+                if self.alloc.ensure(row, n):
+                    changed = True
+        finally:
+            if changed:
+                self.upload_tables()
 
     def upload_tables(self) -> None:
         host = torch.full(tuple(self.page_table.shape), -1, dtype=torch.int32)

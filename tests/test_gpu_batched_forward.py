@@ -164,3 +164,30 @@ def test_graph_replays_equal_eager_steps(gpu, lengths):
         got = fwd.step(xs[s].clone())
         torch.cuda.synchronize()
         assert torch.equal(got.cpu(), replayed[s - 1].cpu()), f"replay {s}"
+
+
+def test_graph_replay_with_an_mlp_that_returns_a_new_tensor(gpu):
+    announce("batched forward: captured step with a non-in-place mlp (x * 0.5) == eager steps, bit for bit")
+    _, st, fwd = _setup(gpu, split_tokens=0)
+
+    def mlp(m, x):
+        return x * 0.5  # a new tensor every layer: the step's output is not its input buffer
+
+    xs = torch.randn((4, len(LENGTHS), 2048), generator=torch.Generator().manual_seed(92)).to(gpu)
+    fwd.step(xs[0].clone(), mlp=mlp)
+    snaps = [st.save_row(r) for r in range(len(LENGTHS))]
+    graph = fwd.capture(3, mlp=mlp)
+    assert graph.out.data_ptr() != graph.x.data_ptr()
+    replayed = []
+    for s in range(1, 4):
+        graph.x.copy_(xs[s])
+        junk = torch.randn_like(xs[s])  # allocations between replays must not land on the graph's buffers
+        replayed.append(graph.replay().clone())
+        torch.cuda.synchronize()
+        del junk
+    for r, snap in enumerate(snaps):
+        st.restore_row(r, snap)
+    for s in range(1, 4):
+        got = fwd.step(xs[s].clone(), mlp=mlp)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), replayed[s - 1].cpu()), f"replay {s}"

@@ -73,3 +73,31 @@ def test_k_tile_index_is_the_mfma_operand_order() -> None:
             t, g = lane % 16, lane // 16
             seg = flat[(kk * 64 + lane) * 8:(kk * 64 + lane) * 8 + 8].tolist()
             assert seg == [t * 1000 + 64 * g + 8 * kk + j for j in range(8)]
+
+
+def _tables_tensor(cache: PagedKVCache) -> torch.Tensor:
+    host = torch.full(tuple(cache.page_table.shape), -1, dtype=torch.int32)
+    for row, table in enumerate(cache.alloc.tables):
+        host[row, : len(table)] = torch.tensor(table, dtype=torch.int32) if table else host[row, :0]
+    return host
+
+
+def test_ensure_many_is_all_or_nothing_on_pool_exhaustion() -> None:
+    cache = PagedKVCache(1, 10, 3, 8, num_kv_heads=2, device="cpu", shuffle_seed=3)
+    cache.ensure_many([40, 16, 1])  # 3 + 1 + 1 pages
+    before = [list(t) for t in cache.alloc.tables]
+    free_before = cache.alloc.free_pages
+    # rows 0 and 1 could grow, row 2 cannot: nothing may change
+    with pytest.raises(RuntimeError, match="exhausted"):
+        cache.ensure_many([64, 48, 80])
+    assert [list(t) for t in cache.alloc.tables] == before
+    assert cache.alloc.free_pages == free_before
+    assert torch.equal(cache.page_table, _tables_tensor(cache))
+    # a row whose table is too narrow fails the same way
+    with pytest.raises(RuntimeError, match="page table holds"):
+        cache.ensure_many([48, 200, 1])
+    assert [list(t) for t in cache.alloc.tables] == before
+    # a request that fits goes through, and the device table follows the host tables
+    cache.ensure_many([64, 32, 17])
+    assert torch.equal(cache.page_table, _tables_tensor(cache))
+    assert cache.alloc.free_pages == 10 - 4 - 2 - 2

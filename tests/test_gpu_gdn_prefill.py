@@ -109,4 +109,5 @@ def test_prefill_16384_tokens_single_layer(gpu):
     print(f"16384-token prefill: max |out err| {(got - want).abs().max().item():.3e}, "
           f"state rel err {state_rel_err(state[None], s_want):.3e}", flush=True)
     assert_act_close(got, want, "all 16384 outputs")
-    assert_act_close(state[None], s_want, "final state")
+    # the fp32 state after 16384 tokens, within the stated 1e-4 relative bound
+    assert_state_close(state[None], s_want, "final state after 16384 tokens")

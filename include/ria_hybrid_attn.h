@@ -33,7 +33,9 @@
  *   DeltaNet conv ring        bf16 [pool, 4 (slot), conv_dim]; the input of
  *                              step n lives in slot n mod 4.  The reference
  *                              keeps the same four inputs as a shifting
- *                              window [1, conv_dim, 4] (:207-209).
+ *                              window [1, conv_dim, 4] (:207-209), which
+ *                              ria_gdn_decode_ex / ria_conv1d_window_step
+ *                              also take (RIA_CONV_WINDOW).
  *   conv weight               bf16 [conv_dim, 4] (== [conv_dim, 1, 4])
  *   K cache (one layer)       kv_dtype [num_pages, Hkv, 8, 4, 16 (token), 8]: the
  *                              (page, head) tile in MFMA operand order; key
@@ -60,7 +62,7 @@
 extern "C" {
 #endif
 
-#define RIA_ABI_VERSION 3
+#define RIA_ABI_VERSION 4
 
 enum ria_dtype { RIA_DT_BF16 = 0, RIA_DT_F16 = 1, RIA_DT_F32 = 2 };
 
@@ -133,6 +135,91 @@ int ria_conv1d_step(int batch, int channels,
                     const void* conv_weight, void* conv_ring, const int32_t* seq_slot,
                     const int32_t* conv_pos, int32_t conv_pos_scalar,
                     void* out, int out_dtype, void* stream);
+
+/*
+ * ria_conv1d_step on the reference's own conv state: window_in [batch,
+ * channels, 4] bf16 holds each row's last four inputs, oldest first
+ * (qwen36_attention_cache.py:202-209); window_out receives the shifted window
+ * (inputs 2..4 and the current one), which may be window_in itself (in
+ * place).  Replaces _causal_conv1d_step (:176-221) with its state tensor
+ * layout unchanged.  Windows and conv_weight 8-byte aligned.
+ */
+int ria_conv1d_window_step(int batch, int channels,
+                           const void* x, int x_dtype, int64_t x_row_stride,
+                           const void* conv_weight, const void* window_in, void* window_out,
+                           void* out, int out_dtype, void* stream);
+
+/* Where the conv state of a ria_gdn_decode_ex call lives. */
+enum ria_conv_layout {
+  RIA_CONV_NONE = 0,   /* no conv: x already holds the convolved q|k|v */
+  RIA_CONV_RING = 1,   /* conv_ring / conv_pos, as in ria_gdn_decode with fuse_conv = 1 */
+  RIA_CONV_WINDOW = 2  /* the reference's window [pool, conv_dim, 4], oldest first (:202-209) */
+};
+
+/* How q and k arrive in a ria_gdn_decode_ex call. */
+enum ria_qk_mode {
+  /* x holds the raw q|k of num_k_heads QK heads; l2norm and q * 128^-0.5 run
+   * here, and QK head h / (Hv / Hk) serves V head h (:237-254). */
+  RIA_QK_RAW = 0,
+  /* x (RIA_CONV_NONE only) holds per V head the caller's l2-normalised q
+   * (already scaled by 128^-0.5) and k: [Hv*128 q | Hv*128 k | Hv*128 v]
+   * (the reference's q, k after :252-254). */
+  RIA_QK_NORMALIZED = 1
+};
+
+/*
+ * One ria_gdn_decode_ex call.  Fields not named here are as in
+ * ria_gdn_decode.
+ *   conv_layout      see ria_conv_layout.  RIA_CONV_WINDOW reads each row's
+ *                    window from conv_window_in and writes the shifted window
+ *                    to conv_window_out, which must not overlap it (other
+ *                    workgroups read the q/k channels a workgroup shifts).
+ *   state_in/out     f32 [pool, Hv, 128, 128]: S is read from state_in and
+ *                    S_new written to state_out, the same buffer (in place)
+ *                    or a disjoint one (the reference stores a new state
+ *                    tensor each step, :261-265).
+ *   qk_mode          see ria_qk_mode.
+ */
+typedef struct ria_gdn_decode_desc {
+  int batch;
+  int num_k_heads;
+  int num_v_heads;
+  const void* x;
+  int x_dtype;
+  int64_t x_row_stride;
+  int conv_layout;
+  const void* conv_weight;
+  void* conv_ring;
+  const int32_t* conv_pos;
+  int32_t conv_pos_scalar;
+  const void* conv_window_in;
+  void* conv_window_out;
+  const float* state_in;
+  float* state_out;
+  const int32_t* seq_slot;
+  const float* gate_a;
+  const float* gate_b;
+  int64_t gate_row_stride;
+  int gate_mode;
+  const float* A_log;
+  const float* dt_bias;
+  int qk_mode;
+  void* out;
+  int out_dtype;
+  const void* z;
+  int z_dtype;
+  int64_t z_row_stride;
+  const float* norm_weight;
+} ria_gdn_decode_desc;
+
+/*
+ * ria_gdn_decode with the state layouts of the reference's AttentionState:
+ * a new state tensor per step and the conv window (the drop-in
+ * qwen36_attention_cache keeps its dicts as the reference's tensors, :27-32,
+ * :202-209, :256-265), and q/k normalised by the caller when the module's
+ * _l2norm is replaced (:252-254).  Replaces qwen36_attention_cache.py:235-271.
+ */
+int ria_gdn_decode_ex(const ria_gdn_decode_desc* desc, void* stream);
 
 /*
  * Row-wise l2 normalisation x * rsqrt(sum(x^2) + eps) in fp32 over rows of

@@ -33,11 +33,20 @@ struct GdnDecodeArgs {
   const void* x;
   int64_t x_stride;
   const uint16_t* conv_w;  // [conv_dim, 4] bf16
-  uint16_t* conv_ring;     // [pool, 4, conv_dim] bf16
+  uint16_t* conv_ring;     // [pool, 4, conv_dim] bf16 (ring layout)
   const int32_t* conv_pos;
   int32_t conv_pos_scalar;
-  float* state;  // [pool, Hv, 128, 128]
+  // window layout (the reference's [1, conv_dim, 4], oldest input first):
+  // the window is read from win_in and the shifted one written to win_out
+  int conv_window;
+  const uint16_t* win_in;  // [pool, conv_dim, 4] bf16
+  uint16_t* win_out;
+  const float* state_in;  // [pool, Hv, 128, 128]
+  float* state_out;       // == state_in for the in-place update
   const int32_t* seq_slot;
+  // q and k arrive l2-normalised (q also scaled by 128^-0.5) per V head:
+  // x = [Hv*128 q | Hv*128 k | Hv*128 v]; only without the fused conv
+  int qk_prenorm;
   const float* gate_a;
   const float* gate_b;
   int64_t gate_stride;
@@ -56,19 +65,38 @@ struct GdnDecodeArgs {
 
 // Post-conv value of channel c for batch row b, as the reference sees it
 // after `_causal_conv1d_step` returns (cast back to the input dtype).  When
-// `write` is set the current input is stored into ring slot n mod 4.
-template <int XT, bool FUSE>
+// `write` is set the conv state takes the current input: ring slot n mod 4
+// in the ring layout, or the shifted window (the last three inputs and this
+// one, oldest first, :207-209) in the window layout.
+// (The layout is a template parameter: a run-time branch around the history
+// loads would make the compiler wait for them at the join, before the state
+// loads that follow are issued.)
+template <int XT, int CONV>
 __device__ __forceinline__ float conv_channel(const GdnDecodeArgs& a, int b, int row, int n, int c,
                                               bool write) {
   const float xv = load_act<XT>(a.x, (int64_t)b * a.x_stride + c);
-  if constexpr (!FUSE) {
+  if constexpr (CONV == RIA_CONV_NONE) {
     return xv;
   } else {
     const uint16_t xb = f32_to_bf16_bits(xv);  // mixed_qkv.to(conv_dtype)
-    uint16_t* ring = a.conv_ring + (int64_t)row * kConvRing * a.conv_dim;
-    const float h0 = bf16_bits_to_f32(ring[((n - 3) & 3) * a.conv_dim + c]);
-    const float h1 = bf16_bits_to_f32(ring[((n - 2) & 3) * a.conv_dim + c]);
-    const float h2 = bf16_bits_to_f32(ring[((n - 1) & 3) * a.conv_dim + c]);
+    float h0, h1, h2;
+    if constexpr (CONV == RIA_CONV_WINDOW) {
+      // history = cat(window, x); the conv reads window slots 1..3 and x
+      const int64_t wi = ((int64_t)row * a.conv_dim + c) * kConvTaps;
+      const uint2 hv = *reinterpret_cast<const uint2*>(a.win_in + wi);
+      h0 = bf16_bits_to_f32(hv.x >> 16);
+      h1 = bf16_bits_to_f32(hv.y & 0xffffu);
+      h2 = bf16_bits_to_f32(hv.y >> 16);
+      if (write)
+        *reinterpret_cast<uint2*>(a.win_out + wi) =
+            uint2{(hv.x >> 16) | (hv.y << 16), (hv.y >> 16) | (uint32_t(xb) << 16)};
+    } else {
+      uint16_t* ring = a.conv_ring + (int64_t)row * kConvRing * a.conv_dim;
+      h0 = bf16_bits_to_f32(ring[((n - 3) & 3) * a.conv_dim + c]);
+      h1 = bf16_bits_to_f32(ring[((n - 2) & 3) * a.conv_dim + c]);
+      h2 = bf16_bits_to_f32(ring[((n - 1) & 3) * a.conv_dim + c]);
+      if (write) ring[(n & 3) * a.conv_dim + c] = xb;
+    }
     const uint2 wv = *reinterpret_cast<const uint2*>(a.conv_w + (int64_t)c * kConvTaps);
     const float w0 = bf16_bits_to_f32(wv.x & 0xffffu), w1 = bf16_bits_to_f32(wv.x >> 16);
     const float w2 = bf16_bits_to_f32(wv.y & 0xffffu), w3 = bf16_bits_to_f32(wv.y >> 16);
@@ -77,13 +105,13 @@ __device__ __forceinline__ float conv_channel(const GdnDecodeArgs& a, int b, int
     acc = fmaf(w2, h2, acc);
     acc = fmaf(w3, bf16_bits_to_f32(xb), acc);
     const float y = round_bf16(silu_f(round_bf16(acc)));
-    if (write) ring[(n & 3) * a.conv_dim + c] = xb;
     return through_dtype<XT>(y);
   }
 }
 
-template <int COLS, int XT, int OT, bool FUSE, int GM, bool NORM>
+template <int COLS, int XT, int OT, int CONV, int GM, bool NORM>
 __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
+  constexpr bool FUSE = CONV != RIA_CONV_NONE;
   static_assert(!NORM || COLS == kGdnHeadDim, "the gated norm needs whole heads");
   constexpr int TPR = COLS / 4;         // threads per state row
   constexpr int RG = 256 / TPR;         // row groups in the workgroup
@@ -100,8 +128,9 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
   const int row = a.seq_slot ? a.seq_slot[b] : b;
   const int col0 = cb * COLS;
   const int group = a.num_v_heads / a.num_k_heads;
-  const int hk = h / group;
-  const int kdim = a.num_k_heads * kGdnHeadDim;
+  // the QK head serving V head h, and the q (and k) section width of x
+  const int hk = a.qk_prenorm ? h : h / group;
+  const int kdim = (a.qk_prenorm ? a.num_v_heads : a.num_k_heads) * kGdnHeadDim;
   const int n = a.conv_pos ? a.conv_pos[b] : a.conv_pos_scalar;
 
   const int cg = tid % TPR;
@@ -119,9 +148,9 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
   // Conv / projection inputs first, so their latency overlaps the state loads.
   const bool qk_writer = FUSE && (h % group == 0) && cb == 0;
   const int qk_c = tid < 128 ? hk * kGdnHeadDim + tid : kdim + hk * kGdnHeadDim + (tid - 128);
-  float qk_raw = conv_channel<XT, FUSE>(a, b, row, n, qk_c, qk_writer);
+  float qk_raw = conv_channel<XT, CONV>(a, b, row, n, qk_c, qk_writer);
   float v_raw = 0.f;
-  if (tid < COLS) v_raw = conv_channel<XT, FUSE>(a, b, row, n, 2 * kdim + h * kGdnHeadDim + col0 + tid, FUSE);
+  if (tid < COLS) v_raw = conv_channel<XT, CONV>(a, b, row, n, 2 * kdim + h * kGdnHeadDim + col0 + tid, FUSE);
   // The gated norm's z (as the raw 32-bit word holding it; every thread loads
   // one, threads past COLS a repeat, so no branch makes the wait early) and w.
   ActWord z_word{};
@@ -132,7 +161,8 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     w_raw = a.norm_w[tc];
   }
 
-  float* S = a.state + ((int64_t)row * a.num_v_heads + h) * (kGdnHeadDim * kGdnHeadDim);
+  const int64_t tile = ((int64_t)row * a.num_v_heads + h) * (kGdnHeadDim * kGdnHeadDim);
+  const float* S = a.state_in + tile;
   f32x4 s[RPT];
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
@@ -164,10 +194,13 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     }
   }
   __syncthreads();
-  const float inv = 1.0f / sqrtf((tid < 128 ? scal_s[0] + scal_s[1] : scal_s[2] + scal_s[3]) + 1e-6f);
-  float qk_n = mul_rn(qk_raw, inv);
+  float qk_n = qk_raw;
+  if (!a.qk_prenorm) {
+    const float inv = 1.0f / sqrtf((tid < 128 ? scal_s[0] + scal_s[1] : scal_s[2] + scal_s[3]) + 1e-6f);
+    qk_n = mul_rn(qk_raw, inv);
+    if (tid < 128) qk_n = mul_rn(qk_n, 0.08838834764831845f);
+  }
   if (tid < 128) {
-    qk_n = mul_rn(qk_n, 0.08838834764831845f);
     q_s[tid] = qk_n;
   } else {
     k_s[tid - 128] = qk_n;
@@ -224,14 +257,15 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     oo[c] = fmaf(dj[c], kq, ot);
   }
 
-  // Rank-1 update, written back in place.
+  // Rank-1 update, written to state_out (in place when it is state_in).
+  float* So = a.state_out + tile;
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
     const int i = rg + RG * r;
     const float ki = k_s[i];
 #pragma unroll
     for (int c = 0; c < 4; ++c) s[r][c] = add_rn(s[r][c], mul_rn(ki, dj[c]));
-    st_stream(reinterpret_cast<f32x4*>(S + i * kGdnHeadDim + col0 + jl), s[r]);
+    st_stream(reinterpret_cast<f32x4*>(So + i * kGdnHeadDim + col0 + jl), s[r]);
   }
 
   if constexpr (NORM) {
@@ -253,7 +287,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
 }
 
 // Standalone conv step (one thread per channel).
-template <int XT, int OT>
+template <int XT, int OT, int CONV>
 __global__ __launch_bounds__(256) void conv1d_step_kernel(GdnDecodeArgs a) {
   const int b = blockIdx.y;
   const int c = blockIdx.x * 256 + threadIdx.x;
@@ -262,61 +296,202 @@ __global__ __launch_bounds__(256) void conv1d_step_kernel(GdnDecodeArgs a) {
   const int n = a.conv_pos ? a.conv_pos[b] : a.conv_pos_scalar;
   // The reference returns the bf16 conv result cast to the input dtype; the
   // caller-selected output dtype is applied on top of that.
-  const float y = conv_channel<XT, true>(a, b, row, n, c, true);
+  const float y = conv_channel<XT, CONV>(a, b, row, n, c, true);
   store_act<OT>(a.out, (int64_t)b * a.conv_dim + c, y);
 }
 
-template <int COLS, int XT, int OT, bool FUSE, bool NORM>
+template <int COLS, int XT, int OT, int CONV, bool NORM>
 static void launch_gdn_gm(const GdnDecodeArgs& a, int gate_mode, int blocks, hipStream_t st) {
   if (gate_mode == RIA_GATE_RAW)
-    hipLaunchKernelGGL((gdn_decode_kernel<COLS, XT, OT, FUSE, RIA_GATE_RAW, NORM>), dim3(blocks), dim3(256), 0, st,
+    hipLaunchKernelGGL((gdn_decode_kernel<COLS, XT, OT, CONV, RIA_GATE_RAW, NORM>), dim3(blocks), dim3(256), 0, st,
                        a);
   else
-    hipLaunchKernelGGL((gdn_decode_kernel<COLS, XT, OT, FUSE, RIA_GATE_PRECOMPUTED, NORM>), dim3(blocks), dim3(256),
+    hipLaunchKernelGGL((gdn_decode_kernel<COLS, XT, OT, CONV, RIA_GATE_PRECOMPUTED, NORM>), dim3(blocks), dim3(256),
                        0, st, a);
 }
 
-template <int COLS, int XT, int OT, bool FUSE>
+template <int COLS, int XT, int OT, int CONV>
 static void launch_gdn_norm(const GdnDecodeArgs& a, int gate_mode, int blocks, hipStream_t st) {
   if constexpr (COLS == kGdnHeadDim) {
     if (a.z) {
-      launch_gdn_gm<COLS, XT, OT, FUSE, true>(a, gate_mode, blocks, st);
+      launch_gdn_gm<COLS, XT, OT, CONV, true>(a, gate_mode, blocks, st);
       return;
     }
   }
-  launch_gdn_gm<COLS, XT, OT, FUSE, false>(a, gate_mode, blocks, st);
+  launch_gdn_gm<COLS, XT, OT, CONV, false>(a, gate_mode, blocks, st);
 }
 
 template <int COLS, int XT, int OT>
-static void launch_gdn_fuse(const GdnDecodeArgs& a, bool fuse, int gate_mode, int blocks, hipStream_t st) {
-  if (fuse)
-    launch_gdn_norm<COLS, XT, OT, true>(a, gate_mode, blocks, st);
+static void launch_gdn_fuse(const GdnDecodeArgs& a, int conv, int gate_mode, int blocks, hipStream_t st) {
+  if (conv == RIA_CONV_RING)
+    launch_gdn_norm<COLS, XT, OT, RIA_CONV_RING>(a, gate_mode, blocks, st);
+  else if (conv == RIA_CONV_WINDOW)
+    launch_gdn_norm<COLS, XT, OT, RIA_CONV_WINDOW>(a, gate_mode, blocks, st);
   else
-    launch_gdn_norm<COLS, XT, OT, false>(a, gate_mode, blocks, st);
+    launch_gdn_norm<COLS, XT, OT, RIA_CONV_NONE>(a, gate_mode, blocks, st);
 }
 
 template <int COLS, int XT>
-static void launch_gdn_ot(const GdnDecodeArgs& a, int ot, bool fuse, int gate_mode, int blocks, hipStream_t st) {
+static void launch_gdn_ot(const GdnDecodeArgs& a, int ot, int conv, int gate_mode, int blocks, hipStream_t st) {
   if (ot == RIA_DT_BF16)
-    launch_gdn_fuse<COLS, XT, RIA_DT_BF16>(a, fuse, gate_mode, blocks, st);
+    launch_gdn_fuse<COLS, XT, RIA_DT_BF16>(a, conv, gate_mode, blocks, st);
   else if (ot == RIA_DT_F16)
-    launch_gdn_fuse<COLS, XT, RIA_DT_F16>(a, fuse, gate_mode, blocks, st);
+    launch_gdn_fuse<COLS, XT, RIA_DT_F16>(a, conv, gate_mode, blocks, st);
   else
-    launch_gdn_fuse<COLS, XT, RIA_DT_F32>(a, fuse, gate_mode, blocks, st);
+    launch_gdn_fuse<COLS, XT, RIA_DT_F32>(a, conv, gate_mode, blocks, st);
 }
 
 template <int COLS>
-static void launch_gdn_xt(const GdnDecodeArgs& a, int xt, int ot, bool fuse, int gate_mode, int blocks,
+static void launch_gdn_xt(const GdnDecodeArgs& a, int xt, int ot, int conv, int gate_mode, int blocks,
                           hipStream_t st) {
   if (xt == RIA_DT_BF16)
-    launch_gdn_ot<COLS, RIA_DT_BF16>(a, ot, fuse, gate_mode, blocks, st);
+    launch_gdn_ot<COLS, RIA_DT_BF16>(a, ot, conv, gate_mode, blocks, st);
   else if (xt == RIA_DT_F16)
-    launch_gdn_ot<COLS, RIA_DT_F16>(a, ot, fuse, gate_mode, blocks, st);
+    launch_gdn_ot<COLS, RIA_DT_F16>(a, ot, conv, gate_mode, blocks, st);
   else
-    launch_gdn_ot<COLS, RIA_DT_F32>(a, ot, fuse, gate_mode, blocks, st);
+    launch_gdn_ot<COLS, RIA_DT_F32>(a, ot, conv, gate_mode, blocks, st);
 }
 
 static bool valid_dtype(int dt) { return dt == RIA_DT_BF16 || dt == RIA_DT_F16 || dt == RIA_DT_F32; }
+
+// Validates a decode description and launches it (shared by ria_gdn_decode
+// and ria_gdn_decode_ex).
+static int gdn_decode_launch(const ria_gdn_decode_desc& d, void* stream, const char* who) {
+  if (d.batch < 0) return set_error(RIA_ERR_INVALID, "%s: batch must be >= 0", who);
+  if (d.batch == 0) return RIA_OK;
+  const int num_k_heads = d.num_k_heads, num_v_heads = d.num_v_heads;
+  if (num_k_heads <= 0 || num_v_heads <= 0 || num_v_heads % num_k_heads != 0)
+    return set_error(RIA_ERR_INVALID, "%s: num_v_heads (%d) must be a positive multiple of num_k_heads (%d)", who,
+                     num_v_heads, num_k_heads);
+  if (!valid_dtype(d.x_dtype) || !valid_dtype(d.out_dtype)) return set_error(RIA_ERR_INVALID, "%s: unknown dtype code", who);
+  if (!d.x || !d.state_in || !d.state_out || !d.gate_a || !d.gate_b || !d.out)
+    return set_error(RIA_ERR_INVALID, "%s: null tensor pointer", who);
+  if (d.conv_layout != RIA_CONV_NONE && d.conv_layout != RIA_CONV_RING && d.conv_layout != RIA_CONV_WINDOW)
+    return set_error(RIA_ERR_INVALID, "%s: unknown conv_layout %d", who, d.conv_layout);
+  const bool fuse = d.conv_layout != RIA_CONV_NONE;
+  if (fuse && !d.conv_weight) return set_error(RIA_ERR_INVALID, "%s: the fused conv needs conv_weight", who);
+  if (d.conv_layout == RIA_CONV_RING && !d.conv_ring)
+    return set_error(RIA_ERR_INVALID, "%s: RIA_CONV_RING needs conv_ring", who);
+  if (d.qk_mode != RIA_QK_RAW && d.qk_mode != RIA_QK_NORMALIZED)
+    return set_error(RIA_ERR_INVALID, "%s: unknown qk_mode %d", who, d.qk_mode);
+  if (d.qk_mode == RIA_QK_NORMALIZED && fuse)
+    return set_error(RIA_ERR_INVALID, "%s: RIA_QK_NORMALIZED takes convolved inputs (conv_layout RIA_CONV_NONE)", who);
+  if (d.gate_mode == RIA_GATE_RAW && (!d.A_log || !d.dt_bias))
+    return set_error(RIA_ERR_INVALID, "%s: RIA_GATE_RAW needs A_log and dt_bias", who);
+  if (d.gate_mode != RIA_GATE_RAW && d.gate_mode != RIA_GATE_PRECOMPUTED)
+    return set_error(RIA_ERR_INVALID, "%s: unknown gate_mode %d", who, d.gate_mode);
+  if (reinterpret_cast<uintptr_t>(d.state_in) % 16 || reinterpret_cast<uintptr_t>(d.state_out) % 16 ||
+      (fuse && reinterpret_cast<uintptr_t>(d.conv_weight) % 8 != 0))
+    return set_error(RIA_ERR_INVALID, "%s: states must be 16-byte and conv_weight 8-byte aligned", who);
+  const int conv_dim = (2 * num_k_heads + num_v_heads) * kGdnHeadDim;
+  const int64_t x_width =
+      d.qk_mode == RIA_QK_NORMALIZED ? (int64_t)3 * num_v_heads * kGdnHeadDim : (int64_t)conv_dim;
+  if (d.x_row_stride < x_width) return set_error(RIA_ERR_INVALID, "%s: x_row_stride < %lld", who, (long long)x_width);
+  if (d.gate_row_stride < num_v_heads) return set_error(RIA_ERR_INVALID, "%s: gate_row_stride < Hv", who);
+  if (d.z && (!d.norm_weight || !valid_dtype(d.z_dtype) || d.z_row_stride < (int64_t)num_v_heads * kGdnHeadDim))
+    return set_error(RIA_ERR_INVALID, "%s: a gate z needs norm_weight, a dtype code and row stride >= Hv*128", who);
+  if (d.z && (reinterpret_cast<uintptr_t>(d.z) % 4 || d.z_row_stride % 2))
+    return set_error(RIA_ERR_INVALID, "%s: z must be 4-byte aligned with an even row stride", who);
+  // The state tiles of one launch are read and written by one workgroup each,
+  // so in place is safe; a partial overlap would let a workgroup read a tile
+  // another one has already written.
+  const int64_t pool_bytes_lo = (int64_t)d.batch * num_v_heads * kGdnHeadDim * kGdnHeadDim * 4;
+  if (d.state_in != d.state_out && !d.seq_slot) {
+    const char* i0 = reinterpret_cast<const char*>(d.state_in);
+    const char* o0 = reinterpret_cast<const char*>(d.state_out);
+    if (i0 < o0 + pool_bytes_lo && o0 < i0 + pool_bytes_lo)
+      return set_error(RIA_ERR_INVALID, "%s: state_out overlaps state_in without being it", who);
+  }
+  if (d.conv_layout == RIA_CONV_WINDOW) {
+    if (!d.conv_window_in || !d.conv_window_out)
+      return set_error(RIA_ERR_INVALID, "%s: RIA_CONV_WINDOW needs conv_window_in and conv_window_out", who);
+    if (reinterpret_cast<uintptr_t>(d.conv_window_in) % 8 || reinterpret_cast<uintptr_t>(d.conv_window_out) % 8)
+      return set_error(RIA_ERR_INVALID, "%s: conv windows must be 8-byte aligned", who);
+    // other workgroups read the channels a workgroup shifts: out must not overlap in
+    const int64_t wbytes = (int64_t)d.batch * conv_dim * kConvTaps * 2;
+    const char* i0 = static_cast<const char*>(d.conv_window_in);
+    const char* o0 = static_cast<const char*>(d.conv_window_out);
+    if (!d.seq_slot && i0 < o0 + wbytes && o0 < i0 + wbytes)
+      return set_error(RIA_ERR_INVALID, "%s: conv_window_out must not overlap conv_window_in", who);
+    if (d.seq_slot && i0 == o0)
+      return set_error(RIA_ERR_INVALID, "%s: conv_window_out must not overlap conv_window_in", who);
+  }
+
+  GdnDecodeArgs a{};
+  a.x = d.x;
+  a.x_stride = d.x_row_stride;
+  a.conv_w = static_cast<const uint16_t*>(d.conv_weight);
+  a.conv_ring = static_cast<uint16_t*>(d.conv_ring);
+  a.conv_pos = d.conv_pos;
+  a.conv_pos_scalar = d.conv_pos_scalar;
+  a.conv_window = d.conv_layout == RIA_CONV_WINDOW ? 1 : 0;
+  a.win_in = static_cast<const uint16_t*>(d.conv_window_in);
+  a.win_out = static_cast<uint16_t*>(d.conv_window_out);
+  a.state_in = d.state_in;
+  a.state_out = d.state_out;
+  a.seq_slot = d.seq_slot;
+  a.qk_prenorm = d.qk_mode == RIA_QK_NORMALIZED ? 1 : 0;
+  a.gate_a = d.gate_a;
+  a.gate_b = d.gate_b;
+  a.gate_stride = d.gate_row_stride;
+  a.A_log = d.A_log;
+  a.dt_bias = d.dt_bias;
+  a.out = d.out;
+  a.z = d.z;
+  a.z_stride = d.z_row_stride;
+  a.z_dtype = d.z_dtype;
+  a.norm_w = d.norm_weight;
+  a.num_k_heads = num_k_heads;
+  a.num_v_heads = num_v_heads;
+  a.conv_dim = conv_dim;
+
+  // Column blocking: enough workgroups to cover 256 CUs several times over;
+  // the gated norm needs whole heads.
+  const int64_t tiles = (int64_t)d.batch * num_v_heads;
+  int cols = 128;
+  if (!d.z) {
+    if (tiles < 256) cols = 32;
+    else if (tiles < 1024) cols = 64;
+  }
+  a.ncb = kGdnHeadDim / cols;
+  const int64_t blocks64 = tiles * a.ncb;
+  if (blocks64 > 0x7fffffff) return set_error(RIA_ERR_INVALID, "%s: grid too large", who);
+  const int blocks = static_cast<int>(blocks64);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (cols == 128)
+    launch_gdn_xt<128>(a, d.x_dtype, d.out_dtype, d.conv_layout, d.gate_mode, blocks, st);
+  else if (cols == 64)
+    launch_gdn_xt<64>(a, d.x_dtype, d.out_dtype, d.conv_layout, d.gate_mode, blocks, st);
+  else
+    launch_gdn_xt<32>(a, d.x_dtype, d.out_dtype, d.conv_layout, d.gate_mode, blocks, st);
+  return check_launch(who);
+}
+
+// Standalone conv step over `channels` channels for `batch` rows, in the ring
+// or the window layout (shared by ria_conv1d_step and ria_conv1d_window_step).
+static int conv_step_launch(const GdnDecodeArgs& a, int batch, int channels, int x_dtype, int out_dtype,
+                            hipStream_t st) {
+  dim3 grid((channels + 255) / 256, batch);
+#define RIA_CONV_LAUNCH(XT_, OT_)                                                                            \
+  if (a.conv_window)                                                                                        \
+    hipLaunchKernelGGL((conv1d_step_kernel<XT_, OT_, RIA_CONV_WINDOW>), grid, dim3(256), 0, st, a);        \
+  else                                                                                                      \
+    hipLaunchKernelGGL((conv1d_step_kernel<XT_, OT_, RIA_CONV_RING>), grid, dim3(256), 0, st, a)
+#define RIA_CONV_OT(XT_)                                          \
+  if (out_dtype == RIA_DT_BF16) RIA_CONV_LAUNCH(XT_, RIA_DT_BF16); \
+  else if (out_dtype == RIA_DT_F16) RIA_CONV_LAUNCH(XT_, RIA_DT_F16); \
+  else RIA_CONV_LAUNCH(XT_, RIA_DT_F32);
+  if (x_dtype == RIA_DT_BF16) {
+    RIA_CONV_OT(RIA_DT_BF16)
+  } else if (x_dtype == RIA_DT_F16) {
+    RIA_CONV_OT(RIA_DT_F16)
+  } else {
+    RIA_CONV_OT(RIA_DT_F32)
+  }
+#undef RIA_CONV_OT
+#undef RIA_CONV_LAUNCH
+  return RIA_OK;
+}
 
 }  // namespace ria
 
@@ -329,75 +504,40 @@ extern "C" int ria_gdn_decode(int batch, int num_k_heads, int num_v_heads, const
                               int64_t gate_row_stride, int gate_mode, const float* A_log, const float* dt_bias,
                               void* out, int out_dtype, const void* z, int z_dtype, int64_t z_row_stride,
                               const float* norm_weight, void* stream) {
-  if (batch < 0) return set_error(RIA_ERR_INVALID, "ria_gdn_decode: batch must be >= 0");
-  if (batch == 0) return RIA_OK;
-  if (num_k_heads <= 0 || num_v_heads <= 0 || num_v_heads % num_k_heads != 0)
-    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: num_v_heads (%d) must be a positive multiple of num_k_heads (%d)",
-                     num_v_heads, num_k_heads);
-  if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype))
-    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: unknown dtype code");
-  if (!mixed_qkv || !state || !gate_a || !gate_b || !out)
-    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: null tensor pointer");
-  if (fuse_conv && (!conv_weight || !conv_ring))
-    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: fuse_conv needs conv_weight and conv_ring");
-  if (gate_mode == RIA_GATE_RAW && (!A_log || !dt_bias))
-    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: RIA_GATE_RAW needs A_log and dt_bias");
-  if (gate_mode != RIA_GATE_RAW && gate_mode != RIA_GATE_PRECOMPUTED)
-    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: unknown gate_mode %d", gate_mode);
-  if (reinterpret_cast<uintptr_t>(state) % 16 != 0 || (fuse_conv && reinterpret_cast<uintptr_t>(conv_weight) % 8 != 0))
-    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: state must be 16-byte and conv_weight 8-byte aligned");
-  const int conv_dim = (2 * num_k_heads + num_v_heads) * kGdnHeadDim;
-  if (x_row_stride < conv_dim) return set_error(RIA_ERR_INVALID, "ria_gdn_decode: x_row_stride < conv_dim");
-  if (gate_row_stride < num_v_heads) return set_error(RIA_ERR_INVALID, "ria_gdn_decode: gate_row_stride < Hv");
-  if (z && (!norm_weight || !valid_dtype(z_dtype) || z_row_stride < (int64_t)num_v_heads * kGdnHeadDim))
-    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: a gate z needs norm_weight, a dtype code and row stride >= Hv*128");
-  if (z && (reinterpret_cast<uintptr_t>(z) % 4 || z_row_stride % 2))
-    return set_error(RIA_ERR_INVALID, "ria_gdn_decode: z must be 4-byte aligned with an even row stride");
+  ria_gdn_decode_desc d{};
+  d.batch = batch;
+  d.num_k_heads = num_k_heads;
+  d.num_v_heads = num_v_heads;
+  d.x = mixed_qkv;
+  d.x_dtype = x_dtype;
+  d.x_row_stride = x_row_stride;
+  d.conv_layout = fuse_conv ? RIA_CONV_RING : RIA_CONV_NONE;
+  d.conv_weight = conv_weight;
+  d.conv_ring = conv_ring;
+  d.conv_pos = conv_pos;
+  d.conv_pos_scalar = conv_pos_scalar;
+  d.state_in = state;
+  d.state_out = state;
+  d.seq_slot = seq_slot;
+  d.gate_a = gate_a;
+  d.gate_b = gate_b;
+  d.gate_row_stride = gate_row_stride;
+  d.gate_mode = gate_mode;
+  d.A_log = A_log;
+  d.dt_bias = dt_bias;
+  d.qk_mode = RIA_QK_RAW;
+  d.out = out;
+  d.out_dtype = out_dtype;
+  d.z = z;
+  d.z_dtype = z_dtype;
+  d.z_row_stride = z_row_stride;
+  d.norm_weight = norm_weight;
+  return gdn_decode_launch(d, stream, "ria_gdn_decode");
+}
 
-  GdnDecodeArgs a{};
-  a.x = mixed_qkv;
-  a.x_stride = x_row_stride;
-  a.conv_w = static_cast<const uint16_t*>(conv_weight);
-  a.conv_ring = static_cast<uint16_t*>(conv_ring);
-  a.conv_pos = conv_pos;
-  a.conv_pos_scalar = conv_pos_scalar;
-  a.state = state;
-  a.seq_slot = seq_slot;
-  a.gate_a = gate_a;
-  a.gate_b = gate_b;
-  a.gate_stride = gate_row_stride;
-  a.A_log = A_log;
-  a.dt_bias = dt_bias;
-  a.out = out;
-  a.z = z;
-  a.z_stride = z_row_stride;
-  a.z_dtype = z_dtype;
-  a.norm_w = norm_weight;
-  a.num_k_heads = num_k_heads;
-  a.num_v_heads = num_v_heads;
-  a.conv_dim = conv_dim;
-
-  // Column blocking: enough workgroups to cover 256 CUs several times over;
-  // the gated norm needs whole heads.
-  const int64_t tiles = (int64_t)batch * num_v_heads;
-  int cols = 128;
-  if (!z) {
-    if (tiles < 256) cols = 32;
-    else if (tiles < 1024) cols = 64;
-  }
-  a.ncb = kGdnHeadDim / cols;
-  const int64_t blocks64 = tiles * a.ncb;
-  if (blocks64 > 0x7fffffff) return set_error(RIA_ERR_INVALID, "ria_gdn_decode: grid too large");
-  const int blocks = static_cast<int>(blocks64);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool fuse = fuse_conv != 0;
-  if (cols == 128)
-    launch_gdn_xt<128>(a, x_dtype, out_dtype, fuse, gate_mode, blocks, st);
-  else if (cols == 64)
-    launch_gdn_xt<64>(a, x_dtype, out_dtype, fuse, gate_mode, blocks, st);
-  else
-    launch_gdn_xt<32>(a, x_dtype, out_dtype, fuse, gate_mode, blocks, st);
-  return check_launch("ria_gdn_decode");
+extern "C" int ria_gdn_decode_ex(const ria_gdn_decode_desc* desc, void* stream) {
+  if (!desc) return set_error(RIA_ERR_INVALID, "ria_gdn_decode_ex: null description");
+  return gdn_decode_launch(*desc, stream, "ria_gdn_decode_ex");
 }
 
 extern "C" int ria_conv1d_step(int batch, int channels, const void* x, int x_dtype, int64_t x_row_stride,
@@ -422,21 +562,33 @@ extern "C" int ria_conv1d_step(int batch, int channels, const void* x, int x_dty
   a.seq_slot = seq_slot;
   a.out = out;
   a.conv_dim = channels;
-  dim3 grid((channels + 255) / 256, batch);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-#define RIA_CONV_LAUNCH(XT_, OT_) hipLaunchKernelGGL((conv1d_step_kernel<XT_, OT_>), grid, dim3(256), 0, st, a)
-#define RIA_CONV_OT(XT_)                                          \
-  if (out_dtype == RIA_DT_BF16) RIA_CONV_LAUNCH(XT_, RIA_DT_BF16); \
-  else if (out_dtype == RIA_DT_F16) RIA_CONV_LAUNCH(XT_, RIA_DT_F16); \
-  else RIA_CONV_LAUNCH(XT_, RIA_DT_F32);
-  if (x_dtype == RIA_DT_BF16) {
-    RIA_CONV_OT(RIA_DT_BF16)
-  } else if (x_dtype == RIA_DT_F16) {
-    RIA_CONV_OT(RIA_DT_F16)
-  } else {
-    RIA_CONV_OT(RIA_DT_F32)
-  }
-#undef RIA_CONV_OT
-#undef RIA_CONV_LAUNCH
+  conv_step_launch(a, batch, channels, x_dtype, out_dtype, static_cast<hipStream_t>(stream));
   return check_launch("ria_conv1d_step");
+}
+
+extern "C" int ria_conv1d_window_step(int batch, int channels, const void* x, int x_dtype, int64_t x_row_stride,
+                                      const void* conv_weight, const void* window_in, void* window_out, void* out,
+                                      int out_dtype, void* stream) {
+  if (batch < 0 || channels <= 0) return set_error(RIA_ERR_INVALID, "ria_conv1d_window_step: bad batch/channels");
+  if (batch == 0) return RIA_OK;
+  if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype))
+    return set_error(RIA_ERR_INVALID, "ria_conv1d_window_step: unknown dtype code");
+  if (!x || !conv_weight || !window_in || !window_out || !out)
+    return set_error(RIA_ERR_INVALID, "ria_conv1d_window_step: null pointer");
+  if (reinterpret_cast<uintptr_t>(conv_weight) % 8 || reinterpret_cast<uintptr_t>(window_in) % 8 ||
+      reinterpret_cast<uintptr_t>(window_out) % 8)
+    return set_error(RIA_ERR_INVALID, "ria_conv1d_window_step: conv_weight and windows must be 8-byte aligned");
+  if (x_row_stride < channels) return set_error(RIA_ERR_INVALID, "ria_conv1d_window_step: x_row_stride < channels");
+  // one thread per channel reads its window and writes the shifted one: in place is safe here
+  GdnDecodeArgs a{};
+  a.x = x;
+  a.x_stride = x_row_stride;
+  a.conv_w = static_cast<const uint16_t*>(conv_weight);
+  a.conv_window = 1;
+  a.win_in = static_cast<const uint16_t*>(window_in);
+  a.win_out = static_cast<uint16_t*>(window_out);
+  a.out = out;
+  a.conv_dim = channels;
+  conv_step_launch(a, batch, channels, x_dtype, out_dtype, static_cast<hipStream_t>(stream));
+  return check_launch("ria_conv1d_window_step");
 }

@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIB_ENV = "RIA_HIP_LIB"
 DEFAULT_LIB = Path(__file__).resolve().parent / "_lib" / "libria_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 RIA_DT_BF16 = 0
 RIA_DT_F16 = 1
@@ -28,6 +28,11 @@ RIA_ATTN_BOTH = 3
 RIA_PREFILL_APPEND = 1
 RIA_PREFILL_ATTEND = 2
 RIA_PREFILL_BOTH = 3
+RIA_CONV_NONE = 0
+RIA_CONV_RING = 1
+RIA_CONV_WINDOW = 2
+RIA_QK_RAW = 0
+RIA_QK_NORMALIZED = 1
 
 _c_int = ctypes.c_int
 _c_i32 = ctypes.c_int32
@@ -48,6 +53,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _vp, _vp, _c_i32, _vp, _c_int, _vp],
     ),
+    "ria_conv1d_window_step": (
+        _c_int,
+        [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _vp, _vp, _vp, _c_int, _vp],
+    ),
+    "ria_gdn_decode_ex": (_c_int, [_vp, _vp]),
     "ria_l2norm": (_c_int, [_c_i64, _c_int, _vp, _c_int, _c_f32, _vp, _vp]),
     "ria_rmsnorm": (_c_int, [_c_i64, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_f32, _vp, _c_int, _c_i64, _vp]),
     "ria_gated_rmsnorm": (
@@ -123,6 +133,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
 }
 
+
+
+class GdnDecodeDesc(ctypes.Structure):
+    """struct ria_gdn_decode_desc: one ria_gdn_decode_ex call."""
+    _fields_ = [("batch", _c_int), ("num_k_heads", _c_int), ("num_v_heads", _c_int), ("x", _vp),
+                ("x_dtype", _c_int), ("x_row_stride", _c_i64), ("conv_layout", _c_int), ("conv_weight", _vp),
+                ("conv_ring", _vp), ("conv_pos", _vp), ("conv_pos_scalar", _c_i32), ("conv_window_in", _vp),
+                ("conv_window_out", _vp), ("state_in", _vp), ("state_out", _vp), ("seq_slot", _vp),
+                ("gate_a", _vp), ("gate_b", _vp), ("gate_row_stride", _c_i64), ("gate_mode", _c_int),
+                ("A_log", _vp), ("dt_bias", _vp), ("qk_mode", _c_int), ("out", _vp), ("out_dtype", _c_int),
+                ("z", _vp), ("z_dtype", _c_int), ("z_row_stride", _c_i64), ("norm_weight", _vp)]
 
 
 class Fp8Proj(ctypes.Structure):

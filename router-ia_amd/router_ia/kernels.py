@@ -165,6 +165,144 @@ def gdn_decode(
     return out
 
 
+def gdn_decode_ex(
+    x: torch.Tensor,
+    state_in: torch.Tensor,
+    state_out: torch.Tensor,
+    gate_a: torch.Tensor,
+    gate_b: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    num_k_heads: int,
+    num_v_heads: int,
+    conv_layout: int = nat.RIA_CONV_NONE,
+    conv_weight: torch.Tensor | None = None,
+    conv_ring: torch.Tensor | None = None,
+    conv_pos: torch.Tensor | int = 0,
+    conv_window_in: torch.Tensor | None = None,
+    conv_window_out: torch.Tensor | None = None,
+    seq_slot: torch.Tensor | None = None,
+    gate_mode: int = nat.RIA_GATE_PRECOMPUTED,
+    A_log: torch.Tensor | None = None,
+    dt_bias: torch.Tensor | None = None,
+    qk_mode: int = nat.RIA_QK_RAW,
+    z: torch.Tensor | None = None,
+    norm_weight: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """DeltaNet decode step with a separate output state and the conv state in ring or window layout.
+
+    ``state_out`` may be ``state_in`` (in place) or a disjoint tensor of the
+    same shape.  ``conv_layout``: RIA_CONV_NONE (x already convolved),
+    RIA_CONV_RING (``conv_ring`` / ``conv_pos``) or RIA_CONV_WINDOW (the
+    reference's window [pool, conv_dim, 4] in ``conv_window_in``, the shifted
+    one written to ``conv_window_out``).  ``qk_mode`` RIA_QK_NORMALIZED takes x
+    as [B, Hv*128 q | Hv*128 k | Hv*128 v] with q, k normalised by the caller
+    (ria_gdn_decode_ex).
+    """
+    batch = int(x.shape[0])
+    dev = x.device
+    cdim = conv_dim(num_k_heads, num_v_heads)
+    for name, t in (("x", x), ("state_in", state_in), ("state_out", state_out), ("gate_a", gate_a),
+                    ("gate_b", gate_b), ("out", out), ("conv_weight", conv_weight), ("conv_ring", conv_ring),
+                    ("conv_window_in", conv_window_in), ("conv_window_out", conv_window_out),
+                    ("seq_slot", seq_slot), ("A_log", A_log), ("dt_bias", dt_bias)):
+        _require_gpu(name, t, dev)
+    width = 3 * num_v_heads * GDN_HEAD_DIM if qk_mode == nat.RIA_QK_NORMALIZED else cdim
+    x_stride = _row_stride("x", x, batch, width)
+    for name, st in (("state_in", state_in), ("state_out", state_out)):
+        if st.dtype != torch.float32 or st.dim() != 4 or tuple(st.shape[1:]) != (num_v_heads, 128, 128) \
+                or not st.is_contiguous():
+            raise ValueError(f"{name} must be contiguous fp32 [pool, {num_v_heads}, 128, 128], got {tuple(st.shape)}")
+        if seq_slot is None and st.shape[0] < batch:
+            raise ValueError(f"{name} pool smaller than batch")
+    if state_out.data_ptr() != state_in.data_ptr() and state_out.shape[0] != state_in.shape[0]:
+        raise ValueError("state_out must be state_in or a tensor of its shape")
+    if gate_a.dtype != torch.float32 or gate_b.dtype != torch.float32:
+        raise ValueError("gate_a / gate_b must be fp32")
+    g_stride = _row_stride("gate_a", gate_a, batch, num_v_heads)
+    if _row_stride("gate_b", gate_b, batch, num_v_heads) != g_stride:
+        raise ValueError("gate_a and gate_b must share a row stride")
+    if tuple(out.shape) != (batch, num_v_heads, GDN_HEAD_DIM) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{batch}, {num_v_heads}, 128]")
+    if conv_layout == nat.RIA_CONV_RING:
+        if conv_weight is None or conv_ring is None:
+            raise ValueError("RIA_CONV_RING needs conv_weight and conv_ring")
+        _check_conv_tensors(conv_weight, conv_ring, cdim, batch if seq_slot is None else 0)
+    elif conv_layout == nat.RIA_CONV_WINDOW:
+        if conv_weight is None or conv_window_in is None or conv_window_out is None:
+            raise ValueError("RIA_CONV_WINDOW needs conv_weight, conv_window_in and conv_window_out")
+        _check_conv_window(conv_weight, conv_window_in, conv_window_out, cdim, batch if seq_slot is None else 0)
+    elif conv_layout != nat.RIA_CONV_NONE:
+        raise ValueError(f"unknown conv_layout {conv_layout}")
+    if gate_mode == nat.RIA_GATE_RAW:
+        for name, t in (("A_log", A_log), ("dt_bias", dt_bias)):
+            if t is None or t.dtype != torch.float32 or t.numel() != num_v_heads or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous fp32 tensor of {num_v_heads} values")
+    if seq_slot is not None:
+        _rows_i32("seq_slot", seq_slot, batch, dev)
+    pos_t, pos_s = _rows_i32("conv_pos", conv_pos, batch, dev)
+    z_stride = 0
+    if (z is None) != (norm_weight is None):
+        raise ValueError("the gated norm needs both z and norm_weight")
+    if z is not None:
+        _require_gpu("z", z, dev)
+        z_stride = _row_stride("z", z, batch, num_v_heads * GDN_HEAD_DIM)
+    w_ptr = _norm_weight("norm_weight", norm_weight, GDN_HEAD_DIM, dev)
+
+    def addr(t):
+        return None if t is None else t.data_ptr()
+
+    d = nat.GdnDecodeDesc(
+        batch=batch, num_k_heads=num_k_heads, num_v_heads=num_v_heads, x=addr(x), x_dtype=dtype_code(x),
+        x_row_stride=x_stride, conv_layout=int(conv_layout),
+        conv_weight=addr(conv_weight) if conv_layout != nat.RIA_CONV_NONE else None,
+        conv_ring=addr(conv_ring) if conv_layout == nat.RIA_CONV_RING else None, conv_pos=addr(pos_t),
+        conv_pos_scalar=pos_s,
+        conv_window_in=addr(conv_window_in) if conv_layout == nat.RIA_CONV_WINDOW else None,
+        conv_window_out=addr(conv_window_out) if conv_layout == nat.RIA_CONV_WINDOW else None,
+        state_in=addr(state_in), state_out=addr(state_out), seq_slot=addr(seq_slot), gate_a=addr(gate_a),
+        gate_b=addr(gate_b), gate_row_stride=g_stride, gate_mode=int(gate_mode),
+        A_log=addr(A_log) if gate_mode == nat.RIA_GATE_RAW else None,
+        dt_bias=addr(dt_bias) if gate_mode == nat.RIA_GATE_RAW else None, qk_mode=int(qk_mode), out=addr(out),
+        out_dtype=dtype_code(out), z=addr(z), z_dtype=dtype_code(z) if z is not None else 0, z_row_stride=z_stride,
+        norm_weight=w_ptr.value if w_ptr is not None else None)
+    rc = nat.load().ria_gdn_decode_ex(ctypes.byref(d), _stream(dev))
+    nat.check(rc, "ria_gdn_decode_ex")
+    return out
+
+
+def _check_conv_window(conv_weight: torch.Tensor, window_in: torch.Tensor, window_out: torch.Tensor, channels: int,
+                       min_pool: int) -> None:
+    if conv_weight.dtype != torch.bfloat16 or conv_weight.numel() != channels * CONV_TAPS \
+            or not conv_weight.is_contiguous():
+        raise ValueError(f"conv_weight must be contiguous bf16 [{channels}, 1, 4]")
+    for name, w in (("conv_window_in", window_in), ("conv_window_out", window_out)):
+        if w.dtype != torch.bfloat16 or w.dim() != 3 or tuple(w.shape[1:]) != (channels, CONV_TAPS) \
+                or not w.is_contiguous():
+            raise ValueError(f"{name} must be contiguous bf16 [pool, {channels}, 4], got {tuple(w.shape)}")
+        if w.shape[0] < min_pool:
+            raise ValueError(f"{name} pool smaller than batch")
+
+
+def conv1d_window_step(x: torch.Tensor, conv_weight: torch.Tensor, window_in: torch.Tensor,
+                       window_out: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """Depthwise causal conv step + SiLU on the reference's window [B, C, 4] (ria_conv1d_window_step)."""
+    batch, channels = int(x.shape[0]), int(x.shape[-1])
+    dev = x.device
+    for name, t in (("x", x), ("conv_weight", conv_weight), ("window_in", window_in), ("window_out", window_out),
+                    ("out", out)):
+        _require_gpu(name, t, dev)
+    stride = _row_stride("x", x, batch, channels)
+    _check_conv_window(conv_weight, window_in, window_out, channels, batch)
+    if tuple(out.shape) != (batch, channels) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{batch}, {channels}]")
+    rc = nat.load().ria_conv1d_window_step(batch, channels, _ptr(x), dtype_code(x), stride, _ptr(conv_weight),
+                                           _ptr(window_in), _ptr(window_out), _ptr(out), dtype_code(out),
+                                           _stream(dev))
+    nat.check(rc, "ria_conv1d_window_step")
+    return out
+
+
 def _check_conv_tensors(conv_weight: torch.Tensor, conv_ring: torch.Tensor, channels: int, min_pool: int) -> None:
     if conv_weight.dtype != torch.bfloat16 or conv_weight.numel() != channels * CONV_TAPS \
             or not conv_weight.is_contiguous():
@@ -376,7 +514,8 @@ def kv_append(
     rc = nat.load().ria_kv_append(batch, num_kv_heads, _ptr(k), dtype_code(k), ks, _ptr(v), dtype_code(v), vs,
                                   _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table), pts,
                                   _ptr(seq_slot),
-                                  _ptr(pos_t), pos_s, _ptr(slot_t), slot_s, _ptr(inv_freq), 2 * int(inv_freq.numel()),
+                                  _ptr(pos_t), pos_s, _ptr(slot_t), slot_s, _ptr(inv_freq),
+                                  0 if inv_freq is None else 2 * int(inv_freq.numel()),
                                   _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev), _stream(dev))
     nat.check(rc, "ria_kv_append")
 

@@ -1,17 +1,17 @@
 """Persistent attention state for Qwen3.6 decoding, on gfx950 HIP kernels.
 
 Drop-in for v2/src/router_ia/qwen36_attention_cache.py: the same module-level
-names, signatures, errors and snapshot keys, with the per-token arithmetic
-moved into the HIP library (include/ria_hybrid_attn.h):
+names, signatures, errors, snapshot keys and state dicts, with the per-token
+arithmetic moved into the HIP library (include/ria_hybrid_attn.h):
 
   reference (file:line)                      here
   ----------------------------------------   ----------------------------------
   AttentionState + registry  :27-134         same dataclass / functions
   _rope / _apply_rope        :137-162        ria_rope_table / ria_rope_apply
   _l2norm                    :169-173        ria_l2norm
-  _causal_conv1d_step        :176-221        ria_conv1d_step (4-slot conv ring)
+  _causal_conv1d_step        :176-221        ria_conv1d_window_step
   _linear_stateful           :224-282        ria_rmsnorm (input norm) +
-                                             ria_gdn_decode (conv + gating +
+                                             ria_gdn_decode_ex (conv + gating +
                                              l2norm + recurrence + read-out +
                                              gated RMSNorm)
   _full_stateful             :285-324        ria_rmsnorm (input norm) +
@@ -21,28 +21,42 @@ moved into the HIP library (include/ria_hybrid_attn.h):
   _append_full_kv            :334-373        limits on the host, then
                                              ria_kv_append into 16-bit pages
   step_attention / stats     :376-404        same
+  rmsnorm / gated_rmsnorm    qwen36_op_probe.py:55-67,
+                             qwen36_gated_norm_probe.py:19-36
+                                             ria_rmsnorm / ria_gated_rmsnorm
 
-Differences a caller can observe, all inside the stated tolerances:
-  * GPU KV is stored in 16-bit 16-token pages (fp16 on the step_attention
-    path, whose projections are fp16 like the reference's GPU path; bf16 for
-    bf16 tokens); ``full_keys[layer]`` / ``full_values[layer]`` hold
-    ``PagedKVView`` objects with the reference's shape [1, Hkv, T, 256] and
-    byte accounting of what is really stored.  ``.materialize()`` gathers
-    the contiguous tensor.
-  * The conv state is a 4-slot ring (token n in slot n mod 4) exposed with
-    the reference's shape [1, conv_dim, 4]; ``conv_state_window`` returns the
-    reference's shifting-window order.
-  * Tensors on the CPU raise: the arithmetic exists only as HIP kernels.
-    ``_append_full_kv`` on CPU tensors keeps the reference's contiguous
-    storage, because the reference's limit semantics are tested with CPU
-    tensors and that path only stores.
+The state dicts hold what the reference holds:
+  * ``linear_states[layer]``: a new fp32 [1, 32, 128, 128] tensor per step
+    (the kernel reads the dict's tensor and writes the next one).
+  * ``linear_conv_states[layer]``: the conv-weight-dtype (bf16) window
+    [1, conv_dim, 4] of the last four inputs, oldest first, a new tensor per
+    step.
+  * ``full_keys[layer]`` / ``full_values[layer]``: [1, Hkv, T, 256] tensors in
+    the dtype of the appended tokens (fp32 on the step path), read out of
+    the layer's 16-bit KV pages when used (``PagedKVTensor``).  Their
+    ``numel() * element_size()`` is what the reference's tensors would
+    occupy, so the byte budget and ``snapshot()`` count exactly as in the
+    reference; ``paged_kv_bytes()`` gives the bytes the pages really use.
+A tensor a caller stores into one of the dicts is what the next step reads.
+
+Module attributes the reference's probes replace are looked up at call time:
+``rmsnorm``, ``gated_rmsnorm``, ``_l2norm``, ``_apply_rope``,
+``_causal_conv1d_step``, ``_append_full_kv`` and ``_projection``.  While all of
+them are the originals, a layer runs its fused launches; once one is
+replaced, that layer runs the reference's sequence of calls through the
+module attributes, with the HIP kernels for what remains.
+
+Differences a caller can observe, all inside the stated tolerances: keys and
+values are stored as 16-bit values (fp16 for the fp32 and fp16 tokens of the
+step path, bf16 for bf16 tokens), so a key read back differs from the fp32
+token by at most one fp16 rounding.  Tensors on the CPU raise: the
+arithmetic exists only as HIP kernels.  ``_append_full_kv`` on CPU tensors
+keeps the reference's contiguous storage, because the reference's limit
+semantics are tested with CPU tensors and that path only stores.
 
 Projections and weight loading are outside the accelerated path and use
 torch (``weights``), keeping the reference's dtype order (fp16 projections on
-the GPU).  The norms run in the HIP library: the layer-input RMSNorm as its
-own launch, q_norm / k_norm and the DeltaNet gated RMSNorm fused into the
-attention launches.  ``rmsnorm`` / ``gated_rmsnorm`` remain module
-attributes (the torch forms, usable on any device) as in the reference.
+the GPU).
 """
 
 from __future__ import annotations
@@ -53,14 +67,13 @@ from typing import Any
 
 import torch
 import torch.nn.functional as F
+from torch.utils._pytree import tree_map
 
 from . import _native as nat
 from . import kernels as K
 from . import qwen36_40layer_loop as base
 from . import weights as cached
 from .batched_state import rope_inv_freq
-from .device_utils import is_cuda
-from .norms import gated_rmsnorm, rmsnorm
 
 ROPE_THETA = 10_000_000.0
 ROPE_DIM = int(base.FULL_HEAD_DIM * 0.25)
@@ -71,58 +84,77 @@ LINEAR_CONV_STATE = LINEAR_CONV_KERNEL
 LINEAR_CONV_DIM = base.LINEAR_KEY_DIM * 2 + base.LINEAR_VALUE_DIM
 
 _PAGE = K.PAGE_TOKENS
+NORM_EPS = 1e-6
 
 
-class PagedKVView:
-    """One layer's keys or values in the paged 16-bit cache, seen as [1, Hkv, T, 256]."""
+def _on_gpu(device: str | torch.device) -> bool:
+    """True for a ROCm GPU device (PyTorch names it ``cuda``)."""
+    return torch.device(device).type == "cuda"
 
-    def __init__(self, store: "_LayerKV", which: str):
-        self._store = store
-        self._which = which
 
-    @property
-    def shape(self) -> torch.Size:
-        return torch.Size((1, self._store.num_kv_heads, self._store.length, K.ATTN_HEAD_DIM))
+class PagedKVTensor(torch.Tensor):
+    """Keys or values [1, Hkv, T, 256] of one layer, read out of its KV pages when used.
 
-    @property
-    def dtype(self) -> torch.dtype:
-        return self._store.dtype
+    Shape, dtype, device and ``requires_grad`` (False: the cache is detached,
+    :365-372) are known without touching the pages; any other use (``detach``,
+    ``float``, indexing, arithmetic, comparisons) gathers the first T tokens
+    in logical order (ria_kv_gather) and converts them to the tensor's dtype.
+    Pages only grow, so a tensor taken before later appends keeps reading
+    the T tokens it was created with.
+    """
 
-    @property
-    def device(self) -> torch.device:
-        return self._store.device
+    @staticmethod
+    def __new__(cls, store: "_LayerKV", which: str, length: int):
+        shape = (1, store.num_kv_heads, int(length), K.ATTN_HEAD_DIM)
+        t = torch.Tensor._make_wrapper_subclass(cls, shape, dtype=store.dtype, device=store.device,
+                                                requires_grad=False)
+        t._store = store
+        t._which = which
+        t._length = int(length)
+        return t
 
-    def numel(self) -> int:
-        return self._store.num_kv_heads * self._store.length * K.ATTN_HEAD_DIM
+    def __init__(self, store: "_LayerKV", which: str, length: int):
+        super().__init__()
 
-    def element_size(self) -> int:
-        return 2
+    __torch_function__ = torch._C._disabled_torch_function_impl
 
     def materialize(self) -> torch.Tensor:
-        k, v = self._store.gather()
-        return k if self._which == "k" else v
+        """The contiguous [1, Hkv, T, 256] tensor, in this tensor's dtype."""
+        k, v = self._store.gather(self._length)
+        return (k if self._which == "k" else v).to(self.dtype)
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        def unwrap(x):
+            return x.materialize() if isinstance(x, PagedKVTensor) else x
+
+        return func(*tree_map(unwrap, args), **tree_map(unwrap, kwargs or {}))
 
     def __repr__(self) -> str:
-        return f"PagedKVView({self._which}, shape={tuple(self.shape)}, dtype={self.dtype}, device={self.device})"
+        return f"PagedKVTensor({self.materialize()!r})"
 
 
 class _LayerKV:
     """Paged KV of one full-attention layer of one sequence (identity page table, grown by doubling).
 
-    Elements are fp16 when the activations come from fp16 projections (the
-    GPU path) and bf16 for bf16 activations, so appended values stay exact.
+    ``dtype`` is the dtype of the appended tokens, in which the dict tensors
+    report and materialise; the pages hold bf16 for bf16 tokens and fp16
+    otherwise (fp16 keeps the fp16 projection outputs of the GPU path exact).
     """
 
     def __init__(self, num_kv_heads: int, device: torch.device, dtype: torch.dtype, pages: int = 16):
         self.num_kv_heads = num_kv_heads
-        self.device = device
+        self.device = torch.device(device)
         self.dtype = dtype
+        self.page_dtype = torch.bfloat16 if dtype == torch.bfloat16 else torch.float16
         self.length = 0
+        self.views: tuple[PagedKVTensor, PagedKVTensor] | None = None
         self._alloc(pages)
 
     def _alloc(self, pages: int) -> None:
-        k = torch.zeros((pages, self.num_kv_heads, *K.K_TILE_SHAPE), dtype=self.dtype, device=self.device)
-        v = torch.zeros((pages, self.num_kv_heads, K.ATTN_HEAD_DIM, _PAGE), dtype=self.dtype, device=self.device)
+        k = torch.zeros((pages, self.num_kv_heads, *K.K_TILE_SHAPE), dtype=self.page_dtype, device=self.device)
+        v = torch.zeros((pages, self.num_kv_heads, K.ATTN_HEAD_DIM, _PAGE), dtype=self.page_dtype,
+                        device=self.device)
         if hasattr(self, "k"):
             used = (self.length + _PAGE - 1) // _PAGE
             k[:used].copy_(self.k[:used])
@@ -138,14 +170,30 @@ class _LayerKV:
                 pages *= 2
             self._alloc(pages)
 
-    def gather(self) -> tuple[torch.Tensor, torch.Tensor]:
-        return K.kv_gather(self.k, self.v, self.page_table, batch=1, start=0, count=self.length)
+    def gather(self, count: int) -> tuple[torch.Tensor, torch.Tensor]:
+        return K.kv_gather(self.k, self.v, self.page_table, batch=1, start=0, count=int(count))
+
+    def publish(self) -> tuple[PagedKVTensor, PagedKVTensor]:
+        """The dict tensors of the current length (kept to recognise them on the next step)."""
+        self.views = (PagedKVTensor(self, "k", self.length), PagedKVTensor(self, "v", self.length))
+        return self.views
+
+    def import_tokens(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Store [1, Hkv, T, 256] keys (already rotated) and values as tokens 0..T-1."""
+        count = int(k.shape[-2])
+        self.reserve(count + 1)
+        if count:
+            k_rows = k.reshape(self.num_kv_heads, count, K.ATTN_HEAD_DIM).transpose(0, 1).contiguous()
+            v_rows = v.reshape(self.num_kv_heads, count, K.ATTN_HEAD_DIM).transpose(0, 1).contiguous()
+            K.kv_append_seq(k_rows, v_rows.to(k_rows.dtype), self.k, self.v, self.page_table[0], start=0,
+                            inv_freq=None)
+        self.length = count
 
 
 @dataclass
 class AttentionState:
-    full_keys: dict[int, Any] = field(default_factory=dict)
-    full_values: dict[int, Any] = field(default_factory=dict)
+    full_keys: dict[int, torch.Tensor] = field(default_factory=dict)
+    full_values: dict[int, torch.Tensor] = field(default_factory=dict)
     linear_states: dict[int, torch.Tensor] = field(default_factory=dict)
     linear_conv_states: dict[int, torch.Tensor] = field(default_factory=dict)
     # Zero disables a limit.  There is no sliding window: limits fail before a
@@ -154,8 +202,7 @@ class AttentionState:
     max_full_kv_bytes: int = 0
     tokens_seen: int = 0
     device: str | None = None
-    # Per-layer conv step counters (ring slot of the next input) and GPU KV stores.
-    conv_steps: dict[int, int] = field(default_factory=dict, repr=False)
+    # The KV pages behind full_keys / full_values, per layer.
     kv_stores: dict[int, _LayerKV] = field(default_factory=dict, repr=False)
 
     def reset(self) -> None:
@@ -163,7 +210,6 @@ class AttentionState:
         self.full_values.clear()
         self.linear_states.clear()
         self.linear_conv_states.clear()
-        self.conv_steps.clear()
         self.kv_stores.clear()
         self.tokens_seen = 0
 
@@ -205,6 +251,10 @@ class AttentionState:
             "linear_conv_bytes": conv_bytes,
             "bytes": full_bytes + linear_bytes + conv_bytes,
         }
+
+    def paged_kv_bytes(self) -> int:
+        """Bytes the resident keys and values occupy in their 16-bit pages (2 bytes per element)."""
+        return sum(2 * 2 * s.num_kv_heads * s.length * K.ATTN_HEAD_DIM for s in self.kv_stores.values())
 
 
 _STATES: dict[Path, AttentionState] = {}
@@ -267,6 +317,50 @@ def _require_gpu_tensor(name: str, t: torch.Tensor) -> None:
         raise RuntimeError(f"{name}: the attention arithmetic runs only on a ROCm GPU; got a tensor on {t.device}")
 
 
+def _f32_weight(w: torch.Tensor) -> torch.Tensor:
+    """A norm weight as the kernels take it: contiguous, 16-byte aligned fp32."""
+    if w.dtype == torch.float32 and w.is_contiguous() and w.data_ptr() % 16 == 0:
+        return w
+    return w.float().contiguous().clone()
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """Qwen RMSNorm over the last dim: fp32 normalisation, (1 + w) affine, cast back to x's dtype (ria_rmsnorm).
+
+    The reference's ``rmsnorm`` (qwen36_op_probe.py:55-67), used for the layer
+    input (:227, :291) and the q / k norms (:304-305).
+    """
+    _require_gpu_tensor("rmsnorm", x)
+    dim = int(x.shape[-1])
+    rows = x.reshape(-1, dim)
+    if rows.shape[0] > 1 and rows.stride(0) != dim or dim > 1 and rows.stride(1) != 1:
+        rows = rows.contiguous()
+    return K.rmsnorm(rows, _f32_weight(weight), eps=NORM_EPS).reshape(x.shape)
+
+
+def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor,
+                  weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Qwen gated RMSNorm (qwen36_gated_norm_probe.py:19-36): returns (out, weighted, gate).
+
+    ``out`` = (w * RMSNorm(x).to(x.dtype) * SiLU(z)).to(x.dtype) comes from
+    ria_gated_rmsnorm; ``weighted`` and ``gate``, the intermediates the
+    reference also returns, are formed with torch ops on x's device.
+    """
+    if x.shape != z.shape:
+        raise ValueError(f"x/z shape mismatch: {tuple(x.shape)} vs {tuple(z.shape)}")
+    if x.ndim != 3 or x.shape[1:] != (base.LINEAR_NUM_V_HEADS, 128):
+        raise ValueError(f"Expected (batch, {base.LINEAR_NUM_V_HEADS}, 128), got {tuple(x.shape)}")
+    if weight.numel() != 128:
+        raise ValueError(f"Expected norm weight with 128 values, got {weight.numel()}")
+    _require_gpu_tensor("gated_rmsnorm", x)
+    out = K.gated_rmsnorm(x.contiguous(), z.contiguous(), _f32_weight(weight), eps=NORM_EPS)
+    x32 = x.float()
+    normalized = (x32 * torch.rsqrt(x32.pow(2).mean(dim=-1, keepdim=True) + NORM_EPS)).to(x.dtype)
+    weighted = weight.reshape(1, 1, 128) * normalized
+    gate = F.silu(z.float())
+    return out, weighted, gate
+
+
 def _rope(position: int, device: torch.device, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
     if ROPE_DIM <= 0 or ROPE_DIM % 2:
         raise ValueError(f"Invalid rotary dimension: {ROPE_DIM}")
@@ -300,24 +394,15 @@ def _l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     return K.l2norm(x, eps)
 
 
-def _conv_ring(state: AttentionState, layer: int, device: torch.device) -> torch.Tensor:
-    """The layer's conv ring [1, 4, conv_dim] (created zeroed, like the reference's zero state)."""
-    view = state.linear_conv_states.get(int(layer))
+def _conv_window(state: AttentionState, layer: int, device: torch.device) -> torch.Tensor:
+    """The layer's conv window [1, conv_dim, 4] as the kernels read it (zeros when missing, :202-205)."""
+    window = state.linear_conv_states.get(int(layer))
     expected = (1, LINEAR_CONV_DIM, LINEAR_CONV_STATE)
-    if view is None or view.device != device or tuple(view.shape) != expected or view.dtype != torch.bfloat16:
-        ring = torch.zeros((1, LINEAR_CONV_STATE, LINEAR_CONV_DIM), dtype=torch.bfloat16, device=device)
-        state.linear_conv_states[int(layer)] = ring.permute(0, 2, 1)
-        state.conv_steps[int(layer)] = 0
-        return ring
-    return view.permute(0, 2, 1)
-
-
-def conv_state_window(state: AttentionState, layer: int) -> torch.Tensor:
-    """The layer's conv state in the reference's order: the last four inputs, oldest first."""
-    view = state.linear_conv_states[int(layer)]
-    n = state.conv_steps.get(int(layer), 0)
-    slots = [(n - 4 + m) % 4 for m in range(4)]
-    return view[:, :, slots]
+    if window is None or window.device != device or tuple(window.shape) != expected:
+        return torch.zeros(expected, dtype=torch.bfloat16, device=device)
+    if window.dtype != torch.bfloat16 or not window.is_contiguous() or window.data_ptr() % 8:
+        window = window.to(torch.bfloat16).contiguous().clone()
+    return window
 
 
 def _causal_conv1d_step(
@@ -326,7 +411,7 @@ def _causal_conv1d_step(
     mixed_qkv: torch.Tensor,
     conv_weight: torch.Tensor,
 ) -> torch.Tensor:
-    """One-token causal depthwise conv (kernel 4) + SiLU with the rolling conv state."""
+    """One-token causal depthwise conv (kernel 4) + SiLU; the layer's window moves on by one input."""
     if mixed_qkv.ndim != 2 or mixed_qkv.shape != (1, LINEAR_CONV_DIM):
         raise ValueError(f"Unexpected mixed_qkv shape: {tuple(mixed_qkv.shape)}")
     if conv_weight.ndim != 3:
@@ -340,41 +425,46 @@ def _causal_conv1d_step(
     _require_gpu_tensor("_causal_conv1d_step", mixed_qkv)
     if conv_weight.dtype != torch.bfloat16:
         raise TypeError("_causal_conv1d_step: the HIP conv computes in bf16 and needs a bf16 conv weight")
-    ring = _conv_ring(state, layer, mixed_qkv.device)
-    out = torch.empty_like(mixed_qkv)
-    K.conv1d_step(mixed_qkv.contiguous(), conv_weight.contiguous(), ring, out,
-                  conv_pos=state.conv_steps[int(layer)])
-    state.conv_steps[int(layer)] += 1
+    window_in = _conv_window(state, layer, mixed_qkv.device)
+    window_out = torch.empty_like(window_in)
+    out = torch.empty_like(mixed_qkv, memory_format=torch.contiguous_format)
+    K.conv1d_window_step(mixed_qkv.contiguous(), conv_weight.contiguous(), window_in, window_out, out)
+    state.linear_conv_states[int(layer)] = window_out
     return out
 
 
-_ORIGINAL_CONV_STEP = _causal_conv1d_step
-
-
 def _linear_state(state: AttentionState, layer: int, device: torch.device) -> torch.Tensor:
+    """The layer's recurrent state as the kernel reads it (zeros when missing, :256-259)."""
     expected = (1, base.LINEAR_NUM_V_HEADS, 128, 128)
     s = state.linear_states.get(int(layer))
-    if s is None or s.device != device or tuple(s.shape) != expected or s.dtype != torch.float32 \
-            or not s.is_contiguous():
-        s = torch.zeros(expected, device=device, dtype=torch.float32)
-        state.linear_states[int(layer)] = s
+    if s is None or s.device != device or tuple(s.shape) != expected:
+        return torch.zeros(expected, device=device, dtype=torch.float32)
+    if s.dtype != torch.float32 or not s.is_contiguous() or s.data_ptr() % 16:
+        s = s.float().contiguous().clone()
     return s
 
 
 def _input_norm(x0: torch.Tensor, weight: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
-    """rmsnorm(x0, input_layernorm) (:227, :291) cast to the layer's compute dtype, in one launch."""
+    """rmsnorm(x0, input_layernorm).to(out_dtype) (:227-230, :291-294).
+
+    With the module's own ``rmsnorm`` this is one launch that writes the
+    compute dtype directly; a replaced ``rmsnorm`` is called as the reference
+    calls it.
+    """
+    norm = globals()["rmsnorm"]
+    if norm is not _HIP_RMSNORM:
+        return norm(x0, weight).to(dtype=out_dtype)
     x = x0.reshape(1, base.HIDDEN).contiguous()
     out = torch.empty((1, base.HIDDEN), device=x.device, dtype=out_dtype)
-    return K.rmsnorm(x, weight.float().contiguous(), out=out)
+    return K.rmsnorm(x, _f32_weight(weight), out=out, eps=NORM_EPS)
 
 
 def _linear_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> torch.Tensor:
     state = active(root, device)
     prefix = base.layer_prefix(layer)
-    if not is_cuda(device):
+    if not _on_gpu(device):
         raise RuntimeError("_linear_stateful: the attention arithmetic runs only on a ROCm GPU device")
     input_norm = base.load_layer_weight(root, layer, "input_layernorm.weight", device)
-    # rmsnorm(x0) in fp32, then .to(bf16) (:227-229), in one launch
     h_compute = _input_norm(x0, input_norm, torch.bfloat16)
 
     qkv_w = _projection(root, prefix + "linear_attn.in_proj_qkv", device)
@@ -391,46 +481,89 @@ def _linear_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> t
 
     z_w = _projection(root, prefix + "linear_attn.in_proj_z", device)
     z = F.linear(h_compute.to(dtype=z_w.dtype), z_w).reshape(1, base.LINEAR_NUM_V_HEADS, 128)
-    norm_w = base.load_layer_weight(root, layer, "linear_attn.norm.weight", device).float().contiguous()
+    norm_w = base.load_layer_weight(root, layer, "linear_attn.norm.weight", device)
     out_w = _projection(root, prefix + "linear_attn.out_proj", device)
 
     dev = x0.device
-    linear_state = _linear_state(state, layer, dev)
-    # the read-out leaves the kernel through the gated RMSNorm (:268-271), cast
-    # to the out_proj dtype as the reference casts `gated` (:273-275)
-    gated = torch.empty((1, base.LINEAR_NUM_V_HEADS, 128), device=dev, dtype=out_w.dtype)
+    s_in = _linear_state(state, layer, dev)
+    s_out = torch.empty_like(s_in)  # the reference stores a new state tensor every step (:261-265)
     conv_step = globals()["_causal_conv1d_step"]
-    if conv_step is _ORIGINAL_CONV_STEP:
+    l2norm = globals()["_l2norm"]
+    fused_norm = globals()["gated_rmsnorm"] is _HIP_GATED_RMSNORM
+    # the read-out leaves the kernel through the gated RMSNorm (:268-271), cast
+    # to the out_proj dtype as the reference casts `gated` (:273-275); with a
+    # replaced gated_rmsnorm the kernel returns the fp32 read-out instead
+    attn = torch.empty((1, base.LINEAR_NUM_V_HEADS, 128), device=dev,
+                       dtype=out_w.dtype if fused_norm else torch.float32)
+    common = dict(num_k_heads=base.LINEAR_NUM_K_HEADS, num_v_heads=base.LINEAR_NUM_V_HEADS,
+                  gate_mode=nat.RIA_GATE_RAW, A_log=a_log.contiguous(), dt_bias=dt_bias.contiguous(),
+                  z=z if fused_norm else None, norm_weight=_f32_weight(norm_w) if fused_norm else None)
+    if conv_step is _HIP_CONV_STEP and l2norm is _HIP_L2NORM:
         if conv_w.dtype != torch.bfloat16:
             raise TypeError("_linear_stateful: the HIP conv computes in bf16 and needs a bf16 conv weight")
-        ring = _conv_ring(state, layer, dev)
-        K.gdn_decode(mixed, linear_state, a_raw.contiguous(), b_raw.contiguous(), gated,
-                     num_k_heads=base.LINEAR_NUM_K_HEADS, num_v_heads=base.LINEAR_NUM_V_HEADS, fuse_conv=True,
-                     conv_weight=conv_w.contiguous(), conv_ring=ring, conv_pos=state.conv_steps[int(layer)],
-                     gate_mode=nat.RIA_GATE_RAW, A_log=a_log.contiguous(), dt_bias=dt_bias.contiguous(),
-                     z=z, norm_weight=norm_w)
-        state.conv_steps[int(layer)] += 1
+        window_in = _conv_window(state, layer, dev)
+        window_out = torch.empty_like(window_in)
+        K.gdn_decode_ex(mixed, s_in, s_out, a_raw.contiguous(), b_raw.contiguous(), attn,
+                        conv_layout=nat.RIA_CONV_WINDOW, conv_weight=conv_w.contiguous(), conv_window_in=window_in,
+                        conv_window_out=window_out, **common)
+        state.linear_conv_states[int(layer)] = window_out
     else:
-        # A replaced conv step (probes swap this module attribute): run it, then
-        # the recurrence on its output.
+        # A replaced seam: the reference's calls in its order (:236-254), each
+        # through the module attribute, then the recurrence on their results.
         mixed = conv_step(state, layer, mixed, conv_w)
-        K.gdn_decode(mixed.contiguous(), linear_state, a_raw.contiguous(), b_raw.contiguous(), gated,
-                     num_k_heads=base.LINEAR_NUM_K_HEADS, num_v_heads=base.LINEAR_NUM_V_HEADS, fuse_conv=False,
-                     gate_mode=nat.RIA_GATE_RAW, A_log=a_log.contiguous(), dt_bias=dt_bias.contiguous(),
-                     z=z, norm_weight=norm_w)
+        if l2norm is _HIP_L2NORM:
+            K.gdn_decode_ex(mixed.contiguous(), s_in, s_out, a_raw.contiguous(), b_raw.contiguous(), attn,
+                            **common)
+        else:
+            q, k, v = torch.split(mixed, [base.LINEAR_KEY_DIM, base.LINEAR_KEY_DIM, base.LINEAR_VALUE_DIM], dim=-1)
+            q = q.reshape(1, base.LINEAR_NUM_K_HEADS, 128).repeat_interleave(2, dim=1)
+            k = k.reshape(1, base.LINEAR_NUM_K_HEADS, 128).repeat_interleave(2, dim=1)
+            q = l2norm(q)
+            q = q * (128 ** -0.5)
+            k = l2norm(k)
+            qkv = torch.cat((q.reshape(1, -1).float(), k.reshape(1, -1).float(), v.reshape(1, -1).float()), dim=-1)
+            K.gdn_decode_ex(qkv, s_in, s_out, a_raw.contiguous(), b_raw.contiguous(), attn,
+                            qk_mode=nat.RIA_QK_NORMALIZED, **common)
+    state.linear_states[int(layer)] = s_out
 
-    gated_compute = gated.reshape(1, base.LINEAR_VALUE_DIM)
+    if fused_norm:
+        gated_compute = attn.reshape(1, base.LINEAR_VALUE_DIM)
+    else:
+        gated, _, _ = globals()["gated_rmsnorm"](attn, z, norm_w)
+        gated_compute = gated.reshape(1, base.LINEAR_VALUE_DIM).to(dtype=out_w.dtype)
     attn_projected = F.linear(gated_compute, out_w).float()
     return x0.reshape(1, base.HIDDEN).float() + attn_projected
 
 
 def _full_store(state: AttentionState, layer: int, device: torch.device, dtype: torch.dtype) -> _LayerKV:
-    store = state.kv_stores.get(int(layer))
-    if store is None or store.device != device:
+    """The pages behind full_keys[layer] / full_values[layer].
+
+    The dict tensors are the state: if they are not the ones the pages last
+    published (a caller stored other tensors, or removed them), the pages are
+    rebuilt from what the dicts hold.
+    """
+    key = int(layer)
+    store = state.kv_stores.get(key)
+    full_k, full_v = state.full_keys.get(key), state.full_values.get(key)
+    if store is not None and store.device == device and store.views is not None \
+            and full_k is store.views[0] and full_v is store.views[1]:
+        return store
+    if (full_k is None) != (full_v is None):
+        raise RuntimeError(f"full_keys and full_values disagree for layer {key}")
+    if full_k is not None and full_k.device == device:
+        if full_k.shape != full_v.shape or full_k.dim() != 4 or full_k.shape[0] != 1 \
+                or full_k.shape[1] != base.FULL_NUM_KV_HEADS or full_k.shape[-1] != K.ATTN_HEAD_DIM:
+            raise RuntimeError(f"full-attention cache of layer {key} has shape {tuple(full_k.shape)}, "
+                               f"expected [1, {base.FULL_NUM_KV_HEADS}, T, {K.ATTN_HEAD_DIM}]")
+        store = _LayerKV(base.FULL_NUM_KV_HEADS, device, full_k.dtype)
+        store.import_tokens(full_k.detach(), full_v.detach())
+    else:
         store = _LayerKV(base.FULL_NUM_KV_HEADS, device, dtype)
-        state.kv_stores[int(layer)] = store
-        state.full_keys[int(layer)] = PagedKVView(store, "k")
-        state.full_values[int(layer)] = PagedKVView(store, "v")
+    state.kv_stores[key] = store
+    state.full_keys[key], state.full_values[key] = store.publish()
+    if store.length == 0:
+        # an empty cache is no entry at all in the reference (:365-367)
+        del state.full_keys[key], state.full_values[key]
     return store
 
 
@@ -459,27 +592,25 @@ def _check_full_kv_limits(state: AttentionState, layer: int, append_bytes: int) 
 
 
 def _paged_append(state: AttentionState, layer: int, k_token: torch.Tensor, v_token: torch.Tensor,
-                  position: int | None, kv_dtype: torch.dtype,
+                  position: int | None, dtype: torch.dtype,
                   k_norm_weight: torch.Tensor | None = None) -> _LayerKV:
     """Append [1, Hkv, 1, 256] k/v into the layer's pages (k_norm, then RoPE on k, when position is given)."""
-    store = _full_store(state, layer, k_token.device, kv_dtype)
+    store = _full_store(state, layer, k_token.device, dtype)
     store.reserve(store.length + 1)
     k2 = k_token.reshape(1, base.FULL_NUM_KV_HEADS, K.ATTN_HEAD_DIM).contiguous()
     v2 = v_token.reshape(1, base.FULL_NUM_KV_HEADS, K.ATTN_HEAD_DIM).contiguous()
-    if position is None:
-        inv = torch.empty(0, device=k_token.device)  # rope_dim 0: k is already rotated
-    else:
-        inv = _inv_freq(k_token.device)
+    inv = None if position is None else _inv_freq(k_token.device)  # no RoPE: k is already rotated
     K.kv_append(k2, v2, store.k, store.v, store.page_table, positions=int(position or 0), slots=store.length,
                 inv_freq=inv, k_norm_weight=k_norm_weight)
     store.length += 1
+    state.full_keys[int(layer)], state.full_values[int(layer)] = store.publish()
     return store
 
 
 def _full_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> torch.Tensor:
     state = active(root, device)
     prefix = base.layer_prefix(layer)
-    if not is_cuda(device):
+    if not _on_gpu(device):
         raise RuntimeError("_full_stateful: the attention arithmetic runs only on a ROCm GPU device")
     # RoPE uses the absolute position even if a cache policy changes how many
     # earlier entries stay resident.
@@ -494,17 +625,31 @@ def _full_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> tor
     q, gate = torch.chunk(q_gate, 2, dim=-1)
     k = F.linear(h_compute.to(dtype=k_w.dtype), k_w).reshape(1, base.FULL_NUM_KV_HEADS, base.FULL_HEAD_DIM)
     v = F.linear(h_compute.to(dtype=v_w.dtype), v_w).reshape(1, base.FULL_NUM_KV_HEADS, base.FULL_HEAD_DIM)
-    # q_norm / k_norm (:302-305) run inside the append and attention launches:
-    # RMSNorm in fp32, cast back to the projection dtype, then RoPE
-    q_norm_w = base.load_layer_weight(root, layer, "self_attn.q_norm.weight", device).float().contiguous()
-    k_norm_w = base.load_layer_weight(root, layer, "self_attn.k_norm.weight", device).float().contiguous()
-    q = q.contiguous()
-    k = k.contiguous()
-    v = v.float().contiguous()
+    q_norm_w = base.load_layer_weight(root, layer, "self_attn.q_norm.weight", device)
+    k_norm_w = base.load_layer_weight(root, layer, "self_attn.k_norm.weight", device)
+    gate = gate.contiguous()
+    norm = globals()["rmsnorm"]
+    rope = globals()["_apply_rope"]
+    append = globals()["_append_full_kv"]
 
-    _check_full_kv_limits(state, layer, append_bytes=2 * base.FULL_NUM_KV_HEADS * base.FULL_HEAD_DIM * 2)
-    store = _paged_append(state, layer, k, v, position, torch.float16, k_norm_weight=k_norm_w)
-    attn = _attend(store, q, gate.contiguous(), position, q_norm_weight=q_norm_w)
+    if norm is _HIP_RMSNORM and rope is _HIP_APPLY_ROPE and append is _HIP_APPEND_FULL_KV:
+        # q_norm / k_norm (:302-305) and RoPE run inside the append and
+        # attention launches: RMSNorm in fp32, cast back to the projection
+        # dtype, then RoPE.  The tokens the reference appends are fp32 (:306-307).
+        token_bytes = base.FULL_NUM_KV_HEADS * base.FULL_HEAD_DIM * 4
+        _check_full_kv_limits(state, layer, append_bytes=2 * token_bytes)
+        store = _paged_append(state, layer, k.contiguous(), v.float().contiguous(), position, torch.float32,
+                              k_norm_weight=_f32_weight(k_norm_w))
+        attn = _attend(store, q.contiguous(), gate, position, q_norm_weight=_f32_weight(q_norm_w))
+    else:
+        # A replaced seam: the reference's sequence (:304-308) through the
+        # module attributes, then attention over the cache they produced.
+        q = norm(q, q_norm_w).float().unsqueeze(2)
+        k = norm(k, k_norm_w).float().unsqueeze(2)
+        q, k_token = rope(q, k, position)
+        v_token = v.float().unsqueeze(2)
+        full_k, full_v = append(state, layer, k_token, v_token)
+        attn = _attend_tensors(state, layer, full_k, full_v, q.squeeze(2).contiguous(), gate)
     if attn.shape != (1, base.FULL_NUM_HEADS, base.FULL_HEAD_DIM):
         raise RuntimeError(f"Unexpected full-attention output shape: {tuple(attn.shape)}")
     attn_flat = attn.reshape(1, base.FULL_Q_DIM).to(dtype=compute_dtype)
@@ -513,9 +658,13 @@ def _full_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> tor
     return x0.reshape(1, base.HIDDEN).float() + attn_projected
 
 
-def _attend(store: _LayerKV, q: torch.Tensor, gate: torch.Tensor, position: int,
+def _attend(store: _LayerKV, q: torch.Tensor, gate: torch.Tensor, position: int | None,
             q_norm_weight: torch.Tensor | None = None) -> torch.Tensor:
-    """softmax(RoPE(q_norm(q)) K^T / 16) V * sigmoid(gate) over the store's resident tokens (fp32 out)."""
+    """softmax(q K^T / 16) V * sigmoid(gate) over the store's resident tokens (fp32 out).
+
+    With a position, q is q_norm'd (when a weight is given) and rotated in the
+    launch; without one, q arrives rotated.
+    """
     dev = q.device
     ctx = store.length
     pages_cap = int(store.page_table.shape[1]) * _PAGE
@@ -523,10 +672,22 @@ def _attend(store: _LayerKV, q: torch.Tensor, gate: torch.Tensor, position: int,
     ws = torch.empty(K.attn_decode_workspace_bytes(1, base.FULL_NUM_HEADS, base.FULL_NUM_KV_HEADS, max(ctx, 1),
                                                    split), dtype=torch.uint8, device=dev)
     out = torch.empty((1, base.FULL_NUM_HEADS, base.FULL_HEAD_DIM), dtype=torch.float32, device=dev)
-    K.attn_decode(q, gate, store.k, store.v, store.page_table, out, positions=int(position), ctx_lens=ctx,
-                  max_ctx=min(ctx, pages_cap), inv_freq=_inv_freq(dev), scale=base.FULL_HEAD_DIM ** -0.5,
-                  workspace=ws, split_tokens=split, q_norm_weight=q_norm_weight)
+    K.attn_decode(q, gate, store.k, store.v, store.page_table, out, positions=int(position or 0), ctx_lens=ctx,
+                  max_ctx=min(ctx, pages_cap), inv_freq=None if position is None else _inv_freq(dev),
+                  scale=base.FULL_HEAD_DIM ** -0.5, workspace=ws, split_tokens=split, q_norm_weight=q_norm_weight)
     return out
+
+
+def _attend_tensors(state: AttentionState, layer: int, full_k: torch.Tensor, full_v: torch.Tensor,
+                    q_rot: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    """Attention of the rotated q [1, Hq, 256] over the cache tensors an _append_full_kv returned (:309-317)."""
+    store = state.kv_stores.get(int(layer))
+    if not (store is not None and store.views is not None and full_k is store.views[0] and full_v is store.views[1]):
+        if full_k.device != q_rot.device:
+            raise RuntimeError(f"full-attention cache of layer {layer} is on {full_k.device}, q on {q_rot.device}")
+        store = _LayerKV(base.FULL_NUM_KV_HEADS, q_rot.device, full_k.dtype)
+        store.import_tokens(full_k.detach(), full_v.detach())
+    return _attend(store, q_rot, gate, None)
 
 
 def _full_kv_bytes(state: AttentionState) -> int:
@@ -541,19 +702,16 @@ def _append_full_kv(
     layer: int,
     k_token: torch.Tensor,
     v_token: torch.Tensor,
-) -> tuple[Any, Any]:
+) -> tuple[torch.Tensor, torch.Tensor]:
     """Append one (already rotated) full-attention token after enforcing the hard limits."""
-    if k_token.device.type == "cuda":
-        # Budgets count what the cache stores: 16-bit elements on the GPU.
-        _check_full_kv_limits(state, layer, append_bytes=2 * (k_token.numel() + v_token.numel()))
-        kv_dtype = torch.bfloat16 if k_token.dtype == torch.bfloat16 else torch.float16
-        _paged_append(state, layer, k_token, v_token, None, kv_dtype)
-        return state.full_keys[int(layer)], state.full_values[int(layer)]
     append_bytes = int(k_token.numel() * k_token.element_size()) + int(v_token.numel() * v_token.element_size())
     _check_full_kv_limits(state, layer, append_bytes)
+    if k_token.device.type == "cuda":
+        _paged_append(state, layer, k_token, v_token, None, k_token.dtype)
+        return state.full_keys[int(layer)], state.full_values[int(layer)]
     full_k = state.full_keys.get(int(layer))
     full_v = state.full_values.get(int(layer))
-    if full_k is None or full_v is None or isinstance(full_k, PagedKVView) or full_k.device != k_token.device:
+    if full_k is None or full_v is None or full_k.device != k_token.device:
         full_k = k_token.detach()
         full_v = v_token.detach()
     else:
@@ -593,3 +751,13 @@ def stats(root: Path) -> dict[str, int | float]:
             "bytes": 0,
         }
     )
+
+
+# The module's own forms of the replaceable seams: a layer runs fused while
+# the module attributes are these objects.
+_HIP_RMSNORM = rmsnorm
+_HIP_GATED_RMSNORM = gated_rmsnorm
+_HIP_L2NORM = _l2norm
+_HIP_APPLY_ROPE = _apply_rope
+_HIP_CONV_STEP = _causal_conv1d_step
+_HIP_APPEND_FULL_KV = _append_full_kv

@@ -16,7 +16,6 @@ from pathlib import Path
 import torch
 from safetensors import safe_open
 
-from .device_utils import is_cuda
 
 BLOCK = 128
 
@@ -82,7 +81,7 @@ def cached_load_projection(root: Path, prefix: str, device: str) -> torch.Tensor
         out = dequantize_fp8_blockwise(weight, scale)
     else:
         out = weight.float()
-    if is_cuda(device):
+    if torch.device(device).type == "cuda":  # a ROCm GPU
         out = out.to(device=device, dtype=torch.float16)
     _PROJ_CACHE[key] = out
     return out

@@ -140,3 +140,57 @@ def test_fp8_projection_host_validation() -> None:
     arr[0] = nat.Fp8Proj(256, 256, 256, 64, 64, 1, 1)  # accumulating into fp16
     rc = lib.ria_linear_fp8_group(1, 2048, fake, 1, 2048, 1, ctypes.addressof(arr), None)
     assert rc == 1 and b"y_add" in lib.ria_last_error()
+
+
+def _c_layout(struct: str, fields: list[str], tmp_path: Path) -> list[int]:
+    """sizeof and field offsets of a header struct, from a host program compiled with gcc."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    inc = HEADERS[0].parent
+    body = "".join(f'  printf("%zu\\n", offsetof({struct}, {f}));\n' for f in fields)
+    src = tmp_path / "layout.c"
+    src.write_text(f'#include <stddef.h>\n#include <stdio.h>\n#include "ria_hybrid_attn.h"\n'
+                   f'int main(void) {{\n  printf("%zu\\n", sizeof({struct}));\n{body}  return 0;\n}}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{inc}", str(src), "-o", str(exe)], check=True)
+    return [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+
+
+@pytest.mark.parametrize("cls,struct", [(nat.GdnDecodeDesc, "ria_gdn_decode_desc"), (nat.Fp8Proj, "ria_fp8_proj")])
+def test_ctypes_structs_match_the_header(cls, struct, tmp_path) -> None:
+    names = [name for name, _ in cls._fields_]
+    want = _c_layout(struct, names, tmp_path)
+    got = [ctypes.sizeof(cls)] + [getattr(cls, n).offset for n in names]
+    assert got == want, dict(zip(["sizeof"] + names, zip(got, want)))
+
+
+def test_gdn_decode_ex_and_window_conv_host_validation() -> None:
+    lib = nat.load()
+    fake = ctypes.c_void_p(256)
+
+    def desc(**kw):
+        d = nat.GdnDecodeDesc(batch=1, num_k_heads=16, num_v_heads=32, x=256, x_dtype=0, x_row_stride=8192,
+                              conv_layout=nat.RIA_CONV_WINDOW, conv_weight=256, conv_window_in=1 << 20,
+                              conv_window_out=1 << 21, state_in=1 << 24, state_out=1 << 26, gate_a=256, gate_b=256,
+                              gate_row_stride=32, gate_mode=0, qk_mode=0, out=256, out_dtype=2)
+        for k, v in kw.items():
+            setattr(d, k, v)
+        return lib.ria_gdn_decode_ex(ctypes.byref(d), None)
+
+    assert lib.ria_gdn_decode_ex(None, None) == 1 and b"null" in lib.ria_last_error()
+    assert desc(conv_layout=7) == 1 and b"conv_layout" in lib.ria_last_error()
+    assert desc(qk_mode=nat.RIA_QK_NORMALIZED) == 1 and b"RIA_CONV_NONE" in lib.ria_last_error()
+    assert desc(conv_window_out=(1 << 20) + 8) == 1 and b"overlap" in lib.ria_last_error()
+    assert desc(conv_window_out=None) == 1 and b"conv_window_out" in lib.ria_last_error()
+    assert desc(state_out=(1 << 24) + 4096) == 1 and b"overlaps" in lib.ria_last_error()
+    assert desc(conv_layout=nat.RIA_CONV_NONE, qk_mode=nat.RIA_QK_NORMALIZED,
+                x_row_stride=8192) == 1 and b"x_row_stride" in lib.ria_last_error()
+    assert desc(conv_layout=nat.RIA_CONV_RING) == 1 and b"conv_ring" in lib.ria_last_error()
+    assert desc(batch=0) == 0  # nothing to launch
+    rc = lib.ria_conv1d_window_step(1, 8192, fake, 0, 8192, fake, ctypes.c_void_p(260), fake, fake, 2, None)
+    assert rc == 1 and b"aligned" in lib.ria_last_error()
+    rc = lib.ria_conv1d_window_step(1, 8192, fake, 0, 4096, fake, fake, fake, fake, 2, None)
+    assert rc == 1 and b"x_row_stride" in lib.ria_last_error()

@@ -143,3 +143,75 @@ def test_step_attention_refuses_cpu_device(tmp_path: Path) -> None:
               str(tmp_path / "model.safetensors"))
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ac.step_attention(tmp_path, 0, torch.zeros(1, 2048), "cpu")
+
+
+class _HostPages:
+    """A stand-in for a layer's KV pages on the CPU: gather(count) returns the first `count` tokens."""
+
+    num_kv_heads = 2
+    device = torch.device("cpu")
+
+    def __init__(self, dtype: torch.dtype, tokens: int):
+        g = torch.Generator().manual_seed(tokens)
+        self.dtype = dtype
+        self.k = torch.randn((1, 2, tokens, 256), generator=g).to(torch.float16)
+        self.v = torch.randn((1, 2, tokens, 256), generator=g).to(torch.float16)
+        self.gathered = 0
+
+    def gather(self, count: int):
+        self.gathered += 1
+        return self.k[:, :, :count], self.v[:, :, :count]
+
+
+def test_paged_kv_tensor_behaves_as_the_reference_cache_tensor() -> None:
+    pages = _HostPages(torch.float32, 40)
+    k = ac.PagedKVTensor(pages, "k", 33)
+    v = ac.PagedKVTensor(pages, "v", 33)
+    # metadata without touching the pages
+    assert isinstance(k, torch.Tensor) and k.shape == (1, 2, 33, 256) and k.shape[-2] == 33
+    assert k.dtype == torch.float32 and not k.requires_grad and not v.requires_grad
+    assert k.numel() * k.element_size() == 2 * 33 * 256 * 4  # the bytes the reference's fp32 tensor holds
+    assert pages.gathered == 0
+    # every use reads the first 33 tokens, converted to the tensor's dtype
+    want_k, want_v = pages.k[:, :, :33].float(), pages.v[:, :, :33].float()
+    assert torch.equal(k.detach().float(), want_k)
+    assert torch.equal(v.detach().clone(), want_v)
+    assert torch.equal(k + 1, want_k + 1)
+    assert torch.equal(k[:, :, 5:7], want_k[:, :, 5:7])
+    assert torch.equal(torch.cat((k, want_k[:, :, :1]), dim=2)[:, :, 33], want_k[:, :, 0])
+    assert torch.equal(k.repeat_interleave(8, dim=1).float(), want_k.repeat_interleave(8, dim=1))
+    torch.testing.assert_close(k, want_k)
+    assert type(k.detach()) is torch.Tensor  # what a caller keeps is a plain tensor
+    # a tensor taken earlier keeps its own length
+    assert ac.PagedKVTensor(pages, "k", 7).shape[-2] == 7
+
+
+def test_snapshot_and_limits_count_the_reference_bytes_for_paged_tensors() -> None:
+    pages = _HostPages(torch.float32, 40)
+    state = AttentionState()
+    state.full_keys[3] = ac.PagedKVTensor(pages, "k", 10)
+    state.full_values[3] = ac.PagedKVTensor(pages, "v", 10)
+    state.tokens_seen = 10
+    snap = state.snapshot()
+    assert snap["full_tokens_resident"] == 10 and snap["full_layers_cached"] == 1
+    assert snap["full_bytes"] == 2 * 2 * 10 * 256 * 4
+    assert pages.gathered == 0  # snapshot() reads shapes only
+    state.configure(max_full_kv_bytes=2 * 2 * 10 * 256 * 4 + 1)
+    with pytest.raises(RuntimeError, match="max_full_kv_bytes"):
+        ac._check_full_kv_limits(state, 3, append_bytes=2 * 2 * 256 * 4)
+    state.configure(max_context_tokens=10)
+    with pytest.raises(RuntimeError, match="max_context_tokens=10"):
+        ac._check_full_kv_limits(state, 3, append_bytes=0)
+
+
+def test_replaceable_seams_are_module_attributes() -> None:
+    # the probes of the reference swap these module attributes; the layers look them up at call time
+    for name in ("rmsnorm", "gated_rmsnorm", "_l2norm", "_apply_rope", "_causal_conv1d_step", "_append_full_kv",
+                 "_projection", "step_attention"):
+        assert callable(getattr(ac, name))
+    assert ac._HIP_RMSNORM is ac.rmsnorm and ac._HIP_CONV_STEP is ac._causal_conv1d_step
+    assert ac._HIP_APPEND_FULL_KV is ac._append_full_kv and ac._HIP_APPLY_ROPE is ac._apply_rope
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ac.rmsnorm(torch.zeros(1, 8), torch.zeros(8))
+    with pytest.raises(ValueError, match="x/z shape mismatch"):
+        ac.gated_rmsnorm(torch.zeros(1, 32, 128), torch.zeros(1, 32, 64), torch.zeros(128))

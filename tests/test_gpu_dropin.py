@@ -57,12 +57,15 @@ def test_step_attention_matches_reference_composites(gpu, ckpt):
     assert_state_close(st.linear_states[0].cpu(), ref.linear[0], "DeltaNet state", rel=1e-3)
     # conv state: the bf16 projection outputs of the last four tokens (GPU and CPU fp16 GEMVs may
     # round a few elements differently, hence a bf16-ulp tolerance rather than equality)
-    torch.testing.assert_close(ac.conv_state_window(st, 0).cpu().float(), ref.conv[0].float(), rtol=1.6e-2, atol=1e-3)
+    # the dict holds the reference's window [1, 8192, 4], oldest input first (6 tokens: not a multiple of 4)
+    conv = st.linear_conv_states[0]
+    assert conv.shape == (1, 8192, 4) and conv.dtype == torch.bfloat16
+    torch.testing.assert_close(conv.cpu().float(), ref.conv[0].float(), rtol=1.6e-2, atol=1e-3)
     snap = st.snapshot()
     assert snap["full_tokens_resident"] == 6 and snap["tokens_seen"] == 6
-    assert snap["full_bytes"] == 6 * 2 * 2 * 256 * 2  # bf16 K and V, 2 heads x 256
+    assert snap["full_bytes"] == 6 * 2 * 2 * 256 * 4  # the reference's fp32 K and V, 2 heads x 256
     assert snap["linear_bytes"] == 32 * 128 * 128 * 4 and snap["linear_conv_bytes"] == 8192 * 4 * 2
-    k_mat = st.full_keys[1].materialize().cpu().float()
+    k_mat = st.full_keys[1].detach().cpu().float()
     torch.testing.assert_close(k_mat, ref.keys[1].to(torch.float16).float(), rtol=2e-2, atol=2e-3)
 
 
@@ -113,10 +116,10 @@ def test_module_helpers_match_oracle(gpu):
         out = ac._causal_conv1d_step(st, 0, m.cuda(), w.cuda())
         want, state = O.causal_conv1d_step(state, m, w)
         torch.testing.assert_close(out.cpu(), want, rtol=8e-3, atol=1e-6)
-    assert torch.equal(ac.conv_state_window(st, 0).cpu(), state)
+    assert torch.equal(st.linear_conv_states[0].cpu(), state)  # the reference's window, bit for bit
 
 
-def test_append_full_kv_limits_on_gpu_count_stored_bytes(gpu):
+def test_append_full_kv_limits_on_gpu_count_the_reference_bytes(gpu):
     announce("drop-in: _append_full_kv limits with GPU tensors")
     from router_ia import qwen36_attention_cache as ac
 
@@ -133,10 +136,11 @@ def test_append_full_kv_limits_on_gpu_count_stored_bytes(gpu):
     with pytest.raises(RuntimeError, match="max_context_tokens=3"):
         ac._append_full_kv(st, 5, *tok())
     assert st.full_keys[5].shape[-2] == 3
-    mat = st.full_keys[5].materialize().cpu()
-    assert mat.dtype == torch.float16  # fp32 tokens are held in fp16 pages
-    assert torch.equal(mat, torch.cat(keys, dim=2).cpu().to(torch.float16))
-    token_bytes = 2 * 2 * 256 * 2
+    mat = st.full_keys[5].detach().cpu()
+    assert mat.dtype == torch.float32  # the dtype of the tokens; they are held in fp16 pages
+    assert torch.equal(mat, torch.cat(keys, dim=2).cpu().to(torch.float16).float())
+    assert st.paged_kv_bytes() == 3 * 2 * 2 * 256 * 2
+    token_bytes = 2 * 2 * 256 * 4  # fp32 k and v tokens, counted as the reference counts them
     st2 = ac.AttentionState(max_full_kv_bytes=2 * token_bytes)
     ac._append_full_kv(st2, 0, *tok())
     ac._append_full_kv(st2, 0, *tok())

@@ -454,6 +454,33 @@ int ria_attn_decode_append(int batch, int num_q_heads, int num_kv_heads,
                            void* out, int out_dtype, int phase, void* stream);
 
 /*
+ * ria_attn_decode_append with no workspace argument and no allocation: the
+ * split-K partials go into a 16 MiB array the library holds on each GPU it
+ * runs on (a file-scope device array, resolved once per device).  No
+ * counterpart in the reference: this entry point is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  Arguments are those of
+ * ria_attn_decode_append without workspace / workspace_bytes; sizes whose
+ * partials (ria_attn_decode_workspace_bytes) exceed 16 MiB return
+ * RIA_ERR_WORKSPACE before any launch (the balanced schedule fits up to about
+ * 1,500 (sequence, KV head) units).  Every call on one GPU shares the array:
+ * calls that overlap on one GPU (concurrent streams, or another call between
+ * a RIA_ATTN_SPLITK and its RIA_ATTN_COMBINE) race.
+ */
+int ria_attn_decode_append_noalloc(int batch, int num_q_heads, int num_kv_heads,
+                                   const void* q, int q_dtype, int64_t q_row_stride,
+                                   const void* gate, int gate_dtype, int64_t gate_row_stride,
+                                   const void* k, int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                   const float* k_norm_weight,
+                                   void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                                   const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                                   const int32_t* positions, int32_t position_scalar,
+                                   const int32_t* ctx_lens, int32_t ctx_scalar, int max_ctx,
+                                   const float* inv_freq, int rope_dim, const float* q_norm_weight,
+                                   float scale, int split_tokens,
+                                   void* out, int out_dtype, int phase, void* stream);
+
+/*
  * Workspace bytes ria_gdn_prefill needs to process `segment_tokens` tokens
  * per pass (it walks longer prompts in segments of whole 64-token chunks).
  */

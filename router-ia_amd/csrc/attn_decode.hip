@@ -33,6 +33,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "ria_common.h"
 
@@ -1254,6 +1255,75 @@ extern "C" int ria_attn_decode_append(int batch, int num_q_heads, int num_kv_hea
                           gate_row_stride, k_cache, v_cache, kv_dtype, num_pages, page_table, page_table_stride,
                           seq_slot, positions, position_scalar, ctx_lens, ctx_scalar, max_ctx, inv_freq, rope_dim,
                           q_norm_weight, scale, split_tokens, workspace, workspace_bytes, out, out_dtype, phase, &app,
+                          stream);
+}
+
+// ---- ria_attn_decode_append without a caller workspace
+// The split-K partials of ria_attn_decode_append_noalloc live in this
+// library-owned array instead of a caller workspace, for callers that cannot
+// allocate.  16 MiB holds the balanced schedule's unit table and partials
+// (8 KiB per partial at 8 query heads per KV head, #workgroups + #units
+// partials) for up to about 1,500 (sequence, KV head) units, i.e. 750
+// sequences of the model's 2 KV heads.  Each GPU the library runs on holds
+// its own copy until the process ends.  Nothing in it has to start at zero:
+// every partial and partition entry the combine launch reads is written by
+// the same call's split-K launch.  All calls on one GPU share the array, so
+// calls that overlap on one GPU (concurrent streams, or another call between
+// a SPLITK and its COMBINE phase) race.
+constexpr int64_t kScratchBytes = int64_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// The array's device address, looked up once per device with that device
+// current (the array's name is only a host-side stand-in).
+constexpr int kMaxScratchDevices = 64;
+static void* g_scratch_addr[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+static int scratch_address(void** addr, const char* who) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return set_error(RIA_ERR_LAUNCH, "%s: no current HIP device below index %d", who, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(RIA_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                       hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return RIA_OK;
+}
+
+extern "C" int ria_attn_decode_append_noalloc(int batch, int num_q_heads, int num_kv_heads, const void* q,
+                                              int q_dtype, int64_t q_row_stride, const void* gate, int gate_dtype,
+                                              int64_t gate_row_stride, const void* k, int64_t k_row_stride,
+                                              const void* v, int64_t v_row_stride, const float* k_norm_weight,
+                                              void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                                              const int32_t* page_table, int64_t page_table_stride,
+                                              const int32_t* seq_slot, const int32_t* positions,
+                                              int32_t position_scalar, const int32_t* ctx_lens, int32_t ctx_scalar,
+                                              int max_ctx, const float* inv_freq, int rope_dim,
+                                              const float* q_norm_weight, float scale, int split_tokens, void* out,
+                                              int out_dtype, int phase, void* stream) {
+  static const char* who = "ria_attn_decode_append_noalloc";
+  void* ws = nullptr;
+  if (batch > 0) {
+    const int64_t need = ria_attn_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_ctx, split_tokens);
+    if (need > kScratchBytes)
+      return set_error(RIA_ERR_WORKSPACE,
+                       "%s: these sizes need %lld bytes of partials, more than the library's %lld-byte scratch "
+                       "array; call ria_attn_decode_append with a workspace",
+                       who, (long long)need, (long long)kScratchBytes);
+    const int rc = scratch_address(&ws, who);
+    if (rc != RIA_OK) return rc;
+  }
+  const AppendIn app{k, k_row_stride, v, v_row_stride, k_norm_weight};
+  return attn_decode_impl(batch, num_q_heads, num_kv_heads, q, q_dtype, q_row_stride, gate, gate_dtype,
+                          gate_row_stride, k_cache, v_cache, kv_dtype, num_pages, page_table, page_table_stride,
+                          seq_slot, positions, position_scalar, ctx_lens, ctx_scalar, max_ctx, inv_freq, rope_dim,
+                          q_norm_weight, scale, split_tokens, ws, kScratchBytes, out, out_dtype, phase, &app,
                           stream);
 }
 

@@ -91,6 +91,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _vp, _vp, _c_int, _c_int, _vp, _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _vp,
          _c_f32, _c_int, _vp, _c_i64, _vp, _c_int, _c_int, _vp],
     ),
+    "ria_attn_decode_append_noalloc": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp,
+         _vp, _vp, _c_int, _c_int, _vp, _c_i64, _vp, _vp, _c_i32, _vp, _c_i32, _c_int, _vp, _c_int, _vp,
+         _c_f32, _c_int, _vp, _c_int, _c_int, _vp],
+    ),
     "ria_gdn_prefill_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int]),
     "ria_gdn_prefill": (
         _c_int,

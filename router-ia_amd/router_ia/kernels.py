@@ -879,7 +879,7 @@ def attn_decode_append(
     max_ctx: int,
     inv_freq: torch.Tensor | None,
     scale: float,
-    workspace: torch.Tensor,
+    workspace: torch.Tensor | None,
     seq_slot: torch.Tensor | None = None,
     split_tokens: int = 0,
     phase: int = nat.RIA_ATTN_BOTH,
@@ -893,6 +893,9 @@ def attn_decode_append(
     stops before it, the combine launch computes it with kv_append's
     arithmetic (the pages hold the same bits), writes it into the page and
     folds it into the row's softmax.  Both phases take the same arguments.
+    With ``workspace=None`` the partials go into the library's own scratch
+    array (ria_attn_decode_append_noalloc): nothing is allocated, and calls
+    that overlap on one GPU race.
     """
     batch = int(q.shape[0])
     num_q_heads = int(q.shape[1])
@@ -900,7 +903,7 @@ def attn_decode_append(
     dev = q.device
     for name, t in (("q", q), ("gate", gate), ("k", k), ("v", v), ("k_cache", k_cache), ("v_cache", v_cache),
                     ("out", out), ("inv_freq", inv_freq), ("workspace", workspace), ("seq_slot", seq_slot)):
-        _require_gpu(name, t, dev)
+        _require_gpu(name, t, dev)  # (a None workspace passes: the library's scratch array)
     if k.dtype != q.dtype or v.dtype != q.dtype or gate.dtype != q.dtype:
         raise ValueError("attn_decode_append: q, gate, k and v must share one dtype")
     qs = _row_stride("q", q, batch, num_q_heads * ATTN_HEAD_DIM)
@@ -915,22 +918,27 @@ def attn_decode_append(
         raise ValueError("page table has fewer rows than batch")
     if tuple(out.shape) != (batch, num_q_heads, ATTN_HEAD_DIM) or not out.is_contiguous():
         raise ValueError(f"out must be contiguous [{batch}, {num_q_heads}, 256]")
-    if not workspace.is_contiguous():
+    if workspace is not None and not workspace.is_contiguous():
         raise ValueError("workspace must be contiguous")
     pos_t, pos_s = _rows_i32("positions", positions, batch, dev)
     ctx_t, ctx_s = _rows_i32("ctx_lens", ctx_lens, batch, dev)
     if seq_slot is not None:
         _rows_i32("seq_slot", seq_slot, batch, dev)
     rope_dim = 0 if inv_freq is None else 2 * int(inv_freq.numel())
-    ws_bytes = workspace.numel() * workspace.element_size()
-    rc = nat.load().ria_attn_decode_append(
-        batch, num_q_heads, num_kv_heads, _ptr(q), dtype_code(q), qs, _ptr(gate), dtype_code(gate), gs,
-        _ptr(k), ks, _ptr(v), vs, _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev),
-        _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table), pts, _ptr(seq_slot),
-        _ptr(pos_t), pos_s, _ptr(ctx_t), ctx_s, int(max_ctx), _ptr(inv_freq), rope_dim,
-        _norm_weight("q_norm_weight", q_norm_weight, ATTN_HEAD_DIM, dev), float(scale), int(split_tokens),
-        _ptr(workspace), ws_bytes, _ptr(out), dtype_code(out), int(phase), _stream(dev))
-    nat.check(rc, "ria_attn_decode_append")
+    head = (batch, num_q_heads, num_kv_heads, _ptr(q), dtype_code(q), qs, _ptr(gate), dtype_code(gate), gs,
+            _ptr(k), ks, _ptr(v), vs, _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev),
+            _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table), pts, _ptr(seq_slot),
+            _ptr(pos_t), pos_s, _ptr(ctx_t), ctx_s, int(max_ctx), _ptr(inv_freq), rope_dim,
+            _norm_weight("q_norm_weight", q_norm_weight, ATTN_HEAD_DIM, dev), float(scale), int(split_tokens))
+    tail = (_ptr(out), dtype_code(out), int(phase), _stream(dev))
+    lib = nat.load()
+    if workspace is None:
+        rc = lib.ria_attn_decode_append_noalloc(*head, *tail)
+        nat.check(rc, "ria_attn_decode_append_noalloc")
+    else:
+        ws_bytes = workspace.numel() * workspace.element_size()
+        rc = lib.ria_attn_decode_append(*head, _ptr(workspace), ws_bytes, *tail)
+        nat.check(rc, "ria_attn_decode_append")
     return out
 
 def kv_append_seq(

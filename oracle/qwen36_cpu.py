@@ -15,7 +15,11 @@ Pinning (tests/test_oracle_*.py): each function is checked against an
 independent float64 brute force (oracle/fp64.py), closed forms and
 invariants, torch library routines (conv1d, scaled_dot_product_attention),
 the transformers 5.15.0 functions the reference itself defers to, and the
-committed fixtures under tests/golden/.
+committed fixtures under tests/golden/.  The layer composites
+(linear_layer_step, full_layer_step) are checked against transformers'
+Qwen3.5-MoE GatedDeltaNet and attention modules driven as cached one-token
+decodes, and their GPU-path casts against the reference's dtype order
+(tests/test_oracle_composites.py).
 """
 
 from __future__ import annotations
@@ -264,6 +268,17 @@ def gated_rmsnorm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor) -> tor
     return (weighted * F.silu(z.float())).to(x.dtype)
 
 
+def layer_compute_dtype(kind: str, gpu_dtypes: bool) -> torch.dtype:
+    """The dtype the normed input h is cast to before a layer's projections.
+
+    qwen36_attention_cache.py:229-230 (DeltaNet: bf16 on the GPU path) and
+    :293-294 (attention: fp16 on the GPU path); fp32 on the CPU path.
+    """
+    if not gpu_dtypes:
+        return torch.float32
+    return torch.bfloat16 if kind == "linear" else torch.float16
+
+
 def linear_layer_step(w: dict[str, torch.Tensor], st: SequenceState, layer: int, x0: torch.Tensor,
                       gpu_dtypes: bool = False) -> torch.Tensor:
     """qwen36_attention_cache.py:224-282 for one token of one sequence (projections included).
@@ -274,7 +289,7 @@ def linear_layer_step(w: dict[str, torch.Tensor], st: SequenceState, layer: int,
     """
     proj = (lambda t: t.to(torch.float16)) if gpu_dtypes else (lambda t: t.float())
     h = rmsnorm(x0, w["input_layernorm.weight"])
-    h_c = h.to(torch.bfloat16 if gpu_dtypes else torch.float32)
+    h_c = h.to(layer_compute_dtype("linear", gpu_dtypes))
     qkv_w = proj(w["linear_attn.in_proj_qkv.weight"])
     mixed = F.linear(h_c.to(qkv_w.dtype), qkv_w).reshape(1, CONV_DIM)
     mixed, st.conv[layer] = causal_conv1d_step(st.conv.get(layer), mixed, w["linear_attn.conv1d.weight"])
@@ -297,7 +312,7 @@ def full_layer_step(w: dict[str, torch.Tensor], st: SequenceState, layer: int, x
     """qwen36_attention_cache.py:285-324 for one token of one sequence at position st.tokens_seen."""
     proj = (lambda t: t.to(torch.float16)) if gpu_dtypes else (lambda t: t.float())
     h = rmsnorm(x0, w["input_layernorm.weight"])
-    h_c = h.to(torch.float16 if gpu_dtypes else torch.float32)
+    h_c = h.to(layer_compute_dtype("full", gpu_dtypes))
     q_w, k_w, v_w = (proj(w[f"self_attn.{n}_proj.weight"]) for n in ("q", "k", "v"))
     q_gate = F.linear(h_c.to(q_w.dtype), q_w).reshape(1, FULL_NUM_HEADS, FULL_HEAD_DIM * 2)
     q, gate = torch.chunk(q_gate, 2, dim=-1)

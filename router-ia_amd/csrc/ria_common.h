@@ -67,6 +67,29 @@ __device__ __forceinline__ float load_act(const void* p, int64_t i) {
   }
 }
 
+// load_act split in two: the raw element (16 or 32 bits) now, its fp32
+// value later, so that a caller can issue more loads before any widening
+// makes the compiler wait for this one.
+template <int DT>
+__device__ __forceinline__ uint32_t load_act_bits(const void* p, int64_t i) {
+  if constexpr (DT == RIA_DT_F32) {
+    return static_cast<const uint32_t*>(p)[i];
+  } else {
+    return static_cast<const uint16_t*>(p)[i];
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float act_from_bits(uint32_t b) {
+  if constexpr (DT == RIA_DT_BF16) {
+    return bf16_bits_to_f32(static_cast<uint16_t>(b));
+  } else if constexpr (DT == RIA_DT_F16) {
+    return f16_bits_to_f32(static_cast<uint16_t>(b));
+  } else {
+    return __uint_as_float(b);
+  }
+}
+
 // load_act with the dtype code known only at run time (side inputs such as
 // the gated norm's z, where a template parameter would multiply instances).
 __device__ __forceinline__ float load_act_dt(const void* p, int64_t i, int dt) {

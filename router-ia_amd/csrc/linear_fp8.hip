@@ -140,15 +140,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// The fp16 result v stored as y_dtype, or (y_add) added to the fp32 y in
-// one rounding: the reference's `x0.float() + F.linear(...).float()`.
-__device__ __forceinline__ void store_result(void* y, int64_t i, float v, int y_dtype, int y_add) {
-  if (y_add)
-    static_cast<float*>(y)[i] = add_rn(static_cast<const float*>(y)[i], v);
-  else
-    store_act_dt(y, i, v, y_dtype);
-}
-
 // One producer thread's weight bytes of a chunk: 8 (CT 1), 16 (CT 2) or 32 (CT 4).
 template <int CT>
 struct WeightSlot {
@@ -310,18 +301,54 @@ __global__ __launch_bounds__(512) void linear_fp8_kernel(const LinearArgs a) {
     static_for<kLinRing>([&](auto u) {
       if (u < tail) step(u, groups * kLinRing + u);
     });
-    // D tile rows 4 g4 + i, column n16; F.linear's fp16 result, stored as y_dtype
+    // D tile rows 4 g4 + i, column n16; F.linear's fp16 result, stored as
+    // y_dtype or (y_add) added to the fp32 y.  The y values an add needs are
+    // all loaded before the first store: a store between them would make each
+    // load wait for the one before (the compiler cannot tell they never
+    // overlap).  Whole tiles (the usual case) store with no per-element
+    // branch, which would make the compiler wait for every memory operation
+    // before each store.
+    auto y_index = [&](int rt, int ct, int i) {
+      return (int64_t)(m0 + 32 * wave + 16 * rt + 4 * g4 + i) * y_stride + n0 + 16 * ct + n16;
+    };
+    auto in_range = [&](int rt, int ct, int i) {
+      return 32 * wave + 16 * rt + 4 * g4 + i < rows && n0 + 16 * ct + n16 < n;
+    };
+    auto finish = [&](auto whole) {
+      constexpr bool W = decltype(whole)::value;
+      if (y_add) {
+        float* yf = static_cast<float*>(y);
+        float v[2][CT][4];
 #pragma unroll
-    for (int rt = 0; rt < NT; ++rt)
+        for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
+          for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 32 * wave + 16 * rt + 4 * g4 + i;
-          if (r < rows && n0 + 16 * ct + n16 < n)
-            store_result(y, (int64_t)(m0 + r) * y_stride + n0 + 16 * ct + n16,
-                         through_dtype<RIA_DT_F16>(acc[rt][ct][i]), y_dtype, y_add);
-        }
+            for (int i = 0; i < 4; ++i) v[rt][ct][i] = W || in_range(rt, ct, i) ? yf[y_index(rt, ct, i)] : 0.f;
+#pragma unroll
+        for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              v[rt][ct][i] = add_rn(v[rt][ct][i], through_dtype<RIA_DT_F16>(acc[rt][ct][i]));
+              if (W || in_range(rt, ct, i)) yf[y_index(rt, ct, i)] = v[rt][ct][i];
+            }
+      } else {
+#pragma unroll
+        for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (W || in_range(rt, ct, i))
+                store_act_dt(y, y_index(rt, ct, i), through_dtype<RIA_DT_F16>(acc[rt][ct][i]), y_dtype);
+      }
+    };
+    if (32 * wave + 16 * NT <= rows && n0 + 16 * CT <= n)
+      finish(std::true_type{});
+    else
+      finish(std::false_type{});
   };
   if (32 * wave + 16 < rows)
     consume(std::integral_constant<int, 2>{});
@@ -518,12 +545,24 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
 #pragma unroll
       for (int i = 0; i < 4; ++i) t[i] += u[i];
     }
-    // D rows (tokens) 4 g4 + i, column (feature) c16; F.linear's fp16 result, stored as y_dtype
+    // D rows (tokens) 4 g4 + i, column (feature) c16; F.linear's fp16 result,
+    // stored as y_dtype or added to the fp32 y (every y load before the first store)
+    if (y_add) {
+      float* yf = static_cast<float*>(y);
+      float prev[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * g4 + i;
-      if (r < rows)
-        store_result(y, (int64_t)(m0 + r) * y_stride + n0 + c16, through_dtype<RIA_DT_F16>(t[i]), y_dtype, y_add);
+      for (int i = 0; i < 4; ++i)
+        prev[i] = 4 * g4 + i < rows ? yf[(int64_t)(m0 + 4 * g4 + i) * y_stride + n0 + c16] : 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) prev[i] = add_rn(prev[i], through_dtype<RIA_DT_F16>(t[i]));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * g4 + i < rows) yf[(int64_t)(m0 + 4 * g4 + i) * y_stride + n0 + c16] = prev[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * g4 + i < rows)
+          store_act_dt(y, (int64_t)(m0 + 4 * g4 + i) * y_stride + n0 + c16, through_dtype<RIA_DT_F16>(t[i]), y_dtype);
     }
   }
 }

@@ -74,6 +74,35 @@ def test_linear_fp8_matches_oracle(gpu, m, n, k, xdt):
     assert e_got <= 1.5 * e_ref + 1e-6, (e_got, e_ref)
 
 
+STREAMING_F16 = [  # fp16 x past 16 rows (the forward loop's projections): the streaming kernel's
+    (96, 12288, 2048),   # tile shapes, with whole and partial row blocks and column tiles
+    (128, 8192, 2048),
+    (100, 20480, 2048),
+    (64, 8192, 512),
+    (128, 2048, 4096),   # the output projections' shape
+    (70, 2048, 4096),
+    (17, 512, 512),
+    (33, 96, 128),       # one chunk of K, a partial last column tile
+]
+
+
+@pytest.mark.parametrize("m,n,k", STREAMING_F16)
+def test_streaming_kernel_fp16_x_matches_oracle(gpu, m, n, k):
+    announce(f"linear_fp8 streaming: M={m} N={n} K={k} x fp16")
+    w8, s = W.fp8_block_weight(250 + m, n, k)
+    g = torch.Generator().manual_seed(350 + m)
+    wide = torch.randn((m, k + 64), generator=g).to(torch.float16)
+    x = wide[:, :k]
+    got = K.linear_fp8(x.to(gpu), w8.to(gpu), s.to(gpu)).cpu()
+    want = O.projection_fp8(x, w8, s)
+    assert_act_close(got, want, f"M={m} N={n} K={k}")
+    w16 = O.dequantize_fp8_blockwise(w8, s).to(torch.float16)
+    exact = x.double() @ w16.double().T
+    e_got = (got.double() - exact).abs().max().item()
+    e_ref = (want.double() - exact).abs().max().item()
+    assert e_got <= 1.5 * e_ref + 1e-6, (e_got, e_ref)
+
+
 @pytest.mark.parametrize("m", [9, 100])
 def test_linear_fp8_output_dtypes_round_through_fp16(gpu, m):
     announce(f"linear_fp8: M={m} fp32 and bf16 outputs carry the fp16 result")
@@ -97,11 +126,12 @@ GROUPS = [  # (m, [n_j], k): a DeltaNet layer's input projections, attention q/k
 ]
 
 
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,ns,k", GROUPS)
-def test_linear_fp8_group_equals_separate_calls(gpu, m, ns, k):
-    announce(f"linear_fp8_group: M={m} N={ns} K={k}")
+def test_linear_fp8_group_equals_separate_calls(gpu, m, ns, k, xdt):
+    announce(f"linear_fp8_group: M={m} N={ns} K={k} x {xdt}")
     proj = [W.fp8_block_weight(500 + j, n, k) for j, n in enumerate(ns)]
-    x = torch.randn((m, k), generator=torch.Generator().manual_seed(510 + m)).to(torch.bfloat16).to(gpu)
+    x = torch.randn((m, k), generator=torch.Generator().manual_seed(510 + m)).to(xdt).to(gpu)
     proj_d = [(w.to(gpu), s.to(gpu)) for w, s in proj]
     dts = [torch.bfloat16, torch.float32, torch.float16, torch.float32][:len(ns)]  # each projection its own dtype
     ys = K.linear_fp8_group(x, proj_d, out_dtype=dts)
@@ -115,7 +145,7 @@ def test_linear_fp8_group_equals_separate_calls(gpu, m, ns, k):
         assert_act_close(ys[j].cpu(), want, f"projection {j}")
 
 
-@pytest.mark.parametrize("m", [3, 100])
+@pytest.mark.parametrize("m", [3, 100, 128])  # one-pass kernel; streaming with partial and with whole row blocks
 def test_linear_fp8_group_accumulates_into_fp32(gpu, m):
     announce(f"linear_fp8_group: M={m} y += fp16 result (residual add)")
     w8, s = W.fp8_block_weight(600, 2048, 4096)

@@ -502,13 +502,13 @@ static int gdn_decode_launch(const ria_gdn_decode_desc& d, void* stream, const c
   a.conv_dim = conv_dim;
 
   // Column blocking: enough workgroups to cover 256 CUs several times over;
-  // the gated norm needs whole heads.
+  // the gated norm needs whole heads.  From 1024 tiles on, 64-column blocks
+  // (8 state vectors per thread) stream slightly faster than whole heads
+  // (measured on MI355X in one process: 47.96 against 50.33 us at 2048
+  // tiles, 93.7 against 94.2 us at 4096, even at 1024).
   const int64_t tiles = (int64_t)d.batch * num_v_heads;
   int cols = 128;
-  if (!d.z) {
-    if (tiles < 256) cols = 32;
-    else if (tiles < 1024) cols = 64;
-  }
+  if (!d.z) cols = tiles < 256 ? 32 : 64;
   a.ncb = kGdnHeadDim / cols;
   const int64_t blocks64 = tiles * a.ncb;
   if (blocks64 > 0x7fffffff) return set_error(RIA_ERR_INVALID, "%s: grid too large", who);

@@ -117,12 +117,11 @@ def test_gdn_decode_fused_gated_norm(gpu, batch):
                                 out_dtype=torch.float32)
     fused16, _ = _gdn_steps(gpu, params, inputs, zs, w, steps, batch, state0, ring0, fused=True,
                             out_dtype=torch.bfloat16)
-    # the norm leaves the state alone; below 32 rows the unfused launch splits
-    # heads into column blocks, which sums the read-out in another order
-    if batch >= 32:
-        assert torch.equal(s_fused, s_plain)
-    else:
-        assert_state_close(s_fused, s_plain, "state, fused vs unfused")
+    # the norm leaves the state alone; the unfused launch splits heads into
+    # column blocks (32 or 64 columns; the fused one needs whole heads), which
+    # sums the read-out in another order, so the states agree to the state
+    # tolerance rather than bit for bit
+    assert_state_close(s_fused, s_plain, "state, fused vs unfused")
     for t in range(steps):
         sep = K.gated_rmsnorm(plain[t].to(gpu), zs[t].to(gpu), w.to(gpu)).cpu()
         _ulp_close(fused[t], sep, torch.float32, f"step {t}: fused vs separate norm launch")

@@ -78,6 +78,7 @@ struct PrefillArgs {
   int num_k_heads;
   int num_v_heads;
   int conv_dim;
+  int x_pairs;  // bf16 x, 4-byte aligned rows: a thread's two channels are one 32-bit load
 };
 
 // ---------------------------------------------------------------- helpers
@@ -117,8 +118,14 @@ __device__ __forceinline__ void load8(const float* p, float* v) {
 }
 
 // ---------------------------------------------------------------- conv
-// Two adjacent channels per thread (one 32-bit load per token for bf16
-// inputs), tokens in batches of 8 so several loads are in flight.
+// Two adjacent channels per thread, a tile of 64 tokens per workgroup row.
+// With bf16 inputs every load of the tile is issued at once (one 32-bit load
+// per token for the two channels), then the arithmetic runs: issued in
+// batches, each batch's latency was exposed (187 -> 144 us per 16k-token
+// prompt in one process).  Other input dtypes load tokens in batches of 8.
+// SiLU keeps the accurate fp32 form: on the hardware exp2 and reciprocal the
+// launch took 96 us, but the final state of a 130-token prefill then missed
+// its 1e-4 bound (1.8e-3).
 constexpr int kConvTile = 64;
 
 template <int XT>
@@ -144,28 +151,45 @@ __global__ __launch_bounds__(256) void prefill_conv_kernel(PrefillArgs a) {
   };
   float ha[3], hb[3];
   for (int i = 0; i < 3; ++i) input(t_begin - 3 + i, ha[i], hb[i]);
-  for (int tb = t_begin; tb < t_end; tb += 8) {
-    float xa[8], xb[8];
+  auto emit = [&](int t, float xa, float xb) {
+    float acc_a = wa[0] * ha[0], acc_b = wb[0] * hb[0];
+    acc_a = fmaf(wa[1], ha[1], acc_a);
+    acc_b = fmaf(wb[1], hb[1], acc_b);
+    acc_a = fmaf(wa[2], ha[2], acc_a);
+    acc_b = fmaf(wb[2], hb[2], acc_b);
+    acc_a = fmaf(wa[3], xa, acc_a);
+    acc_b = fmaf(wb[3], xb, acc_b);
+    const uint32_t y = f32_to_bf16_bits(silu_f(round_bf16(acc_a))) |
+                       (uint32_t(f32_to_bf16_bits(silu_f(round_bf16(acc_b)))) << 16);
+    *reinterpret_cast<uint32_t*>(a.post + (int64_t)(t - a.tok0) * a.conv_dim + c) = y;
+    ha[0] = ha[1]; ha[1] = ha[2]; ha[2] = xa;
+    hb[0] = hb[1]; hb[1] = hb[2]; hb[2] = xb;
+  };
+  if (XT == RIA_DT_BF16 && a.x_pairs) {
+    // every load of the tile at once (token index clamped to the segment)
+    uint32_t xr[kConvTile];
+    const uint16_t* xp = static_cast<const uint16_t*>(a.x) + c;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (tb + u < t_end) input(tb + u, xa[u], xb[u]);
-      else xa[u] = xb[u] = 0.f;
+    for (int u = 0; u < kConvTile; ++u)
+      xr[u] = *reinterpret_cast<const uint32_t*>(xp + (int64_t)min(t_begin + u, t_end - 1) * a.x_stride);
+#pragma unroll
+    for (int u = 0; u < kConvTile; ++u) {
+      if (t_begin + u >= t_end) break;
+      emit(t_begin + u, bf16_bits_to_f32(xr[u] & 0xffffu), bf16_bits_to_f32(xr[u] >> 16));
     }
+  } else {
+    for (int tb = t_begin; tb < t_end; tb += 8) {
+      float xa[8], xb[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (tb + u >= t_end) break;
-      float acc_a = wa[0] * ha[0], acc_b = wb[0] * hb[0];
-      acc_a = fmaf(wa[1], ha[1], acc_a);
-      acc_b = fmaf(wb[1], hb[1], acc_b);
-      acc_a = fmaf(wa[2], ha[2], acc_a);
-      acc_b = fmaf(wb[2], hb[2], acc_b);
-      acc_a = fmaf(wa[3], xa[u], acc_a);
-      acc_b = fmaf(wb[3], xb[u], acc_b);
-      const uint32_t y = f32_to_bf16_bits(silu_f(round_bf16(acc_a))) |
-                         (uint32_t(f32_to_bf16_bits(silu_f(round_bf16(acc_b)))) << 16);
-      *reinterpret_cast<uint32_t*>(a.post + (int64_t)(tb + u - a.tok0) * a.conv_dim + c) = y;
-      ha[0] = ha[1]; ha[1] = ha[2]; ha[2] = xa[u];
-      hb[0] = hb[1]; hb[1] = hb[2]; hb[2] = xb[u];
+      for (int u = 0; u < 8; ++u) {
+        if (tb + u < t_end) input(tb + u, xa[u], xb[u]);
+        else xa[u] = xb[u] = 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (tb + u >= t_end) break;
+        emit(tb + u, xa[u], xb[u]);
+      }
     }
   }
 }
@@ -619,13 +643,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   auto process = [&](int cl, const ChunkOps& o) {
     const int chunk = a.chunk0 + cl;
-    // (i) v' = U - W S and o_inter = exp(G) q S for token tile `wave`
-    f32x4 vn = o.u, oi = {0.f, 0.f, 0.f, 0.f};
+    // (i) v' = U - W S and o_inter = exp(G) q S for token tile `wave`.
+    // Each product accumulates in two chains (k-steps 0-1 and 2-3), added at
+    // the end: four independent MFMA chains keep the pipe issuing where two
+    // would wait on each other's results.
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 vn2[2] = {o.u, z4}, oi2[2] = {z4, z4};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const u32x4 bh = lds16(&STh[n][32 * s + 8 * g4]), bl = lds16(&STl[n][32 * s + 8 * g4]);
-      vn = mfma3(o.wn[s][0], o.wn[s][1], bh, bl, vn);
-      oi = mfma3(o.qt[s][0], o.qt[s][1], bh, bl, oi);
+      vn2[s >> 1] = mfma3(o.wn[s][0], o.wn[s][1], bh, bl, vn2[s >> 1]);
+      oi2[s >> 1] = mfma3(o.qt[s][0], o.qt[s][1], bh, bl, oi2[s >> 1]);
+    }
+    f32x4 vn, oi;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      vn[i4] = vn2[0][i4] + vn2[1][i4];
+      oi[i4] = oi2[0][i4] + oi2[1][i4];
     }
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
@@ -635,13 +669,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
     lds_barrier();
     // (ii) o = o_inter + ((q k^T) o D) v'   (lower triangular: token tiles <= wave)
+    f32x4 oq2[2] = {z4, z4};
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       if (32 * s <= 16 * wave + 15) {
         const u32x4 bh = lds16(&VTh[n][32 * s + 8 * g4]), bl = lds16(&VTl[n][32 * s + 8 * g4]);
-        oi = mfma3(o.qk[s][0], o.qk[s][1], bh, bl, oi);
+        oq2[s] = mfma3(o.qk[s][0], o.qk[s][1], bh, bl, oq2[s]);
       }
     }
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) oi[i4] += oq2[0][i4] + oq2[1][i4];
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int t = chunk * kChunk + 16 * wave + 4 * g4 + i4;
@@ -649,17 +686,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         store_act<OT>(a.out, ((int64_t)(t - a.out_tok0) * a.num_v_heads + h) * kDim + cb * 16 + n, oi[i4]);
     }
     // (iii) S <- exp(G_C) S + Kt^T v' for dk tiles 2 wave, 2 wave + 1
+    // (four independent chains: two tiles x two k-steps)
+    f32x4 sk[2][2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const u32x4 bh = lds16(&VTh[n][32 * s + 8 * g4]), bl = lds16(&VTl[n][32 * s + 8 * g4]);
+#pragma unroll
+      for (int tk = 0; tk < 2; ++tk) sk[tk][s] = mfma3(o.kt[tk][s][0], o.kt[tk][s][1], bh, bl, z4);
+    }
 #pragma unroll
     for (int tk = 0; tk < 2; ++tk) {
       const int dt = 2 * wave + tk;
       f32x4 sn;
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) sn[i4] = o.gl * S32[16 * dt + 4 * g4 + i4][n];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const u32x4 bh = lds16(&VTh[n][32 * s + 8 * g4]), bl = lds16(&VTl[n][32 * s + 8 * g4]);
-        sn = mfma3(o.kt[tk][s][0], o.kt[tk][s][1], bh, bl, sn);
-      }
+      for (int i4 = 0; i4 < 4; ++i4) sn[i4] = o.gl * S32[16 * dt + 4 * g4 + i4][n] + (sk[tk][0][i4] + sk[tk][1][i4]);
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const int r = 16 * dt + 4 * g4 + i4;
@@ -784,6 +824,7 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
   PrefillArgs a{};
   a.x = mixed_qkv;
   a.x_stride = x_row_stride;
+  a.x_pairs = x_dtype == RIA_DT_BF16 && reinterpret_cast<uintptr_t>(mixed_qkv) % 4 == 0 && x_row_stride % 2 == 0;
   a.conv_w = static_cast<const uint16_t*>(conv_weight);
   a.conv_ring = static_cast<uint16_t*>(conv_ring);
   a.n0 = conv_pos;

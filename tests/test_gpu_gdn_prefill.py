@@ -111,3 +111,34 @@ def test_prefill_16384_tokens_single_layer(gpu):
     assert_act_close(got, want, "all 16384 outputs")
     # the fp32 state after 16384 tokens, within the stated 1e-4 relative bound
     assert_state_close(state[None], s_want, "final state after 16384 tokens")
+
+
+def test_prefill_conv_load_paths_agree(gpu):
+    """bf16 rows at an even stride load a thread's two channels as one 32-bit
+    word, all of a tile's tokens at once; an odd row stride takes the
+    per-channel batched loads.  Same arithmetic: the same bits."""
+    announce("gdn_prefill: paired 32-bit conv loads vs per-channel loads (odd row stride), 200 tokens")
+    params = W.gdn_layer_params(51)
+    inputs = W.gdn_step_inputs(52, 200, 1)
+    state0, ring0 = _init(53)
+    length = 200
+    mixed = inputs["mixed"][:length, 0]
+    wide = torch.zeros((length, W.CONV_DIM + 1), dtype=mixed.dtype)
+    wide[:, :W.CONV_DIM] = mixed
+    res = []
+    for x in (mixed.to(gpu), wide.to(gpu)[:, :W.CONV_DIM]):  # row stride 8192, then 8193
+        state = state0.clone().to(gpu)
+        ring = ring0.clone().to(gpu)
+        ws = torch.empty(K.gdn_prefill_workspace_bytes(16, 32, length), dtype=torch.uint8, device=gpu)
+        out = torch.empty((length, 32, 128), dtype=torch.float32, device=gpu)
+        K.gdn_prefill(x, state, inputs["a_raw"][:length, 0].to(gpu), inputs["b_raw"][:length, 0].to(gpu), out,
+                      num_k_heads=16, num_v_heads=32, conv_weight=params["conv_weight"].to(gpu), conv_ring=ring,
+                      conv_pos=5, workspace=ws, gate_mode=nat.RIA_GATE_RAW, A_log=params["A_log"].to(gpu),
+                      dt_bias=params["dt_bias"].to(gpu))
+        torch.cuda.synchronize()
+        res.append((out.cpu(), state.cpu(), ring.cpu()))
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+    assert torch.equal(res[0][2], res[1][2])
+    want, s_want, _ = _oracle_tokens(params, inputs, length, state0[None], ring_to_window(ring0, 5))
+    assert_act_close(res[0][0], want, "outputs vs oracle")
+    assert_state_close(res[0][1][None], s_want, "final state vs oracle")

@@ -595,20 +595,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g4 = lane >> 4;
 
-  __shared__ float S32[kDim][17];  // state block S[:, 16 cb + c], fp32
-  __shared__ __attribute__((aligned(16))) uint16_t STh[16][kDim + 8];  // S^T hi / lo (bf16)
-  __shared__ __attribute__((aligned(16))) uint16_t STl[16][kDim + 8];
-  __shared__ __attribute__((aligned(16))) uint16_t VTh[16][kChunk + 8];  // v'^T hi / lo (bf16)
-  __shared__ __attribute__((aligned(16))) uint16_t VTl[16][kChunk + 8];
+  // LDS in 16-byte entries [row group][column n] (column n = state column
+  // 16 cb + n): 4 rows of fp32 S, or 8 rows of bf16 S hi / lo or v' hi / lo
+  // (v' rows are tokens).  A lane reads the entry [row group][n] of its own
+  // column, so each 16-lane quarter of a wave reads 256 contiguous bytes.
+  // Measured on gfx950 with a probe kernel: a 16-byte access is free of bank
+  // conflicts only when each 16-lane quarter covers 256 contiguous bytes
+  // (other spacings cost 4 cycles, a 256-byte pitch 28), an 8-byte store only
+  // when each quarter covers 128 contiguous bytes.  Every access here is one
+  // of those (0.01 conflict cycles per LDS instruction, against 3.5 for a
+  // row-major fp32 block and transposed 2-byte stores); the lane-pair trade
+  // that makes the bf16 stores whole entries costs ~5% of the scan (its
+  // VALU work lies on the chunk's dependency chain), as conflicts cost nothing
+  // measurable: they overlap the MFMA chain.
+  __shared__ __attribute__((aligned(16))) float S32[kDim / 4][16][4];          // S fp32
+  __shared__ __attribute__((aligned(16))) uint16_t STh[kDim / 8][16][8];       // S hi / lo (bf16)
+  __shared__ __attribute__((aligned(16))) uint16_t STl[kDim / 8][16][8];
+  __shared__ __attribute__((aligned(16))) uint16_t VTh[kChunk / 8][16][8];     // v' hi / lo (bf16)
+  __shared__ __attribute__((aligned(16))) uint16_t VTl[kChunk / 8][16][8];
+  // A lane's four rows of a column (rows 4 g4 .. 4 g4 + 3 of a 16-row tile)
+  // are half of an 8-row entry; the other half is in lane +-16 (g4 ^ 1).
+  // The pair trades halves (one permlane16 swap per 32-bit word), so the
+  // even lane stores the whole hi entry and the odd lane the whole lo entry,
+  // each one 16-byte store.
+  const bool even = (g4 & 1) == 0;
+  auto store_hl = [&](uint16_t (*hp)[16][8], uint16_t (*lp)[16][8], int rg, const f32x4& x) {
+    uint32_t h2[2], l2[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint16_t a0 = f32_to_bf16_bits(x[2 * j]), a1 = f32_to_bf16_bits(x[2 * j + 1]);
+      h2[j] = a0 | (uint32_t(a1) << 16);
+      l2[j] = f32_to_bf16_bits(x[2 * j] - bf16_bits_to_f32(a0)) |
+              (uint32_t(f32_to_bf16_bits(x[2 * j + 1] - bf16_bits_to_f32(a1))) << 16);
+    }
+    uint32_t got[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t give = even ? l2[j] : h2[j];
+      const auto r = __builtin_amdgcn_permlane16_swap(give, give, false, false);  // {row 2i's, row 2i+1's}
+      got[j] = even ? r[1] : r[0];
+    }
+    const u32x4 e = even ? u32x4{h2[0], h2[1], got[0], got[1]} : u32x4{got[0], got[1], l2[0], l2[1]};
+    *reinterpret_cast<u32x4*>(even ? hp[rg][n] : lp[rg][n]) = e;
+  };
 
   float* Sg = a.state + (int64_t)h * kDim * kDim + cb * 16;
   for (int e = tid; e < kDim * 16; e += 256) {
     const int r = e >> 4, c = e & 15;
     const float v = Sg[r * kDim + c];
-    S32[r][c] = v;
+    S32[r >> 2][c][r & 3] = v;
     const uint16_t hb = f32_to_bf16_bits(v);
-    STh[c][r] = hb;
-    STl[c][r] = f32_to_bf16_bits(v - bf16_bits_to_f32(hb));
+    STh[r >> 3][c][r & 7] = hb;
+    STl[r >> 3][c][r & 7] = f32_to_bf16_bits(v - bf16_bits_to_f32(hb));
   }
   lds_barrier();
 
@@ -643,42 +681,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   auto process = [&](int cl, const ChunkOps& o) {
     const int chunk = a.chunk0 + cl;
-    // (i) v' = U - W S and o_inter = exp(G) q S for token tile `wave`.
-    // Each product accumulates in two chains (k-steps 0-1 and 2-3), added at
-    // the end: four independent MFMA chains keep the pipe issuing where two
-    // would wait on each other's results.
-    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-    f32x4 vn2[2] = {o.u, z4}, oi2[2] = {z4, z4};
+    // (i) v' = U - W S and o_inter = exp(G) q S for token tile `wave`
+    f32x4 vn = o.u, oi = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4 bh = lds16(&STh[n][32 * s + 8 * g4]), bl = lds16(&STl[n][32 * s + 8 * g4]);
-      vn2[s >> 1] = mfma3(o.wn[s][0], o.wn[s][1], bh, bl, vn2[s >> 1]);
-      oi2[s >> 1] = mfma3(o.qt[s][0], o.qt[s][1], bh, bl, oi2[s >> 1]);
+      const u32x4 bh = lds16(STh[4 * s + g4][n]), bl = lds16(STl[4 * s + g4][n]);
+      vn = mfma3(o.wn[s][0], o.wn[s][1], bh, bl, vn);
+      oi = mfma3(o.qt[s][0], o.qt[s][1], bh, bl, oi);
     }
-    f32x4 vn, oi;
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      vn[i4] = vn2[0][i4] + vn2[1][i4];
-      oi[i4] = oi2[0][i4] + oi2[1][i4];
-    }
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const uint16_t hb = f32_to_bf16_bits(vn[i4]);
-      VTh[n][16 * wave + 4 * g4 + i4] = hb;
-      VTl[n][16 * wave + 4 * g4 + i4] = f32_to_bf16_bits(vn[i4] - bf16_bits_to_f32(hb));
-    }
+    store_hl(VTh, VTl, 2 * wave + (g4 >> 1), vn);
     lds_barrier();
     // (ii) o = o_inter + ((q k^T) o D) v'   (lower triangular: token tiles <= wave)
-    f32x4 oq2[2] = {z4, z4};
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       if (32 * s <= 16 * wave + 15) {
-        const u32x4 bh = lds16(&VTh[n][32 * s + 8 * g4]), bl = lds16(&VTl[n][32 * s + 8 * g4]);
-        oq2[s] = mfma3(o.qk[s][0], o.qk[s][1], bh, bl, oq2[s]);
+        const u32x4 bh = lds16(VTh[4 * s + g4][n]), bl = lds16(VTl[4 * s + g4][n]);
+        oi = mfma3(o.qk[s][0], o.qk[s][1], bh, bl, oi);
       }
     }
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) oi[i4] += oq2[0][i4] + oq2[1][i4];
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int t = chunk * kChunk + 16 * wave + 4 * g4 + i4;
@@ -686,28 +706,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         store_act<OT>(a.out, ((int64_t)(t - a.out_tok0) * a.num_v_heads + h) * kDim + cb * 16 + n, oi[i4]);
     }
     // (iii) S <- exp(G_C) S + Kt^T v' for dk tiles 2 wave, 2 wave + 1
-    // (four independent chains: two tiles x two k-steps)
-    f32x4 sk[2][2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const u32x4 bh = lds16(&VTh[n][32 * s + 8 * g4]), bl = lds16(&VTl[n][32 * s + 8 * g4]);
-#pragma unroll
-      for (int tk = 0; tk < 2; ++tk) sk[tk][s] = mfma3(o.kt[tk][s][0], o.kt[tk][s][1], bh, bl, z4);
-    }
 #pragma unroll
     for (int tk = 0; tk < 2; ++tk) {
-      const int dt = 2 * wave + tk;
-      f32x4 sn;
+      const int r0 = 16 * (2 * wave + tk) + 4 * g4;
+      f32x4 sn = *reinterpret_cast<const f32x4*>(S32[r0 >> 2][n]);
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) sn[i4] = o.gl * S32[16 * dt + 4 * g4 + i4][n] + (sk[tk][0][i4] + sk[tk][1][i4]);
+      for (int i4 = 0; i4 < 4; ++i4) sn[i4] = o.gl * sn[i4];
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int r = 16 * dt + 4 * g4 + i4;
-        S32[r][n] = sn[i4];
-        const uint16_t hb = f32_to_bf16_bits(sn[i4]);
-        STh[n][r] = hb;
-        STl[n][r] = f32_to_bf16_bits(sn[i4] - bf16_bits_to_f32(hb));
+      for (int s = 0; s < 2; ++s) {
+        const u32x4 bh = lds16(VTh[4 * s + g4][n]), bl = lds16(VTl[4 * s + g4][n]);
+        sn = mfma3(o.kt[tk][s][0], o.kt[tk][s][1], bh, bl, sn);
       }
+      *reinterpret_cast<f32x4*>(S32[r0 >> 2][n]) = sn;
+      store_hl(STh, STl, r0 >> 3, sn);
     }
     lds_barrier();
   };
@@ -755,7 +766,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   for (int e = tid; e < kDim * 16; e += 256) {
     const int r = e >> 4, c = e & 15;
-    Sg[r * kDim + c] = S32[r][c];
+    Sg[r * kDim + c] = S32[r >> 2][c][r & 3];
   }
 }
 

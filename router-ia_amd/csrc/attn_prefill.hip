@@ -22,13 +22,9 @@
 //     the block's tokens in an order that leaves lane group g with exactly 8
 //     consecutive tokens of one page, whose V^T column is then one 16-byte
 //     operand of O^T = V^T P^T (16x16x32, k = those 32 keys);
-//   * with a bf16 cache the rotated q is carried as a bf16 hi + lo pair
-//     (near-fp32 scores: a bf16 q alone would move a score of 20 log2 units
-//     by ~0.04, a few percent of its weight) and the probabilities P as bf16
-//     (2^-9 relative per weight, ~0.2% of |v| in the output, ten times inside
-//     the activation tolerance; the lo products of P cost 17% of the kernel's
-//     time); with an fp16 cache q and P are fp16 (11 significant bits); the
-//     row sums l add the same rounded P in fp32; the online softmax is kept in log2
+//   * with a bf16 cache the rotated q and the probabilities are carried as
+//     bf16 hi + lo pairs (near-fp32 operands on MFMA); with an fp16 cache the
+//     fp16 hi part alone (11 significant bits); the online softmax is kept in log2
 //     units (q is pre-scaled) with a lazy rescale (only when a block max
 //     exceeds the running max by 2^8); row statistics combine across lane
 //     groups with permlane swaps;
@@ -100,9 +96,8 @@ template <int AT, int KVT>
 __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(
     PrefillAttnArgs a, const int32_t* __restrict__ pt) {
   using KV = Kv16<KVT>;
-  // bf16 operands carry q as a hi + lo pair; fp16 ones keep 11 significant
-  // bits in the hi part alone, which is enough here.  P is a single 16-bit
-  // operand either way.
+  // bf16 operands carry q and the probabilities as hi + lo pairs; fp16 ones
+  // keep 11 significant bits in the hi part alone, which is enough here
   constexpr bool kSplit = KVT == RIA_DT_BF16;
   const int nqb = (a.length + 15) / 16;
   const int qb = nqb - 1 - static_cast<int>(blockIdx.x) / a.num_kv_heads;  // heaviest blocks first
@@ -324,20 +319,17 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     float pr[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) pr[j] = __builtin_amdgcn_exp2f(s[j] - m_run);
-    // P runs as one 16-bit operand; the row sums add the same rounded
-    // values, so each output is a convex combination of v rows
-    u32x4 ph;
-    float pq[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      ph[j] = KV::pack2(pr[2 * j], pr[2 * j + 1]);
-      pq[2 * j] = KV::lo_f32(ph[j]);
-      pq[2 * j + 1] = KV::hi_f32(ph[j]);
-    }
-    l_run += ((pq[0] + pq[1]) + (pq[2] + pq[3])) + ((pq[4] + pq[5]) + (pq[6] + pq[7]));
+    l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+    u32x4 ph, pl;
+    pack(pr, ph, pl);
     __builtin_amdgcn_sched_barrier(0);
+    // all hi products, then all lo products: 16 MFMAs between dependent ones
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) o[dt] = KV::mfma_k32(vop[dt], ph, o[dt]);
+    if (kSplit) {
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) o[dt] = KV::mfma_k32(vop[dt], pl, o[dt]);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 

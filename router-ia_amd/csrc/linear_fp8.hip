@@ -23,7 +23,12 @@
 //                        buffered), and four consumer waves (32 rows of x
 //                        each) run 16x16x32 f16 MFMAs with x operands loaded
 //                        one chunk ahead.  Decode-sized M is bound by the
-//                        weight stream.
+//                        weight stream.  Used past 16 rows for bf16 and
+//                        fp32 x.
+//   linear_fp8_ks_kernel past 16 rows with fp16 x (the forward loop's
+//                        projections): one workgroup per tile of rows x
+//                        features over the whole K, split between its waves,
+//                        each streaming its own x and weights into registers.
 #include <algorithm>
 #include <type_traits>
 #include <utility>
@@ -567,6 +572,180 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
   }
 }
 
+// Past 16 rows with fp16 x: one workgroup per tile of 16 RT rows x 16 CT
+// features over the whole of K, whose NW waves split K between them: wave w
+// takes the 64-K chunks w, w + NW, w + 2 NW, ...  Each wave loads its own x
+// and weight bytes straight into registers, D chunks deep, with no LDS and no
+// barrier in the loop (every byte the workgroup needs is loaded once, by one
+// wave), dequantises each weight once and feeds it to RT MFMAs.  The waves'
+// partial tiles meet in LDS at the end and are added in wave order.  K order
+// inside a chunk: a lane's 16 weight bytes at K = 64 c + 16 g .. + 15 feed two
+// MFMAs (the low 8 bytes the first, the high 8 the second, as k group g of
+// each), and its x operands take the same K.  CH > 0: every wave has exactly
+// CH chunks (K = 64 NW CH), unrolled; CH = 0: any K, in groups of D chunks.
+constexpr int kKsChunk = 64;
+
+template <int RT, int CT, int NW, int D, int CH>
+__global__ __launch_bounds__(64 * NW) void linear_fp8_ks_kernel(const LinearArgs a) {
+  using F16 = Kv16<RIA_DT_F16>;
+  static_assert(kFp8Block % (16 * CT) == 0, "a tile's features lie in one scale block");
+  static_assert((RT * CT) % NW == 0, "the waves share the tiles of the epilogue evenly");
+  constexpr int kTiles = RT * CT;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n16 = lane & 15, g4 = lane >> 4;
+  const int bx = blockIdx.x;
+  const uint8_t* w = a.p[0].w;
+  const float* scale = a.p[0].scale;
+  void* y = a.p[0].y;
+  int64_t y_stride = a.p[0].y_stride;
+  int n = a.p[0].n, y_dtype = a.p[0].y_dtype, y_add = a.p[0].y_add, tile0 = 0;
+#pragma unroll
+  for (int j = 1; j < kLinGroup; ++j)
+    if (j < a.count && bx >= a.p[j].tile0) {
+      w = a.p[j].w;
+      scale = a.p[j].scale;
+      y = a.p[j].y;
+      y_stride = a.p[j].y_stride;
+      n = a.p[j].n;
+      y_dtype = a.p[j].y_dtype;
+      y_add = a.p[j].y_add;
+      tile0 = a.p[j].tile0;
+    }
+  const int n0 = (bx - tile0) * 16 * CT;
+  const int m0 = blockIdx.y * 16 * RT;
+  const int chunks = a.k / kKsChunk;
+  const int cnt = (chunks - wave + NW - 1) / NW;  // this wave's chunks (0 when K has fewer than NW)
+  const uint16_t* x = static_cast<const uint16_t*>(a.x);
+  // rows past the last token and features past n repeat the last one: their
+  // results are computed and never stored.  Offsets fit 32 bits (checked on
+  // the host), which keeps the address registers to one per operand row.
+  uint32_t xo[RT], wo[CT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+    xo[rt] = static_cast<uint32_t>(min(m0 + 16 * rt + n16, a.m - 1) * a.x_stride + 16 * g4);
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) wo[ct] = static_cast<uint32_t>(min(n0 + 16 * ct + n16, n - 1) * a.k + 16 * g4);
+  const float* sp = scale + (int64_t)(n0 / kFp8Block) * (a.k / kFp8Block);
+
+  struct Stage {
+    u32x4 x[RT][2];
+    u32x4 w[CT];
+    float s;
+  };
+  Stage st[D];
+  // chunk i of this wave into s (past the wave's last chunk: the last one again, never used)
+  auto load = [&](Stage& s, int i) {
+    const int c = wave + NW * min(i, cnt - 1);
+    const uint32_t ko = static_cast<uint32_t>(c * kKsChunk);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      s.x[rt][0] = *reinterpret_cast<const u32x4*>(x + xo[rt] + ko);
+      s.x[rt][1] = *reinterpret_cast<const u32x4*>(x + xo[rt] + ko + 8);
+    }
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) s.w[ct] = *reinterpret_cast<const u32x4*>(w + wo[ct] + ko);
+    s.s = sp[c * kKsChunk / kFp8Block];
+  };
+  f32x4 acc[RT][CT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (cnt > 0) {
+    static_for<D - 1>([&](auto u) { load(st[u], u); });
+    // chunk i sits in slot i % D; step i refills the slot chunk i - 1 left
+    // with chunk i + D - 1.  The scheduling barrier keeps the refill loads
+    // ahead of the MFMAs (the scheduler would otherwise sink each load next
+    // to its use, which leaves one chunk in flight).
+    auto step = [&](auto u, auto i, bool refill) {
+      if (refill) load(st[(u + D - 1) % D], i + D - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const Stage& s = st[u];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const u32x4 v = s.w[ct];
+        const u32x4 b0{dequant_pair<false>(v[0], s.s), dequant_pair<true>(v[0], s.s), dequant_pair<false>(v[1], s.s),
+                       dequant_pair<true>(v[1], s.s)};
+        const u32x4 b1{dequant_pair<false>(v[2], s.s), dequant_pair<true>(v[2], s.s), dequant_pair<false>(v[3], s.s),
+                       dequant_pair<true>(v[3], s.s)};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = F16::mfma_k32(s.x[rt][0], b0, acc[rt][ct]);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = F16::mfma_k32(s.x[rt][1], b1, acc[rt][ct]);
+      }
+    };
+    if constexpr (CH > 0) {
+      // CH chunks per wave, straight-line code: a loop would join the ring's
+      // loads at its head, where the compiler waits for every load in flight
+      static_for<CH>([&](auto i) {
+        step(std::integral_constant<int, i % D>{}, i, i + D - 1 < CH);
+      });
+    } else {
+      const int groups = cnt / D, tail = cnt - groups * D;
+      for (int gi = 0; gi < groups; ++gi) static_for<D>([&](auto u) { step(u, gi * D + u, true); });
+      static_for<D>([&](auto u) {
+        if (u < tail) step(u, groups * D + u, true);
+      });
+    }
+  }
+
+  // ---- the waves' partial tiles, added in wave order; wave w finishes tiles w, w + NW, ..
+  __shared__ f32x4 part[NW][kTiles][64];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) part[wave][rt * CT + ct][lane] = acc[rt][ct];
+  __syncthreads();
+  constexpr int TPW = kTiles / NW;
+  f32x4 tot[TPW];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int t = wave + NW * j;
+    tot[j] = part[0][t][lane];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) {
+      const f32x4 u = part[q][t][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tot[j][i] += u[i];
+    }
+  }
+  // D tile rows 4 g4 + i, column n16: F.linear's fp16 result, stored as
+  // y_dtype or (y_add) added to the fp32 y, every y value loaded before the
+  // first store
+  auto row_of = [&](int j, int i) { return m0 + 16 * ((wave + NW * j) / CT) + 4 * g4 + i; };
+  auto col_of = [&](int j) { return n0 + 16 * ((wave + NW * j) % CT) + n16; };
+  if (y_add) {
+    float* yf = static_cast<float*>(y);
+    float v[TPW][4];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[j][i] = row_of(j, i) < a.m && col_of(j) < n ? yf[(int64_t)row_of(j, i) * y_stride + col_of(j)] : 0.f;
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[j][i] = add_rn(v[j][i], through_dtype<RIA_DT_F16>(tot[j][i]));
+        if (row_of(j, i) < a.m && col_of(j) < n) yf[(int64_t)row_of(j, i) * y_stride + col_of(j)] = v[j][i];
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (row_of(j, i) < a.m && col_of(j) < n)
+          store_act_dt(y, (int64_t)row_of(j, i) * y_stride + col_of(j), through_dtype<RIA_DT_F16>(tot[j][i]), y_dtype);
+  }
+}
+
+// Tile shapes of the K-split kernel (rows 16 RT, features 16 CT)
+struct KsShape {
+  int rt, ct;
+};
+constexpr KsShape kKsShapes[] = {{4, 8}, {4, 4}, {2, 2}};
+
 template <int XT, bool NORM = false>
 static void launch_gemv(const LinearArgs& a, dim3 grid, hipStream_t st) {
   const int waves = a.k / kGemvSlice;
@@ -582,6 +761,34 @@ static void launch_linear(const LinearArgs& a, int ct, dim3 grid, hipStream_t st
     hipLaunchKernelGGL((linear_fp8_kernel<XT, 2>), grid, dim3(512), 0, st, a);
   else
     hipLaunchKernelGGL((linear_fp8_kernel<XT, 1>), grid, dim3(512), 0, st, a);
+}
+
+template <int RT, int CT, int D>
+static void launch_ks_k(const LinearArgs& a, dim3 grid, hipStream_t st) {
+  constexpr int NW = 4;
+  if (a.k == kKsChunk * NW * 8)
+    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 8>), grid, dim3(64 * NW), 0, st, a);
+  else if (a.k == kKsChunk * NW * 16)
+    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 16>), grid, dim3(64 * NW), 0, st, a);
+  else
+    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 0>), grid, dim3(64 * NW), 0, st, a);
+}
+
+static void launch_ks(const LinearArgs& a, KsShape s, dim3 grid, hipStream_t st) {
+  if (s.rt == 4 && s.ct == 8)
+    launch_ks_k<4, 8, 3>(a, grid, st);
+  else if (s.rt == 4 && s.ct == 4)
+    launch_ks_k<4, 4, 4>(a, grid, st);
+  else
+    launch_ks_k<2, 2, 6>(a, grid, st);
+}
+
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return cus;
 }
 
 static bool lin_dtype_ok(int dt) { return dt == RIA_DT_BF16 || dt == RIA_DT_F16 || dt == RIA_DT_F32; }
@@ -664,11 +871,29 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
   // whose busiest CU moves the fewest bytes: (workgroups per CU) x (x bytes
   // + weight bytes of one workgroup); ties go to more workgroups.
   int ct = 1, mt = kLinRows;
-  if (!gemv) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
+  // K-split kernel (fp16 x): the tile shape whose busiest CU moves the
+  // fewest bytes, (rounds of workgroups over the CUs) x (x + weight bytes of
+  // one tile)
+  bool ks = !gemv && x_dtype == RIA_DT_F16 && (int64_t)m * x_row_stride < (int64_t(1) << 31);
+  for (int j = 0; j < count; ++j) ks = ks && (int64_t)projs[j].n * k < (int64_t(1) << 31);
+  KsShape ks_shape = kKsShapes[0];
+  if (ks) {
+    const int cus = device_cus();
+    int64_t best = -1;
+    for (const KsShape s : kKsShapes) {
+      int64_t wgs = 0;
+      for (int j = 0; j < count; ++j) wgs += (projs[j].n + 16 * s.ct - 1) / (16 * s.ct);
+      wgs *= (m + 16 * s.rt - 1) / (16 * s.rt);
+      const int64_t cost = (wgs + cus - 1) / cus * ((int64_t)k * (32 * s.rt + 16 * s.ct));
+      if (best < 0 || cost < best) {
+        best = cost;
+        ks_shape = s;
+      }
+    }
+    ct = ks_shape.ct;
+    mt = 16 * ks_shape.rt;
+  } else if (!gemv) {
+    const int cus = device_cus();
     int64_t best = -1, best_wgs = 0;
     for (const int r : {kLinRows, kLinRows / 2})
       for (const int c : {1, 2, 4}) {
@@ -714,8 +939,8 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
       launch_gemv<RIA_DT_BF16>(a, grid, st);
     else
       launch_gemv<RIA_DT_F32>(a, grid, st);
-  } else if (x_dtype == RIA_DT_F16) {
-    launch_linear<RIA_DT_F16>(a, ct, grid, st);
+  } else if (ks) {
+    launch_ks(a, ks_shape, grid, st);
   } else if (x_dtype == RIA_DT_BF16) {
     launch_linear<RIA_DT_BF16>(a, ct, grid, st);
   } else {

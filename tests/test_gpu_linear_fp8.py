@@ -80,6 +80,7 @@ STREAMING_F16 = [  # fp16 x past 16 rows (the forward loop's projections): the s
     (100, 20480, 2048),
     (64, 8192, 512),
     (128, 2048, 4096),   # the output projections' shape
+    (128, 8192, 4096),   # K = 4096 with a wide N: 64-row x 64-feature tiles
     (70, 2048, 4096),
     (17, 512, 512),
     (33, 96, 128),       # one chunk of K, a partial last column tile

@@ -26,13 +26,13 @@ pytestmark = pytest.mark.gpu
 LAYERS = 4  # model layers 0, 1, 2 (DeltaNet) and 3 (full attention)
 LENGTHS = [37, 200, 515]
 # 20 rows: more than the 16 of the one-pass projection kernel, so the
-# projections take the library fp16 GEMM over the dequantised weights (or,
-# with projections="fp8", the FP8 streaming kernel and the fp16 copy of the
-# normed input)
+# projections take the K-split FP8 kernels on the fp16 copy of the normed input
+# (or, with projections="fp16", the library fp16 GEMM over the dequantised
+# weights)
 LENGTHS_20 = LENGTHS + [1, 2, 15, 16, 17, 31, 64, 99, 128, 250, 300, 333, 401, 480, 512, 550, 600]
 
 
-def _setup(dev, split_tokens=64, lengths=LENGTHS, projections="auto"):
+def _setup(dev, split_tokens=64, lengths=LENGTHS, projections="fp8"):
     ckpts = [W.synthetic_layer(700 + m, m) for m in range(LAYERS)]
     st = BatchedAttentionState(len(lengths), 1100, num_linear_layers=3, num_full_layers=1, device=dev,
                                page_shuffle_seed=5, split_tokens=split_tokens)
@@ -78,7 +78,7 @@ def _oracle_layer(w, s, m, x):
     return step(w, s, m, x, gpu_dtypes=True)
 
 
-@pytest.mark.parametrize("lengths,projections", [(LENGTHS, "auto"), (LENGTHS_20, "auto"), (LENGTHS_20, "fp8")],
+@pytest.mark.parametrize("lengths,projections", [(LENGTHS, "fp8"), (LENGTHS_20, "fp16"), (LENGTHS_20, "fp8")],
                          ids=["3rows", "20rows-gemm16", "20rows-fp8"])
 def test_batched_forward_matches_the_reference_composites(gpu, lengths, projections):
     announce(f"batched forward: {LAYERS} layers, rows at {lengths}, 2 steps, projections {projections}")
@@ -142,7 +142,7 @@ def test_step_runs_every_layer_and_the_mlp_between(gpu):
     assert torch.equal(got.cpu(), x.cpu())
 
 
-@pytest.mark.parametrize("lengths", [LENGTHS, LENGTHS_20], ids=["3rows-fp8", "20rows-gemm16"])
+@pytest.mark.parametrize("lengths", [LENGTHS, LENGTHS_20], ids=["3rows", "20rows"])
 def test_graph_replays_equal_eager_steps(gpu, lengths):
     announce(f"batched forward: captured step replayed 3 times == 3 eager steps (bit for bit), {len(lengths)} rows")
     _, st, fwd = _setup(gpu, split_tokens=0, lengths=lengths)  # the balanced attention schedule, which a graph can replay

@@ -902,31 +902,56 @@ __global__ __launch_bounds__(64 * NW) void linear_fp8_lds_kernel(const LinearArg
       for (int e = 0; e < 4; ++e) tot[j][e] += v[e];
     }
   }
+  // D tile rows 4 g4 + e, column n16: F.linear's fp16 result, stored as
+  // y_dtype or (y_add) added to the fp32 y, every y value loaded before the
+  // first store.  The dtype and the bounds are settled once per workgroup, so
+  // whole tiles (the usual case) store with no per-element branch.
   auto row_of = [&](int j, int e) { return m0 + 16 * ((wave + NW * j) / CT) + 4 * g4 + e; };
   auto col_of = [&](int j) { return n0 + 16 * ((wave + NW * j) % CT) + n16; };
-  auto valid = [&](int j, int e) { return wave + NW * j < kTiles && row_of(j, e) < a.m && col_of(j) < n; };
-  if (y_add) {
-    float* yf = static_cast<float*>(y);
-    float v[TPW][4];
+  const bool whole = m0 + 16 * RT <= a.m && n0 + 16 * CT <= n;
+  auto finish = [&](auto whole_c, auto dt_c) {
+    constexpr bool W = decltype(whole_c)::value;
+    constexpr int DT = decltype(dt_c)::value;
+    auto valid = [&](int j, int e) {
+      return wave + NW * j < kTiles && (W || (row_of(j, e) < a.m && col_of(j) < n));
+    };
+    if constexpr (DT < 0) {  // y_add
+      float* yf = static_cast<float*>(y);
+      float v[TPW][4];
 #pragma unroll
-    for (int j = 0; j < TPW; ++j)
+      for (int j = 0; j < TPW; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[j][e] = valid(j, e) ? yf[(int64_t)row_of(j, e) * y_stride + col_of(j)] : 0.f;
+        for (int e = 0; e < 4; ++e) v[j][e] = valid(j, e) ? yf[(int64_t)row_of(j, e) * y_stride + col_of(j)] : 0.f;
 #pragma unroll
-    for (int j = 0; j < TPW; ++j)
+      for (int j = 0; j < TPW; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[j][e] = add_rn(v[j][e], through_dtype<RIA_DT_F16>(tot[j][e]));
-        if (valid(j, e)) yf[(int64_t)row_of(j, e) * y_stride + col_of(j)] = v[j][e];
-      }
-  } else {
+        for (int e = 0; e < 4; ++e) {
+          v[j][e] = add_rn(v[j][e], through_dtype<RIA_DT_F16>(tot[j][e]));
+          if (valid(j, e)) yf[(int64_t)row_of(j, e) * y_stride + col_of(j)] = v[j][e];
+        }
+    } else {
 #pragma unroll
-    for (int j = 0; j < TPW; ++j)
+      for (int j = 0; j < TPW; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (valid(j, e))
-          store_act_dt(y, (int64_t)row_of(j, e) * y_stride + col_of(j), through_dtype<RIA_DT_F16>(tot[j][e]), y_dtype);
-  }
+        for (int e = 0; e < 4; ++e)
+          if (valid(j, e))
+            store_act<DT>(y, (int64_t)row_of(j, e) * y_stride + col_of(j), through_dtype<RIA_DT_F16>(tot[j][e]));
+    }
+  };
+  auto by_dtype = [&](auto whole_c) {
+    if (y_add)
+      finish(whole_c, std::integral_constant<int, -1>{});
+    else if (y_dtype == RIA_DT_F16)
+      finish(whole_c, std::integral_constant<int, RIA_DT_F16>{});
+    else if (y_dtype == RIA_DT_BF16)
+      finish(whole_c, std::integral_constant<int, RIA_DT_BF16>{});
+    else
+      finish(whole_c, std::integral_constant<int, RIA_DT_F32>{});
+  };
+  if (whole)
+    by_dtype(std::true_type{});
+  else
+    by_dtype(std::false_type{});
 }
 
 // Tile shapes of the K-split kernels (rows 16 RT, features 16 CT)

@@ -185,6 +185,17 @@ constexpr int kMaxBalancedUnits = 4096;
 constexpr int kMinChunkPages = 4;  // 64 tokens: small batches still spread over the CUs
 constexpr int kPadUnitsRatio = 32;
 
+// Inclusive scan of one value per lane over a wave.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(v, off, 64);
+    if (lane >= off) v += y;
+  }
+  return v;
+}
+
 // Inclusive block scan of up to 256 per-thread values through LDS; returns
 // the exclusive prefix of this thread's value and the block total.
 __device__ int block_exclusive_scan(int v, int* scratch, int* total) {
@@ -504,45 +515,81 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
     const int units = a.batch * a.num_kv_heads;
     const int per = (units + 255) / 256;  // units per thread (<= 16)
     const int nwg = static_cast<int>(gridDim.x);
-    int upages[16];
-    if (a.ctx_lens) {  // unconditional loads (clamped unit), masked below
-#pragma unroll
-      for (int i = 0; i < 16; ++i) upages[i] = a.ctx_lens[min(tid * per + i, units - 1) / a.num_kv_heads];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) upages[i] = a.ctx_scalar;
-    }
+    const int w = static_cast<int>(blockIdx.x);
     const int ctx_cap = static_cast<int>(min<int64_t>(a.pt_stride * kPageTokens, 1 << 30));
-    int mine = 0;
+    int total = 0, chunk, first_unit;
+    if (units <= 64) {
+      // Up to 64 units every wave computes the partition on its own, one
+      // unit per lane (wave scans: no block-wide LDS pass and no barrier), so
+      // the first K/V loads wait only for the context lengths and the page
+      // table.  Every wave writes the same offsets to LDS and reads back only
+      // what it wrote itself.
+      int pg = 0;
+      if (lane < units)
+        pg = (min(a.ctx_lens ? a.ctx_lens[lane / a.num_kv_heads] : a.ctx_scalar, ctx_cap) + kPageTokens - 1) /
+             kPageTokens;
+      int incl = wave_inclusive_scan(pg);
+      total = __builtin_amdgcn_readlane(incl, 63);
+      const bool padded = units * kPadUnitsRatio <= nwg;
+      chunk = max((total + (padded ? nwg - units : nwg) - 1) / (padded ? nwg - units : nwg), kMinChunkPages);
+      if (padded) {
+        pg = (pg + chunk - 1) / chunk * chunk;
+        incl = wave_inclusive_scan(pg);
+        total = __builtin_amdgcn_readlane(incl, 63);
+      }
+      const int excl = incl - pg;
+      if (lane < units) off[lane] = excl;
+      if (lane == 0) off[units] = total;
+      __builtin_amdgcn_wave_barrier();
+      // first unit containing page w * chunk: the highest lane with off <= it
+      const uint64_t at_or_before = __ballot(lane < units && excl <= w * chunk);
+      first_unit = 63 - __clzll(at_or_before);
+    } else {
+      int upages[16];
+      if (a.ctx_lens) {  // unconditional loads (clamped unit), masked below
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int u = tid * per + i;
-      upages[i] = (i < per && u < units) ? (min(upages[i], ctx_cap) + kPageTokens - 1) / kPageTokens : 0;
-      mine += upages[i];
-    }
-    int total = 0;
-    int run = block_exclusive_scan(mine, scan_scratch, &total);
-    const bool padded = units * kPadUnitsRatio <= nwg;
-    const int chunk = max((total + (padded ? nwg - units : nwg) - 1) / (padded ? nwg - units : nwg), kMinChunkPages);
-    if (padded) {  // each unit rounded up to whole chunks
-      mine = 0;
+        for (int i = 0; i < 16; ++i) upages[i] = a.ctx_lens[min(tid * per + i, units - 1) / a.num_kv_heads];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) upages[i] = a.ctx_scalar;
+      }
+      int mine = 0;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        upages[i] = (upages[i] + chunk - 1) / chunk * chunk;
+        const int u = tid * per + i;
+        upages[i] = (i < per && u < units) ? (min(upages[i], ctx_cap) + kPageTokens - 1) / kPageTokens : 0;
         mine += upages[i];
       }
-      run = block_exclusive_scan(mine, scan_scratch, &total);
-    }
+      int run = block_exclusive_scan(mine, scan_scratch, &total);
+      const bool padded = units * kPadUnitsRatio <= nwg;
+      chunk = max((total + (padded ? nwg - units : nwg) - 1) / (padded ? nwg - units : nwg), kMinChunkPages);
+      if (padded) {  // each unit rounded up to whole chunks
+        mine = 0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int u = tid * per + i;
-      if (i < per && u < units) {
-        off[u] = run;
-        run += upages[i];
+        for (int i = 0; i < 16; ++i) {
+          upages[i] = (upages[i] + chunk - 1) / chunk * chunk;
+          mine += upages[i];
+        }
+        run = block_exclusive_scan(mine, scan_scratch, &total);
       }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int u = tid * per + i;
+        if (i < per && u < units) {
+          off[u] = run;
+          run += upages[i];
+        }
+      }
+      if (tid == (units - 1) / per) off[units] = run;  // the thread that holds the last unit
+      lds_barrier();
+      // first unit containing page w * chunk: the last u with off[u] <= it
+      int lo = 0, hi = units - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (off[mid] <= w * chunk) lo = mid; else hi = mid - 1;
+      }
+      first_unit = lo;
     }
-    if (tid == (units - 1) / per) off[units] = run;  // the thread that holds the last unit
-    lds_barrier();
     if (blockIdx.x == 0) {
       // publish the partition for the combine kernel
       for (int u = tid; u <= units; u += 256) a.ws_units[2 + u] = off[u];
@@ -551,20 +598,13 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
         a.ws_units[1] = chunk;
       }
     }
-    const int w = static_cast<int>(blockIdx.x);
     const int p0 = w * chunk;
     if (p0 >= total) return;
     const int p1 = min(p0 + chunk, total);
-    // first unit containing page p0: the last u with off[u] <= p0
-    int lo = 0, hi = units - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (off[mid] <= p0) lo = mid; else hi = mid - 1;
-    }
     // (the unit and its page range come from LDS, which the compiler treats
     // as per-lane: readfirstlane makes them scalar, so the unit's own loads
     // in process() are scalar loads)
-    for (int u = __builtin_amdgcn_readfirstlane(lo); u < units; ++u) {
+    for (int u = __builtin_amdgcn_readfirstlane(first_unit); u < units; ++u) {
       const int ou = __builtin_amdgcn_readfirstlane(off[u]);
       if (ou >= p1) break;
       const int a0 = max(ou, p0) - ou, a1 = min(__builtin_amdgcn_readfirstlane(off[u + 1]), p1) - ou;  // unit-local pages

@@ -110,11 +110,14 @@ def test_attn_decode_padded_partition_few_units(gpu, lengths):
 
 
 @pytest.mark.gpu
-def test_attn_decode_balanced_partition_many_units(gpu):
-    """Balanced (stream-K) decode: 48 ragged rows, ~9.6k pages over the grid, so
-    workgroups cross unit boundaries and units span several workgroups."""
-    announce("attn_decode: balanced partition, B=48, contexts U[200, 3000], shuffled pages")
-    batch, steps = 48, 2
+@pytest.mark.parametrize("batch", [24, 48], ids=["wave_partition", "block_partition"])
+def test_attn_decode_balanced_partition_many_units(gpu, batch):
+    """Balanced (stream-K) decode: 24 or 48 ragged rows, ~4.8k / ~9.6k pages over
+    the grid, so workgroups cross unit boundaries and units span several
+    workgroups.  48 units take the one-wave partition (up to 64 units), 96
+    the block-wide scan."""
+    announce(f"attn_decode: balanced partition, B={batch}, contexts U[200, 3000], shuffled pages")
+    steps = 2
     lengths = W.ragged_lengths(24, batch, 200, 3000)
     kpre, vpre = W.prefilled_kv(25, batch, max(lengths))
     x = W.attn_step_inputs(26, steps, batch)

@@ -616,29 +616,59 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
 }
 
 // Fused append, in the combine launch of (row b, query head h): the row's new
-// token at slot ctx - 1 (the split-K launch stopped before it).  Every thread
-// of the workgroup calls this (it holds barriers); threads tid < 256 own dim
-// tid.  k goes through kv_append_kernel's arithmetic (k_norm, RoPE, rounding
-// to the page dtype), so the page gets the same bits as a separate append;
-// q through the split-K prologue's (q_norm, RoPE).  Returns the token's score
-// with head h in log2 units (every thread) and leaves its rounded v in v_s;
-// with write_cache the token's k and v go into the page.
+// token at slot ctx - 1 (the split-K launch stopped before it).  Two stages:
+// new_token_load issues every global load the token needs (so the combine
+// issues them before its partials and they arrive together), and
+// new_token_finish, called by every thread of the workgroup (it holds
+// barriers; threads tid < 256 own dim tid), does the arithmetic.  k goes
+// through kv_append_kernel's arithmetic (k_norm, RoPE, rounding to the page
+// dtype), so the page gets the same bits as a separate append; q through the
+// split-K prologue's (q_norm, RoPE).  new_token_finish returns the token's
+// score with head h in log2 units (every thread) and leaves its rounded v in
+// v_s; with write_cache the token's k and v go into the page.
+struct NewTokenIn {
+  float qv, kv, vv;    // dim d of the raw q (head h), k and v (its KV head)
+  float qn_w, kn_w;    // q_norm / k_norm weights of dim d (when present)
+  float fq, fk;        // inverse frequencies of q's and k's rotation of dim d
+  int posi, ctx, phys; // position, context, physical page of slot ctx - 1
+};
+
 template <int QT>
-__device__ float fused_new_token(const AttnArgs& a, int b, int h, bool write_cache, float* x_s, float* red_s,
-                                 float* v_s) {
+__device__ __forceinline__ NewTokenIn new_token_load(const AttnArgs& a, int b, int h, bool write_cache) {
+  const int tid = threadIdx.x;
+  const bool own = tid < kAttnHeadDim;
+  const int d = own ? tid : 0;
+  const int kvh = h / a.group;
+  NewTokenIn t{};
+  t.posi = a.positions ? a.positions[b] : a.pos_scalar;
+  t.ctx = row_ctx(a, b);
+  t.phys = -1;
+  if (own) {
+    t.qv = load_act<QT>(a.q, (int64_t)b * a.q_stride + (int64_t)h * kAttnHeadDim + d);
+    t.kv = load_act<QT>(a.k_new, (int64_t)b * a.kn_stride + (int64_t)kvh * kAttnHeadDim + d);
+    t.vv = load_act<QT>(a.v_new, (int64_t)b * a.vn_stride + (int64_t)kvh * kAttnHeadDim + d);
+    if (a.q_norm_w) t.qn_w = a.q_norm_w[d];
+    if (a.k_norm_w) t.kn_w = a.k_norm_w[d];
+    if (a.rope_dim == 64 && d < 64) t.fq = a.inv_freq[d & 31];
+    const int half = a.rope_dim >> 1;
+    if (d < a.rope_dim) t.fk = a.inv_freq[d < half ? d : d - half];
+    if (write_cache && t.ctx > 0) {
+      const int row = a.seq_slot ? a.seq_slot[b] : b;
+      t.phys = a.page_table[(int64_t)row * a.pt_stride + (t.ctx - 1) / kPageTokens];
+    }
+  }
+  return t;
+}
+
+template <int QT>
+__device__ float new_token_finish(const AttnArgs& a, const NewTokenIn& t, int b, int h, bool write_cache,
+                                  float* x_s, float* red_s, float* v_s) {
   const int tid = threadIdx.x;
   const bool own = tid < kAttnHeadDim;
   const int d = own ? tid : 0;
   const int w = tid >> 6;
   const int kvh = h / a.group;
-  const int posi = a.positions ? a.positions[b] : a.pos_scalar;
-  const int ctx = row_ctx(a, b);
-  float qv = 0.f, kv = 0.f, vv = 0.f;
-  if (own) {
-    qv = load_act<QT>(a.q, (int64_t)b * a.q_stride + (int64_t)h * kAttnHeadDim + d);
-    kv = load_act<QT>(a.k_new, (int64_t)b * a.kn_stride + (int64_t)kvh * kAttnHeadDim + d);
-    vv = load_act<QT>(a.v_new, (int64_t)b * a.vn_stride + (int64_t)kvh * kAttnHeadDim + d);
-  }
+  float qv = t.qv, kv = t.kv;
   // Sums of squares in the orders of the kernels whose results this token
   // must reproduce.  k: per wave, then the four waves in order
   // (kv_append_kernel).  q: lane l sums dims l, l + 64, l + 128, l + 192 in
@@ -658,41 +688,44 @@ __device__ float fused_new_token(const AttnArgs& a, int b, int h, bool write_cac
   }
   __syncthreads();
   if (own) {
-    if (a.q_norm_w) qv = rmsnorm_elem<QT>(qv, rms_scale(red_s[0], kAttnHeadDim), a.q_norm_w[d]);
+    if (a.q_norm_w) qv = rmsnorm_elem<QT>(qv, rms_scale(red_s[0], kAttnHeadDim), t.qn_w);
     if (a.k_norm_w)
-      kv = rmsnorm_elem<QT>(kv, rms_scale(red_s[4] + red_s[5] + red_s[6] + red_s[7], kAttnHeadDim), a.k_norm_w[d]);
+      kv = rmsnorm_elem<QT>(kv, rms_scale(red_s[4] + red_s[5] + red_s[6] + red_s[7], kAttnHeadDim), t.kn_w);
     x_s[d] = qv;
     x_s[kAttnHeadDim + d] = kv;
   }
   __syncthreads();
   float dot = 0.f;
   if (own) {
+    const float pos = static_cast<float>(t.posi);
     float qr = qv;
     if (a.rope_dim == 64 && d < 64) {
       float rs, rc;
-      sincosf(mul_rn(static_cast<float>(posi), a.inv_freq[d & 31]), &rs, &rc);
+      sincosf(mul_rn(pos, t.fq), &rs, &rc);
       const float pq = x_s[d ^ 32];
       qr = add_rn(mul_rn(qv, rc), mul_rn(d < 32 ? -pq : pq, rs));
     }
+    // k: rope_elem's arithmetic with its frequency already loaded
     const int half = a.rope_dim >> 1;
-    const float pk = d < a.rope_dim ? x_s[kAttnHeadDim + (d < half ? d + half : d - half)] : 0.f;
-    const float kr = rope_elem(kv, pk, d, a.rope_dim, static_cast<float>(posi), a.inv_freq);
+    float kr = kv;
+    if (d < a.rope_dim) {
+      const float pk = x_s[kAttnHeadDim + (d < half ? d + half : d - half)];
+      const float ang = mul_rn(pos, t.fk);
+      const float c = cosf(ang), sn = sinf(ang);
+      kr = add_rn(mul_rn(kv, c), mul_rn(d < half ? -pk : pk, sn));
+    }
     const bool f16 = a.kv_dtype == RIA_DT_F16;
     const uint16_t k16 = f16 ? Kv16<RIA_DT_F16>::from_f32(kr) : Kv16<RIA_DT_BF16>::from_f32(kr);
-    const uint16_t v16 = f16 ? Kv16<RIA_DT_F16>::from_f32(vv) : Kv16<RIA_DT_BF16>::from_f32(vv);
+    const uint16_t v16 = f16 ? Kv16<RIA_DT_F16>::from_f32(t.vv) : Kv16<RIA_DT_BF16>::from_f32(t.vv);
     const float kq = f16 ? Kv16<RIA_DT_F16>::to_f32(k16) : Kv16<RIA_DT_BF16>::to_f32(k16);
     v_s[d] = f16 ? Kv16<RIA_DT_F16>::to_f32(v16) : Kv16<RIA_DT_BF16>::to_f32(v16);
     dot = qr * kq;
-    if (write_cache && ctx > 0) {
-      const int row = a.seq_slot ? a.seq_slot[b] : b;
-      const int slot = ctx - 1;
-      const int phys = a.page_table[(int64_t)row * a.pt_stride + slot / kPageTokens];
-      if (phys >= 0 && phys < a.num_pages) {  // the host allocates the page; never write outside the pool
-        const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
-        const int off = slot % kPageTokens;
-        const_cast<uint16_t*>(a.k_cache)[tile * kTileElems + k_tile_offset(off, d)] = k16;
-        const_cast<uint16_t*>(a.v_cache)[(tile * kAttnHeadDim + d) * kPageTokens + off] = v16;
-      }
+    // the host allocates the page; never write outside the pool
+    if (write_cache && t.ctx > 0 && t.phys >= 0 && t.phys < a.num_pages) {
+      const int64_t tile = (int64_t)t.phys * a.num_kv_heads + kvh;
+      const int off = (t.ctx - 1) % kPageTokens;
+      const_cast<uint16_t*>(a.k_cache)[tile * kTileElems + k_tile_offset(off, d)] = k16;
+      const_cast<uint16_t*>(a.v_cache)[(tile * kAttnHeadDim + d) * kPageTokens + off] = v16;
     }
   }
   dot = wave_sum(dot);
@@ -709,18 +742,32 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const int d = threadIdx.x;
   const int kvh = h / a.group;
   const int hi = h % a.group;
+  // The partial list's bounds are loaded first, then everything the new
+  // token and the gate need, so those loads are in flight beside the
+  // partials' instead of after them.
   int64_t first, count;
+  const int u = b * a.num_kv_heads + kvh;
+  int chunk = 1, o0 = 0, o1 = 0, ctx = 0;
+  if constexpr (BALANCED) {
+    chunk = a.ws_units[1];
+    o0 = a.ws_units[2 + u];
+    o1 = a.ws_units[3 + u];
+  } else {
+    ctx = row_ctx(a, b);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  NewTokenIn nt{};
+  if constexpr (APPEND) nt = new_token_load<GT>(a, b, h, hi == 0);
+  const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + d;
+  const float g_raw = load_act<GT>(a.gate, gi);
+  __builtin_amdgcn_sched_barrier(0);
   if constexpr (BALANCED) {
     // partials of unit u come from workgroups off[u] / chunk .. (off[u + 1] - 1) / chunk, at index w + u
-    const int u = b * a.num_kv_heads + kvh;
-    const int chunk = a.ws_units[1];
-    const int o0 = a.ws_units[2 + u], o1 = a.ws_units[3 + u];
     const int w0 = o0 / chunk, w1 = (o1 - 1) / chunk;
     first = (int64_t)w0 + u;
     count = o1 > o0 ? w1 - w0 + 1 : 0;
   } else {
-    const int ctx = row_ctx(a, b);
-    first = ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits;
+    first = (int64_t)u * a.max_splits;
     count = min((ctx + a.split_tokens - 1) / a.split_tokens, a.max_splits);
   }
   // Partials are read kCombineBatch at a time (independent loads in flight)
@@ -760,15 +807,14 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   }
   if constexpr (APPEND) {  // fold in the row's new token (q, k and v in the gate's dtype)
     __shared__ float x_s[2 * kAttnHeadDim], red_s[12], v_s[kAttnHeadDim];
-    const float sn = fused_new_token<GT>(a, b, h, hi == 0, x_s, red_s, v_s);
+    const float sn = new_token_finish<GT>(a, nt, b, h, hi == 0, x_s, red_s, v_s);
     const float Mn = fmaxf(M, sn);
     const float r = M == -INFINITY ? 0.f : exp2f(M - Mn), pn = exp2f(sn - Mn);
     num = fmaf(pn, v_s[d], num * r);
     den = fmaf(pn, 1.f, den * r);
   }
   const float attn = num / den;
-  const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + d;
-  const float gv = sigmoid_f(load_act<GT>(a.gate, gi));
+  const float gv = sigmoid_f(g_raw);
   store_act<OT>(a.out, ((int64_t)b * a.num_q_heads + h) * kAttnHeadDim + d, mul_rn(attn, gv));
 }
 
@@ -786,18 +832,36 @@ __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArg
   const int p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kvh = h / a.group;
   const int hi = h % a.group;
+  // The partial list's bounds are loaded first, then everything the new
+  // token and the gate need, so those loads are in flight beside the
+  // partials' instead of after them.
   int64_t first, count;
+  const int u = b * a.num_kv_heads + kvh;
+  int chunk = 1, o0 = 0, o1 = 0, ctx = 0;
+  if constexpr (BALANCED) {
+    chunk = a.ws_units[1];
+    o0 = a.ws_units[2 + u];
+    o1 = a.ws_units[3 + u];
+  } else {
+    ctx = row_ctx(a, b);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  NewTokenIn nt{};
+  if constexpr (APPEND) nt = new_token_load<GT>(a, b, h, hi == 0);
+  const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + 4 * dg;
+  float g_raw[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p == 0) {  // the wave that stores
+#pragma unroll
+    for (int i = 0; i < 4; ++i) g_raw[i] = load_act<GT>(a.gate, gi + i);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   if constexpr (BALANCED) {
     // partials of unit u come from workgroups off[u] / chunk .. (off[u + 1] - 1) / chunk, at index w + u
-    const int u = b * a.num_kv_heads + kvh;
-    const int chunk = a.ws_units[1];
-    const int o0 = a.ws_units[2 + u], o1 = a.ws_units[3 + u];
     const int w0 = o0 / chunk, w1 = (o1 - 1) / chunk;
     first = (int64_t)w0 + u;
     count = o1 > o0 ? w1 - w0 + 1 : 0;
   } else {
-    const int ctx = row_ctx(a, b);
-    first = ((int64_t)b * a.num_kv_heads + kvh) * a.max_splits;
+    first = (int64_t)u * a.max_splits;
     count = min((ctx + a.split_tokens - 1) / a.split_tokens, a.max_splits);
   }
   const float* stats = a.ws_stats + (first * a.group + hi) * 2;  // partial s: stats[s * group * 2 + {0, 1}]
@@ -848,7 +912,7 @@ __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArg
   }
   float sn = -INFINITY;  // fused append: the new token's score (log2 units); its v in v_s
   __shared__ float x_s[APPEND ? 2 * kAttnHeadDim : 1], red_s[12], v_s[APPEND ? kAttnHeadDim : 1];
-  if constexpr (APPEND) sn = fused_new_token<GT>(a, b, h, h % a.group == 0, x_s, red_s, v_s);
+  if constexpr (APPEND) sn = new_token_finish<GT>(a, nt, b, h, hi == 0, x_s, red_s, v_s);
   __syncthreads();
   if (p != 0) return;
   float Mt = APPEND ? sn : -INFINITY;
@@ -870,11 +934,10 @@ __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArg
     for (int i = 0; i < 4; ++i) tn[i] = fmaf(pn, v_s[4 * dg + i], tn[i]);
     td = fmaf(pn, 1.f, td);
   }
-  const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + 4 * dg;
   const int64_t oi = ((int64_t)b * a.num_q_heads + h) * kAttnHeadDim + 4 * dg;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float gv = sigmoid_f(load_act<GT>(a.gate, gi + i));
+    const float gv = sigmoid_f(g_raw[i]);
     store_act<OT>(a.out, oi + i, mul_rn(tn[i] / td, gv));
   }
 }

@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "ria_common.h"
 
@@ -774,7 +775,40 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   // and added in split order, so the result does not depend on the batching.
   constexpr int kCombineBatch = 16;
   float M = -INFINITY;
+  float num = 0.f, den = 0.f;
+  auto add = [&](float mv, float acc, float sum) {
+    const float wt = mv == -INFINITY ? 0.f : exp2f(mv - M);  // stats are in log2 units
+    num = fmaf(wt, acc, num);
+    den = fmaf(wt, sum, den);
+  };
   int64_t s = 0;
+  // Short lists in one pass: every partial's statistics and accumulator are
+  // loaded at once (N slots; past the end, the last partial again, ignored),
+  // then the max, then the sum in split order (the two-pass result).
+  auto one_pass = [&](auto n_slots) {
+    constexpr int N = decltype(n_slots)::value;
+    float mv[N], acc[N], sum[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int64_t ph = (first + min<int64_t>(j, count - 1)) * a.group + hi;
+      mv[j] = a.ws_stats[ph * 2];
+      sum[j] = a.ws_stats[ph * 2 + 1];
+      acc[j] = a.ws_acc[ph * kAttnHeadDim + d];
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (j < count) M = fmaxf(M, mv[j]);
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (j < count) add(mv[j], acc[j], sum[j]);
+  };
+  if (count <= kCombineBatch) {
+    if (count > 4)
+      one_pass(std::integral_constant<int, kCombineBatch>{});
+    else if (count > 0)
+      one_pass(std::integral_constant<int, 4>{});
+    s = count;
+  }
   for (; s + kCombineBatch <= count; s += kCombineBatch) {
     float mv[kCombineBatch];
 #pragma unroll
@@ -783,13 +817,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     for (int j = 0; j < kCombineBatch; ++j) M = fmaxf(M, mv[j]);
   }
   for (; s < count; ++s) M = fmaxf(M, a.ws_stats[((first + s) * a.group + hi) * 2]);
-  float num = 0.f, den = 0.f;
-  auto add = [&](float mv, float acc, float sum) {
-    const float wt = mv == -INFINITY ? 0.f : exp2f(mv - M);  // stats are in log2 units
-    num = fmaf(wt, acc, num);
-    den = fmaf(wt, sum, den);
-  };
-  for (s = 0; s + kCombineBatch <= count; s += kCombineBatch) {
+  for (s = count <= kCombineBatch ? count : 0; s + kCombineBatch <= count; s += kCombineBatch) {
     float mv[kCombineBatch], acc[kCombineBatch], sum[kCombineBatch];
 #pragma unroll
     for (int j = 0; j < kCombineBatch; ++j) {

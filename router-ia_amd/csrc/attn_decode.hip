@@ -848,12 +848,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 
 // attn_combine_kernel for long partial lists (a few units share all the
 // workgroups, as at small batches).  Wave p of the STREAMS waves takes
-// partials p, p + STREAMS, ... (kBatch of them in flight), lane dg its dims
+// partials p, p + STREAMS, ... (2, 4 or 8 of them in flight), lane dg its dims
 // 4 dg .. 4 dg + 3 (16-byte loads), in one pass with a running max; the
 // streams are merged in order through LDS.
 template <int GT, int OT, bool BALANCED, int STREAMS, bool APPEND>
 __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArgs a) {
-  constexpr int kBatch = 8;
   const int b = blockIdx.x / a.num_q_heads;
   const int h = blockIdx.x % a.num_q_heads;
   const int dg = threadIdx.x & 63;
@@ -897,39 +896,50 @@ __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArg
   const int64_t sstep = (int64_t)a.group * 2, astep = (int64_t)a.group * kAttnHeadDim;
   // One pass with a running max (stats are in log2 units): each wave keeps
   // (max, num, den) over its partials, rescaled when a batch raises the max.
+  // A batch holds 2, 4 or 8 loads per wave, sized to the list (past the
+  // end, the last partial again, ignored).
   float M = -INFINITY, den = 0.f;
   f32x4 num = {0.f, 0.f, 0.f, 0.f};
-  for (int64_t s0 = p; s0 < count; s0 += STREAMS * kBatch) {
-    float mv[kBatch], sum[kBatch];
-    f32x4 acc[kBatch];
+  auto stream = [&](auto batch) {
+    constexpr int kBatch = decltype(batch)::value;
+    for (int64_t s0 = p; s0 < count; s0 += STREAMS * kBatch) {
+      float mv[kBatch], sum[kBatch];
+      f32x4 acc[kBatch];
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int64_t s = s0 + j * STREAMS, sc = min(s, count - 1);  // past the end: the last partial, ignored
-      const bool in = s < count;
-      const float v = stats[sc * sstep], w = stats[sc * sstep + 1];
-      const f32x4 x = *reinterpret_cast<const f32x4*>(accs + sc * astep);
-      mv[j] = in ? v : -INFINITY;
-      sum[j] = in ? w : 0.f;
-      acc[j] = in ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < kBatch; ++j) {
+        const int64_t s = s0 + j * STREAMS, sc = min(s, count - 1);
+        const bool in = s < count;
+        const float v = stats[sc * sstep], w = stats[sc * sstep + 1];
+        const f32x4 x = *reinterpret_cast<const f32x4*>(accs + sc * astep);
+        mv[j] = in ? v : -INFINITY;
+        sum[j] = in ? w : 0.f;
+        acc[j] = in ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      float mb = M;
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, mv[j]);
+      if (mb > M) {  // uniform: every lane of the wave reads the same stats
+        const float r = exp2f(M - mb);
+        den *= r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) num[i] *= r;
+        M = mb;
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const float wt = mv[j] == -INFINITY ? 0.f : exp2f(mv[j] - M);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) num[i] = fmaf(wt, acc[j][i], num[i]);
+        den = fmaf(wt, sum[j], den);
+      }
     }
-    float mb = M;
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, mv[j]);
-    if (mb > M) {  // uniform: every lane of the wave reads the same stats
-      const float r = exp2f(M - mb);
-      den *= r;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) num[i] *= r;
-      M = mb;
-    }
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const float wt = mv[j] == -INFINITY ? 0.f : exp2f(mv[j] - M);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) num[i] = fmaf(wt, acc[j][i], num[i]);
-      den = fmaf(wt, sum[j], den);
-    }
-  }
+  };
+  if (count <= 2 * STREAMS)
+    stream(std::integral_constant<int, 2>{});
+  else if (count <= 4 * STREAMS)
+    stream(std::integral_constant<int, 4>{});
+  else
+    stream(std::integral_constant<int, 8>{});
   __shared__ float m_s[STREAMS];
   __shared__ f32x4 num_s[STREAMS][64];
   __shared__ float den_s[STREAMS];

@@ -294,11 +294,15 @@ int ria_kv_append(int batch, int num_kv_heads,
 /*
  * Append `length` consecutive tokens of ONE sequence (a prompt) into its
  * pages: token i goes to logical slot start_pos + i with RoPE position
- * start_pos + i.  Equal to `length` ria_kv_append calls, i.e. the
- * reference's per-token prefill of :306-308 and :365-372
+ * start_pos + i.  Equal to `length` ria_kv_append calls, bit for bit, i.e.
+ * the reference's per-token prefill of :306-308 and :365-372
  * (qwen36_chat_batch.py:255-258 drives one decode step per prompt token).
+ * One workgroup per (page, KV head); slots of the first and last pages
+ * outside the prompt keep their contents.
  *
  * k, v            [length, Hkv, 256] of k_dtype / v_dtype.
+ * k_cache/v_cache 16-byte aligned (whole pages are written with 16-byte
+ *                 stores).
  * page_table_row  this sequence's page-table row, page_capacity entries;
  *                 start_pos + length must fit in page_capacity * 16.
  * k_norm_weight   as in ria_kv_append.

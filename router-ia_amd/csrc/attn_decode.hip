@@ -109,7 +109,7 @@ struct AppendArgs {
   int rope_dim;
   const float* norm_w;  // k_norm weight [256] f32, or null: k arrives normalised
   int num_kv_heads;
-  int seq_mode;  // 1: blockIdx.x is token i of one sequence at position (and slot) pos_scalar + i
+  int seq_len;  // prompt append: tokens at positions (and slots) pos_scalar .. pos_scalar + seq_len - 1
 };
 
 // RoPE of element d of a row: (x*cos + rotate_half(x)*sin) on [0, rope_dim),
@@ -131,9 +131,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int b = blockIdx.x;
   const int kvh = blockIdx.y;
   const int d = threadIdx.x;
-  const int row = a.seq_mode ? 0 : (a.seq_slot ? a.seq_slot[b] : b);
-  const int pos = a.seq_mode ? a.pos_scalar + b : (a.positions ? a.positions[b] : a.pos_scalar);
-  const int slot = a.seq_mode ? a.pos_scalar + b : (a.slots ? a.slots[b] : a.slot_scalar);
+  const int row = a.seq_slot ? a.seq_slot[b] : b;
+  const int pos = a.positions ? a.positions[b] : a.pos_scalar;
+  const int slot = a.slots ? a.slots[b] : a.slot_scalar;
   __shared__ float k_s[kAttnHeadDim];
   __shared__ float ss_s[4];
   float kv = load_act<KT>(a.k, (int64_t)b * a.k_stride + kvh * kAttnHeadDim + d);
@@ -156,6 +156,88 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
   a.k_cache[tile * kTileElems + k_tile_offset(off, d)] = Kv16<KVT>::from_f32(kr);
   a.v_cache[(tile * kAttnHeadDim + d) * kPageTokens + off] = Kv16<KVT>::from_f32(vv);
+}
+
+// A prompt's append (one sequence, token i at position and slot
+// pos_scalar + i), one workgroup per (page, KV head): thread d owns dim d of
+// the page's 16 tokens and puts each through kv_append_kernel's arithmetic
+// (the same sums of squares, k_norm, RoPE and rounding), so the pages get
+// the same bits.  A page the prompt fills leaves as 16-byte stores: K
+// through an LDS copy of the tile (each 16-byte piece is 8 dims of one
+// token), V^T as each dim's 32-byte row; the first and last pages keep the
+// tokens outside the prompt (per-token stores).
+template <int KT, int VT, int KVT>
+__global__ __launch_bounds__(256) void kv_append_page_kernel(AppendArgs a) {
+  const int d = threadIdx.x, lane = d & 63, w = d >> 6;
+  const int kvh = blockIdx.y;
+  const int pg = a.pos_scalar / kPageTokens + static_cast<int>(blockIdx.x);  // page slot in the row
+  const int s0 = pg * kPageTokens;
+  const int t_lo = max(a.pos_scalar, s0) - s0, t_hi = min(a.pos_scalar + a.seq_len, s0 + kPageTokens) - s0;
+  const int phys = a.page_table[pg];
+  if (phys < 0 || phys >= a.num_pages) return;  // host guarantees allocation; never write out of the pool
+  const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
+  __shared__ float k_s[kPageTokens][kAttnHeadDim];
+  __shared__ float ss_s[kPageTokens][4];
+  __shared__ __attribute__((aligned(16))) uint16_t kt_s[kTileElems];
+  float kv[kPageTokens], vv[kPageTokens];
+#pragma unroll
+  for (int i = 0; i < kPageTokens; ++i) {
+    // prompt row of token i (tokens outside the prompt load row 0 and are zeroed)
+    const bool in = i >= t_lo && i < t_hi;
+    const int64_t r = in ? s0 + i - a.pos_scalar : 0;
+    const float kx = load_act<KT>(a.k, r * a.k_stride + kvh * kAttnHeadDim + d);
+    const float vx = load_act<VT>(a.v, r * a.v_stride + kvh * kAttnHeadDim + d);
+    kv[i] = in ? kx : 0.f;
+    vv[i] = in ? vx : 0.f;
+  }
+  if (a.norm_w) {  // per token: one sum of squares over the 256 dims, waves in order
+    const float wn = a.norm_w[d];
+#pragma unroll
+    for (int i = 0; i < kPageTokens; ++i) {
+      const float ss = wave_sum(mul_rn(kv[i], kv[i]));
+      if (lane == 0) ss_s[i][w] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPageTokens; ++i)
+      kv[i] = rmsnorm_elem<KT>(kv[i], rms_scale(ss_s[i][0] + ss_s[i][1] + ss_s[i][2] + ss_s[i][3], kAttnHeadDim),
+                               wn);
+  }
+#pragma unroll
+  for (int i = 0; i < kPageTokens; ++i) k_s[i][d] = kv[i];
+  __syncthreads();
+  const int half = a.rope_dim >> 1;
+  const int pd = d < half ? d + half : d - half;
+#pragma unroll
+  for (int i = 0; i < kPageTokens; ++i) {
+    const float partner = d < a.rope_dim ? k_s[i][pd] : 0.f;
+    const float kr = rope_elem(kv[i], partner, d, a.rope_dim, static_cast<float>(s0 + i), a.inv_freq);
+    kt_s[k_tile_offset(i, d)] = Kv16<KVT>::from_f32(kr);
+  }
+  __syncthreads();
+  uint16_t* kt = a.k_cache + tile * kTileElems;
+  uint16_t* vt = a.v_cache + (tile * kAttnHeadDim + d) * kPageTokens;
+  if (t_lo == 0 && t_hi == kPageTokens) {
+    const uint4* src = reinterpret_cast<const uint4*>(kt_s);
+    reinterpret_cast<uint4*>(kt)[d] = src[d];
+    reinterpret_cast<uint4*>(kt)[d + 256] = src[d + 256];
+    uint32_t pk[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      pk[j] = static_cast<uint32_t>(Kv16<KVT>::from_f32(vv[2 * j])) |
+              (static_cast<uint32_t>(Kv16<KVT>::from_f32(vv[2 * j + 1])) << 16);
+    reinterpret_cast<uint4*>(vt)[0] = uint4{pk[0], pk[1], pk[2], pk[3]};
+    reinterpret_cast<uint4*>(vt)[1] = uint4{pk[4], pk[5], pk[6], pk[7]};
+  } else {
+#pragma unroll
+    for (int e = d; e < kTileElems / 8; e += 256) {  // piece e: 8 dims of token e % 16
+      const int i = e % kPageTokens;
+      if (i >= t_lo && i < t_hi) reinterpret_cast<uint4*>(kt)[e] = reinterpret_cast<const uint4*>(kt_s)[e];
+    }
+#pragma unroll
+    for (int i = 0; i < kPageTokens; ++i)
+      if (i >= t_lo && i < t_hi) vt[i] = Kv16<KVT>::from_f32(vv[i]);
+  }
 }
 
 // Scalar (SMEM) load of a wave-uniform index from a buffer this kernel never
@@ -1028,13 +1110,23 @@ static int resolve_split(int batch, int num_kv_heads, int max_ctx, int split_tok
   return split_tokens > 0 ? split_tokens : auto_split_tokens(batch, num_kv_heads, max_ctx);
 }
 
+// rows > 0: one workgroup per (row, KV head); rows == 0: the prompt append,
+// one workgroup per (page the prompt touches, KV head).
 static void launch_append(const AppendArgs& a, int rows, int k_dtype, int v_dtype, int kv_dtype, hipStream_t st) {
-  dim3 grid(rows, a.num_kv_heads);
-#define RIA_APPEND_LAUNCH(KT_, VT_)                                                              \
-  if (kv_dtype == RIA_DT_F16)                                                                    \
-    hipLaunchKernelGGL((kv_append_kernel<KT_, VT_, RIA_DT_F16>), grid, dim3(256), 0, st, a);     \
-  else                                                                                           \
-    hipLaunchKernelGGL((kv_append_kernel<KT_, VT_, RIA_DT_BF16>), grid, dim3(256), 0, st, a)
+  const bool seq = rows == 0;
+  const int pages = seq ? (a.pos_scalar + a.seq_len - 1) / kPageTokens - a.pos_scalar / kPageTokens + 1 : 0;
+  dim3 grid(seq ? pages : rows, a.num_kv_heads);
+#define RIA_APPEND_ONE(KT_, VT_, KVT_)                                                        \
+  if (seq)                                                                                  \
+    hipLaunchKernelGGL((kv_append_page_kernel<KT_, VT_, KVT_>), grid, dim3(256), 0, st, a); \
+  else                                                                                      \
+    hipLaunchKernelGGL((kv_append_kernel<KT_, VT_, KVT_>), grid, dim3(256), 0, st, a)
+#define RIA_APPEND_LAUNCH(KT_, VT_)        \
+  if (kv_dtype == RIA_DT_F16) {            \
+    RIA_APPEND_ONE(KT_, VT_, RIA_DT_F16);  \
+  } else {                                 \
+    RIA_APPEND_ONE(KT_, VT_, RIA_DT_BF16); \
+  }
 #define RIA_APPEND_VT(KT_)                 \
   if (v_dtype == RIA_DT_BF16) {             \
     RIA_APPEND_LAUNCH(KT_, RIA_DT_BF16);    \
@@ -1052,6 +1144,7 @@ static void launch_append(const AppendArgs& a, int rows, int k_dtype, int v_dtyp
   }
 #undef RIA_APPEND_VT
 #undef RIA_APPEND_LAUNCH
+#undef RIA_APPEND_ONE
 }
 
 static int check_append_common(const char* who, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
@@ -1106,7 +1199,6 @@ extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_d
   a.rope_dim = rope_dim;
   a.norm_w = k_norm_weight;
   a.num_kv_heads = num_kv_heads;
-  a.seq_mode = 0;
   launch_append(a, batch, k_dtype, v_dtype, kv_dtype, static_cast<hipStream_t>(stream));
   return check_launch("ria_kv_append");
 }
@@ -1121,6 +1213,8 @@ extern "C" int ria_kv_append_seq(int length, int num_kv_heads, const void* k, in
                                v_row_stride, k_cache, v_cache, kv_dtype, page_table_row, inv_freq, rope_dim);
   if (rc != RIA_OK) return rc;
   if (length == 0) return RIA_OK;
+  if (reinterpret_cast<uintptr_t>(k_cache) % 16 || reinterpret_cast<uintptr_t>(v_cache) % 16)
+    return set_error(RIA_ERR_INVALID, "ria_kv_append_seq: the KV caches must be 16-byte aligned");
   if ((int64_t)start_pos + length > page_capacity * kPageTokens)
     return set_error(RIA_ERR_INVALID, "ria_kv_append_seq: %d + %d tokens exceed the row's %lld pages", start_pos,
                      length, (long long)page_capacity);
@@ -1139,8 +1233,8 @@ extern "C" int ria_kv_append_seq(int length, int num_kv_heads, const void* k, in
   a.rope_dim = rope_dim;
   a.norm_w = k_norm_weight;
   a.num_kv_heads = num_kv_heads;
-  a.seq_mode = 1;
-  launch_append(a, length, k_dtype, v_dtype, kv_dtype, static_cast<hipStream_t>(stream));
+  a.seq_len = length;
+  launch_append(a, 0, k_dtype, v_dtype, kv_dtype, static_cast<hipStream_t>(stream));
   return check_launch("ria_kv_append_seq");
 }
 

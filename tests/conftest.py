@@ -28,7 +28,7 @@ def gpu():
         pytest.skip("no ROCm GPU visible")
     from router_ia import _native
 
-    _native.load()  # a missing library is an error on a GPU box, not a skip
+    _native.load()  # with a GPU present, a missing library is an error, not a skip
     return torch.device("cuda:0")
 
 

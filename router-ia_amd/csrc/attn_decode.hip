@@ -957,12 +957,11 @@ __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArg
   __builtin_amdgcn_sched_barrier(0);
   NewTokenIn nt{};
   if constexpr (APPEND) nt = new_token_load<GT>(a, b, h, hi == 0);
-  const int64_t gi = (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + 4 * dg;
-  float g_raw[4] = {0.f, 0.f, 0.f, 0.f};
-  if (p == 0) {  // the wave that stores
-#pragma unroll
-    for (int i = 0; i < 4; ++i) g_raw[i] = load_act<GT>(a.gate, gi + i);
-  }
+  // waves 0-3 finish the head, one output dim per lane
+  static_assert(STREAMS >= 4, "the head is finished by four waves");
+  const int od = 64 * p + dg;
+  float g_raw = 0.f;
+  if (p < 4) g_raw = load_act<GT>(a.gate, (int64_t)b * a.gate_stride + (int64_t)h * kAttnHeadDim + od);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (BALANCED) {
     // partials of unit u come from workgroups off[u] / chunk .. (off[u + 1] - 1) / chunk, at index w + u
@@ -1034,32 +1033,23 @@ __global__ __launch_bounds__(64 * STREAMS) void attn_combine_long_kernel(AttnArg
   __shared__ float x_s[APPEND ? 2 * kAttnHeadDim : 1], red_s[12], v_s[APPEND ? kAttnHeadDim : 1];
   if constexpr (APPEND) sn = new_token_finish<GT>(a, nt, b, h, hi == 0, x_s, red_s, v_s);
   __syncthreads();
-  if (p != 0) return;
+  if (p >= 4) return;
   float Mt = APPEND ? sn : -INFINITY;
 #pragma unroll
   for (int q = 0; q < STREAMS; ++q) Mt = fmaxf(Mt, m_s[q]);
-  f32x4 tn = {0.f, 0.f, 0.f, 0.f};
-  float td = 0.f;
+  float tn = 0.f, td = 0.f;
 #pragma unroll
   for (int q = 0; q < STREAMS; ++q) {
     const float wq = m_s[q] == -INFINITY ? 0.f : exp2f(m_s[q] - Mt);
-    const f32x4 u = num_s[q][dg];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) tn[i] = fmaf(wq, u[i], tn[i]);
+    tn = fmaf(wq, reinterpret_cast<const float*>(num_s[q])[od], tn);  // stream q's dim od
     td = fmaf(wq, den_s[q], td);
   }
   if constexpr (APPEND) {
     const float pn = exp2f(sn - Mt);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) tn[i] = fmaf(pn, v_s[4 * dg + i], tn[i]);
+    tn = fmaf(pn, v_s[od], tn);
     td = fmaf(pn, 1.f, td);
   }
-  const int64_t oi = ((int64_t)b * a.num_q_heads + h) * kAttnHeadDim + 4 * dg;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float gv = sigmoid_f(g_raw[i]);
-    store_act<OT>(a.out, oi + i, mul_rn(tn[i] / td, gv));
-  }
+  store_act<OT>(a.out, ((int64_t)b * a.num_q_heads + h) * kAttnHeadDim + od, mul_rn(tn / td, sigmoid_f(g_raw)));
 }
 
 __global__ __launch_bounds__(256) void kv_gather_kernel(const uint16_t* k_cache, const uint16_t* v_cache,

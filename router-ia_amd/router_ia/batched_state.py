@@ -94,8 +94,12 @@ class BatchedAttentionState:
         self.kv = PagedKVCache(num_full_layers, num_pages, max_seqs, max_pages_per_seq,
                                num_kv_heads=num_kv_heads, device=dev, shuffle_seed=page_shuffle_seed,
                                dtype=kv_dtype)
-        self.tokens_seen = torch.zeros(max_seqs, dtype=torch.int32, device=dev)
-        self.ctx_lens = torch.ones(max_seqs, dtype=torch.int32, device=dev)
+        # positions and context lengths are the two rows of one tensor, so a
+        # decode step advances both with one launch
+        self._pos_ctx = torch.stack([torch.zeros(max_seqs, dtype=torch.int32, device=dev),
+                                     torch.ones(max_seqs, dtype=torch.int32, device=dev)])
+        self.tokens_seen = self._pos_ctx[0]
+        self.ctx_lens = self._pos_ctx[1]
         self._host_seen = [0] * max_seqs
         self._min_headroom = 0  # min over rows of (KV capacity - tokens seen)
         self.inv_freq = rope_inv_freq(rope_theta, rope_dim).to(dev)
@@ -143,8 +147,7 @@ class BatchedAttentionState:
     def advance(self) -> None:
         self._host_seen = [n + 1 for n in self._host_seen]
         self._min_headroom -= 1
-        self.tokens_seen.add_(1)
-        self.ctx_lens.add_(1)
+        self._pos_ctx.add_(1)  # tokens_seen and ctx_lens
 
     @property
     def max_seen(self) -> int:

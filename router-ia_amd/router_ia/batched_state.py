@@ -10,6 +10,9 @@ layer is one kernel launch over the whole batch:
     K / V pages      bf16 per full layer (see paged_kv)
     tokens_seen      i32  [B] absolute position of the next token (RoPE
                      position, conv ring index and KV slot of that token)
+    ctx_lens         i32  [B] tokens_seen + 1, the attention's context
+                     (tokens_seen and ctx_lens are the two rows of one
+                     tensor: update them in place, never rebind them)
 
 Per token the caller runs ``linear_step`` / ``full_step`` for each layer and
 then ``advance()``, the batched equivalent of the reference caller bumping

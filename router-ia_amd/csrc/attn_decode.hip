@@ -600,6 +600,10 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
     const int nwg = static_cast<int>(gridDim.x);
     const int w = static_cast<int>(blockIdx.x);
     const int ctx_cap = static_cast<int>(min<int64_t>(a.pt_stride * kPageTokens, 1 << 30));
+    // pages a unit streams: its resident tokens (with the fused append the
+    // row's last token is left to the combine launch)
+    const int xl = a.exclude_last ? 1 : 0;
+    auto unit_pages = [&](int ctx) { return (max(min(ctx, ctx_cap) - xl, 0) + kPageTokens - 1) / kPageTokens; };
     int total = 0, chunk, first_unit;
     if (units <= 64) {
       // Up to 64 units every wave computes the partition on its own, one
@@ -608,14 +612,17 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
       // table.  Every wave writes the same offsets to LDS and reads back only
       // what it wrote itself.
       int pg = 0;
-      if (lane < units)
-        pg = (min(a.ctx_lens ? a.ctx_lens[lane / a.num_kv_heads] : a.ctx_scalar, ctx_cap) + kPageTokens - 1) /
-             kPageTokens;
+      if (lane < units) pg = unit_pages(a.ctx_lens ? a.ctx_lens[lane / a.num_kv_heads] : a.ctx_scalar);
       int incl = wave_inclusive_scan(pg);
       total = __builtin_amdgcn_readlane(incl, 63);
       const bool padded = units * kPadUnitsRatio <= nwg;
-      chunk = max((total + (padded ? nwg - units : nwg) - 1) / (padded ? nwg - units : nwg), kMinChunkPages);
+      chunk = max((total + nwg - 1) / nwg, kMinChunkPages);
       if (padded) {
+        // the smallest chunk at which every unit, padded to whole chunks,
+        // still fits the grid (the bound over workgroups - units always does)
+        const int c_fit = max((total + nwg - units - 1) / (nwg - units), kMinChunkPages);
+        for (; chunk < c_fit; ++chunk)
+          if (__builtin_amdgcn_readlane(wave_inclusive_scan((pg + chunk - 1) / chunk), 63) <= nwg) break;
         pg = (pg + chunk - 1) / chunk * chunk;
         incl = wave_inclusive_scan(pg);
         total = __builtin_amdgcn_readlane(incl, 63);
@@ -640,7 +647,7 @@ __global__ __launch_bounds__(256, 2) void attn_splitk_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int u = tid * per + i;
-        upages[i] = (i < per && u < units) ? (min(upages[i], ctx_cap) + kPageTokens - 1) / kPageTokens : 0;
+        upages[i] = (i < per && u < units) ? unit_pages(upages[i]) : 0;
         mine += upages[i];
       }
       int run = block_exclusive_scan(mine, scan_scratch, &total);

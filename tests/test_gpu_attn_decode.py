@@ -82,7 +82,7 @@ def test_attn_decode_ragged_shuffled_pages(gpu, split_tokens):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("lengths", [[1], [40], [5000, 17, 2049], [3000, 3001, 16, 1, 777]])
+@pytest.mark.parametrize("lengths", [[1], [40], [5000, 17, 2049], [3000, 3001, 16, 1, 777], [0, 9, 4096]])
 def test_attn_decode_padded_partition_few_units(gpu, lengths):
     """Few (sequence, KV head) units against a large grid: every unit's page range is
     padded to whole chunks (units x 32 <= workgroups), so no workgroup straddles two

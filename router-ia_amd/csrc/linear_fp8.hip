@@ -25,8 +25,8 @@
 //                        one chunk ahead.  Decode-sized M is bound by the
 //                        weight stream.  Used past 16 rows for bf16 and
 //                        fp32 x.
-//   linear_fp8_lds_kernel past 16 rows with fp16 x and K = 2048 or 4096 (the
-//                        forward loop's projections): one workgroup per tile
+//   linear_fp8_lds_kernel past 16 rows with fp16 x and K = 2048 (the forward
+//                        loop's input projections): one workgroup per tile
 //                        of rows x features over the whole K, split between
 //                        its waves; each wave copies its x and weight rows
 //                        into its own LDS ring with row-contiguous
@@ -982,17 +982,18 @@ static void launch_ks_k(const LinearArgs& a, dim3 grid, hipStream_t st) {
   hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, 4, D, 0>), grid, dim3(256), 0, st, a);
 }
 
-// K = 2048 (the model's hidden width) and 4096 (its value width) take the
-// LDS-staged kernel: four waves at K = 2048, eight at K = 4096 (where the
-// tiles are narrow and more waves keep more loads in flight); any other K the
-// register-streaming kernel with four waves.  The wave count depends on K
+// K = 2048 (the model's hidden width) takes the LDS-staged kernel with four
+// waves; any other K, the value width 4096 included, the register-streaming
+// kernel with four waves.  (The eight-wave LDS-staged instances for K = 4096
+// are not launched: twice in about ten full test runs one of their results
+// differed from a repeat of the same call, and no cause has been found.)  The wave count depends on K
 // alone, and every shape runs the waves over the same chunks in the same
 // order, so a projection's result does not depend on the tile shape chosen
 // for it (grouped and separate calls agree bit for bit).
 static bool ks_shape_ok(KsShape s, int k) { return !(k == 4096 && s.rt == 4 && s.ct == 8); }
 
 static void launch_ks(const LinearArgs& a, KsShape s, dim3 grid, hipStream_t st) {
-  const dim3 b4(256), b8(512);
+  const dim3 b4(256);
   if (a.k == 2048) {
     if (s.rt == 4 && s.ct == 8)
       hipLaunchKernelGGL((linear_fp8_lds_kernel<4, 8, 4, 2, 8>), grid, b4, 0, st, a);
@@ -1000,11 +1001,6 @@ static void launch_ks(const LinearArgs& a, KsShape s, dim3 grid, hipStream_t st)
       hipLaunchKernelGGL((linear_fp8_lds_kernel<4, 4, 4, 3, 8>), grid, b4, 0, st, a);
     else
       hipLaunchKernelGGL((linear_fp8_lds_kernel<2, 2, 4, 6, 8>), grid, b4, 0, st, a);
-  } else if (a.k == 4096) {
-    if (s.rt == 4 && s.ct == 4)
-      hipLaunchKernelGGL((linear_fp8_lds_kernel<4, 4, 8, 1, 8>), grid, b8, 0, st, a);
-    else
-      hipLaunchKernelGGL((linear_fp8_lds_kernel<2, 2, 8, 3, 8>), grid, b8, 0, st, a);
   } else if (s.rt == 4 && s.ct == 8) {
     launch_ks_k<4, 8, 3>(a, grid, st);
   } else if (s.rt == 4 && s.ct == 4) {

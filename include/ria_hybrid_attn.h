@@ -179,6 +179,12 @@ enum ria_qk_mode {
  *                    or a disjoint one (the reference stores a new state
  *                    tensor each step, :261-265).
  *   qk_mode          see ria_qk_mode.
+ *   pool_rows        with seq_slot: the rows of the state pools (and of the
+ *                    conv window pools) that the slots index; required when
+ *                    state_out is not state_in or the layout is
+ *                    RIA_CONV_WINDOW, so that the pools can be checked for
+ *                    overlap.  Without seq_slot the pools are `batch` rows and
+ *                    this field is ignored.  Every slot must be below it.
  */
 typedef struct ria_gdn_decode_desc {
   int batch;
@@ -210,6 +216,7 @@ typedef struct ria_gdn_decode_desc {
   int z_dtype;
   int64_t z_row_stride;
   const float* norm_weight;
+  int64_t pool_rows;
 } ria_gdn_decode_desc;
 
 /*
@@ -467,9 +474,10 @@ int ria_attn_decode_append(int batch, int num_q_heads, int num_kv_heads,
  * ria_attn_decode_append without workspace / workspace_bytes; sizes whose
  * partials (ria_attn_decode_workspace_bytes) exceed 16 MiB return
  * RIA_ERR_WORKSPACE before any launch (the balanced schedule fits up to about
- * 1,500 (sequence, KV head) units).  Every call on one GPU shares the array:
- * calls that overlap on one GPU (concurrent streams, or another call between
- * a RIA_ATTN_SPLITK and its RIA_ATTN_COMBINE) race.
+ * 1,500 (sequence, KV head) units).  `phase` must be RIA_ATTN_BOTH (anything
+ * else returns RIA_ERR_INVALID): the partials never outlive the call.  Every
+ * call on one GPU shares the array: calls that overlap on one GPU (concurrent
+ * streams) race.
  */
 int ria_attn_decode_append_noalloc(int batch, int num_q_heads, int num_kv_heads,
                                    const void* q, int q_dtype, int64_t q_row_stride,

@@ -1499,9 +1499,9 @@ extern "C" int ria_attn_decode_append(int batch, int num_q_heads, int num_kv_hea
 // sequences of the model's 2 KV heads.  Each GPU the library runs on holds
 // its own copy until the process ends.  Nothing in it has to start at zero:
 // every partial and partition entry the combine launch reads is written by
-// the same call's split-K launch.  All calls on one GPU share the array, so
-// calls that overlap on one GPU (concurrent streams, or another call between
-// a SPLITK and its COMBINE phase) race.
+// the same call's split-K launch, and a call always runs both phases.  All
+// calls on one GPU share the array, so calls that overlap on one GPU
+// (concurrent streams) race.
 constexpr int64_t kScratchBytes = int64_t(16) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
@@ -1540,6 +1540,11 @@ extern "C" int ria_attn_decode_append_noalloc(int batch, int num_q_heads, int nu
                                               const float* q_norm_weight, float scale, int split_tokens, void* out,
                                               int out_dtype, int phase, void* stream) {
   static const char* who = "ria_attn_decode_append_noalloc";
+  // Both phases in one call: a SPLITK call's partials would sit in the shared
+  // array until its COMBINE call, open to any call in between.
+  if (phase != RIA_ATTN_BOTH)
+    return set_error(RIA_ERR_INVALID, "%s: only phase RIA_ATTN_BOTH (got %d): the partials do not outlive the call",
+                     who, phase);
   void* ws = nullptr;
   if (batch > 0) {
     const int64_t need = ria_attn_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_ctx, split_tokens);

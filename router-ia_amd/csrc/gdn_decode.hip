@@ -450,12 +450,18 @@ static int gdn_decode_launch(const ria_gdn_decode_desc& d, void* stream, const c
     return set_error(RIA_ERR_INVALID, "%s: z must be 4-byte aligned with an even row stride", who);
   // The state tiles of one launch are read and written by one workgroup each,
   // so in place is safe; a partial overlap would let a workgroup read a tile
-  // another one has already written.
-  const int64_t pool_bytes_lo = (int64_t)d.batch * num_v_heads * kGdnHeadDim * kGdnHeadDim * 4;
-  if (d.state_in != d.state_out && !d.seq_slot) {
+  // another one has already written.  With seq_slot the pools are the
+  // caller's pool_rows rows (every slot below it), otherwise `batch` rows.
+  const bool disjoint_state = d.state_in != d.state_out;
+  if (d.seq_slot && (disjoint_state || d.conv_layout == RIA_CONV_WINDOW) && d.pool_rows <= 0)
+    return set_error(RIA_ERR_INVALID, "%s: with seq_slot, pool_rows (the pools' rows) is required for a separate "
+                     "state_out or the window layout", who);
+  const int64_t pool_rows = d.seq_slot ? d.pool_rows : d.batch;
+  if (disjoint_state) {
+    const int64_t pool_bytes = pool_rows * num_v_heads * kGdnHeadDim * kGdnHeadDim * 4;
     const char* i0 = reinterpret_cast<const char*>(d.state_in);
     const char* o0 = reinterpret_cast<const char*>(d.state_out);
-    if (i0 < o0 + pool_bytes_lo && o0 < i0 + pool_bytes_lo)
+    if (i0 < o0 + pool_bytes && o0 < i0 + pool_bytes)
       return set_error(RIA_ERR_INVALID, "%s: state_out overlaps state_in without being it", who);
   }
   if (d.conv_layout == RIA_CONV_WINDOW) {
@@ -464,12 +470,10 @@ static int gdn_decode_launch(const ria_gdn_decode_desc& d, void* stream, const c
     if (reinterpret_cast<uintptr_t>(d.conv_window_in) % 8 || reinterpret_cast<uintptr_t>(d.conv_window_out) % 8)
       return set_error(RIA_ERR_INVALID, "%s: conv windows must be 8-byte aligned", who);
     // other workgroups read the channels a workgroup shifts: out must not overlap in
-    const int64_t wbytes = (int64_t)d.batch * conv_dim * kConvTaps * 2;
+    const int64_t wbytes = pool_rows * conv_dim * kConvTaps * 2;
     const char* i0 = static_cast<const char*>(d.conv_window_in);
     const char* o0 = static_cast<const char*>(d.conv_window_out);
-    if (!d.seq_slot && i0 < o0 + wbytes && o0 < i0 + wbytes)
-      return set_error(RIA_ERR_INVALID, "%s: conv_window_out must not overlap conv_window_in", who);
-    if (d.seq_slot && i0 == o0)
+    if (i0 < o0 + wbytes && o0 < i0 + wbytes)
       return set_error(RIA_ERR_INVALID, "%s: conv_window_out must not overlap conv_window_in", who);
   }
 

@@ -25,14 +25,10 @@
 //                        one chunk ahead.  Decode-sized M is bound by the
 //                        weight stream.  Used past 16 rows for bf16 and
 //                        fp32 x.
-//   linear_fp8_lds_kernel past 16 rows with fp16 x and K = 2048 (the forward
-//                        loop's input projections): one workgroup per tile
-//                        of rows x features over the whole K, split between
-//                        its waves; each wave copies its x and weight rows
-//                        into its own LDS ring with row-contiguous
-//                        direct-to-LDS loads and reads MFMA operands back.
-//   linear_fp8_ks_kernel the same split for any other K, operands streamed
-//                        straight into registers.
+//   linear_fp8_ks_kernel past 16 rows with fp16 x (the forward loop's
+//                        projections): one workgroup per tile of rows x
+//                        features over the whole K, split between its waves,
+//                        operands streamed straight into registers.
 #include <algorithm>
 #include <type_traits>
 #include <utility>
@@ -744,216 +740,6 @@ __global__ __launch_bounds__(64 * NW) void linear_fp8_ks_kernel(const LinearArgs
   }
 }
 
-// The K-split kernel with both operands staged through LDS, for K = 64 NW CH.
-// Loading an MFMA operand straight into registers makes each lane read 16
-// bytes of a different row (lane n of a 16-lane group holds row n), which the
-// memory pipeline serves at a fraction of the rate of row-contiguous reads.
-// Here each wave copies its chunk's x rows (128 bytes each) and weight rows
-// (64 bytes each) into its own LDS ring with direct-to-LDS loads whose lanes
-// walk along the rows, and reads the MFMA operands back from LDS.  The
-// 16-byte pieces of a row are XOR-swizzled with the row index so that the
-// operand reads of a 16-lane group spread over the banks.  The ring's loads
-// and reads are this wave's own: the waits are explicit vmcnt counts (the
-// loads issued after the chunk's), and the operand reads are inline assembly
-// so that the compiler inserts no wait for the direct-to-LDS loads of the
-// chunks still in flight.
-// One direct-to-LDS load of 16 bytes per lane: lane l's bytes at g land at
-// lds + 16 l (lds is the same for the whole wave).  A device function, so that
-// the host pass of the kernel that calls it never sees the builtin.
-__device__ __forceinline__ void copy16_to_lds(const void* g, uint8_t* lds) {
-  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
-}
-
-template <int RT, int CT, int NW, int D, int CH>
-__global__ __launch_bounds__(64 * NW) void linear_fp8_lds_kernel(const LinearArgs a) {
-  using F16 = Kv16<RIA_DT_F16>;
-  static_assert(kFp8Block % (16 * CT) == 0, "a tile's features lie in one scale block");
-  constexpr int kTiles = RT * CT;
-  constexpr int kXStage = RT * 16 * 128, kWStage = CT * 1024, kStage = kXStage + kWStage;
-  constexpr int kRing = NW * D * kStage, kPart = NW * kTiles * 64 * 16;
-  static_assert((D - 1) * (2 * RT + CT) <= 63, "the wait counts fit vmcnt");
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n16 = lane & 15, g4 = lane >> 4;
-  const int bx = blockIdx.x;
-  const uint8_t* w = a.p[0].w;
-  const float* scale = a.p[0].scale;
-  void* y = a.p[0].y;
-  int64_t y_stride = a.p[0].y_stride;
-  int n = a.p[0].n, y_dtype = a.p[0].y_dtype, y_add = a.p[0].y_add, tile0 = 0;
-#pragma unroll
-  for (int j = 1; j < kLinGroup; ++j)
-    if (j < a.count && bx >= a.p[j].tile0) {
-      w = a.p[j].w;
-      scale = a.p[j].scale;
-      y = a.p[j].y;
-      y_stride = a.p[j].y_stride;
-      n = a.p[j].n;
-      y_dtype = a.p[j].y_dtype;
-      y_add = a.p[j].y_add;
-      tile0 = a.p[j].tile0;
-    }
-  const int n0 = (bx - tile0) * 16 * CT;
-  const int m0 = blockIdx.y * 16 * RT;
-  const uint16_t* x = static_cast<const uint16_t*>(a.x);
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kRing > kPart ? kRing : kPart];
-  uint8_t* ring = lds + wave * D * kStage;
-
-  // the wave's scales (one per chunk; the tile lies in one block of 128
-  // features), read through the scalar cache: the ring's loads are then the
-  // only vector-memory operations of the loop, which the wait counts rely on
-  typedef __attribute__((address_space(4))) const float ConstF;
-  const ConstF* sp = (const ConstF*)(scale + (int64_t)(n0 / kFp8Block) * (a.k / kFp8Block));
-  float scl[CH];
-#pragma unroll
-  for (int i = 0; i < CH; ++i) scl[i] = sp[(wave + NW * i) * kKsChunk / kFp8Block];
-
-  // Copy of chunk c into ring slot u.  x: rows 8 j .. 8 j + 7 of the tile per
-  // load, lane l reading row 8 j + l / 8, piece (l % 8) ^ (row % 8).  Weights:
-  // the 16 rows of tile ct per load, lane l reading row l / 4, piece
-  // (l % 4) ^ (row / 4).  Rows past the last token or feature repeat the last.
-  const int xr = lane >> 3, xq = (lane & 7) ^ xr;
-  const int wr = lane >> 2, wq = (lane & 3) ^ (wr >> 2);
-  int64_t xrow[2 * RT], wrow[CT];
-#pragma unroll
-  for (int j = 0; j < 2 * RT; ++j) xrow[j] = (int64_t)min(m0 + 8 * j + xr, a.m - 1) * a.x_stride + 8 * xq;
-#pragma unroll
-  for (int ct = 0; ct < CT; ++ct) wrow[ct] = (int64_t)min(n0 + 16 * ct + wr, n - 1) * a.k + 16 * wq;
-  auto copy = [&](int u, int i) {
-    const int c = wave + NW * i;
-    uint8_t* slot = ring + u * kStage;
-#pragma unroll
-    for (int j = 0; j < 2 * RT; ++j)
-      copy16_to_lds(x + xrow[j] + c * kKsChunk, slot + 1024 * j);
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-      copy16_to_lds(w + wrow[ct] + c * kKsChunk, slot + kXStage + 1024 * ct);
-  };
-  // operand read addresses within a slot: x piece 2 g4 + h of row 16 rt + n16,
-  // weight piece g4 of row n16 of tile ct
-  const uint32_t xa0 = 1024 * (n16 >> 3) + 128 * (n16 & 7) + 16 * ((2 * g4) ^ (n16 & 7));
-  const uint32_t xa1 = 1024 * (n16 >> 3) + 128 * (n16 & 7) + 16 * ((2 * g4 + 1) ^ (n16 & 7));
-  const uint32_t wa = kXStage + 16 * (4 * n16 + (g4 ^ (n16 >> 2)));
-
-  f32x4 acc[RT][CT];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-  static_for<D - 1>([&](auto u) { copy(u, u); });
-  __builtin_amdgcn_sched_barrier(0);
-  static_for<CH>([&](auto i) {
-    constexpr int u = i % D;
-    constexpr int later = i + D - 1 < CH ? D - 1 : CH - 1 - i;  // chunks copied after this one
-    if constexpr (i + D - 1 < CH) copy((u + D - 1) % D, i + D - 1);
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(later * (2 * RT + CT)) : "memory");
-    const uint32_t sbase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring + u * kStage));
-    u32x4 xv[RT][2], wv[CT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-      asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3"
-                   : "=v"(xv[rt][0]), "=v"(xv[rt][1])
-                   : "v"(sbase + xa0 + 2048 * rt), "v"(sbase + xa1 + 2048 * rt)
-                   : "memory");
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-      asm volatile("ds_read_b128 %0, %1" : "=v"(wv[ct]) : "v"(sbase + wa + 1024 * ct) : "memory");
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    // the values are used only after the wait
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) asm volatile("" : "+v"(xv[rt][0]), "+v"(xv[rt][1]));
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) asm volatile("" : "+v"(wv[ct]));
-    const float s = scl[i];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      const u32x4 v = wv[ct];
-      const u32x4 b0{dequant_pair<false>(v[0], s), dequant_pair<true>(v[0], s), dequant_pair<false>(v[1], s),
-                     dequant_pair<true>(v[1], s)};
-      const u32x4 b1{dequant_pair<false>(v[2], s), dequant_pair<true>(v[2], s), dequant_pair<false>(v[3], s),
-                     dequant_pair<true>(v[3], s)};
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = F16::mfma_k32(xv[rt][0], b0, acc[rt][ct]);
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = F16::mfma_k32(xv[rt][1], b1, acc[rt][ct]);
-    }
-  });
-
-  // ---- the waves' partial tiles (in the ring's memory), added in wave order
-  __syncthreads();  // every wave is done with its ring
-  auto part = reinterpret_cast<f32x4(*)[kTiles][64]>(lds);
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) part[wave][rt * CT + ct][lane] = acc[rt][ct];
-  __syncthreads();
-  // wave w finishes tiles w, w + NW, .. (waves past the last tile idle)
-  constexpr int TPW = (kTiles + NW - 1) / NW;
-  f32x4 tot[TPW];
-#pragma unroll
-  for (int j = 0; j < TPW; ++j) {
-    const int t = min(wave + NW * j, kTiles - 1);
-    tot[j] = part[0][t][lane];
-#pragma unroll
-    for (int q = 1; q < NW; ++q) {
-      const f32x4 v = part[q][t][lane];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) tot[j][e] += v[e];
-    }
-  }
-  // D tile rows 4 g4 + e, column n16: F.linear's fp16 result, stored as
-  // y_dtype or (y_add) added to the fp32 y, every y value loaded before the
-  // first store.  The dtype and the bounds are settled once per workgroup, so
-  // whole tiles (the usual case) store with no per-element branch.
-  auto row_of = [&](int j, int e) { return m0 + 16 * ((wave + NW * j) / CT) + 4 * g4 + e; };
-  auto col_of = [&](int j) { return n0 + 16 * ((wave + NW * j) % CT) + n16; };
-  const bool whole = m0 + 16 * RT <= a.m && n0 + 16 * CT <= n;
-  auto finish = [&](auto whole_c, auto dt_c) {
-    constexpr bool W = decltype(whole_c)::value;
-    constexpr int DT = decltype(dt_c)::value;
-    auto valid = [&](int j, int e) {
-      return wave + NW * j < kTiles && (W || (row_of(j, e) < a.m && col_of(j) < n));
-    };
-    if constexpr (DT < 0) {  // y_add
-      float* yf = static_cast<float*>(y);
-      float v[TPW][4];
-#pragma unroll
-      for (int j = 0; j < TPW; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[j][e] = valid(j, e) ? yf[(int64_t)row_of(j, e) * y_stride + col_of(j)] : 0.f;
-#pragma unroll
-      for (int j = 0; j < TPW; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[j][e] = add_rn(v[j][e], through_dtype<RIA_DT_F16>(tot[j][e]));
-          if (valid(j, e)) yf[(int64_t)row_of(j, e) * y_stride + col_of(j)] = v[j][e];
-        }
-    } else {
-#pragma unroll
-      for (int j = 0; j < TPW; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (valid(j, e))
-            store_act<DT>(y, (int64_t)row_of(j, e) * y_stride + col_of(j), through_dtype<RIA_DT_F16>(tot[j][e]));
-    }
-  };
-  auto by_dtype = [&](auto whole_c) {
-    if (y_add)
-      finish(whole_c, std::integral_constant<int, -1>{});
-    else if (y_dtype == RIA_DT_F16)
-      finish(whole_c, std::integral_constant<int, RIA_DT_F16>{});
-    else if (y_dtype == RIA_DT_BF16)
-      finish(whole_c, std::integral_constant<int, RIA_DT_BF16>{});
-    else
-      finish(whole_c, std::integral_constant<int, RIA_DT_F32>{});
-  };
-  if (whole)
-    by_dtype(std::true_type{});
-  else
-    by_dtype(std::false_type{});
-}
-
 // Tile shapes of the K-split kernels (rows 16 RT, features 16 CT)
 struct KsShape {
   int rt, ct;
@@ -977,37 +763,30 @@ static void launch_linear(const LinearArgs& a, int ct, dim3 grid, hipStream_t st
     hipLaunchKernelGGL((linear_fp8_kernel<XT, 1>), grid, dim3(512), 0, st, a);
 }
 
+// Every K takes the register-streaming K-split kernel with four waves,
+// straight-line for 8 or 16 chunks per wave (K = 2048, the hidden width, and
+// K = 4096, the value width).  The wave count is fixed and every shape runs
+// the waves over the same chunks in the same order, so a projection's result
+// does not depend on the tile shape chosen for it (grouped and separate
+// calls agree bit for bit).
 template <int RT, int CT, int D>
 static void launch_ks_k(const LinearArgs& a, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, 4, D, 0>), grid, dim3(256), 0, st, a);
+  constexpr int NW = 4;
+  if (a.k == kKsChunk * NW * 8)
+    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 8>), grid, dim3(64 * NW), 0, st, a);
+  else if (a.k == kKsChunk * NW * 16)
+    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 16>), grid, dim3(64 * NW), 0, st, a);
+  else
+    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 0>), grid, dim3(64 * NW), 0, st, a);
 }
 
-// K = 2048 (the model's hidden width) takes the LDS-staged kernel with four
-// waves; any other K, the value width 4096 included, the register-streaming
-// kernel with four waves.  (The eight-wave LDS-staged instances for K = 4096
-// are not launched: twice in about ten full test runs one of their results
-// differed from a repeat of the same call, and no cause has been found.)  The wave count depends on K
-// alone, and every shape runs the waves over the same chunks in the same
-// order, so a projection's result does not depend on the tile shape chosen
-// for it (grouped and separate calls agree bit for bit).
-static bool ks_shape_ok(KsShape s, int k) { return !(k == 4096 && s.rt == 4 && s.ct == 8); }
-
 static void launch_ks(const LinearArgs& a, KsShape s, dim3 grid, hipStream_t st) {
-  const dim3 b4(256);
-  if (a.k == 2048) {
-    if (s.rt == 4 && s.ct == 8)
-      hipLaunchKernelGGL((linear_fp8_lds_kernel<4, 8, 4, 2, 8>), grid, b4, 0, st, a);
-    else if (s.rt == 4 && s.ct == 4)
-      hipLaunchKernelGGL((linear_fp8_lds_kernel<4, 4, 4, 3, 8>), grid, b4, 0, st, a);
-    else
-      hipLaunchKernelGGL((linear_fp8_lds_kernel<2, 2, 4, 6, 8>), grid, b4, 0, st, a);
-  } else if (s.rt == 4 && s.ct == 8) {
+  if (s.rt == 4 && s.ct == 8)
     launch_ks_k<4, 8, 3>(a, grid, st);
-  } else if (s.rt == 4 && s.ct == 4) {
+  else if (s.rt == 4 && s.ct == 4)
     launch_ks_k<4, 4, 4>(a, grid, st);
-  } else {
+  else
     launch_ks_k<2, 2, 6>(a, grid, st);
-  }
 }
 
 static int device_cus() {
@@ -1108,7 +887,6 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
     const int cus = device_cus();
     int64_t best = -1;
     for (const KsShape s : kKsShapes) {
-      if (!ks_shape_ok(s, k)) continue;
       int64_t wgs = 0;
       for (int j = 0; j < count; ++j) wgs += (projs[j].n + 16 * s.ct - 1) / (16 * s.ct);
       wgs *= (m + 16 * s.rt - 1) / (16 * s.rt);

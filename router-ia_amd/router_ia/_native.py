@@ -149,7 +149,8 @@ class GdnDecodeDesc(ctypes.Structure):
                 ("conv_window_out", _vp), ("state_in", _vp), ("state_out", _vp), ("seq_slot", _vp),
                 ("gate_a", _vp), ("gate_b", _vp), ("gate_row_stride", _c_i64), ("gate_mode", _c_int),
                 ("A_log", _vp), ("dt_bias", _vp), ("qk_mode", _c_int), ("out", _vp), ("out_dtype", _c_int),
-                ("z", _vp), ("z_dtype", _c_int), ("z_row_stride", _c_i64), ("norm_weight", _vp)]
+                ("z", _vp), ("z_dtype", _c_int), ("z_row_stride", _c_i64), ("norm_weight", _vp),
+                ("pool_rows", _c_i64)]
 
 
 class Fp8Proj(ctypes.Structure):

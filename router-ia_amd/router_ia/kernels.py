@@ -232,6 +232,8 @@ def gdn_decode_ex(
         if conv_weight is None or conv_window_in is None or conv_window_out is None:
             raise ValueError("RIA_CONV_WINDOW needs conv_weight, conv_window_in and conv_window_out")
         _check_conv_window(conv_weight, conv_window_in, conv_window_out, cdim, batch if seq_slot is None else 0)
+        if seq_slot is not None and {conv_window_in.shape[0], conv_window_out.shape[0]} != {state_in.shape[0]}:
+            raise ValueError("with seq_slot the conv window pools must have the state pool's rows")
     elif conv_layout != nat.RIA_CONV_NONE:
         raise ValueError(f"unknown conv_layout {conv_layout}")
     if gate_mode == nat.RIA_GATE_RAW:
@@ -265,7 +267,7 @@ def gdn_decode_ex(
         A_log=addr(A_log) if gate_mode == nat.RIA_GATE_RAW else None,
         dt_bias=addr(dt_bias) if gate_mode == nat.RIA_GATE_RAW else None, qk_mode=int(qk_mode), out=addr(out),
         out_dtype=dtype_code(out), z=addr(z), z_dtype=dtype_code(z) if z is not None else 0, z_row_stride=z_stride,
-        norm_weight=w_ptr.value if w_ptr is not None else None)
+        norm_weight=w_ptr.value if w_ptr is not None else None, pool_rows=int(state_in.shape[0]))
     rc = nat.load().ria_gdn_decode_ex(ctypes.byref(d), _stream(dev))
     nat.check(rc, "ria_gdn_decode_ex")
     return out
@@ -879,7 +881,7 @@ def attn_decode_append(
     max_ctx: int,
     inv_freq: torch.Tensor | None,
     scale: float,
-    workspace: torch.Tensor | None,
+    workspace: torch.Tensor,
     seq_slot: torch.Tensor | None = None,
     split_tokens: int = 0,
     phase: int = nat.RIA_ATTN_BOTH,
@@ -893,17 +895,59 @@ def attn_decode_append(
     stops before it, the combine launch computes it with kv_append's
     arithmetic (the pages hold the same bits), writes it into the page and
     folds it into the row's softmax.  Both phases take the same arguments.
-    With ``workspace=None`` the partials go into the library's own scratch
-    array (ria_attn_decode_append_noalloc): nothing is allocated, and calls
-    that overlap on one GPU race.
+    ``workspace`` (the split-K partials) is required; callers that cannot
+    allocate use attn_decode_append_noalloc.
     """
+    if workspace is None:
+        raise ValueError("attn_decode_append: workspace is required (attn_decode_append_noalloc needs none)")
+    return _attn_decode_append(q, gate, k, v, k_cache, v_cache, page_table, out, positions=positions,
+                               ctx_lens=ctx_lens, max_ctx=max_ctx, inv_freq=inv_freq, scale=scale,
+                               workspace=workspace, seq_slot=seq_slot, split_tokens=split_tokens, phase=phase,
+                               q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight)
+
+
+def attn_decode_append_noalloc(
+    q: torch.Tensor,
+    gate: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    positions: torch.Tensor | int,
+    ctx_lens: torch.Tensor | int,
+    max_ctx: int,
+    inv_freq: torch.Tensor | None,
+    scale: float,
+    seq_slot: torch.Tensor | None = None,
+    split_tokens: int = 0,
+    q_norm_weight: torch.Tensor | None = None,
+    k_norm_weight: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """attn_decode_append with no workspace (ria_attn_decode_append_noalloc).
+
+    The split-K partials go into the library's own 16 MiB device array, one
+    per GPU: nothing is allocated, both phases run in the one call, sizes
+    whose partials exceed the array raise, and calls that overlap on one GPU
+    (concurrent streams) race.
+    """
+    return _attn_decode_append(q, gate, k, v, k_cache, v_cache, page_table, out, positions=positions,
+                               ctx_lens=ctx_lens, max_ctx=max_ctx, inv_freq=inv_freq, scale=scale, workspace=None,
+                               seq_slot=seq_slot, split_tokens=split_tokens, phase=nat.RIA_ATTN_BOTH,
+                               q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight)
+
+
+def _attn_decode_append(q, gate, k, v, k_cache, v_cache, page_table, out, *, positions, ctx_lens, max_ctx, inv_freq,
+                        scale, workspace, seq_slot, split_tokens, phase, q_norm_weight, k_norm_weight):
     batch = int(q.shape[0])
     num_q_heads = int(q.shape[1])
     num_kv_heads = int(k_cache.shape[1])
     dev = q.device
     for name, t in (("q", q), ("gate", gate), ("k", k), ("v", v), ("k_cache", k_cache), ("v_cache", v_cache),
                     ("out", out), ("inv_freq", inv_freq), ("workspace", workspace), ("seq_slot", seq_slot)):
-        _require_gpu(name, t, dev)  # (a None workspace passes: the library's scratch array)
+        _require_gpu(name, t, dev)  # (a None workspace is the no-alloc path's)
     if k.dtype != q.dtype or v.dtype != q.dtype or gate.dtype != q.dtype:
         raise ValueError("attn_decode_append: q, gate, k and v must share one dtype")
     qs = _row_stride("q", q, batch, num_q_heads * ATTN_HEAD_DIM)

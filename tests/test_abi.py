@@ -190,6 +190,15 @@ def test_gdn_decode_ex_and_window_conv_host_validation() -> None:
                 x_row_stride=8192) == 1 and b"x_row_stride" in lib.ria_last_error()
     assert desc(conv_layout=nat.RIA_CONV_RING) == 1 and b"conv_ring" in lib.ria_last_error()
     assert desc(batch=0) == 0  # nothing to launch
+    # with seq_slot the pools' extent comes from pool_rows: required, and partial overlaps are refused
+    slots = dict(seq_slot=256)
+    assert desc(**slots) == 1 and b"pool_rows" in lib.ria_last_error()
+    state_bytes = 32 * 128 * 128 * 4
+    assert desc(pool_rows=8, state_out=(1 << 24) + 3 * state_bytes, **slots) == 1 \
+        and b"overlaps" in lib.ria_last_error()
+    window_bytes = 8192 * 4 * 2
+    assert desc(pool_rows=8, conv_window_out=(1 << 20) + window_bytes, **slots) == 1 \
+        and b"conv_window_out" in lib.ria_last_error()
     rc = lib.ria_conv1d_window_step(1, 8192, fake, 0, 8192, fake, ctypes.c_void_p(260), fake, fake, 2, None)
     assert rc == 1 and b"aligned" in lib.ria_last_error()
     rc = lib.ria_conv1d_window_step(1, 8192, fake, 0, 4096, fake, fake, fake, fake, 2, None)

@@ -1,8 +1,9 @@
 """Host logic of the drop-in attention cache (no GPU needed).
 
-The first two tests restate the reference's own unit tests
-(v2/tests/test_qwen36_attention_cache.py:15-52) against this package's
-``router_ia.qwen36_attention_cache``: same inputs, same assertions.
+The limit tests check the semantics the reference's unit tests pin
+(v2/tests/test_qwen36_attention_cache.py): a KV limit raises before the cache
+is mutated, with the messages its callers match, and the byte budget counts
+the stored tensors' own dtype.
 """
 
 from __future__ import annotations
@@ -22,43 +23,58 @@ SNAPSHOT_KEYS = [
 ]
 
 
-def _token() -> tuple[torch.Tensor, torch.Tensor]:
-    # (batch, kv_heads, sequence, head_dim), matching the cache layout.
-    return torch.zeros((1, 1, 1, 2)), torch.zeros((1, 1, 1, 2))
+def _kv(fill: float, heads: int = 2, dim: int = 8, dtype: torch.dtype = torch.float32):
+    """One decode token's k and v, [batch=1, kv heads, 1 token, head dim]."""
+    k = torch.full((1, heads, 1, dim), fill, dtype=dtype)
+    return k, k + 0.5
 
 
-def test_full_kv_growth_stops_before_exceeding_context_limit() -> None:
-    state = AttentionState(max_context_tokens=3)
-    for absolute_position in range(3):
-        state.tokens_seen = absolute_position
-        key, value = _token()
-        _append_full_kv(state, 0, key, value)
-        assert state.full_keys[0].shape[-2] <= 3
-        assert state.full_values[0].shape[-2] <= 3
+def _fill(state: AttentionState, layer: int, count: int) -> None:
+    """Append `count` tokens at positions 0 .. count - 1 (the caller advances tokens_seen)."""
+    for pos in range(count):
+        state.tokens_seen = pos
+        _append_full_kv(state, layer, *_kv(float(pos)))
+
+
+@pytest.mark.parametrize("limit", [1, 5])
+def test_context_limit_refuses_the_next_token_and_leaves_the_cache_as_it_was(limit: int) -> None:
+    # qwen36_attention_cache.py:341-352: the check runs before any tensor is touched
+    state = AttentionState(max_context_tokens=limit)
+    _fill(state, 2, limit)
+    keys_before = state.full_keys[2].clone()
+    values_before = state.full_values[2].clone()
+    state.tokens_seen = limit
+    with pytest.raises(RuntimeError, match=rf"max_context_tokens={limit}\b"):
+        _append_full_kv(state, 2, *_kv(99.0))
+    assert torch.equal(state.full_keys[2], keys_before)
+    assert torch.equal(state.full_values[2], values_before)
+    snap = state.snapshot()
+    assert (snap["absolute_position"], snap["full_tokens_resident"], snap["kv_start_position"]) == (limit, limit, 0)
+    assert snap["full_token_entries"] == limit
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_byte_budget_counts_the_stored_dtype_and_refuses_before_mutation(dtype: torch.dtype) -> None:
+    # qwen36_attention_cache.py:327-339, 353-364: bytes are those of the tensors
+    # as given (element_size of their dtype), both k and v of every layer
+    k, v = _kv(1.0, heads=2, dim=8, dtype=dtype)
+    per_token = 2 * k.numel() * k.element_size()
+    budget = 3 * per_token + per_token // 2  # room for three tokens, not four
+    state = AttentionState(max_full_kv_bytes=budget)
+    for pos in range(3):
+        state.tokens_seen = pos
+        _append_full_kv(state, 0, k, v)
+    assert state.snapshot()["full_bytes"] == 3 * per_token
     state.tokens_seen = 3
-    key, value = _token()
-    with pytest.raises(RuntimeError, match=r"max_context_tokens=3"):
-        _append_full_kv(state, 0, key, value)
-    stats = state.snapshot()
-    assert state.full_keys[0].shape[-2] == 3
-    assert stats["absolute_position"] == 3
-    assert stats["full_tokens_resident"] == 3
-    assert stats["kv_start_position"] == 0
-
-
-def test_full_kv_growth_stops_before_exceeding_byte_budget() -> None:
-    key, value = _token()
-    token_bytes = key.numel() * key.element_size() + value.numel() * value.element_size()
-    state = AttentionState(max_full_kv_bytes=token_bytes * 2)
-    for absolute_position in range(2):
-        state.tokens_seen = absolute_position
-        _append_full_kv(state, 0, key, value)
-        assert state.snapshot()["full_bytes"] <= token_bytes * 2
-    state.tokens_seen = 2
     with pytest.raises(RuntimeError, match=r"max_full_kv_bytes"):
-        _append_full_kv(state, 0, key, value)
-    assert state.full_keys[0].shape[-2] == 2
-    assert state.snapshot()["full_bytes"] == token_bytes * 2
+        _append_full_kv(state, 0, k, v)
+    assert state.full_keys[0].shape[-2] == 3 and state.full_values[0].shape[-2] == 3
+    assert state.snapshot()["full_bytes"] == 3 * per_token
+    # a second layer's tokens count against the same budget
+    state.tokens_seen = 0
+    with pytest.raises(RuntimeError, match=r"max_full_kv_bytes"):
+        _append_full_kv(state, 7, k, v)
+    assert 7 not in state.full_keys
 
 
 def test_append_keeps_tokens_in_order() -> None:

@@ -46,9 +46,11 @@ def _call(st, inputs, norms, out, workspace):
     q, gate, k, v = inputs
     qn, kn = norms
     kc, vc = st.kv.layer(0)
-    return K.attn_decode_append(q, gate, k, v, kc, vc, st.kv.page_table, out, positions=st.tokens_seen,
-                                ctx_lens=st.ctx_lens, max_ctx=st.max_seen + 1, inv_freq=st.inv_freq, scale=st.scale,
-                                workspace=workspace, q_norm_weight=qn, k_norm_weight=kn)
+    common = dict(positions=st.tokens_seen, ctx_lens=st.ctx_lens, max_ctx=st.max_seen + 1, inv_freq=st.inv_freq,
+                  scale=st.scale, q_norm_weight=qn, k_norm_weight=kn)
+    if workspace is None:
+        return K.attn_decode_append_noalloc(q, gate, k, v, kc, vc, st.kv.page_table, out, **common)
+    return K.attn_decode_append(q, gate, k, v, kc, vc, st.kv.page_table, out, workspace=workspace, **common)
 
 
 @pytest.mark.parametrize("batch,lo,hi,seed", [(96, 200, 6000, 61), (5, 1, 900, 62)], ids=["B96", "B5-smaller"])
@@ -69,14 +71,25 @@ def test_noalloc_equals_the_workspace_entry_point(gpu, batch, lo, hi, seed):
     assert not torch.equal(st.kv.v, v0)  # the new tokens were written
 
 
+def _noalloc_raw(lib, batch, max_ctx, split_tokens, phase):
+    # every pointer null: the checks under test come first, and a regression
+    # that skipped them would meet the null-pointer refusal, never a launch
+    return lib.ria_attn_decode_append_noalloc(batch, 16, 2, None, 0, 4096, None, 0, 4096, None, 512, None, 512, None,
+                                              None, None, 0, 1, None, 2048, None, None, 0, None, 1, max_ctx, None, 0,
+                                              None, 0.0625, split_tokens, None, 0, phase, None)
+
+
 def test_noalloc_refuses_sizes_beyond_its_array(gpu):
     announce("no-alloc decode append: sizes beyond the 16 MiB array are refused before any launch")
     lib = nat.load()
-    fake = ctypes.c_void_p(256)
     # 4096 rows x 2 KV heads at long fixed splits: far more partials than 16 MiB
     need = lib.ria_attn_decode_workspace_bytes(4096, 16, 2, 32768, 64)
     assert need > 16 << 20
-    rc = lib.ria_attn_decode_append_noalloc(4096, 16, 2, fake, 0, 4096, fake, 0, 4096, fake, 512, fake, 512, None,
-                                            fake, fake, 0, 1, fake, 2048, None, None, 0, None, 1, 32768, None, 0,
-                                            None, 0.0625, 64, fake, 0, nat.RIA_ATTN_BOTH, None)
-    assert rc == 3 and b"scratch" in lib.ria_last_error()
+    assert _noalloc_raw(lib, 4096, 32768, 64, nat.RIA_ATTN_BOTH) == 3 and b"scratch" in lib.ria_last_error()
+
+
+@pytest.mark.parametrize("phase", ["RIA_ATTN_SPLITK", "RIA_ATTN_COMBINE"])
+def test_noalloc_refuses_a_single_phase(gpu, phase):
+    announce(f"no-alloc decode append: {phase} alone is refused (partials do not outlive a call)")
+    lib = nat.load()
+    assert _noalloc_raw(lib, 4, 4096, 0, getattr(nat, phase)) == 1 and b"RIA_ATTN_BOTH" in lib.ria_last_error()

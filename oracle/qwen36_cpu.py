@@ -217,6 +217,39 @@ def attention_over_cache(q_rot: torch.Tensor, full_k: torch.Tensor, full_v: torc
     return attn * torch.sigmoid(gate.float())
 
 
+def attention_over_cache_grouped(q_rot: torch.Tensor, full_k: torch.Tensor, full_v: torch.Tensor,
+                                 gate: torch.Tensor, num_kv_groups: int = FULL_NUM_KV_GROUPS) -> torch.Tensor:
+    """attention_over_cache with the GQA mapping as a grouped product instead of the 8x expansion.
+
+    Query head h reads KV head h // num_kv_groups (qwen36_attention_cache.py:309-310,
+    ``repeat_interleave`` along the head dim), so the expanded einsum equals a
+    product of each KV head's K/V with its group of query rows; the scores,
+    softmax, P V and gate follow :312-317 in fp32.  Used where the expanded
+    copy of a long cache would be too large (every row of a 128-sequence
+    batch).  q_rot [1, Hq, 256]; full_k/full_v [1, Hkv, T, 256].
+    """
+    hq = q_rot.shape[1]
+    hkv = full_k.shape[1]
+    assert hq == hkv * num_kv_groups
+    q = q_rot.float().reshape(hkv, num_kv_groups, FULL_HEAD_DIM)
+    k = full_k[0].float()
+    v = full_v[0].float()
+    scores = torch.bmm(q, k.transpose(1, 2).contiguous()) * (FULL_HEAD_DIM ** -0.5)  # [Hkv, G, T]
+    attn_weights = torch.softmax(scores, dim=-1)
+    attn = torch.bmm(attn_weights, v).reshape(1, hq, FULL_HEAD_DIM)
+    return attn * torch.sigmoid(gate.float())
+
+
+def full_decode_step_grouped(full_k: torch.Tensor | None, full_v: torch.Tensor | None, q: torch.Tensor,
+                             k: torch.Tensor, v: torch.Tensor, gate: torch.Tensor, position: int):
+    """full_decode_step (:304-317) with attention_over_cache_grouped for the attention half."""
+    q = q.float().unsqueeze(2)
+    k = k.float().unsqueeze(2)
+    q, k_token = apply_rope(q, k, position)
+    full_k, full_v = append_full_kv(full_k, full_v, k_token, v.float().unsqueeze(2))
+    return attention_over_cache_grouped(q.squeeze(2), full_k, full_v, gate), full_k, full_v
+
+
 # ----------------------------------------------------------------------------- batched drivers
 class SequenceState:
     """Per-sequence attention state of the oracle (the reference AttentionState's tensors)."""

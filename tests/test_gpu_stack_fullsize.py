@@ -13,6 +13,9 @@ seeded draws made on the device, as the benchmark makes them.
 
 Checked, following the reference's per-sequence semantics
 (v2/src/router_ia/qwen36_attention_cache.py:256-266, 306-317):
+  * every row at step 0: the first DeltaNet layer's output and new state, and
+    the first attention layer's output (over the row's resident tokens read
+    out of the pages, the oracle's grouped GQA product);
   * four sampled rows (the shortest, the longest and two others), exported
     with ``save_row(r).to_reference()`` before the first step and continued
     by the oracle: every layer's output of every step within the activation
@@ -108,6 +111,11 @@ def test_stack_at_full_size_matches_oracle(gpu, case):
     assert free.numel() > 0
     free_k, free_v = st.kv.k[:, free].clone(), st.kv.v[:, free].clone()
 
+    # every row at step 0: the first DeltaNet layer's state before the step
+    lin0_before = st.linear_states[0].cpu()
+    ring0_before = st.conv_rings[0].cpu()
+    first = {}  # step 0's inputs and outputs of model layers 0 and 3, every row
+
     gdn_out = torch.empty((batch, W.NUM_V_HEADS, 128), device=gpu, dtype=torch.bfloat16)
     attn_out = torch.empty((batch, W.FULL_Q_HEADS, W.FULL_HEAD_DIM), device=gpu, dtype=torch.bfloat16)
     appended = []  # (step, layer index, positions, k, v) of every appended token
@@ -134,6 +142,9 @@ def test_stack_at_full_size_matches_oracle(gpu, case):
                                            kv_in[fi, 0][rsel].cpu(), kv_in[fi, 1][rsel].cpu(),
                                            qg[fi, 1][rsel].cpu())
                 appended.append((s, fi, positions, kv_in[fi, 0].clone(), kv_in[fi, 1].clone()))
+                if s == 0 and fi == 0:
+                    first["attn"] = (attn_out.float().cpu(), qg[0, 0].cpu(), qg[0, 1].cpu(), kv_in[0, 0].cpu(),
+                                     kv_in[0, 1].cpu())
             else:
                 li = layer - layer // 4
                 K.gdn_decode(mixed[li], st.linear_states[li], gate_ab[li, 0], gate_ab[li, 1], gdn_out,
@@ -141,6 +152,9 @@ def test_stack_at_full_size_matches_oracle(gpu, case):
                              conv_ring=st.conv_rings[li], conv_pos=st.tokens_seen, gate_mode=nat.RIA_GATE_RAW,
                              A_log=a_log[li], dt_bias=dt_bias[li])
                 out = gdn_out
+                if s == 0 and li == 0:
+                    first["gdn"] = (gdn_out.float().cpu(), st.linear_states[0].cpu(), mixed[0].cpu(),
+                                    gate_ab[0, 0].cpu(), gate_ab[0, 1].cpu())
                 beta, g = O.gating(gate_ab[li, 0][rsel].cpu(), gate_ab[li, 1][rsel].cpu(), a_log[li].cpu(),
                                    dt_bias[li].cpu())
                 want = O.linear_step_batched([oracle[r] for r in rows], li, mixed[li][rsel].cpu(),
@@ -176,3 +190,27 @@ def test_stack_at_full_size_matches_oracle(gpu, case):
             assert_act_close(k_got[b].cpu(), k_rot[0], f"{case}: rotated k, row {b} step {s} layer {fi}")
     assert torch.equal(st.kv.k[:, free], free_k) and torch.equal(st.kv.v[:, free], free_v), \
         f"{case}: a page in no row's table changed"
+
+    # every row, step 0, model layer 0 (DeltaNet) and layer 3 (full attention) against the oracle
+    out0, lin0_after, mixed0, a0, b0 = first["gdn"]
+    beta, g = O.gating(a0, b0, a_log[0].cpu(), dt_bias[0].cpu())
+    for r in range(batch):
+        t = lengths[r]
+        # the ring holds token n's conv input in slot n mod 4; the reference's window is oldest first
+        window = ring0_before[r, [(t - 4 + m) % 4 for m in range(4)]].t().unsqueeze(0)
+        want, _, s_new = O.linear_decode_step(window, lin0_before[r:r + 1], mixed0[r:r + 1], conv_w[0].cpu(),
+                                              beta[r:r + 1], g[r:r + 1])
+        assert_act_close(out0[r:r + 1], want, f"{case}: step 0 layer 0 row {r}")
+        assert_state_close(lin0_after[r:r + 1], s_new, f"{case}: step 0 layer 0 state row {r}")
+    announce(f"{case}: step 0, DeltaNet layer 0 matches the oracle on all {batch} rows")
+    out3, q3, gate3, k3, v3 = first["attn"]
+    for r in range(batch):
+        t = lengths[r]
+        # the row's resident tokens [0, t) in logical order, read out of the pages through the host table
+        phys = torch.tensor(tables[r][:(t + 15) // 16], dtype=torch.long, device=gpu)
+        k_rows = st.kv.k[0][phys].permute(1, 0, 4, 3, 2, 5).reshape(2, -1, 256)[:, :t]  # [Hkv, T, 256]
+        v_rows = st.kv.v[0][phys].permute(1, 0, 3, 2).reshape(2, -1, 256)[:, :t]
+        want, _, _ = O.full_decode_step_grouped(k_rows.float().cpu().unsqueeze(0), v_rows.float().cpu().unsqueeze(0),
+                                                q3[r:r + 1], k3[r:r + 1], v3[r:r + 1], gate3[r:r + 1], t)
+        assert_act_close(out3[r:r + 1], want, f"{case}: step 0 layer 3 row {r} (context {t})")
+    announce(f"{case}: step 0, attention layer 3 matches the oracle on all {batch} rows")

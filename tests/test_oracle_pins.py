@@ -265,6 +265,26 @@ def test_full_decode_matches_sdpa_and_fp64():
                                    atol=1e-5)
 
 
+@pytest.mark.parametrize("t0", [0, 16, 1000])
+def test_grouped_attention_equals_the_expanded_form_and_fp64(t0):
+    # the grouped GQA product (no 8x expanded copy) against the expanded
+    # einsum of full_decode_step and the fp64 brute force per head
+    g = _gen(12 + t0)
+    fk = torch.randn((1, 2, t0, 256), generator=g) if t0 else None
+    fv = torch.randn((1, 2, t0, 256), generator=g) if t0 else None
+    q, gate = torch.randn((1, 16, 256), generator=g), torch.randn((1, 16, 256), generator=g)
+    k, v = torch.randn((1, 2, 256), generator=g), torch.randn((1, 2, 256), generator=g)
+    want, fk_w, fv_w = O.full_decode_step(fk, fv, q, k, v, gate, t0)
+    got, fk_g, fv_g = O.full_decode_step_grouped(fk, fv, q, k, v, gate, t0)
+    assert torch.equal(fk_w, fk_g) and torch.equal(fv_w, fv_g)
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-6)
+    qr = fp64.apply_rope(q.double().numpy(), t0)
+    for h in (0, 5, 8, 15):  # query head h reads KV head h // 8
+        o = fp64.attention(qr[0, h], fk_w[0, h // 8].double().numpy(), fv_w[0, h // 8].double().numpy(), 1 / 16)
+        np.testing.assert_allclose(got[0, h].double().numpy(), o * fp64.sigmoid(gate[0, h].numpy()), rtol=1e-4,
+                                   atol=1e-5)
+
+
 def test_full_decode_gate_is_per_head_and_dim():
     g = _gen(11)
     fk = torch.randn((1, 2, 5, 256), generator=g)

@@ -299,6 +299,24 @@ int ria_kv_append(int batch, int num_kv_heads,
                   const float* inv_freq, int rope_dim, const float* k_norm_weight, void* stream);
 
 /*
+ * ria_kv_append that also returns each row's key as the reference stores it:
+ * k after k_norm and RoPE in fp32, before its rounding to the page dtype, in
+ * k_rot_out [batch, Hkv, 256] fp32 (the fp32 k_token the reference appends
+ * to full_keys, qwen36_attention_cache.py:303-307, 365-372).  The drop-in's
+ * dicts read their keys back from it exactly; the pages are those of
+ * ria_kv_append, bit for bit.
+ */
+int ria_kv_append_out(int batch, int num_kv_heads,
+                      const void* k, int k_dtype, int64_t k_row_stride,
+                      const void* v, int v_dtype, int64_t v_row_stride,
+                      void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                      const int32_t* page_table, int64_t page_table_stride, const int32_t* seq_slot,
+                      const int32_t* positions, int32_t position_scalar,
+                      const int32_t* slots, int32_t slot_scalar,
+                      const float* inv_freq, int rope_dim, const float* k_norm_weight,
+                      float* k_rot_out, void* stream);
+
+/*
  * Append `length` consecutive tokens of ONE sequence (a prompt) into its
  * pages: token i goes to logical slot start_pos + i with RoPE position
  * start_pos + i.  Equal to `length` ria_kv_append calls, bit for bit, i.e.

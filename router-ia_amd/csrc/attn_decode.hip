@@ -110,6 +110,8 @@ struct AppendArgs {
   const float* norm_w;  // k_norm weight [256] f32, or null: k arrives normalised
   int num_kv_heads;
   int seq_len;  // prompt append: tokens at positions (and slots) pos_scalar .. pos_scalar + seq_len - 1
+  float* k_out; // one-token append: row b's k after k_norm and RoPE in fp32 (before the page rounding)
+                // at k_out[(b * Hkv + kvh) * 256 + d], or null
 };
 
 // RoPE of element d of a row: (x*cos + rotate_half(x)*sin) on [0, rope_dim),
@@ -150,6 +152,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int half = a.rope_dim >> 1;
   const float partner = d < a.rope_dim ? k_s[d < half ? d + half : d - half] : 0.f;
   const float kr = rope_elem(kv, partner, d, a.rope_dim, static_cast<float>(pos), a.inv_freq);
+  if (a.k_out) a.k_out[((int64_t)b * a.num_kv_heads + kvh) * kAttnHeadDim + d] = kr;
   const int phys = a.page_table[(int64_t)row * a.pt_stride + slot / kPageTokens];
   if (phys < 0 || phys >= a.num_pages) return;  // host guarantees allocation; never write out of the pool
   const int off = slot % kPageTokens;
@@ -1165,18 +1168,18 @@ static int check_append_common(const char* who, int num_kv_heads, const void* k,
 
 using namespace ria;
 
-extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
-                             const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
-                             int kv_dtype, int num_pages, const int32_t* page_table, int64_t page_table_stride,
-                             const int32_t* seq_slot, const int32_t* positions, int32_t position_scalar,
-                             const int32_t* slots, int32_t slot_scalar, const float* inv_freq, int rope_dim,
-                             const float* k_norm_weight, void* stream) {
-  if (batch < 0) return set_error(RIA_ERR_INVALID, "ria_kv_append: bad batch");
-  int rc = check_append_common("ria_kv_append", num_kv_heads, k, k_dtype, k_row_stride, v, v_dtype, v_row_stride,
+static int kv_append_impl(const char* who, int batch, int num_kv_heads, const void* k, int k_dtype,
+                          int64_t k_row_stride, const void* v, int v_dtype, int64_t v_row_stride, void* k_cache,
+                          void* v_cache, int kv_dtype, int num_pages, const int32_t* page_table,
+                          int64_t page_table_stride, const int32_t* seq_slot, const int32_t* positions,
+                          int32_t position_scalar, const int32_t* slots, int32_t slot_scalar, const float* inv_freq,
+                          int rope_dim, const float* k_norm_weight, float* k_rot_out, void* stream) {
+  if (batch < 0) return set_error(RIA_ERR_INVALID, "%s: bad batch", who);
+  int rc = check_append_common(who, num_kv_heads, k, k_dtype, k_row_stride, v, v_dtype, v_row_stride,
                                k_cache, v_cache, kv_dtype, page_table, inv_freq, rope_dim);
   if (rc != RIA_OK) return rc;
   if (batch == 0) return RIA_OK;
-  if (!slots && slot_scalar < 0) return set_error(RIA_ERR_INVALID, "ria_kv_append: negative slot");
+  if (!slots && slot_scalar < 0) return set_error(RIA_ERR_INVALID, "%s: negative slot", who);
   AppendArgs a{};
   a.k = k;
   a.k_stride = k_row_stride;
@@ -1196,8 +1199,33 @@ extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_d
   a.rope_dim = rope_dim;
   a.norm_w = k_norm_weight;
   a.num_kv_heads = num_kv_heads;
+  a.k_out = k_rot_out;
   launch_append(a, batch, k_dtype, v_dtype, kv_dtype, static_cast<hipStream_t>(stream));
-  return check_launch("ria_kv_append");
+  return check_launch(who);
+}
+
+extern "C" int ria_kv_append(int batch, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
+                             const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
+                             int kv_dtype, int num_pages, const int32_t* page_table, int64_t page_table_stride,
+                             const int32_t* seq_slot, const int32_t* positions, int32_t position_scalar,
+                             const int32_t* slots, int32_t slot_scalar, const float* inv_freq, int rope_dim,
+                             const float* k_norm_weight, void* stream) {
+  return kv_append_impl("ria_kv_append", batch, num_kv_heads, k, k_dtype, k_row_stride, v, v_dtype, v_row_stride,
+                        k_cache, v_cache, kv_dtype, num_pages, page_table, page_table_stride, seq_slot, positions,
+                        position_scalar, slots, slot_scalar, inv_freq, rope_dim, k_norm_weight, nullptr, stream);
+}
+
+extern "C" int ria_kv_append_out(int batch, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
+                                 const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
+                                 int kv_dtype, int num_pages, const int32_t* page_table, int64_t page_table_stride,
+                                 const int32_t* seq_slot, const int32_t* positions, int32_t position_scalar,
+                                 const int32_t* slots, int32_t slot_scalar, const float* inv_freq, int rope_dim,
+                                 const float* k_norm_weight, float* k_rot_out, void* stream) {
+  if (!k_rot_out) return set_error(RIA_ERR_INVALID, "ria_kv_append_out: null k_rot_out");
+  return kv_append_impl("ria_kv_append_out", batch, num_kv_heads, k, k_dtype, k_row_stride, v, v_dtype,
+                        v_row_stride, k_cache, v_cache, kv_dtype, num_pages, page_table, page_table_stride, seq_slot,
+                        positions, position_scalar, slots, slot_scalar, inv_freq, rope_dim, k_norm_weight, k_rot_out,
+                        stream);
 }
 
 extern "C" int ria_kv_append_seq(int length, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,

@@ -71,6 +71,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp, _c_i64,
          _vp, _vp, _c_i32, _vp, _c_i32, _vp, _c_int, _vp, _vp],
     ),
+    "ria_kv_append_out": (
+        _c_int,
+        [_c_int, _c_int, _vp, _c_int, _c_i64, _vp, _c_int, _c_i64, _vp, _vp, _c_int, _c_int, _vp, _c_i64,
+         _vp, _vp, _c_i32, _vp, _c_i32, _vp, _c_int, _vp, _vp, _vp],
+    ),
     "ria_attn_decode_split_tokens": (_c_int, [_c_int, _vp, _c_int]),
     "ria_attn_decode_workspace_bytes": (_c_i64, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "ria_attn_decode": (

@@ -489,11 +489,15 @@ def kv_append(
     inv_freq: torch.Tensor,
     seq_slot: torch.Tensor | None = None,
     k_norm_weight: torch.Tensor | None = None,
+    k_rot_out: torch.Tensor | None = None,
 ) -> None:
     """RoPE k and append k, v of one token per sequence into the paged cache (ria_kv_append).
 
     With the fp32 ``k_norm_weight`` [256], k is RMSNorm'd ((1 + w), cast back
-    to k's dtype) before RoPE (qwen36_attention_cache.py:303-305).
+    to k's dtype) before RoPE (qwen36_attention_cache.py:303-305).  With
+    ``k_rot_out`` (contiguous fp32 [batch, Hkv, 256]) the normed, rotated k
+    is also written there in fp32, before its rounding to the page dtype
+    (ria_kv_append_out).
     """
     batch = int(k.shape[0])
     num_kv_heads = int(k.shape[1]) if k.dim() == 3 else int(k.numel() // max(batch, 1) // ATTN_HEAD_DIM)
@@ -513,13 +517,20 @@ def kv_append(
         raise ValueError(f"slot {slot_s} beyond the page table's {page_table.shape[1] * PAGE_TOKENS} tokens")
     if seq_slot is not None:
         _rows_i32("seq_slot", seq_slot, batch, dev)
-    rc = nat.load().ria_kv_append(batch, num_kv_heads, _ptr(k), dtype_code(k), ks, _ptr(v), dtype_code(v), vs,
-                                  _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table), pts,
-                                  _ptr(seq_slot),
-                                  _ptr(pos_t), pos_s, _ptr(slot_t), slot_s, _ptr(inv_freq),
-                                  0 if inv_freq is None else 2 * int(inv_freq.numel()),
-                                  _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev), _stream(dev))
-    nat.check(rc, "ria_kv_append")
+    args = (batch, num_kv_heads, _ptr(k), dtype_code(k), ks, _ptr(v), dtype_code(v), vs, _ptr(k_cache),
+            _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table), pts, _ptr(seq_slot), _ptr(pos_t), pos_s,
+            _ptr(slot_t), slot_s, _ptr(inv_freq), 0 if inv_freq is None else 2 * int(inv_freq.numel()),
+            _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev))
+    if k_rot_out is None:
+        rc = nat.load().ria_kv_append(*args, _stream(dev))
+        nat.check(rc, "ria_kv_append")
+        return
+    _require_gpu("k_rot_out", k_rot_out, dev)
+    if k_rot_out.dtype != torch.float32 or tuple(k_rot_out.shape) != (batch, num_kv_heads, ATTN_HEAD_DIM) \
+            or not k_rot_out.is_contiguous():
+        raise ValueError(f"k_rot_out must be contiguous fp32 [{batch}, {num_kv_heads}, {ATTN_HEAD_DIM}]")
+    rc = nat.load().ria_kv_append_out(*args, _ptr(k_rot_out), _stream(dev))
+    nat.check(rc, "ria_kv_append_out")
 
 
 def attn_decode_split_tokens(num_kv_heads: int, ctx_lens: list[int]) -> int:

@@ -41,15 +41,18 @@ A tensor a caller stores into one of the dicts is what the next step reads.
 
 Module attributes the reference's probes replace are looked up at call time:
 ``rmsnorm``, ``gated_rmsnorm``, ``_l2norm``, ``_apply_rope``,
-``_causal_conv1d_step``, ``_append_full_kv`` and ``_projection``.  While all of
+``_causal_conv1d_step``, ``_append_full_kv`` and ``_projection``, and the
+``torch.einsum`` / ``torch.softmax`` of the module's ``torch``.  While all of
 them are the originals, a layer runs its fused launches; once one is
 replaced, that layer runs the reference's sequence of calls through the
-module attributes, with the HIP kernels for what remains.
+module attributes, with the HIP kernels for what remains (with einsum or
+softmax replaced, the attention itself is the reference's torch sequence
+over the cache, so the replacements see its operands).
 
-Differences a caller can observe, all inside the stated tolerances: keys and
-values are stored as 16-bit values (fp16 for the fp32 and fp16 tokens of the
-step path, bf16 for bf16 tokens), so a key read back differs from the fp32
-token by at most one fp16 rounding.  Tensors on the CPU raise: the
+The kernels attend over 16-bit pages (fp16 for the fp32 and fp16 tokens of
+the step path, bf16 for bf16 tokens): attention outputs differ from the
+reference's fp32 cache within the stated tolerances, while the dicts read
+fp32 keys and values back exactly as appended.  Tensors on the CPU raise: the
 arithmetic exists only as HIP kernels.  ``_append_full_kv`` on CPU tensors
 keeps the reference's contiguous storage, because the reference's limit
 semantics are tested with CPU tensors and that path only stores.
@@ -97,8 +100,9 @@ class PagedKVTensor(torch.Tensor):
 
     Shape, dtype, device and ``requires_grad`` (False: the cache is detached,
     :365-372) are known without touching the pages; any other use (``detach``,
-    ``float``, indexing, arithmetic, comparisons) gathers the first T tokens
-    in logical order (ria_kv_gather) and converts them to the tensor's dtype.
+    ``float``, indexing, arithmetic, comparisons) reads the first T tokens in
+    logical order (fp32 tokens from the copies kept as appended, others out
+    of the pages with ria_kv_gather) in the tensor's dtype.
     Pages only grow, so a tensor taken before later appends keeps reading
     the T tokens it was created with.
     """
@@ -140,6 +144,10 @@ class _LayerKV:
     ``dtype`` is the dtype of the appended tokens, in which the dict tensors
     report and materialise; the pages hold bf16 for bf16 tokens and fp16
     otherwise (fp16 keeps the fp16 projection outputs of the GPU path exact).
+    fp32 tokens (the step path's, as the reference appends them, :306-307)
+    are also kept as they were appended, token-major [T, Hkv, 256] in
+    ``k32`` / ``v32``, so the dicts read back exactly what the reference
+    stores; the kernels attend over the pages.
     """
 
     def __init__(self, num_kv_heads: int, device: torch.device, dtype: torch.dtype, pages: int = 16):
@@ -147,8 +155,10 @@ class _LayerKV:
         self.device = torch.device(device)
         self.dtype = dtype
         self.page_dtype = torch.bfloat16 if dtype == torch.bfloat16 else torch.float16
+        self.exact = dtype == torch.float32
         self.length = 0
         self.views: tuple[PagedKVTensor, PagedKVTensor] | None = None
+        self.k32 = self.v32 = None
         self._alloc(pages)
 
     def _alloc(self, pages: int) -> None:
@@ -160,6 +170,14 @@ class _LayerKV:
             k[:used].copy_(self.k[:used])
             v[:used].copy_(self.v[:used])
         self.k, self.v = k, v
+        if self.exact:
+            shape = (pages * _PAGE, self.num_kv_heads, K.ATTN_HEAD_DIM)
+            k32 = torch.empty(shape, dtype=torch.float32, device=self.device)
+            v32 = torch.empty(shape, dtype=torch.float32, device=self.device)
+            if self.k32 is not None:
+                k32[:self.length].copy_(self.k32[:self.length])
+                v32[:self.length].copy_(self.v32[:self.length])
+            self.k32, self.v32 = k32, v32
         self.page_table = torch.arange(pages, dtype=torch.int32, device=self.device).reshape(1, pages)
 
     def reserve(self, tokens: int) -> None:
@@ -171,6 +189,11 @@ class _LayerKV:
             self._alloc(pages)
 
     def gather(self, count: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Tokens 0 .. count - 1 as [1, Hkv, count, 256]: the fp32 tokens as appended, else out of the pages."""
+        if self.exact:
+            count = int(count)
+            return (self.k32[:count].transpose(0, 1).unsqueeze(0).contiguous(),
+                    self.v32[:count].transpose(0, 1).unsqueeze(0).contiguous())
         return K.kv_gather(self.k, self.v, self.page_table, batch=1, start=0, count=int(count))
 
     def publish(self) -> tuple[PagedKVTensor, PagedKVTensor]:
@@ -187,6 +210,9 @@ class _LayerKV:
             v_rows = v.reshape(self.num_kv_heads, count, K.ATTN_HEAD_DIM).transpose(0, 1).contiguous()
             K.kv_append_seq(k_rows, v_rows.to(k_rows.dtype), self.k, self.v, self.page_table[0], start=0,
                             inv_freq=None)
+            if self.exact:
+                self.k32[:count].copy_(k_rows)
+                self.v32[:count].copy_(v_rows)
         self.length = count
 
 
@@ -253,7 +279,8 @@ class AttentionState:
         }
 
     def paged_kv_bytes(self) -> int:
-        """Bytes the resident keys and values occupy in their 16-bit pages (2 bytes per element)."""
+        """Bytes the resident keys and values occupy in their 16-bit pages (2 bytes per element; the
+        fp32 copies kept for the dicts are what ``full_bytes`` counts)."""
         return sum(2 * 2 * s.num_kv_heads * s.length * K.ATTN_HEAD_DIM for s in self.kv_stores.values())
 
 
@@ -600,8 +627,18 @@ def _paged_append(state: AttentionState, layer: int, k_token: torch.Tensor, v_to
     k2 = k_token.reshape(1, base.FULL_NUM_KV_HEADS, K.ATTN_HEAD_DIM).contiguous()
     v2 = v_token.reshape(1, base.FULL_NUM_KV_HEADS, K.ATTN_HEAD_DIM).contiguous()
     inv = None if position is None else _inv_freq(k_token.device)  # no RoPE: k is already rotated
-    K.kv_append(k2, v2, store.k, store.v, store.page_table, positions=int(position or 0), slots=store.length,
-                inv_freq=inv, k_norm_weight=k_norm_weight)
+    slot = store.length
+    if store.exact and position is not None:
+        # the kernel returns k after k_norm and RoPE in fp32, the token the reference stores
+        K.kv_append(k2, v2, store.k, store.v, store.page_table, positions=int(position), slots=slot, inv_freq=inv,
+                    k_norm_weight=k_norm_weight, k_rot_out=store.k32[slot:slot + 1])
+    else:
+        K.kv_append(k2, v2, store.k, store.v, store.page_table, positions=int(position or 0), slots=slot,
+                    inv_freq=inv, k_norm_weight=k_norm_weight)
+        if store.exact:
+            store.k32[slot].copy_(k2[0])
+    if store.exact:
+        store.v32[slot].copy_(v2[0])
     store.length += 1
     state.full_keys[int(layer)], state.full_values[int(layer)] = store.publish()
     return store
@@ -632,7 +669,8 @@ def _full_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> tor
     rope = globals()["_apply_rope"]
     append = globals()["_append_full_kv"]
 
-    if norm is _HIP_RMSNORM and rope is _HIP_APPLY_ROPE and append is _HIP_APPEND_FULL_KV:
+    if norm is _HIP_RMSNORM and rope is _HIP_APPLY_ROPE and append is _HIP_APPEND_FULL_KV \
+            and not _attention_ops_replaced():
         # q_norm / k_norm (:302-305) and RoPE run inside the append and
         # attention launches: RMSNorm in fp32, cast back to the projection
         # dtype, then RoPE.  The tokens the reference appends are fp32 (:306-307).
@@ -649,13 +687,40 @@ def _full_stateful(root: Path, layer: int, x0: torch.Tensor, device: str) -> tor
         q, k_token = rope(q, k, position)
         v_token = v.float().unsqueeze(2)
         full_k, full_v = append(state, layer, k_token, v_token)
-        attn = _attend_tensors(state, layer, full_k, full_v, q.squeeze(2).contiguous(), gate)
+        if _attention_ops_replaced():
+            attn = _attend_torch(full_k, full_v, q, gate)
+        else:
+            attn = _attend_tensors(state, layer, full_k, full_v, q.squeeze(2).contiguous(), gate)
     if attn.shape != (1, base.FULL_NUM_HEADS, base.FULL_HEAD_DIM):
         raise RuntimeError(f"Unexpected full-attention output shape: {tuple(attn.shape)}")
     attn_flat = attn.reshape(1, base.FULL_Q_DIM).to(dtype=compute_dtype)
     out_w = _projection(root, prefix + "self_attn.o_proj", device)
     attn_projected = F.linear(attn_flat.to(dtype=out_w.dtype), out_w).float()
     return x0.reshape(1, base.HIDDEN).float() + attn_projected
+
+
+def _attention_ops_replaced() -> bool:
+    """True while a caller has replaced ``torch.einsum`` or ``torch.softmax`` (the module's ``torch``).
+
+    The reference's probes capture the score, softmax and P V intermediates
+    by replacing them (qwen36_full_attention_residual_probe.py:104-153); a
+    layer then attends through them, as the reference does.
+    """
+    return torch.einsum is not _TORCH_EINSUM or torch.softmax is not _TORCH_SOFTMAX
+
+
+def _attend_torch(full_k: torch.Tensor, full_v: torch.Tensor, q: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    """The reference's attention sequence (:309-317) over the cache tensors, through ``torch.einsum`` /
+    ``torch.softmax`` as they are at call time.  Runs only while one of them is replaced."""
+    k_expanded = full_k.repeat_interleave(base.FULL_NUM_KV_GROUPS, dim=1).float()
+    v_expanded = full_v.repeat_interleave(base.FULL_NUM_KV_GROUPS, dim=1).float()
+    q_now = q.squeeze(2)
+    scores = torch.einsum("bhd,bhld->bhl", q_now, k_expanded) * (base.FULL_HEAD_DIM ** -0.5)
+    attn_weights = torch.softmax(scores, dim=-1)
+    attn = torch.einsum("bhl,bhld->bhd", attn_weights, v_expanded)
+    if attn.shape != (1, base.FULL_NUM_HEADS, base.FULL_HEAD_DIM):
+        raise RuntimeError(f"Unexpected full-attention output shape: {tuple(attn.shape)}")
+    return attn * torch.sigmoid(gate.float())
 
 
 def _attend(store: _LayerKV, q: torch.Tensor, gate: torch.Tensor, position: int | None,
@@ -761,3 +826,5 @@ _HIP_L2NORM = _l2norm
 _HIP_APPLY_ROPE = _apply_rope
 _HIP_CONV_STEP = _causal_conv1d_step
 _HIP_APPEND_FULL_KV = _append_full_kv
+_TORCH_EINSUM = torch.einsum
+_TORCH_SOFTMAX = torch.softmax

@@ -188,10 +188,14 @@ def is_full(layer: int) -> bool:
     return layer % 4 == 3
 
 
-def step_bytes(ctx: list[int], norms: bool = False) -> int:
+STACK_KINDS = ["full" if is_full(layer) else "linear" for layer in range(LAYERS)]
+
+
+def step_bytes(ctx: list[int], norms: bool = False, kinds: list[str] | None = None) -> int:
     """Algorithmic bytes of one decode step; ctx[b] = context incl. the new token."""
-    n_lin = sum(1 for layer in range(LAYERS) if not is_full(layer))
-    n_full = LAYERS - n_lin
+    kinds = STACK_KINDS if kinds is None else kinds
+    n_lin = sum(1 for k in kinds if k == "linear")
+    n_full = len(kinds) - n_lin
     b = len(ctx)
     per_seq = GDN_BYTES_PER_SEQ + (GDN_NORM_BYTES_PER_SEQ if norms else 0)
     lin = n_lin * (b * per_seq + GDN_BYTES_PER_LAYER)
@@ -570,12 +574,14 @@ def run_stack_graph(args, wl) -> dict:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     batch = wl["batch"]
+    kinds = wl.get("kinds", STACK_KINDS)
     lengths = W.ragged_lengths(wl["seed"], batch, wl["lo"], wl["hi"])
     warm = max(args.warmup, 1)
     total_new = warm + args.steps
     max_context = max(lengths) + total_new + 16
     num_pages = sum((n + total_new + 15) // 16 for n in lengths) + batch
-    st = BatchedAttentionState(batch, max_context, num_pages=num_pages, device=dev, page_shuffle_seed=wl["seed"])
+    st = BatchedAttentionState(batch, max_context, num_pages=num_pages, device=dev, page_shuffle_seed=wl["seed"],
+                               num_linear_layers=kinds.count("linear"), num_full_layers=kinds.count("full"))
     st.set_positions(lengths)
     st.reserve(total_new)
     gen = torch.Generator(device=dev)
@@ -602,7 +608,7 @@ def run_stack_graph(args, wl) -> dict:
     }
     # each step's inputs packed into one byte row, so feeding a step is one copy
     # into the staging row the graph reads (every size is a multiple of 16 bytes)
-    names = list(pool)
+    names = [k for k in pool if pool[k].numel()]  # a one-kind stack has no inputs of the other kind
     nbytes = [pool[k][0].numel() * pool[k].element_size() for k in names]
     packed = torch.cat([pool[k].reshape(total_new, -1).view(torch.uint8) for k in names], dim=1)
     staging = torch.empty((packed.shape[1],), dtype=torch.uint8, device=dev)
@@ -615,14 +621,15 @@ def run_stack_graph(args, wl) -> dict:
     attn_out = torch.empty((batch, NUM_Q_HEADS, HEAD_DIM_ATTN), device=dev, dtype=torch.bfloat16)
 
     def step():
-        for layer in range(LAYERS):
-            if is_full(layer):
-                fi = layer // 4
+        fi = li = 0
+        for kind in kinds:
+            if kind == "full":
                 st.full_step(fi, inp["qg"][fi, 0], inp["kv"][fi, 0], inp["kv"][fi, 1], inp["qg"][fi, 1], out=attn_out)
+                fi += 1
             else:
-                li = layer - layer // 4
                 st.linear_step(li, inp["mixed"][li], conv_w[li], inp["gate_ab"][li, 0], inp["gate_ab"][li, 1],
                                gate_mode=nat.RIA_GATE_RAW, A_log=a_log[li], dt_bias=dt_bias[li], out=gdn_out)
+                li += 1
         st.advance()
 
     def feed(s):
@@ -653,7 +660,7 @@ def run_stack_graph(args, wl) -> dict:
     torch.cuda.synchronize()
     elapsed = t0.elapsed_time(t1) / 1e3
     step_s = elapsed / args.steps
-    nbytes = step_bytes(ctx)
+    nbytes = step_bytes(ctx, kinds=kinds)
     return {"batch": batch, "ms_per_step": step_s * 1e3, "tok_s": batch / step_s, "step_bytes": nbytes,
             "achieved_GBps": nbytes / step_s / 1e9, "mean_ctx": sum(lengths) / batch}
 
@@ -1027,6 +1034,10 @@ def main() -> int:
             f"FETCH_SIZE*2.0 + WRITE_SIZE per launch from {prof['source']} (rocprofv3 --pmc, same workload); "
             f"algorithmic bytes of those launches {prof['algorithmic']}")
     batches = None if args.no_batches else run_batches()
+    layer_configs = prefill = None
+    if not args.no_batches:
+        layer_configs = run_layer_configs(cpu=not args.no_cpu_baseline)
+        prefill = run_prefill_sub(cpu=not args.no_cpu_baseline)
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU reference path on a sample")
@@ -1056,13 +1067,182 @@ def main() -> int:
         "step_hbm": gpu["step_hbm"],
         "kernels": gpu["kernels"],
         "batches": batches,
+        "layer_configs": layer_configs,
+        "prefill16k": prefill,
+        "device": device_record(),
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
     return 0
 
 
+def device_record() -> dict:
+    """hipGetDeviceProperties of the measured GPU, with the peaks the fractions are quoted against."""
+    from router_ia import _native as nat
+
+    rec = nat.device_record(torch.cuda.current_device())
+    rec["hbm_peak_GBps_used"] = HBM_PEAK_GBPS
+    rec["mfma_bf16_dense_peak_TFLOPs_used"] = MFMA_PEAK_TFLOPS
+    return rec
+
+
+PREFILL_SUB_STEPS, PREFILL_SUB_WARMUP = 5, 2
+
+
+def run_prefill_sub(cpu: bool) -> dict:
+    """The 16384-token prompt (one DeltaNet layer, chunked; one attention layer, causal) as a sub-record:
+    per-call times and MFMA fractions, with the reference's token-by-token CPU path on a sample."""
+    wl = WORKLOADS["prefill16k"]
+    r = run_prefill_gpu(argparse.Namespace(steps=PREFILL_SUB_STEPS, warmup=PREFILL_SUB_WARMUP), wl)
+    gdn = r["kernels"]["gdn_prefill (conv + chunk prep + chunk scan)"]
+    out = {
+        "prompt_tokens": PREFILL_LEN, "steps": PREFILL_SUB_STEPS,
+        "tok_s": round(r["tok_s"], 1), "ms_per_prompt": round(r["ms_per_step"], 4),
+        "deltanet_ms": round(gdn["avg_call_us"] / 1e3, 4), "deltanet_TFLOPs": gdn["achieved_TFLOPs"],
+        "deltanet_mfma_frac": gdn["frac"],
+        "attention_ms": round(r["roofline"]["avg_launch_us"] / 1e3, 4),
+        "attention_TFLOPs": r["roofline"]["achieved"], "attention_mfma_frac": r["roofline"]["frac"],
+        "kv_append_us": r["kernels"]["kv_append_kernel (prompt k/v into pages)"]["avg_call_us"],
+        "peak_TFLOPs": MFMA_PEAK_TFLOPS,
+        "timing": "HIP events around each call",
+    }
+    torch.cuda.empty_cache()
+    if cpu:
+        out["cpu_baseline"] = run_prefill_cpu(wl, 96, 96)
+    log(f"[bench] prefill16k: DeltaNet {out['deltanet_ms']} ms ({out['deltanet_mfma_frac']:.3f} of MFMA peak), "
+        f"attention {out['attention_ms']} ms ({out['attention_mfma_frac']:.3f})")
+    return out
+
+
 BATCH_STEPS, BATCH_WARMUP = 48, 4
+
+# The two single-layer batch-1 decode configurations, each run in full (every
+# step of the configuration, one graph replay per token).
+LAYER_CONFIGS = {
+    "gdn_layer_b1_64": dict(batch=1, lo=0, hi=0, seed=0, kinds=["linear"], steps=64,
+                            desc="single Gated DeltaNet layer, recurrent decode of 64 tokens, batch 1, zero state "
+                                 "(fused conv, raw gates, bf16 inputs)"),
+    "attn_layer_b1_4096_256": dict(batch=1, lo=4096, hi=4096, seed=1, kinds=["full"], steps=256,
+                                   desc="single full-attention layer decode, batch 1, 256 tokens appended to a "
+                                        "prefilled 4096-token bf16 KV cache (partial RoPE, sigmoid gate)"),
+}
+
+
+def run_layer_config_gpu(wl) -> dict:
+    """Every token of a single-layer batch-1 configuration captured as one HIP graph (the launches of all
+    tokens back to back, as a decode loop issues them), replayed from the starting position."""
+    from router_ia import _native as nat
+    from router_ia.batched_state import BatchedAttentionState
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    kinds, steps, ctx0 = wl["kinds"], wl["steps"], wl["lo"]
+    linear = kinds == ["linear"]
+    st = BatchedAttentionState(1, ctx0 + steps + 16, num_pages=(ctx0 + steps + 15) // 16 + 1, device=dev,
+                               page_shuffle_seed=wl["seed"], num_linear_layers=int(linear),
+                               num_full_layers=int(not linear))
+    st.set_positions([ctx0])
+    st.reserve(steps)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(wl["seed"])
+    if linear:
+        conv_w = (torch.randn((CONV_DIM, 1, 4), generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+        a_log = torch.rand((NUM_V_HEADS,), generator=gen, device=dev) * 4.0 - 4.0
+        dt_bias = torch.zeros((NUM_V_HEADS,), device=dev)
+        mixed = torch.randn((steps, 1, CONV_DIM), generator=gen, device=dev, dtype=torch.bfloat16)
+        gate_ab = torch.randn((steps, 2, 1, NUM_V_HEADS), generator=gen, device=dev)
+        out = torch.empty((1, NUM_V_HEADS, 128), device=dev, dtype=torch.bfloat16)
+    else:
+        st.kv.k[0].normal_(0.0, 1.0, generator=gen)
+        st.kv.v[0].normal_(0.0, 1.0, generator=gen)
+        qg = torch.randn((steps, 2, 1, NUM_Q_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev, dtype=torch.bfloat16)
+        kv = torch.randn((steps, 2, 1, NUM_KV_HEADS, HEAD_DIM_ATTN), generator=gen, device=dev, dtype=torch.bfloat16)
+        out = torch.empty((1, NUM_Q_HEADS, HEAD_DIM_ATTN), device=dev, dtype=torch.bfloat16)
+
+    def tokens():
+        for t in range(steps):
+            if linear:
+                st.linear_step(0, mixed[t], conv_w, gate_ab[t, 0], gate_ab[t, 1], gate_mode=nat.RIA_GATE_RAW,
+                               A_log=a_log, dt_bias=dt_bias, out=out)
+            else:
+                st.full_step(0, qg[t, 0], kv[t, 0], kv[t, 1], qg[t, 1], out=out)
+            st.advance()
+
+    pos0 = st._pos_ctx.clone()
+    host = (list(st._host_seen), st._min_headroom)
+
+    def rewind():
+        st._pos_ctx.copy_(pos0)
+        st._host_seen, st._min_headroom = list(host[0]), host[1]
+
+    tokens()  # eager once
+    torch.cuda.synchronize()
+    rewind()
+    graph = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        with torch.cuda.graph(graph, stream=cs):
+            tokens()
+    torch.cuda.current_stream().wait_stream(cs)
+    rewind()
+    graph.replay()
+    rewind()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    per_token = t0.elapsed_time(t1) / 1e3 / steps
+    nbytes = sum(step_bytes([ctx0 + t + 1], kinds=kinds) for t in range(steps)) / steps
+    return {"us_per_token": per_token * 1e6, "tok_s": 1.0 / per_token, "achieved_GBps": nbytes / per_token / 1e9}
+
+
+def run_layer_configs(cpu: bool) -> dict:
+    """The single-layer batch-1 configurations: GPU (all tokens in one graph) and, with `cpu`, the reference's
+    CPU path (the oracle's torch-CPU restatement) over the same number of tokens on this host."""
+    out = {"timing": "HIP events around one replay of the graph of every token; CPU wall time of the oracle"}
+    for name, wl in LAYER_CONFIGS.items():
+        r = run_layer_config_gpu(wl)
+        rec = {"desc": wl["desc"], "tokens": wl["steps"], "gpu_us_per_token": round(r["us_per_token"], 2),
+               "gpu_tok_s": round(r["tok_s"], 1), "achieved_GBps": round(r["achieved_GBps"], 1),
+               "frac": round(r["achieved_GBps"] / HBM_PEAK_GBPS, 4)}
+        torch.cuda.empty_cache()
+        if cpu:
+            cpu_s = time_layer_config_cpu(wl)
+            rec["cpu_tok_s"] = round(wl["steps"] / cpu_s, 2)
+            rec["cpu_cores"] = torch.get_num_threads()
+            rec["cpu_s"] = round(cpu_s, 3)
+        log(f"[bench] {name}: {rec['gpu_us_per_token']} us per token on the GPU"
+            + (f", CPU {rec['cpu_tok_s']} tok/s" if cpu else ""))
+        out[name] = rec
+    return out
+
+
+def time_layer_config_cpu(wl) -> float:
+    """Wall seconds of the oracle over every token of a single-layer configuration (its own seeded inputs)."""
+    from oracle import qwen36_cpu as O
+    from router_ia import workloads as W
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    steps = wl["steps"]
+    if wl["kinds"] == ["linear"]:
+        params = W.gdn_layer_params(wl["seed"])
+        inputs = W.gdn_step_inputs(wl["seed"], steps, 1)
+        conv_s = lin_s = None
+        t0 = time.perf_counter()
+        for t in range(steps):
+            beta, g = O.gating(inputs["a_raw"][t], inputs["b_raw"][t], params["A_log"], params["dt_bias"])
+            _, conv_s, lin_s = O.linear_decode_step(conv_s, lin_s, inputs["mixed"][t], params["conv_weight"], beta, g)
+        return time.perf_counter() - t0
+    kpre, vpre = W.prefilled_kv(wl["seed"], 1, wl["lo"])
+    x = W.attn_step_inputs(wl["seed"], steps, 1)
+    fk, fv = kpre.float(), vpre.float()
+    t0 = time.perf_counter()
+    for t in range(steps):
+        _, fk, fv = O.full_decode_step(fk, fv, x["q"][t], x["k"][t], x["v"][t], x["gate"][t], wl["lo"] + t)
+    return time.perf_counter() - t0
 
 
 def run_batches() -> dict:

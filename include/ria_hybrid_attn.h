@@ -62,7 +62,7 @@
 extern "C" {
 #endif
 
-#define RIA_ABI_VERSION 4
+#define RIA_ABI_VERSION 5
 
 enum ria_dtype { RIA_DT_BF16 = 0, RIA_DT_F16 = 1, RIA_DT_F32 = 2 };
 
@@ -88,6 +88,26 @@ int ria_abi_version(void);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* ria_last_error(void);
+
+/*
+ * The device a measurement ran on (from hipGetDeviceProperties), recorded
+ * beside the figures that are quoted against its published peaks.  No
+ * counterpart in the reference (it has no device path).
+ */
+typedef struct ria_device_record {
+  char name[256];
+  char arch[256];          /* gcnArchName, e.g. gfx950:sramecc+:xnack- */
+  int compute_units;
+  int clock_khz;           /* peak shader clock */
+  int memory_clock_khz;    /* peak memory clock */
+  int memory_bus_bits;
+  int64_t memory_bytes;
+  int l2_bytes;
+  int lds_bytes_per_cu;
+  int wavefront_size;
+} ria_device_record;
+
+int ria_device_info(int device, ria_device_record* out);
 
 /*
  * Gated DeltaNet decode: one token for each of `batch` sequences, one layer.

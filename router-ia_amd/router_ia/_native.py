@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIB_ENV = "RIA_HIP_LIB"
 DEFAULT_LIB = Path(__file__).resolve().parent / "_lib" / "libria_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 RIA_DT_BF16 = 0
 RIA_DT_F16 = 1
@@ -43,6 +43,7 @@ _vp = ctypes.c_void_p
 # name -> (restype, argtypes); mirrors include/ria_hybrid_attn.h.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ria_abi_version": (_c_int, []),
+    "ria_device_info": (_c_int, [_c_int, _vp]),
     "ria_last_error": (ctypes.c_char_p, []),
     "ria_gdn_decode": (
         _c_int,
@@ -156,6 +157,23 @@ class GdnDecodeDesc(ctypes.Structure):
                 ("A_log", _vp), ("dt_bias", _vp), ("qk_mode", _c_int), ("out", _vp), ("out_dtype", _c_int),
                 ("z", _vp), ("z_dtype", _c_int), ("z_row_stride", _c_i64), ("norm_weight", _vp),
                 ("pool_rows", _c_i64)]
+
+
+class DeviceRecord(ctypes.Structure):
+    """struct ria_device_record: the device a measurement ran on."""
+    _fields_ = [("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 256), ("compute_units", _c_int),
+                ("clock_khz", _c_int), ("memory_clock_khz", _c_int), ("memory_bus_bits", _c_int),
+                ("memory_bytes", _c_i64), ("l2_bytes", _c_int), ("lds_bytes_per_cu", _c_int),
+                ("wavefront_size", _c_int)]
+
+
+def device_record(device: int = 0) -> dict:
+    """hipGetDeviceProperties of `device` as a dict (ria_device_info)."""
+    rec = DeviceRecord()
+    check(load().ria_device_info(int(device), ctypes.byref(rec)), "ria_device_info")
+    out = {name: getattr(rec, name) for name, _ in DeviceRecord._fields_}
+    out["name"], out["arch"] = rec.name.decode(errors="replace"), rec.arch.decode(errors="replace")
+    return out
 
 
 class Fp8Proj(ctypes.Structure):

@@ -159,7 +159,8 @@ def _c_layout(struct: str, fields: list[str], tmp_path: Path) -> list[int]:
     return [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
 
 
-@pytest.mark.parametrize("cls,struct", [(nat.GdnDecodeDesc, "ria_gdn_decode_desc"), (nat.Fp8Proj, "ria_fp8_proj")])
+@pytest.mark.parametrize("cls,struct", [(nat.GdnDecodeDesc, "ria_gdn_decode_desc"), (nat.Fp8Proj, "ria_fp8_proj"),
+                                        (nat.DeviceRecord, "ria_device_record")])
 def test_ctypes_structs_match_the_header(cls, struct, tmp_path) -> None:
     names = [name for name, _ in cls._fields_]
     want = _c_layout(struct, names, tmp_path)

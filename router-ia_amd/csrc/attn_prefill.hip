@@ -207,9 +207,8 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   const int q_first = a.start + 16 * qb;         // first query position of the block
 
   // Direct-to-LDS copy of key block b (K and V tiles of pages 2b, 2b+1) into
-  // ring slot b % 4: 4 loads of 16 bytes per thread, always 4 so that the
-  // wait counts below hold; a page past the block's range reads page 0 and
-  // is masked out.
+  // ring slot b % 4: 4 loads of 16 bytes per thread; a page past the block's
+  // range reads page 0 and is masked out.
   auto slot_of = [&](int b) { return ring + (b % kRingSlots) * kSlotVec; };
   auto issue = [&](int b) {
     u32x4* slot = slot_of(b);
@@ -343,12 +342,14 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   issue(0);
   if (nblk > 1) issue(1);
   for (int b = 0; b < nblk; ++b) {
-    // this thread's copies of block b have landed; after the barrier every
-    // thread's have, and every wave is done with slot (b + 2) % 4 (block b - 2)
-    if (b + 1 < nblk)
-      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // every copy this thread has issued (blocks b and b + 1) has landed; after
+    // the barrier every thread's have, and every wave is done with slot
+    // (b + 2) % 4 (block b - 2).  The wait is for all copies, not a count of
+    // them: it relies on no ordering among the direct-to-LDS copies, only on
+    // each being written to LDS when the counter no longer holds it.  Block
+    // b + 1 was issued a whole iteration earlier, so waiting for it costs
+    // little.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (b + 2 < nblk) issue(b + 2);
     u32x4* slot = slot_of(b);
     if (32 * b + 31 > kmax) {

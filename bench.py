@@ -882,9 +882,12 @@ def run_prefill_gpu(args, wl) -> dict:
                       conv_weight=conv_w, conv_ring=ring, conv_pos=0, workspace=ws, gate_mode=nat.RIA_GATE_RAW,
                       A_log=a_log, dt_bias=dt_bias, z=z, norm_weight=gnw)
 
+    stage = torch.empty(K.prefill_stage_bytes(L, NUM_KV_HEADS), dtype=torch.uint8, device=dev)
+
     def attn(phase):
+        # the prompt starts the sequence: its attention reads fp16 copies of its keys (the stage)
         K.attn_prefill(q, k, v, gate, kv.k[0], kv.v[0], kv.page_table[0], attn_out, start=0, inv_freq=inv_freq,
-                       scale=HEAD_DIM_ATTN ** -0.5, phase=phase, q_norm_weight=qnw, k_norm_weight=knw)
+                       scale=HEAD_DIM_ATTN ** -0.5, phase=phase, q_norm_weight=qnw, k_norm_weight=knw, stage=stage)
 
     for _ in range(args.warmup):
         gdn()
@@ -928,8 +931,9 @@ def run_prefill_gpu(args, wl) -> dict:
             "algorithmic_flop_per_launch": attn_flop,
             "avg_launch_us": round(avg["attend"] * 1e6, 1),
             "launches": len(ev["attend"]),
-            "mfma_work_note": ("q and the probabilities run as bf16 hi+lo pairs, so the MFMA pipe executes "
-                               "2x the algorithmic FLOPs"),
+            "mfma_work_note": ("the prompt's keys and values are read from fp16 copies (the stage), so q and the "
+                               "probabilities are single fp16 operands: the MFMA pipe executes the algorithmic "
+                               "FLOPs once"),
         },
         "kernels": {
             "gdn_prefill (conv + chunk prep + chunk scan)": {
@@ -1283,7 +1287,8 @@ def prefill_main(args, wl) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 activations and KV, fp32 state and accumulate (MFMA bf16 hi+lo operands)",
+        "dtype": ("bf16 activations and KV pages, fp32 state and accumulate (DeltaNet: MFMA bf16 hi+lo operands; "
+                  "attention: fp16 copies of the prompt's keys and values, fp16 operands)"),
         "data": "synthetic (seeded random prompt inputs; projections excluded)",
         "config": {
             "workload": wl["desc"],

@@ -410,6 +410,38 @@ int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_heads,
                            void* out, int phase, void* stream);
 
 /*
+ * Bytes of the fp16 stage ria_attn_prefill_staged takes for a prompt of
+ * `length` tokens: the prompt's k and v as fp16 tiles in page layout.
+ */
+int64_t ria_attn_prefill_stage_bytes(int length, int num_kv_heads);
+
+/*
+ * ria_attn_prefill_phase with an fp16 stage (`stage`, stage_bytes >=
+ * ria_attn_prefill_stage_bytes, 16-byte aligned).  For a prompt that starts
+ * the sequence (start_pos 0) the append launch also writes the prompt's
+ * rotated k and its v as fp16 tiles into the stage (the pages get exactly
+ * what ria_attn_prefill_phase writes), and the attention launch reads its
+ * keys and values from the stage: fp16 operands carry 11 significant bits
+ * alone, so q and the probabilities need no bf16 hi + lo pair and the MFMA
+ * work halves, and the keys are nearer the reference's fp32 ones than the
+ * bf16 pages.  Both phases take the same stage.  With start_pos > 0 the call
+ * is ria_attn_prefill_phase (the resident keys are only in the pages).  No
+ * counterpart in the reference beyond :306-317 (its prefill is token by
+ * token).
+ */
+int ria_attn_prefill_staged(int length, int num_q_heads, int num_kv_heads,
+                            const void* q, int64_t q_row_stride,
+                            const void* k, int64_t k_row_stride,
+                            const void* v, int64_t v_row_stride,
+                            const void* gate, int64_t gate_row_stride, int act_dtype,
+                            void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                            const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
+                            const float* inv_freq, int rope_dim,
+                            const float* q_norm_weight, const float* k_norm_weight, float scale,
+                            void* stage, int64_t stage_bytes,
+                            void* out, int phase, void* stream);
+
+/*
  * Split size ria_attn_decode would choose for these context lengths (a host
  * array of `batch` tokens-attended counts): long splits, down to one page
  * per wave when the batch holds too few pages to occupy the GPU.  Passing

@@ -112,6 +112,8 @@ struct AppendArgs {
   int seq_len;  // prompt append: tokens at positions (and slots) pos_scalar .. pos_scalar + seq_len - 1
   float* k_out; // one-token append: row b's k after k_norm and RoPE in fp32 (before the page rounding)
                 // at k_out[(b * Hkv + kvh) * 256 + d], or null
+  uint16_t* stage_k;  // prompt append from slot 0: the prompt's k and v also as fp16 tiles in page
+  uint16_t* stage_v;  // layout, tile (logical page, KV head) at (page * Hkv + kvh) * 4096, or null
 };
 
 // RoPE of element d of a row: (x*cos + rotate_half(x)*sin) on [0, rope_dim),
@@ -182,6 +184,7 @@ __global__ __launch_bounds__(256) void kv_append_page_kernel(AppendArgs a) {
   __shared__ float k_s[kPageTokens][kAttnHeadDim];
   __shared__ float ss_s[kPageTokens][4];
   __shared__ __attribute__((aligned(16))) uint16_t kt_s[kTileElems];
+  __shared__ __attribute__((aligned(16))) uint16_t kt16_s[kTileElems];  // the fp16 copy (stage)
   float kv[kPageTokens], vv[kPageTokens];
 #pragma unroll
   for (int i = 0; i < kPageTokens; ++i) {
@@ -216,8 +219,25 @@ __global__ __launch_bounds__(256) void kv_append_page_kernel(AppendArgs a) {
     const float partner = d < a.rope_dim ? k_s[i][pd] : 0.f;
     const float kr = rope_elem(kv[i], partner, d, a.rope_dim, static_cast<float>(s0 + i), a.inv_freq);
     kt_s[k_tile_offset(i, d)] = Kv16<KVT>::from_f32(kr);
+    if (a.stage_k) kt16_s[k_tile_offset(i, d)] = Kv16<RIA_DT_F16>::from_f32(kr);
   }
   __syncthreads();
+  if (a.stage_k) {
+    // the whole tile (a prompt from slot 0 starts every page at token 0;
+    // tokens past its end hold zeros)
+    const int64_t st_tile = (int64_t)pg * a.num_kv_heads + kvh;
+    uint4* sk = reinterpret_cast<uint4*>(a.stage_k + st_tile * kTileElems);
+    sk[d] = reinterpret_cast<const uint4*>(kt16_s)[d];
+    sk[d + 256] = reinterpret_cast<const uint4*>(kt16_s)[d + 256];
+    uint32_t pk[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      pk[j] = static_cast<uint32_t>(Kv16<RIA_DT_F16>::from_f32(vv[2 * j])) |
+              (static_cast<uint32_t>(Kv16<RIA_DT_F16>::from_f32(vv[2 * j + 1])) << 16);
+    uint4* sv = reinterpret_cast<uint4*>(a.stage_v + (st_tile * kAttnHeadDim + d) * kPageTokens);
+    sv[0] = uint4{pk[0], pk[1], pk[2], pk[3]};
+    sv[1] = uint4{pk[4], pk[5], pk[6], pk[7]};
+  }
   uint16_t* kt = a.k_cache + tile * kTileElems;
   uint16_t* vt = a.v_cache + (tile * kAttnHeadDim + d) * kPageTokens;
   if (t_lo == 0 && t_hi == kPageTokens) {
@@ -1228,12 +1248,34 @@ extern "C" int ria_kv_append_out(int batch, int num_kv_heads, const void* k, int
                         stream);
 }
 
+namespace ria {
+// ria_kv_append_seq, optionally also writing the prompt's k and v as fp16 tiles (start_pos 0 only).
+int kv_append_seq_impl(int length, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
+                       const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache, int kv_dtype,
+                       int num_pages, const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
+                       const float* inv_freq, int rope_dim, const float* k_norm_weight, uint16_t* stage_k,
+                       uint16_t* stage_v, void* stream);
+}  // namespace ria
+
 extern "C" int ria_kv_append_seq(int length, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
                                  const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
                                  int kv_dtype, int num_pages, const int32_t* page_table_row, int64_t page_capacity,
                                  int32_t start_pos, const float* inv_freq, int rope_dim,
                                  const float* k_norm_weight, void* stream) {
+  return kv_append_seq_impl(length, num_kv_heads, k, k_dtype, k_row_stride, v, v_dtype, v_row_stride, k_cache,
+                            v_cache, kv_dtype, num_pages, page_table_row, page_capacity, start_pos, inv_freq,
+                            rope_dim, k_norm_weight, nullptr, nullptr, stream);
+}
+
+int ria::kv_append_seq_impl(int length, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
+                            const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache,
+                            int kv_dtype, int num_pages, const int32_t* page_table_row, int64_t page_capacity,
+                            int32_t start_pos, const float* inv_freq, int rope_dim, const float* k_norm_weight,
+                            uint16_t* stage_k, uint16_t* stage_v, void* stream) {
   if (length < 0 || start_pos < 0) return set_error(RIA_ERR_INVALID, "ria_kv_append_seq: negative length or start");
+  if (stage_k && (start_pos != 0 || !stage_v || (reinterpret_cast<uintptr_t>(stage_k) |
+                                                  reinterpret_cast<uintptr_t>(stage_v)) % 16))
+    return set_error(RIA_ERR_INVALID, "ria_kv_append_seq: an fp16 stage needs start 0 and 16-byte aligned k and v");
   int rc = check_append_common("ria_kv_append_seq", num_kv_heads, k, k_dtype, k_row_stride, v, v_dtype,
                                v_row_stride, k_cache, v_cache, kv_dtype, page_table_row, inv_freq, rope_dim);
   if (rc != RIA_OK) return rc;
@@ -1259,6 +1301,8 @@ extern "C" int ria_kv_append_seq(int length, int num_kv_heads, const void* k, in
   a.norm_w = k_norm_weight;
   a.num_kv_heads = num_kv_heads;
   a.seq_len = length;
+  a.stage_k = stage_k;
+  a.stage_v = stage_v;
   launch_append(a, 0, k_dtype, v_dtype, kv_dtype, static_cast<hipStream_t>(stream));
   return check_launch("ria_kv_append_seq");
 }

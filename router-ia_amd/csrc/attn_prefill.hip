@@ -71,6 +71,7 @@ struct PrefillAttnArgs {
   int num_kv_heads;
   int group;
   void* out;
+  int staged;  // keys from an fp16 stage with tile (page p, KV head) at p * Hkv + kvh, not the page table
 };
 
 // Key held by row r (0..15) of score tile m (0, 1) of a 32-key block, as
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg) {
       const int p = 2 * b + pg;
-      int phys = p < npages ? pt[p] : 0;
+      int phys = p < npages ? (a.staged ? p : pt[p]) : 0;
       phys = (phys < 0 || phys >= a.num_pages) ? 0 : phys;  // unallocated entries never fault
       const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
       const u32x4* kp = reinterpret_cast<const u32x4*>(a.k_cache + tile * kTile);
@@ -423,14 +424,23 @@ using namespace ria;
 
 
 
-extern "C" int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_heads, const void* q,
-                                      int64_t q_row_stride, const void* k, int64_t k_row_stride, const void* v,
-                                      int64_t v_row_stride, const void* gate, int64_t gate_row_stride, int act_dtype,
-                                      void* k_cache, void* v_cache, int kv_dtype, int num_pages,
-                                      const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
-                                      const float* inv_freq, int rope_dim, const float* q_norm_weight,
-                                      const float* k_norm_weight, float scale, void* out, int phase,
-                                      void* stream) {
+namespace ria {
+int kv_append_seq_impl(int length, int num_kv_heads, const void* k, int k_dtype, int64_t k_row_stride,
+                       const void* v, int v_dtype, int64_t v_row_stride, void* k_cache, void* v_cache, int kv_dtype,
+                       int num_pages, const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
+                       const float* inv_freq, int rope_dim, const float* k_norm_weight, uint16_t* stage_k,
+                       uint16_t* stage_v, void* stream);
+
+static int64_t stage_half_bytes(int length, int num_kv_heads) {
+  return (int64_t)((length + kPageTokens - 1) / kPageTokens) * num_kv_heads * kTile * 2;
+}
+
+static int prefill_impl(int length, int num_q_heads, int num_kv_heads, const void* q, int64_t q_row_stride,
+                        const void* k, int64_t k_row_stride, const void* v, int64_t v_row_stride, const void* gate,
+                        int64_t gate_row_stride, int act_dtype, void* k_cache, void* v_cache, int kv_dtype,
+                        int num_pages, const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
+                        const float* inv_freq, int rope_dim, const float* q_norm_weight, const float* k_norm_weight,
+                        float scale, void* stage, int64_t stage_bytes, void* out, int phase, void* stream) {
   if (phase < RIA_PREFILL_APPEND || phase > RIA_PREFILL_BOTH)
     return set_error(RIA_ERR_INVALID, "ria_attn_prefill: phase must be 1 (append), 2 (attention) or 3 (both)");
   if (length < 0 || start_pos < 0) return set_error(RIA_ERR_INVALID, "ria_attn_prefill: negative length or start");
@@ -460,10 +470,23 @@ extern "C" int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_he
   if (length == 0) return RIA_OK;
   const int64_t blocks = (int64_t)((length + 15) / 16) * num_kv_heads;
   if (blocks > 0x7fffffff) return set_error(RIA_ERR_INVALID, "ria_attn_prefill: grid too large");
+  // a prompt from slot 0 with a stage: its keys also go to fp16 tiles, which the attention reads
+  const bool staged = stage && start_pos == 0;
+  uint16_t* stage_k = nullptr;
+  uint16_t* stage_v = nullptr;
+  if (staged) {
+    const int64_t half = stage_half_bytes(length, num_kv_heads);
+    if (stage_bytes < 2 * half)
+      return set_error(RIA_ERR_WORKSPACE, "ria_attn_prefill: stage %lld bytes < required %lld",
+                       (long long)stage_bytes, (long long)(2 * half));
+    if (reinterpret_cast<uintptr_t>(stage) % 16) return set_error(RIA_ERR_INVALID, "ria_attn_prefill: stage must be 16-byte aligned");
+    stage_k = static_cast<uint16_t*>(stage);
+    stage_v = stage_k + half / 2;
+  }
   if (phase & RIA_PREFILL_APPEND) {
-    int rc = ria_kv_append_seq(length, num_kv_heads, k, act_dtype, k_row_stride, v, act_dtype, v_row_stride,
-                               k_cache, v_cache, kv_dtype, num_pages, page_table_row, page_capacity, start_pos,
-                               inv_freq, rope_dim, k_norm_weight, stream);
+    int rc = kv_append_seq_impl(length, num_kv_heads, k, act_dtype, k_row_stride, v, act_dtype, v_row_stride,
+                                k_cache, v_cache, kv_dtype, num_pages, page_table_row, page_capacity, start_pos,
+                                inv_freq, rope_dim, k_norm_weight, stage_k, stage_v, stream);
     if (rc != RIA_OK) return rc;
   }
   if (!(phase & RIA_PREFILL_ATTEND)) return RIA_OK;
@@ -486,15 +509,58 @@ extern "C" int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_he
   a.num_kv_heads = num_kv_heads;
   a.group = group;
   a.out = out;
+  int key_dtype = kv_dtype;
+  if (staged) {  // the prompt's own fp16 tiles, logical page p at tile p
+    a.k_cache = stage_k;
+    a.v_cache = stage_v;
+    a.num_pages = (length + kPageTokens - 1) / kPageTokens;
+    a.staged = 1;
+    key_dtype = RIA_DT_F16;
+  }
   dim3 grid(static_cast<unsigned>(blocks));
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (act_dtype == RIA_DT_BF16)
-    launch_prefill<RIA_DT_BF16>(a, page_table_row, kv_dtype, grid, st);
+    launch_prefill<RIA_DT_BF16>(a, page_table_row, key_dtype, grid, st);
   else if (act_dtype == RIA_DT_F16)
-    launch_prefill<RIA_DT_F16>(a, page_table_row, kv_dtype, grid, st);
+    launch_prefill<RIA_DT_F16>(a, page_table_row, key_dtype, grid, st);
   else
-    launch_prefill<RIA_DT_F32>(a, page_table_row, kv_dtype, grid, st);
+    launch_prefill<RIA_DT_F32>(a, page_table_row, key_dtype, grid, st);
   return check_launch("ria_attn_prefill");
+}
+}  // namespace ria
+
+extern "C" int ria_attn_prefill_phase(int length, int num_q_heads, int num_kv_heads, const void* q,
+                                      int64_t q_row_stride, const void* k, int64_t k_row_stride, const void* v,
+                                      int64_t v_row_stride, const void* gate, int64_t gate_row_stride, int act_dtype,
+                                      void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                                      const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
+                                      const float* inv_freq, int rope_dim, const float* q_norm_weight,
+                                      const float* k_norm_weight, float scale, void* out, int phase,
+                                      void* stream) {
+  return prefill_impl(length, num_q_heads, num_kv_heads, q, q_row_stride, k, k_row_stride, v, v_row_stride, gate,
+                      gate_row_stride, act_dtype, k_cache, v_cache, kv_dtype, num_pages, page_table_row,
+                      page_capacity, start_pos, inv_freq, rope_dim, q_norm_weight, k_norm_weight, scale, nullptr, 0,
+                      out, phase, stream);
+}
+
+extern "C" int64_t ria_attn_prefill_stage_bytes(int length, int num_kv_heads) {
+  if (length <= 0 || num_kv_heads <= 0) return 0;
+  return 2 * stage_half_bytes(length, num_kv_heads);
+}
+
+extern "C" int ria_attn_prefill_staged(int length, int num_q_heads, int num_kv_heads, const void* q,
+                                       int64_t q_row_stride, const void* k, int64_t k_row_stride, const void* v,
+                                       int64_t v_row_stride, const void* gate, int64_t gate_row_stride,
+                                       int act_dtype, void* k_cache, void* v_cache, int kv_dtype, int num_pages,
+                                       const int32_t* page_table_row, int64_t page_capacity, int32_t start_pos,
+                                       const float* inv_freq, int rope_dim, const float* q_norm_weight,
+                                       const float* k_norm_weight, float scale, void* stage, int64_t stage_bytes,
+                                       void* out, int phase, void* stream) {
+  if (!stage) return set_error(RIA_ERR_INVALID, "ria_attn_prefill_staged: null stage");
+  return prefill_impl(length, num_q_heads, num_kv_heads, q, q_row_stride, k, k_row_stride, v, v_row_stride, gate,
+                      gate_row_stride, act_dtype, k_cache, v_cache, kv_dtype, num_pages, page_table_row,
+                      page_capacity, start_pos, inv_freq, rope_dim, q_norm_weight, k_norm_weight, scale, stage,
+                      stage_bytes, out, phase, stream);
 }
 
 extern "C" int ria_attn_prefill(int length, int num_q_heads, int num_kv_heads, const void* q, int64_t q_row_stride,

@@ -143,6 +143,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_int, _c_int, _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _vp, _vp,
          _c_int, _c_int, _vp, _c_i64, _c_i32, _vp, _c_int, _vp, _vp, _c_f32, _vp, _c_int, _vp],
     ),
+    "ria_attn_prefill_stage_bytes": (_c_i64, [_c_int, _c_int]),
+    "ria_attn_prefill_staged": (
+        _c_int,
+        [_c_int, _c_int, _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _vp, _vp,
+         _c_int, _c_int, _vp, _c_i64, _c_i32, _vp, _c_int, _vp, _vp, _c_f32, _vp, _c_i64, _vp, _c_int, _vp],
+    ),
 }
 
 

@@ -112,6 +112,7 @@ class BatchedAttentionState:
         # workspace (about 75 KB per token) is allocated on the first prefill
         self.prefill_segment_tokens = max(64, int(prefill_segment_tokens))
         self.prefill_workspace: torch.Tensor | None = None
+        self.prefill_stage: torch.Tensor | None = None  # fp16 keys of a prompt from slot 0 (attention prefill)
 
     def _size_workspace(self) -> None:
         ws = K.attn_decode_workspace_bytes(self.max_seqs, self.num_q_heads, self.num_kv_heads, self.max_context,
@@ -279,9 +280,18 @@ class BatchedAttentionState:
     ) -> torch.Tensor:
         """Append a prompt's k, v (RoPE on k) to one row and run its causal attention; q, gate [L, Hq, 256]."""
         k_cache, v_cache = self.kv.layer(layer)
+        start = self._host_seen[row]
+        # a prompt that starts the row attends over fp16 copies of its own keys (the stage)
+        stage = self._prefill_stage(int(q.shape[0])) if start == 0 else None
         return K.attn_prefill(q, k, v, gate, k_cache, v_cache, self.kv.page_table[row], out,
-                              start=self._host_seen[row], inv_freq=self.inv_freq, scale=self.scale,
-                              q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight)
+                              start=start, inv_freq=self.inv_freq, scale=self.scale,
+                              q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight, stage=stage)
+
+    def _prefill_stage(self, length: int) -> torch.Tensor:
+        need = K.prefill_stage_bytes(length, self.num_kv_heads)
+        if self.prefill_stage is None or self.prefill_stage.numel() < need:
+            self.prefill_stage = torch.empty(need, dtype=torch.uint8, device=self.device)
+        return self.prefill_stage
 
     def end_prefill(self, row: int, length: int) -> None:
         """The row's position moves past the prompt (after every layer has run it)."""

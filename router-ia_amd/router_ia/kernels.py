@@ -1047,6 +1047,7 @@ def attn_prefill(
     phase: int = nat.RIA_PREFILL_BOTH,
     q_norm_weight: torch.Tensor | None = None,
     k_norm_weight: torch.Tensor | None = None,
+    stage: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Causal GQA prefill of one sequence's prompt over its paged cache (ria_attn_prefill_phase).
 
@@ -1054,7 +1055,11 @@ def attn_prefill(
     k/v are appended at slots start .. start + L - 1 first.  Returns out
     [L, Hq, 256] in that dtype.  phase selects the append launch, the
     attention launch or both (the default).  With the fp32 q_norm / k_norm
-    weights [256], q and k are RMSNorm'd before RoPE.
+    weights [256], q and k are RMSNorm'd before RoPE.  With a ``stage`` (a
+    uint8 device tensor of at least prefill_stage_bytes(L, Hkv); both phases
+    take the same one) a prompt that starts the sequence (start 0) is
+    attended over fp16 copies of its own keys and values
+    (ria_attn_prefill_staged).
     """
     length = int(q.shape[0])
     num_q_heads = int(q.shape[1])
@@ -1079,12 +1084,22 @@ def attn_prefill(
     if tuple(out.shape) != (length, num_q_heads, ATTN_HEAD_DIM) or not out.is_contiguous() or out.dtype != q.dtype:
         raise ValueError(f"out must be contiguous [{length}, {num_q_heads}, 256] of q's dtype")
     rope_dim = 0 if inv_freq is None else 2 * int(inv_freq.numel())
-    rc = nat.load().ria_attn_prefill_phase(length, num_q_heads, num_kv_heads, _ptr(q), qs, _ptr(k), ks, _ptr(v),
-                                           vs, _ptr(gate), gs, dtype_code(q), _ptr(k_cache), _ptr(v_cache),
-                                           dtype_code(k_cache), pages, _ptr(page_table), cap, int(start),
-                                           _ptr(inv_freq), rope_dim,
-                                           _norm_weight("q_norm_weight", q_norm_weight, ATTN_HEAD_DIM, dev),
-                                           _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev),
-                                           float(scale), _ptr(out), int(phase), _stream(dev))
+    head = (length, num_q_heads, num_kv_heads, _ptr(q), qs, _ptr(k), ks, _ptr(v), vs, _ptr(gate), gs, dtype_code(q),
+            _ptr(k_cache), _ptr(v_cache), dtype_code(k_cache), pages, _ptr(page_table), cap, int(start),
+            _ptr(inv_freq), rope_dim, _norm_weight("q_norm_weight", q_norm_weight, ATTN_HEAD_DIM, dev),
+            _norm_weight("k_norm_weight", k_norm_weight, ATTN_HEAD_DIM, dev), float(scale))
+    if stage is None:
+        rc = nat.load().ria_attn_prefill_phase(*head, _ptr(out), int(phase), _stream(dev))
+    else:
+        _require_gpu("stage", stage, dev)
+        if not stage.is_contiguous():
+            raise ValueError("stage must be contiguous")
+        rc = nat.load().ria_attn_prefill_staged(*head, _ptr(stage), stage.numel() * stage.element_size(), _ptr(out),
+                                                int(phase), _stream(dev))
     nat.check(rc, "ria_attn_prefill")
     return out
+
+
+def prefill_stage_bytes(length: int, num_kv_heads: int) -> int:
+    """Bytes of the fp16 stage attn_prefill takes for a prompt of `length` tokens (ria_attn_prefill_stage_bytes)."""
+    return int(nat.load().ria_attn_prefill_stage_bytes(int(length), int(num_kv_heads)))

@@ -27,8 +27,10 @@
 //                        fp32 x.
 //   linear_fp8_ks_kernel past 16 rows with fp16 x (the forward loop's
 //                        projections): one workgroup per tile of rows x
-//                        features over the whole K, split between its waves,
-//                        operands streamed straight into registers.
+//                        features over the whole K, split between its waves;
+//                        operands loaded row-contiguous into registers and
+//                        turned into MFMA operands through each wave's own
+//                        LDS region.
 #include <algorithm>
 #include <type_traits>
 #include <utility>
@@ -38,6 +40,9 @@
 namespace ria {
 
 constexpr int kFp8Block = 128;  // scale block edge (qwen36_dequant.py:13)
+// Word 3 of a raw buffer resource on gfx9-family parts: data format 32 bits
+// (a zero format makes every load return zero), no swizzle, no index stride.
+constexpr int kBufferWord3 = 0x00020000;
 constexpr int kLinRing = 12;    // weight chunks in flight per workgroup
 constexpr int kXAhead = 2;      // chunks of x loaded ahead of the MFMAs
 constexpr int kLinRows = 128;   // most rows of x per workgroup (4 consumer waves x 32)
@@ -575,14 +580,16 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
 // Past 16 rows with fp16 x: one workgroup per tile of 16 RT rows x 16 CT
 // features over the whole of K, whose NW waves split K between them: wave w
 // takes the 64-K chunks w, w + NW, w + 2 NW, ...  Each wave loads its own x
-// and weight bytes straight into registers, D chunks deep, with no LDS and no
-// barrier in the loop (every byte the workgroup needs is loaded once, by one
-// wave), dequantises each weight once and feeds it to RT MFMAs.  The waves'
-// partial tiles meet in LDS at the end and are added in wave order.  K order
-// inside a chunk: a lane's 16 weight bytes at K = 64 c + 16 g .. + 15 feed two
-// MFMAs (the low 8 bytes the first, the high 8 the second, as k group g of
-// each), and its x operands take the same K.  CH > 0: every wave has exactly
-// CH chunks (K = 64 NW CH), unrolled; CH = 0: any K, in groups of D chunks.
+// and weight bytes into registers, D chunks deep, with row-contiguous loads
+// (a few cache lines per load), passes each chunk through its own LDS region
+// to turn the rows into MFMA operands (no barrier in the loop: every byte the
+// workgroup needs is loaded once, by one wave), dequantises each weight once
+// and feeds it to RT MFMAs.  The waves' partial tiles meet in LDS at the end
+// and are added in wave order.  K order inside a chunk: a lane's 16 weight
+// bytes at K = 64 c + 16 g .. + 15 feed two MFMAs (the low 8 bytes the first,
+// the high 8 the second, as k group g of each), and its x operands take the
+// same K.  CH > 0: every wave has exactly CH chunks (K = 64 NW CH), unrolled;
+// CH = 0: any K, in groups of D chunks.
 constexpr int kKsChunk = 64;
 
 template <int RT, int CT, int NW, int D, int CH>
@@ -616,36 +623,89 @@ __global__ __launch_bounds__(64 * NW) void linear_fp8_ks_kernel(const LinearArgs
   const int m0 = blockIdx.y * 16 * RT;
   const int chunks = a.k / kKsChunk;
   const int cnt = (chunks - wave + NW - 1) / NW;  // this wave's chunks (0 when K has fewer than NW)
-  const uint16_t* x = static_cast<const uint16_t*>(a.x);
-  // rows past the last token and features past n repeat the last one: their
-  // results are computed and never stored.  Offsets fit 32 bits (checked on
-  // the host), which keeps the address registers to one per operand row.
-  uint32_t xo[RT], wo[CT];
+  // Operands come through buffer loads: a per-lane byte offset fixed for the
+  // kernel plus the chunk's offset in a scalar register, so a load costs no
+  // address arithmetic.  Byte offsets fit 32 bits (checked on the host).
+  // Rows past the last token and features past n repeat the last one: their
+  // results are computed and never stored.  The loads walk along the rows
+  // (x: load j holds rows 8 j .. 8 j + 7, lane l row 8 j + l / 8, 16-byte
+  // piece l % 8; weights: load ct holds the 16 rows of column tile ct, lane l
+  // row l / 4, piece l % 4), so every load covers whole row segments of a few
+  // cache lines, and the wave's own LDS region turns the pieces into MFMA
+  // operands (lane (n16, g4): row n16, K pieces 2 g4 and 2 g4 + 1 of x, piece
+  // g4 of the weights; the two K orders agree, so each product pairs the
+  // right elements).
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(a.x), 0, static_cast<int>(static_cast<uint32_t>(((int64_t)(a.m - 1) * a.x_stride + a.k) * 2)), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t wr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w), 0, static_cast<int>(static_cast<uint32_t>((int64_t)n * a.k)), kBufferWord3);
+  uint32_t xo[2 * RT], wo[CT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-    xo[rt] = static_cast<uint32_t>(min(m0 + 16 * rt + n16, a.m - 1) * a.x_stride + 16 * g4);
+  for (int j = 0; j < 2 * RT; ++j)
+    xo[j] = static_cast<uint32_t>((min(m0 + 8 * j + (lane >> 3), a.m - 1) * a.x_stride + 8 * (lane & 7)) * 2);
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) wo[ct] = static_cast<uint32_t>(min(n0 + 16 * ct + n16, n - 1) * a.k + 16 * g4);
+  for (int ct = 0; ct < CT; ++ct)
+    wo[ct] = static_cast<uint32_t>(min(n0 + 16 * ct + (lane >> 2), n - 1) * a.k + 16 * (lane & 3));
   const float* sp = scale + (int64_t)(n0 / kFp8Block) * (a.k / kFp8Block);
+  auto bload = [](__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  };
 
   struct Stage {
-    u32x4 x[RT][2];
+    u32x4 x[RT][2];  // the 2 RT row-contiguous x loads, in order
     u32x4 w[CT];
     float s;
   };
   Stage st[D];
   // chunk i of this wave into s (past the wave's last chunk: the last one again, never used)
-  auto load = [&](Stage& s, int i) {
+  auto load = [&](Stage& s, int i) __attribute__((always_inline)) {
     const int c = wave + NW * min(i, cnt - 1);
-    const uint32_t ko = static_cast<uint32_t>(c * kKsChunk);
+    const int ko = c * kKsChunk;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      s.x[rt][0] = *reinterpret_cast<const u32x4*>(x + xo[rt] + ko);
-      s.x[rt][1] = *reinterpret_cast<const u32x4*>(x + xo[rt] + ko + 8);
+      s.x[rt][0] = bload(xr, xo[2 * rt], 2 * ko);
+      s.x[rt][1] = bload(xr, xo[2 * rt + 1], 2 * ko);
     }
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) s.w[ct] = *reinterpret_cast<const u32x4*>(w + wo[ct] + ko);
+    for (int ct = 0; ct < CT; ++ct) s.w[ct] = bload(wr, wo[ct], ko);
     s.s = sp[c * kKsChunk / kFp8Block];
+  };
+  // The wave's LDS region, 16-byte entries.  x: block (row tile rt, piece q)
+  // of 16 entries, tile row r at entry r ^ hx(q); weights: block (column tile
+  // ct, piece p), tile row r at entry r ^ hw(p).  The
+  // XOR patterns make every group of 8 or 16 consecutive lanes hit distinct
+  // entries modulo 8 or 16 for the stores (x: 8 lanes per row, 2 rows per 16
+  // lanes; weights: 4 lanes per row) and for the operand reads (16 rows of
+  // one piece), so neither side has bank conflicts.  The wave writes a chunk
+  // and reads it back in its own order (LDS operations of one wave complete
+  // in order), so one region per wave is enough.
+  auto hx = [](int q) { return q ^ ((q & 1) << 3); };
+  auto hw = [](int p) { return (p << 1) | ((p & 1) << 3); };
+  constexpr int kLtX = RT * 8 * 16, kLtW = CT * 4 * 16;  // entries
+  constexpr int kPartBytes = NW * kTiles * 64 * 16;
+  constexpr int kLtBytes = NW * (kLtX + kLtW) * 16;
+  __shared__ __attribute__((aligned(16))) unsigned char ks_lds[kPartBytes > kLtBytes ? kPartBytes : kLtBytes];
+  u32x4* lt = reinterpret_cast<u32x4*>(ks_lds) + wave * (kLtX + kLtW);
+  auto operands = [&](const Stage& s, u32x4 (&xa)[RT][2], u32x4 (&wb)[CT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 2 * RT; ++j) {
+      const int r = 8 * j + (lane >> 3), q = lane & 7;  // tile row r % 16 of row tile r / 16
+      lt[((r >> 4) * 8 + q) * 16 + ((r & 15) ^ hx(q))] = s.x[j >> 1][j & 1];
+    }
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int r = lane >> 2, p = lane & 3;
+      lt[kLtX + (ct * 4 + p) * 16 + (r ^ hw(p))] = s.w[ct];
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int q = 2 * g4 + h;
+        xa[rt][h] = lt[(rt * 8 + q) * 16 + (n16 ^ hx(q))];
+      }
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) wb[ct] = lt[kLtX + (ct * 4 + g4) * 16 + (n16 ^ hw(g4))];
   };
   f32x4 acc[RT][CT];
 #pragma unroll
@@ -658,21 +718,23 @@ __global__ __launch_bounds__(64 * NW) void linear_fp8_ks_kernel(const LinearArgs
     // with chunk i + D - 1.  The scheduling barrier keeps the refill loads
     // ahead of the MFMAs (the scheduler would otherwise sink each load next
     // to its use, which leaves one chunk in flight).
-    auto step = [&](auto u, auto i, bool refill) {
+    auto step = [&](auto u, auto i, bool refill) __attribute__((always_inline)) {
       if (refill) load(st[(u + D - 1) % D], i + D - 1);
       __builtin_amdgcn_sched_barrier(0);
       const Stage& s = st[u];
+      u32x4 xa[RT][2], wb[CT];
+      operands(s, xa, wb);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        const u32x4 v = s.w[ct];
+        const u32x4 v = wb[ct];
         const u32x4 b0{dequant_pair<false>(v[0], s.s), dequant_pair<true>(v[0], s.s), dequant_pair<false>(v[1], s.s),
                        dequant_pair<true>(v[1], s.s)};
         const u32x4 b1{dequant_pair<false>(v[2], s.s), dequant_pair<true>(v[2], s.s), dequant_pair<false>(v[3], s.s),
                        dequant_pair<true>(v[3], s.s)};
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = F16::mfma_k32(s.x[rt][0], b0, acc[rt][ct]);
+        for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = F16::mfma_k32(xa[rt][0], b0, acc[rt][ct]);
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = F16::mfma_k32(s.x[rt][1], b1, acc[rt][ct]);
+        for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = F16::mfma_k32(xa[rt][1], b1, acc[rt][ct]);
       }
     };
     if constexpr (CH > 0) {
@@ -691,7 +753,8 @@ __global__ __launch_bounds__(64 * NW) void linear_fp8_ks_kernel(const LinearArgs
   }
 
   // ---- the waves' partial tiles, added in wave order; wave w finishes tiles w, w + NW, ..
-  __shared__ f32x4 part[NW][kTiles][64];
+  __syncthreads();  // the partial tiles reuse the waves' LDS regions
+  auto part = reinterpret_cast<f32x4(*)[kTiles][64]>(ks_lds);
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -763,7 +826,7 @@ static void launch_linear(const LinearArgs& a, int ct, dim3 grid, hipStream_t st
     hipLaunchKernelGGL((linear_fp8_kernel<XT, 1>), grid, dim3(512), 0, st, a);
 }
 
-// Every K takes the register-streaming K-split kernel with four waves,
+// Every K takes the K-split kernel with four waves,
 // straight-line for 8 or 16 chunks per wave (K = 2048, the hidden width, and
 // K = 4096, the value width).  The wave count is fixed and every shape runs
 // the waves over the same chunks in the same order, so a projection's result

@@ -737,7 +737,7 @@ def proj_main(args, wl) -> int:
         "config": {"workload": wl["desc"], "batch": gpu["batch"], "fp8_weight_GB": round(gpu["weight_bytes"] / 1e9, 3),
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm",
-                     "kernel": ("gemv_fp8_kernel" if gpu["batch"] <= 16 else "linear_fp8_kernel")
+                     "kernel": ("gemv_fp8_kernel" if gpu["batch"] <= 16 else "linear_fp8_ks_kernel")
                      + " (ria_linear_fp8_group), all launches of the step",
                      "achieved": round(gpu["achieved_GBps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gpu["achieved_GBps"] / HBM_PEAK_GBPS, 4), "traffic": None,

@@ -38,20 +38,27 @@ constexpr int kChunk = 64;
 constexpr int kDim = kGdnHeadDim;  // 128
 
 // Per (chunk, head) phase-A record, consumed by phase B.  Operands are stored
-// pre-split (bf16 hi, bf16 lo) in MFMA 16x16x32 operand order, one 16-byte
-// unit per lane, so phase B loads them as contiguous 1 KiB wavefront reads:
-//   Qt  exp(G) q        A operand, [token tile 4][k-step 4][hi/lo][lane]
-//   Wn  -W              A operand, [token tile 4][k-step 4][hi/lo][lane]
-//   QK  (q k^T) o D     A operand, [token tile 4][k-step 2][hi/lo][lane]
-//   Kt  (exp(G_C-G) k)^T A operand, [dk tile 8][k-step 2][hi/lo][lane]
-//   U   T (beta v)      C tiles in accumulator order, [token tile 4][dim tile 8][lane] x 4 fp32
+// in MFMA 16x16x32 operand order, one 16-byte unit per lane, so phase B loads
+// them as contiguous 1 KiB wavefront reads.  The q and k operands are the
+// conv outputs themselves (bf16, exact), their per-token factors applied by
+// phase B outside the products; W and (q k^T) o D are fp32 values stored
+// pre-split as bf16 hi + lo:
+//   Q   q (bf16)           A operand, [token tile 4][k-step 4][lane]
+//   Wn  -W                 A operand, [token tile 4][k-step 4][hi/lo][lane]
+//   QK  (q k^T) o D        A operand, [token tile 4][k-step 2][hi/lo][lane]
+//   K   k^T (bf16)         A operand, [dk tile 8][k-step 2][lane]
+//   U   T (beta v)         C tiles in accumulator order, [token tile 4][dim tile 8][lane] x 4 fp32
+//   fq  exp(G_t) / |q_t| / sqrt(128), per token (exp(G) q = fq q)
+//   fk  exp(G_C - G_t) / |k_t|, per token (the k of S's update = fk k)
 //   gl  exp(G_C)
 constexpr int kRecQt = 0;
-constexpr int kRecWn = kRecQt + 4 * 4 * 2 * 64 * 16;
+constexpr int kRecWn = kRecQt + 4 * 4 * 64 * 16;
 constexpr int kRecQK = kRecWn + 4 * 4 * 2 * 64 * 16;
 constexpr int kRecKt = kRecQK + 4 * 2 * 2 * 64 * 16;
-constexpr int kRecU = kRecKt + 8 * 2 * 2 * 64 * 16;
-constexpr int kRecGl = kRecU + 4 * 8 * 64 * 16;
+constexpr int kRecU = kRecKt + 8 * 2 * 64 * 16;
+constexpr int kRecFq = kRecU + 4 * 8 * 64 * 16;
+constexpr int kRecFk = kRecFq + 64 * 4;
+constexpr int kRecGl = kRecFk + 64 * 4;
 constexpr int kRecBytes = kRecGl + 256;
 
 struct PrefillArgs {
@@ -261,9 +268,10 @@ __device__ __forceinline__ void prep_qk_kk_tiles(const float (&qv)[4][8], const 
 //   RA: k hi/lo rows [2][64][136] bf16 (steps 2-3) -> T fp32 [64][68] (4-5)
 //       -> (beta v)^T hi/lo [2][128][68] bf16 (6U) -> (beta e^G k)^T hi/lo (6W)
 //       -> -W fp32 [64][132] (7)
-//   RB: (e^{G_C-G} k)^T fp32 [128][68] (2) -> L fp32 [64][68] | (q k^T) o D
+//   RB: k^T bf16 [128][72] (2) -> L fp32 [64][68] | (q k^T) o D
 //       fp32 [64][68] (3-4) -> T hi/lo [2][64][68] bf16 | - (5-6)
 constexpr int kRA = 0;
+constexpr int kKtPitch = 72;  // bf16 per k^T row in RB (16-byte aligned rows)
 constexpr int kRB = kRA + 34816;
 constexpr int kRScal = kRB + 34816;  // beta, G, inverse scratch
 constexpr int kPrepLdsBytes = kRScal + 4 * 64 * 2 + 4 * 4 * 16 * 17;
@@ -281,7 +289,7 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
 
   __shared__ __attribute__((aligned(16))) unsigned char lds[kPrepLdsBytes];
   uint16_t* khl = reinterpret_cast<uint16_t*>(lds + kRA);  // hi at [0, 64*136), lo after
-  float* KtS = reinterpret_cast<float*>(lds + kRB);
+  uint16_t* KtB = reinterpret_cast<uint16_t*>(lds + kRB);  // k^T bf16 [128][kKtPitch]
   float* Lm = reinterpret_cast<float*>(lds + kRB);
   float* QKs = Lm + 64 * 68;
   float* beta_s = reinterpret_cast<float*>(lds + kRScal);
@@ -295,9 +303,10 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   const int t = t0 + row;
   const bool valid = t < a.length;
   float qv[4][8], kv[4][8], vv[4][8];
+  uint4 rq[4], rk[4];  // the conv outputs of q and k (bf16), kept for the record
   {
     const uint16_t* base = a.post + (int64_t)(t - a.tok0) * a.conv_dim;
-    uint4 rq[4], rk[4], rv[4];
+    uint4 rv[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int d = 32 * s + 8 * g4;
@@ -381,10 +390,14 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   const float eg = expf(G_s[row]);                    // e^{G_t}
   const float ekl = expf(G_s[kChunk - 1] - G_s[row]);  // e^{G_C - G_t}
   const float bt = beta_s[row];
-  // k hi/lo rows into RA; exp(G) q straight to the record (A-operand order);
-  // (e^{G_C-G} k)^T into RB.
+  // k hi/lo rows into RA; q (bf16) and the per-token factors straight to the
+  // record (A-operand order); k^T (bf16) into RB.
   {
-    u32x4* qt_rec = reinterpret_cast<u32x4*>(rec + kRecQt);
+    u32x4* q_rec = reinterpret_cast<u32x4*>(rec + kRecQt);
+    if (g4 == 0) {
+      reinterpret_cast<float*>(rec + kRecFq)[row] = mul_rn(mul_rn(iq, 0.08838834764831845f), eg);
+      reinterpret_cast<float*>(rec + kRecFk)[row] = mul_rn(ik, ekl);
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int d = 32 * s + 8 * g4;
@@ -392,28 +405,23 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
       split8(kv[s], hi, lo);
       *reinterpret_cast<u32x4*>(khl + row * 136 + d) = hi;
       *reinterpret_cast<u32x4*>(khl + 64 * 136 + row * 136 + d) = lo;
-      float tmp[8];
+      q_rec[(wave * 4 + s) * 64 + lane] = u32x4{rq[s].x, rq[s].y, rq[s].z, rq[s].w};
+      const uint32_t kw[4] = {rk[s].x, rk[s].y, rk[s].z, rk[s].w};
 #pragma unroll
-      for (int j = 0; j < 8; ++j) tmp[j] = qv[s][j] * eg;
-      split8(tmp, hi, lo);
-      qt_rec[((wave * 4 + s) * 2 + 0) * 64 + lane] = hi;
-      qt_rec[((wave * 4 + s) * 2 + 1) * 64 + lane] = lo;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) KtS[(d + j) * 68 + row] = kv[s][j] * ekl;  // transposed
+      for (int j = 0; j < 4; ++j) {  // transposed: KtB[dim][token]
+        KtB[(d + 2 * j) * kKtPitch + row] = static_cast<uint16_t>(kw[j] & 0xffffu);
+        KtB[(d + 2 * j + 1) * kKtPitch + row] = static_cast<uint16_t>(kw[j] >> 16);
+      }
     }
   }
   lds_barrier();
-  // Kt operand to the record.
+  // k^T operand to the record: lane (n, g4) of job (dk tile dt, k-step s)
+  // takes dim 16 dt + n, tokens 32 s + 8 g4 .. + 7.
   {
-    u32x4* kt_rec = reinterpret_cast<u32x4*>(rec + kRecKt);
+    u32x4* k_rec = reinterpret_cast<u32x4*>(rec + kRecKt);
     for (int job = wave; job < 16; job += 4) {
       const int dt = job >> 1, s = job & 1;
-      float tmp[8];
-      load8(KtS + (16 * dt + n) * 68 + 32 * s + 8 * g4, tmp);
-      u32x4 hi, lo;
-      split8(tmp, hi, lo);
-      kt_rec[((dt * 2 + s) * 2 + 0) * 64 + lane] = hi;
-      kt_rec[((dt * 2 + s) * 2 + 1) * 64 + lane] = lo;
+      k_rec[(dt * 2 + s) * 64 + lane] = lds16(KtB + (16 * dt + n) * kKtPitch + 32 * s + 8 * g4);
     }
   }
   lds_barrier();  // RB free for L and (q k^T) o D
@@ -581,8 +589,8 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
 
 // ---------------------------------------------------------------- phase B
 struct ChunkOps {
-  u32x4 qt[4][2], wn[4][2], qk[2][2], kt[2][2][2];
-  f32x4 u;
+  u32x4 qt[4], wn[4][2], qk[2][2], kt[2][2];
+  f32x4 u, fq, fk;  // fq, fk of the wave's token tile rows 4 g4 .. 4 g4 + 3
   float gl;
 };
 
@@ -613,6 +621,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ __attribute__((aligned(16))) uint16_t STl[kDim / 8][16][8];
   __shared__ __attribute__((aligned(16))) uint16_t VTh[kChunk / 8][16][8];     // v' hi / lo (bf16)
   __shared__ __attribute__((aligned(16))) uint16_t VTl[kChunk / 8][16][8];
+  __shared__ __attribute__((aligned(16))) uint16_t VKh[kChunk / 8][16][8];     // fk v' hi / lo (bf16)
+  __shared__ __attribute__((aligned(16))) uint16_t VKl[kChunk / 8][16][8];
   // A lane's four rows of a column (rows 4 g4 .. 4 g4 + 3 of a 16-row tile)
   // are half of an 8-row entry; the other half is in lane +-16 (g4 ^ 1).
   // The pair trades halves (one permlane16 swap per 32-bit word), so the
@@ -657,21 +667,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const u32x4* qk = reinterpret_cast<const u32x4*>(rec + kRecQK);
     const u32x4* kt = reinterpret_cast<const u32x4*>(rec + kRecKt);
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < 4; ++s) {
+      o.qt[s] = qt[(wave * 4 + s) * 64 + lane];
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        o.qt[s][p] = qt[((wave * 4 + s) * 2 + p) * 64 + lane];
-        o.wn[s][p] = wn[((wave * 4 + s) * 2 + p) * 64 + lane];
-      }
+      for (int p = 0; p < 2; ++p) o.wn[s][p] = wn[((wave * 4 + s) * 2 + p) * 64 + lane];
+    }
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < 2; ++s) {
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        o.qk[s][p] = qk[((wave * 2 + s) * 2 + p) * 64 + lane];
+      for (int p = 0; p < 2; ++p) o.qk[s][p] = qk[((wave * 2 + s) * 2 + p) * 64 + lane];
 #pragma unroll
-        for (int tk = 0; tk < 2; ++tk) o.kt[tk][s][p] = kt[(((2 * wave + tk) * 2 + s) * 2 + p) * 64 + lane];
-      }
+      for (int tk = 0; tk < 2; ++tk) o.kt[tk][s] = kt[((2 * wave + tk) * 2 + s) * 64 + lane];
+    }
     o.u = reinterpret_cast<const f32x4*>(rec + kRecU)[(wave * 8 + cb) * 64 + lane];
+    o.fq = reinterpret_cast<const f32x4*>(rec + kRecFq)[4 * wave + g4];
+    o.fk = reinterpret_cast<const f32x4*>(rec + kRecFk)[4 * wave + g4];
     // a vector load (opaque zero lane offset): a scalar load here would be
     // waited for by the next lds_barrier (lgkmcnt), exposing its latency
     int zero = 0;
@@ -679,46 +689,95 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     o.gl = reinterpret_cast<const float*>(rec + kRecGl)[zero];
   };
 
+  // Each phase reads all of its LDS operands first, then runs its MFMAs; the
+  // three products of a hi/lo pair (hi*hi, hi*lo, lo*hi) go to three
+  // accumulators that are added at the end, so the MFMAs of a phase form six
+  // (or three) short chains instead of two (or one) long dependent ones.
+  using BF = Kv16<RIA_DT_BF16>;
   auto process = [&](int cl, const ChunkOps& o) {
     const int chunk = a.chunk0 + cl;
     // (i) v' = U - W S and o_inter = exp(G) q S for token tile `wave`
-    f32x4 vn = o.u, oi = {0.f, 0.f, 0.f, 0.f};
+    u32x4 sh[4], sl[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4 bh = lds16(STh[4 * s + g4][n]), bl = lds16(STl[4 * s + g4][n]);
-      vn = mfma3(o.wn[s][0], o.wn[s][1], bh, bl, vn);
-      oi = mfma3(o.qt[s][0], o.qt[s][1], bh, bl, oi);
+      sh[s] = lds16(STh[4 * s + g4][n]);
+      sl[s] = lds16(STl[4 * s + g4][n]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // q is exact in bf16: q S takes two products (q S_hi + q S_lo), then fq
+    // scales each token row
+    f32x4 vn0 = o.u, vn1 = {0.f, 0.f, 0.f, 0.f}, vn2 = vn1, oq0 = vn1, oq1 = vn1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      vn0 = BF::mfma_k32(o.wn[s][0], sh[s], vn0);
+      oq0 = BF::mfma_k32(o.qt[s], sh[s], oq0);
+      vn1 = BF::mfma_k32(o.wn[s][0], sl[s], vn1);
+      oq1 = BF::mfma_k32(o.qt[s], sl[s], oq1);
+      vn2 = BF::mfma_k32(o.wn[s][1], sh[s], vn2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const f32x4 vn = (vn0 + vn1) + vn2;
+    f32x4 vk;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) vk[i4] = mul_rn(vn[i4], o.fk[i4]);
     store_hl(VTh, VTl, 2 * wave + (g4 >> 1), vn);
+    store_hl(VKh, VKl, 2 * wave + (g4 >> 1), vk);
+    f32x4 oi0, oi1 = {0.f, 0.f, 0.f, 0.f}, oi2 = oi1;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) oi0[i4] = mul_rn(oq0[i4] + oq1[i4], o.fq[i4]);
     lds_barrier();
+    // v' and fk v' hi / lo operands, and this lane's S rows
+    u32x4 vh[2], vl[2], kh[2], kl[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      vh[s] = lds16(VTh[4 * s + g4][n]);
+      vl[s] = lds16(VTl[4 * s + g4][n]);
+      kh[s] = lds16(VKh[4 * s + g4][n]);
+      kl[s] = lds16(VKl[4 * s + g4][n]);
+    }
+    f32x4 sn[2];
+#pragma unroll
+    for (int tk = 0; tk < 2; ++tk) sn[tk] = *reinterpret_cast<const f32x4*>(S32[(16 * (2 * wave + tk) + 4 * g4) >> 2][n]);
+    __builtin_amdgcn_sched_barrier(0);
     // (ii) o = o_inter + ((q k^T) o D) v'   (lower triangular: token tiles <= wave)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       if (32 * s <= 16 * wave + 15) {
-        const u32x4 bh = lds16(VTh[4 * s + g4][n]), bl = lds16(VTl[4 * s + g4][n]);
-        oi = mfma3(o.qk[s][0], o.qk[s][1], bh, bl, oi);
+        oi0 = BF::mfma_k32(o.qk[s][0], vh[s], oi0);
+        oi1 = BF::mfma_k32(o.qk[s][0], vl[s], oi1);
+        oi2 = BF::mfma_k32(o.qk[s][1], vh[s], oi2);
       }
     }
+    // (iii) S <- exp(G_C) S + k^T (fk v') for dk tiles 2 wave, 2 wave + 1
+    // (k is exact in bf16: two products per k-step)
+    f32x4 sa[2], sb[2];
+#pragma unroll
+    for (int tk = 0; tk < 2; ++tk) {
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) sa[tk][i4] = o.gl * sn[tk][i4];
+      sb[tk] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int tk = 0; tk < 2; ++tk) {
+        sa[tk] = BF::mfma_k32(o.kt[tk][s], kh[s], sa[tk]);
+        sb[tk] = BF::mfma_k32(o.kt[tk][s], kl[s], sb[tk]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    const f32x4 oi = (oi0 + oi1) + oi2;
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int t = chunk * kChunk + 16 * wave + 4 * g4 + i4;
       if (t < a.length)
         store_act<OT>(a.out, ((int64_t)(t - a.out_tok0) * a.num_v_heads + h) * kDim + cb * 16 + n, oi[i4]);
     }
-    // (iii) S <- exp(G_C) S + Kt^T v' for dk tiles 2 wave, 2 wave + 1
 #pragma unroll
     for (int tk = 0; tk < 2; ++tk) {
       const int r0 = 16 * (2 * wave + tk) + 4 * g4;
-      f32x4 sn = *reinterpret_cast<const f32x4*>(S32[r0 >> 2][n]);
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) sn[i4] = o.gl * sn[i4];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const u32x4 bh = lds16(VTh[4 * s + g4][n]), bl = lds16(VTl[4 * s + g4][n]);
-        sn = mfma3(o.kt[tk][s][0], o.kt[tk][s][1], bh, bl, sn);
-      }
-      *reinterpret_cast<f32x4*>(S32[r0 >> 2][n]) = sn;
-      store_hl(STh, STl, r0 >> 3, sn);
+      const f32x4 snew = sa[tk] + sb[tk];
+      *reinterpret_cast<f32x4*>(S32[r0 >> 2][n]) = snew;
+      store_hl(STh, STl, r0 >> 3, snew);
     }
     lds_barrier();
   };

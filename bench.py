@@ -990,6 +990,46 @@ def run_prefill_cpu(wl, n_gdn: int, n_attn: int) -> dict:
     }
 
 
+def run_prefill_cpu_full(wl) -> dict:
+    """The whole 16384-token prompt through the reference's token-by-token CPU path (oracle restatement):
+    every DeltaNet step and every attention step from an empty cache, as the reference prefills.  Takes
+    minutes (the attention's torch.cat cache grows to the prompt's length), so it is an option of its own."""
+    from oracle import qwen36_cpu as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    n = PREFILL_LEN
+    gen = torch.Generator().manual_seed(wl["seed"])
+    conv_w = (torch.randn((CONV_DIM, 1, 4), generator=gen) * 0.5).to(torch.bfloat16)
+    a_log = torch.rand((NUM_V_HEADS,), generator=gen) * 4.0 - 4.0
+    zero_bias = torch.zeros(NUM_V_HEADS)
+    conv_state = lin_state = None
+    t0 = time.perf_counter()
+    for i in range(n):
+        x = torch.randn((1, CONV_DIM), generator=gen).to(torch.bfloat16)
+        ab = torch.randn((2, 1, NUM_V_HEADS), generator=gen)
+        beta, g = O.gating(ab[0], ab[1], a_log, zero_bias)
+        _, conv_state, lin_state = O.linear_decode_step(conv_state, lin_state, x, conv_w, beta, g)
+        if (i + 1) % 4096 == 0:
+            log(f"[bench] CPU DeltaNet prefill: {i + 1} / {n} tokens, {time.perf_counter() - t0:.1f} s")
+    t_gdn = time.perf_counter() - t0
+    fk = fv = torch.zeros((1, NUM_KV_HEADS, 0, HEAD_DIM_ATTN))
+    t0 = time.perf_counter()
+    for i in range(n):
+        q = torch.randn((2, 1, NUM_Q_HEADS, HEAD_DIM_ATTN), generator=gen).to(torch.bfloat16)
+        kv = torch.randn((2, 1, NUM_KV_HEADS, HEAD_DIM_ATTN), generator=gen).to(torch.bfloat16)
+        _, fk, fv = O.full_decode_step(fk, fv, q[0], kv[0], kv[1], q[1], i)
+        if (i + 1) % 1024 == 0:
+            log(f"[bench] CPU attention prefill: {i + 1} / {n} tokens, {time.perf_counter() - t0:.1f} s")
+    t_attn = time.perf_counter() - t0
+    return {
+        "metric": "prefill tok/s of one 16384-token prompt, 1 DeltaNet + 1 attention layer, reference CPU path",
+        "value": round(n / (t_gdn + t_attn), 3), "unit": "tok/s", "cores": torch.get_num_threads(),
+        "kind": "port", "deltanet_s": round(t_gdn, 2), "attention_s": round(t_attn, 2),
+        "sample": "the whole prompt, token by token, as the reference prefills it (torch-CPU restatement, fp32, "
+                  "torch.cat KV cache from empty)",
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1001,9 +1041,14 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batches", action="store_true",
                     help="skip the B=1/8/32 sub-record of the default workload")
+    ap.add_argument("--cpu-prefill-full", action="store_true",
+                    help="only time the whole 16384-token prompt on the reference's CPU path (minutes; no GPU)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run a plain device copy of this many bytes three times (counter calibration)")
     args = ap.parse_args()
+    if args.cpu_prefill_full:
+        print(json.dumps(run_prefill_cpu_full(WORKLOADS["prefill16k"])), flush=True)
+        return 0
     if args.copy_bytes:
         src = torch.ones(args.copy_bytes // 4, device="cuda")
         dst = torch.empty_like(src)

@@ -38,7 +38,7 @@ CASES = [  # (m, n, k, x dtype): decode batches, one and two 128-row blocks, 16-
     (7, 4096, 2048, torch.float16),
     (16, 2048, 4096, torch.float32),
     (9, 256, 512, torch.bfloat16),     # one wave of K
-    (17, 512, 2048, torch.float16),    # one row past the decode kernel: the streaming kernel
+    (17, 512, 2048, torch.float16),    # one row past the decode kernel: the K-split kernel (fp16 x)
     (32, 2048, 4096, torch.float32),
     (128, 2048, 4096, torch.float16),  # 64-row workgroups: two per 16 features
     (70, 2048, 4096, torch.bfloat16),  # .. the second one with 6 rows
@@ -74,7 +74,7 @@ def test_linear_fp8_matches_oracle(gpu, m, n, k, xdt):
     assert e_got <= 1.5 * e_ref + 1e-6, (e_got, e_ref)
 
 
-STREAMING_F16 = [  # fp16 x past 16 rows (the forward loop's projections): the streaming kernel's
+KSPLIT_F16 = [  # fp16 x past 16 rows (the forward loop's projections): the K-split kernel's
     (96, 12288, 2048),   # tile shapes, with whole and partial row blocks and column tiles
     (128, 8192, 2048),
     (100, 20480, 2048),
@@ -87,9 +87,9 @@ STREAMING_F16 = [  # fp16 x past 16 rows (the forward loop's projections): the s
 ]
 
 
-@pytest.mark.parametrize("m,n,k", STREAMING_F16)
-def test_streaming_kernel_fp16_x_matches_oracle(gpu, m, n, k):
-    announce(f"linear_fp8 streaming: M={m} N={n} K={k} x fp16")
+@pytest.mark.parametrize("m,n,k", KSPLIT_F16)
+def test_ksplit_kernel_fp16_x_matches_oracle(gpu, m, n, k):
+    announce(f"linear_fp8 K-split: M={m} N={n} K={k} x fp16")
     w8, s = W.fp8_block_weight(250 + m, n, k)
     g = torch.Generator().manual_seed(350 + m)
     wide = torch.randn((m, k + 64), generator=g).to(torch.float16)
@@ -146,7 +146,7 @@ def test_linear_fp8_group_equals_separate_calls(gpu, m, ns, k, xdt):
         assert_act_close(ys[j].cpu(), want, f"projection {j}")
 
 
-@pytest.mark.parametrize("m", [3, 100, 128])  # one-pass kernel; streaming with partial and with whole row blocks
+@pytest.mark.parametrize("m", [3, 100, 128])  # one-pass kernel; past 16 rows with partial and with whole row blocks
 def test_linear_fp8_group_accumulates_into_fp32(gpu, m):
     announce(f"linear_fp8_group: M={m} y += fp16 result (residual add)")
     w8, s = W.fp8_block_weight(600, 2048, 4096)

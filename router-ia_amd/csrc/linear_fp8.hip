@@ -774,32 +774,63 @@ __global__ __launch_bounds__(64 * NW) void linear_fp8_ks_kernel(const LinearArgs
     }
   }
   // D tile rows 4 g4 + i, column n16: F.linear's fp16 result, stored as
-  // y_dtype or (y_add) added to the fp32 y, every y value loaded before the
-  // first store
-  auto row_of = [&](int j, int i) { return m0 + 16 * ((wave + NW * j) / CT) + 4 * g4 + i; };
-  auto col_of = [&](int j) { return n0 + 16 * ((wave + NW * j) % CT) + n16; };
-  if (y_add) {
-    float* yf = static_cast<float*>(y);
-    float v[TPW][4];
+  // y_dtype or (y_add) added to the fp32 y.  The fp16 values are staged in
+  // LDS row by row, then every thread stores whole 4-column pieces of rows
+  // (one 8- or 16-byte store instead of four 2- or 4-byte stores to four
+  // rows); a y whose rows are not 16-byte aligned takes one value at a time.
+  constexpr int kPitch = 16 * CT + 4;  // floats per staged row (conflict-free stores)
+  static_assert(16 * RT * kPitch * 4 <= (kPartBytes > kLtBytes ? kPartBytes : kLtBytes), "stage fits the LDS block");
+  __syncthreads();  // every wave has read the partial tiles
+  float* stg = reinterpret_cast<float*>(ks_lds);
 #pragma unroll
-    for (int j = 0; j < TPW; ++j)
+  for (int j = 0; j < TPW; ++j) {
+    const int t = wave + NW * j;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        v[j][i] = row_of(j, i) < a.m && col_of(j) < n ? yf[(int64_t)row_of(j, i) * y_stride + col_of(j)] : 0.f;
+    for (int i = 0; i < 4; ++i)
+      stg[(16 * (t / CT) + 4 * g4 + i) * kPitch + 16 * (t % CT) + n16] = through_dtype<RIA_DT_F16>(tot[j][i]);
+  }
+  __syncthreads();
+  const bool vec = reinterpret_cast<uintptr_t>(y) % 16 == 0 && y_stride % 4 == 0;
+  constexpr int kPieces = 16 * RT * 4 * CT;  // 4-column pieces of the tile
 #pragma unroll
-    for (int j = 0; j < TPW; ++j)
+  for (int pc = tid; pc < kPieces; pc += 64 * NW) {
+    const int r = pc / (4 * CT), c = 4 * (pc % (4 * CT));
+    const int row = m0 + r, col = n0 + c;
+    if (row >= a.m) continue;
+    const f32x4 v = *reinterpret_cast<const f32x4*>(stg + r * kPitch + c);
+    const int64_t off = (int64_t)row * y_stride + col;
+    if (vec && col + 4 <= n) {
+      if (y_add) {
+        f32x4* yp = reinterpret_cast<f32x4*>(static_cast<float*>(y) + off);
+        f32x4 o = *yp;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[j][i] = add_rn(v[j][i], through_dtype<RIA_DT_F16>(tot[j][i]));
-        if (row_of(j, i) < a.m && col_of(j) < n) yf[(int64_t)row_of(j, i) * y_stride + col_of(j)] = v[j][i];
+        for (int e = 0; e < 4; ++e) o[e] = add_rn(o[e], v[e]);
+        *yp = o;
+      } else if (y_dtype == RIA_DT_F32) {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(y) + off) = v;
+      } else {
+        uint32_t w0, w1;
+        if (y_dtype == RIA_DT_F16) {
+          w0 = f32_to_f16_bits(v[0]) | (uint32_t(f32_to_f16_bits(v[1])) << 16);
+          w1 = f32_to_f16_bits(v[2]) | (uint32_t(f32_to_f16_bits(v[3])) << 16);
+        } else {
+          w0 = f32_to_bf16_bits(v[0]) | (uint32_t(f32_to_bf16_bits(v[1])) << 16);
+          w1 = f32_to_bf16_bits(v[2]) | (uint32_t(f32_to_bf16_bits(v[3])) << 16);
+        }
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + off) = uint2{w0, w1};
       }
-  } else {
+    } else {
 #pragma unroll
-    for (int j = 0; j < TPW; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (row_of(j, i) < a.m && col_of(j) < n)
-          store_act_dt(y, (int64_t)row_of(j, i) * y_stride + col_of(j), through_dtype<RIA_DT_F16>(tot[j][i]), y_dtype);
+      for (int e = 0; e < 4; ++e) {
+        if (col + e >= n) break;
+        if (y_add) {
+          float* yp = static_cast<float*>(y) + off + e;
+          *yp = add_rn(*yp, v[e]);
+        } else {
+          store_act_dt(y, off + e, v[e], y_dtype);
+        }
+      }
+    }
   }
 }
 

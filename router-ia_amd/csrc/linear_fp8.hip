@@ -23,9 +23,8 @@
 //                        buffered), and four consumer waves (32 rows of x
 //                        each) run 16x16x32 f16 MFMAs with x operands loaded
 //                        one chunk ahead.  Decode-sized M is bound by the
-//                        weight stream.  Used past 16 rows for bf16 and
-//                        fp32 x.
-//   linear_fp8_ks_kernel past 16 rows with fp16 x (the forward loop's
+//                        weight stream.  Used past 16 rows for fp32 x.
+//   linear_fp8_ks_kernel past 16 rows with fp16 or bf16 x (the forward loop's
 //                        projections): one workgroup per tile of rows x
 //                        features over the whole K, split between its waves;
 //                        operands loaded row-contiguous into registers and
@@ -577,7 +576,8 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
   }
 }
 
-// Past 16 rows with fp16 x: one workgroup per tile of 16 RT rows x 16 CT
+// Past 16 rows with fp16 x, or bf16 x (XB) converted to fp16 as it goes into
+// LDS: one workgroup per tile of 16 RT rows x 16 CT
 // features over the whole of K, whose NW waves split K between them: wave w
 // takes the 64-K chunks w, w + NW, w + 2 NW, ...  Each wave loads its own x
 // and weight bytes into registers, D chunks deep, with row-contiguous loads
@@ -592,7 +592,22 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void gemv_fp8_kernel(const Line
 // CH = 0: any K, in groups of D chunks.
 constexpr int kKsChunk = 64;
 
-template <int RT, int CT, int NW, int D, int CH>
+// Eight bf16 values as eight fp16 values (round to nearest even: exact
+// within fp16's normal range), as F.linear's x.to(float16) gives them.
+__device__ __forceinline__ u32x4 bf16x8_to_f16x8(u32x4 v) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  u32x4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    h2 p;
+    p[0] = static_cast<_Float16>(__uint_as_float(v[j] << 16));
+    p[1] = static_cast<_Float16>(__uint_as_float(v[j] & 0xffff0000u));
+    r[j] = __builtin_bit_cast(uint32_t, p);
+  }
+  return r;
+}
+
+template <int RT, int CT, int NW, int D, int CH, bool XB = false>
 __global__ __launch_bounds__(64 * NW) void linear_fp8_ks_kernel(const LinearArgs a) {
   using F16 = Kv16<RIA_DT_F16>;
   static_assert(kFp8Block % (16 * CT) == 0, "a tile's features lie in one scale block");
@@ -690,7 +705,8 @@ __global__ __launch_bounds__(64 * NW) void linear_fp8_ks_kernel(const LinearArgs
 #pragma unroll
     for (int j = 0; j < 2 * RT; ++j) {
       const int r = 8 * j + (lane >> 3), q = lane & 7;  // tile row r % 16 of row tile r / 16
-      lt[((r >> 4) * 8 + q) * 16 + ((r & 15) ^ hx(q))] = s.x[j >> 1][j & 1];
+      const u32x4 xv = s.x[j >> 1][j & 1];
+      lt[((r >> 4) * 8 + q) * 16 + ((r & 15) ^ hx(q))] = XB ? bf16x8_to_f16x8(xv) : xv;
     }
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
@@ -863,24 +879,25 @@ static void launch_linear(const LinearArgs& a, int ct, dim3 grid, hipStream_t st
 // the waves over the same chunks in the same order, so a projection's result
 // does not depend on the tile shape chosen for it (grouped and separate
 // calls agree bit for bit).
-template <int RT, int CT, int D>
+template <int RT, int CT, int D, bool XB>
 static void launch_ks_k(const LinearArgs& a, dim3 grid, hipStream_t st) {
   constexpr int NW = 4;
   if (a.k == kKsChunk * NW * 8)
-    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 8>), grid, dim3(64 * NW), 0, st, a);
+    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 8, XB>), grid, dim3(64 * NW), 0, st, a);
   else if (a.k == kKsChunk * NW * 16)
-    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 16>), grid, dim3(64 * NW), 0, st, a);
+    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 16, XB>), grid, dim3(64 * NW), 0, st, a);
   else
-    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 0>), grid, dim3(64 * NW), 0, st, a);
+    hipLaunchKernelGGL((linear_fp8_ks_kernel<RT, CT, NW, D, 0, XB>), grid, dim3(64 * NW), 0, st, a);
 }
 
+template <bool XB>
 static void launch_ks(const LinearArgs& a, KsShape s, dim3 grid, hipStream_t st) {
   if (s.rt == 4 && s.ct == 8)
-    launch_ks_k<4, 8, 3>(a, grid, st);
+    launch_ks_k<4, 8, 3, XB>(a, grid, st);
   else if (s.rt == 4 && s.ct == 4)
-    launch_ks_k<4, 4, 4>(a, grid, st);
+    launch_ks_k<4, 4, 4, XB>(a, grid, st);
   else
-    launch_ks_k<2, 2, 6>(a, grid, st);
+    launch_ks_k<2, 2, 6, XB>(a, grid, st);
 }
 
 static int device_cus() {
@@ -971,10 +988,10 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
   // whose busiest CU moves the fewest bytes: (workgroups per CU) x (x bytes
   // + weight bytes of one workgroup); ties go to more workgroups.
   int ct = 1, mt = kLinRows;
-  // K-split kernel (fp16 x): the tile shape whose busiest CU moves the
+  // K-split kernel (fp16 or bf16 x): the tile shape whose busiest CU moves the
   // fewest bytes, (rounds of workgroups over the CUs) x (x + weight bytes of
   // one tile)
-  bool ks = !gemv && x_dtype == RIA_DT_F16 && (int64_t)m * x_row_stride < (int64_t(1) << 31);
+  bool ks = !gemv && (x_dtype == RIA_DT_F16 || x_dtype == RIA_DT_BF16) && (int64_t)m * x_row_stride < (int64_t(1) << 31);
   for (int j = 0; j < count; ++j) ks = ks && (int64_t)projs[j].n * k < (int64_t(1) << 31);
   KsShape ks_shape = kKsShapes[0];
   if (ks) {
@@ -1040,7 +1057,10 @@ static int linear_group(const char* who, int m, int k, const void* x, int x_dtyp
     else
       launch_gemv<RIA_DT_F32>(a, grid, st);
   } else if (ks) {
-    launch_ks(a, ks_shape, grid, st);
+    if (x_dtype == RIA_DT_BF16)
+      launch_ks<true>(a, ks_shape, grid, st);
+    else
+      launch_ks<false>(a, ks_shape, grid, st);
   } else if (x_dtype == RIA_DT_BF16) {
     launch_linear<RIA_DT_BF16>(a, ct, grid, st);
   } else {

@@ -213,13 +213,10 @@ class BatchedForward:
             if fused:
                 K.linear_fp8_group(x, projs, out=outs, norm_weight=w.input_norm, norm_dtype=torch.bfloat16)
             else:
+                # bf16(h); the projection kernels take it as F.linear's fp16 x (exact in
+                # fp16's range), converting it as it goes into their operand staging
                 K.rmsnorm(x, w.input_norm, out=self.h_bf16)
-                h = self.h_bf16
-                if b > 16:
-                    # bf16(h) -> fp16 once here (exact in fp16's range, as the projection
-                    # would convert it), rather than in every workgroup of the streaming kernel
-                    h = self.h_f16.copy_(self.h_bf16)
-                K.linear_fp8_group(h, projs, out=outs)
+                K.linear_fp8_group(self.h_bf16, projs, out=outs)
             st.linear_step(i, self.mixed, w.conv_weight, self.gate_a, self.gate_b, gate_mode=nat.RIA_GATE_RAW,
                            A_log=w.A_log, dt_bias=w.dt_bias, out=self.gated, z=self.z, norm_weight=w.norm_weight)
             K.linear_fp8_group(self.gated.view(b, -1), [w.out_proj.pair()], out=[x], accumulate=[True])

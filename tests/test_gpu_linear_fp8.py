@@ -146,6 +146,23 @@ def test_linear_fp8_group_equals_separate_calls(gpu, m, ns, k, xdt):
         assert_act_close(ys[j].cpu(), want, f"projection {j}")
 
 
+@pytest.mark.parametrize("m,n,k", [(100, 8192, 2048), (128, 2048, 4096), (37, 96, 128)])
+def test_bf16_x_equals_its_fp16_conversion(gpu, m, n, k):
+    """F.linear takes h.to(float16): bf16 x past 16 rows is converted inside the
+    K-split kernel, which must give the bits of the same call on x.to(float16)
+    (values spanning fp16's normal range, small ones included)."""
+    announce(f"linear_fp8 bf16 x: M={m} N={n} K={k}")
+    w8, s = W.fp8_block_weight(700 + m, n, k)
+    g = torch.Generator().manual_seed(710 + m)
+    x = torch.randn((m, k), generator=g) * torch.exp2(torch.randint(-12, 8, (m, k), generator=g).float())
+    xb = x.to(torch.bfloat16).to(gpu)
+    wd, sd = w8.to(gpu), s.to(gpu)
+    got = K.linear_fp8(xb, wd, sd)
+    ref = K.linear_fp8(xb.to(torch.float16), wd, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), ref.cpu())
+
+
 @pytest.mark.parametrize("m", [3, 100, 128])  # one-pass kernel; past 16 rows with partial and with whole row blocks
 def test_linear_fp8_group_accumulates_into_fp32(gpu, m):
     announce(f"linear_fp8_group: M={m} y += fp16 result (residual add)")

@@ -14,8 +14,8 @@
 //     wave's softmax (VALU, transcendental) overlaps the other's MFMAs, and
 //     every key block fetched serves 16 tokens x 8 heads;
 //   * key blocks travel HBM/L2 -> LDS by direct-to-LDS loads into a 4-slot
-//     ring, two blocks ahead of the one being computed, with no registers in
-//     flight;
+//     ring, in pairs two blocks ahead of the one being computed, with no
+//     registers in flight and one barrier per pair;
 //   * scores S^T = K Q^T on 16x16x32 MFMA (16 keys x 16 tokens per tile): the
 //     K tile is already in A-operand order (8 dims of one token are 16
 //     contiguous bytes); the two score tiles of a block take their rows from
@@ -333,25 +333,25 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Waves w and w + 4 share a SIMD.  Waves 4..7 run half an iteration behind
-  // (softmax and P V of block b - 1 before the scores of block b), so that
-  // on every SIMD one wave's softmax overlaps the other's MFMAs instead of
-  // both waves reaching the same phase between the same two barriers.  The
-  // slot of block b - 1 stays valid through iteration b (4-slot ring).
-  const bool lag = wave >= 4;
+  // Key blocks arrive in pairs, two blocks ahead.  At an even block every
+  // copy this thread has in flight (the pair b, b + 1, issued two iterations
+  // earlier) is waited for, then the barrier makes every thread's copies
+  // landed and every wave done with blocks b - 2 and b - 1, whose slots take
+  // the next pair.  An odd block's pair has already landed, so odd blocks
+  // pass no barrier and the waves drift apart by up to a block (the two
+  // waves of a SIMD then rarely reach the softmax at once).  The wait is for
+  // all copies, not a count of them: it relies on no ordering among the
+  // direct-to-LDS copies, only on each being written to LDS when the counter
+  // no longer holds it; pairing gives each copy two iterations to land.
   f32x4 sc[2];
   issue(0);
   if (nblk > 1) issue(1);
   for (int b = 0; b < nblk; ++b) {
-    // every copy this thread has issued (blocks b and b + 1) has landed; after
-    // the barrier every thread's have, and every wave is done with slot
-    // (b + 2) % 4 (block b - 2).  The wait is for all copies, not a count of
-    // them: it relies on no ordering among the direct-to-LDS copies, only on
-    // each being written to LDS when the counter no longer holds it.  Block
-    // b + 1 was issued a whole iteration earlier, so waiting for it costs
-    // little.
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (b + 2 < nblk) issue(b + 2);
+    if ((b & 1) == 0) {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (b + 2 < nblk) issue(b + 2);
+      if (b + 3 < nblk) issue(b + 3);
+    }
     u32x4* slot = slot_of(b);
     if (32 * b + 31 > kmax) {
       // last block: zero V of keys past the last one used, so that
@@ -375,15 +375,9 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
       lds_barrier();
     }
 
-    if (!lag) {
-      qk(b, sc);
-      softmax_pv(b, sc);
-    } else {
-      if (b > 0) softmax_pv(b - 1, sc);
-      qk(b, sc);
-    }
+    qk(b, sc);
+    softmax_pv(b, sc);
   }
-  if (lag) softmax_pv(nblk - 1, sc);
 
   // ---- normalise, stage (the ring is dead once every wave has left the loop), gate, store
   lds_barrier();

@@ -29,6 +29,7 @@
 // the cumulative decay, exponentials and the triangular inverse are fp32.
 #include <math.h>
 #include <algorithm>
+#include <type_traits>
 
 #include "ria_common.h"
 
@@ -588,20 +589,33 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------- phase B
-struct ChunkOps {
-  u32x4 qt[4], wn[4][2], qk[2][2], kt[2][2];
-  f32x4 u, fq, fk;  // fq, fk of the wave's token tile rows 4 g4 .. 4 g4 + 3
+// Record operands of one chunk for each role of the scan's waves.
+struct StateOps {  // v' = U - W S, fk v', and S <- e^{G_C} S + k^T (fk v')
+  u32x4 wn[4][2], kt[2][2];
+  f32x4 u, fk;  // fk of the wave's token tile rows 4 g4 .. 4 g4 + 3
   float gl;
+};
+struct OutOps {  // o = fq (q S) + ((q k^T) o D) v'
+  u32x4 qt[4], qk[2][2];
+  f32x4 fq;
 };
 
 template <int OT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void chunk_scan_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void chunk_scan_kernel(PrefillArgs a) {
   // The 8 column blocks of a head share an XCD (workgroup ids congruent mod 8
   // run on one XCD; id = 32 * cb + h), so its records are fetched once per L2.
   const int h = blockIdx.x % a.num_v_heads;
   const int cb = blockIdx.x / a.num_v_heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g4 = lane >> 4;
+  // Two roles, one wave of each per SIMD (waves w and w + 4 share SIMD w):
+  // waves 0-3 carry the state (v' of token tile w, then S rows 32 w .. 32 w
+  // + 31), waves 4-7 the read-out (q S of token tile w, then its intra-chunk
+  // term and the output).  Each chunk is two phases closed by a barrier; per
+  // phase a wave runs at most 12 of the chunk's MFMAs on its chain instead
+  // of 20, and the other role's wave on its SIMD fills the waits.
+  const bool state_role = wave < 4;
+  const int w = wave & 3;
 
   // LDS in 16-byte entries [row group][column n] (column n = state column
   // 16 cb + n): 4 rows of fp32 S, or 8 rows of bf16 S hi / lo or v' hi / lo
@@ -611,11 +625,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // conflicts only when each 16-lane quarter covers 256 contiguous bytes
   // (other spacings cost 4 cycles, a 256-byte pitch 28), an 8-byte store only
   // when each quarter covers 128 contiguous bytes.  Every access here is one
-  // of those (0.01 conflict cycles per LDS instruction, against 3.5 for a
-  // row-major fp32 block and transposed 2-byte stores); the lane-pair trade
-  // that makes the bf16 stores whole entries costs ~5% of the scan (its
-  // VALU work lies on the chunk's dependency chain), as conflicts cost nothing
-  // measurable: they overlap the MFMA chain.
+  // of those.
   __shared__ __attribute__((aligned(16))) float S32[kDim / 4][16][4];          // S fp32
   __shared__ __attribute__((aligned(16))) uint16_t STh[kDim / 8][16][8];       // S hi / lo (bf16)
   __shared__ __attribute__((aligned(16))) uint16_t STl[kDim / 8][16][8];
@@ -650,7 +660,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   };
 
   float* Sg = a.state + (int64_t)h * kDim * kDim + cb * 16;
-  for (int e = tid; e < kDim * 16; e += 256) {
+  for (int e = tid; e < kDim * 16; e += 512) {
     const int r = e >> 4, c = e & 15;
     const float v = Sg[r * kDim + c];
     S32[r >> 2][c][r & 3] = v;
@@ -660,140 +670,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   lds_barrier();
 
-  auto load_ops = [&](int cl, ChunkOps& o) {
-    const char* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecBytes;
-    const u32x4* qt = reinterpret_cast<const u32x4*>(rec + kRecQt);
-    const u32x4* wn = reinterpret_cast<const u32x4*>(rec + kRecWn);
-    const u32x4* qk = reinterpret_cast<const u32x4*>(rec + kRecQK);
-    const u32x4* kt = reinterpret_cast<const u32x4*>(rec + kRecKt);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      o.qt[s] = qt[(wave * 4 + s) * 64 + lane];
-#pragma unroll
-      for (int p = 0; p < 2; ++p) o.wn[s][p] = wn[((wave * 4 + s) * 2 + p) * 64 + lane];
-    }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-#pragma unroll
-      for (int p = 0; p < 2; ++p) o.qk[s][p] = qk[((wave * 2 + s) * 2 + p) * 64 + lane];
-#pragma unroll
-      for (int tk = 0; tk < 2; ++tk) o.kt[tk][s] = kt[((2 * wave + tk) * 2 + s) * 64 + lane];
-    }
-    o.u = reinterpret_cast<const f32x4*>(rec + kRecU)[(wave * 8 + cb) * 64 + lane];
-    o.fq = reinterpret_cast<const f32x4*>(rec + kRecFq)[4 * wave + g4];
-    o.fk = reinterpret_cast<const f32x4*>(rec + kRecFk)[4 * wave + g4];
-    // a vector load (opaque zero lane offset): a scalar load here would be
-    // waited for by the next lds_barrier (lgkmcnt), exposing its latency
-    int zero = 0;
-    asm volatile("" : "+v"(zero));
-    o.gl = reinterpret_cast<const float*>(rec + kRecGl)[zero];
-  };
-
-  // Each phase reads all of its LDS operands first, then runs its MFMAs; the
-  // three products of a hi/lo pair (hi*hi, hi*lo, lo*hi) go to three
-  // accumulators that are added at the end, so the MFMAs of a phase form six
-  // (or three) short chains instead of two (or one) long dependent ones.
-  using BF = Kv16<RIA_DT_BF16>;
-  auto process = [&](int cl, const ChunkOps& o) {
-    const int chunk = a.chunk0 + cl;
-    // (i) v' = U - W S and o_inter = exp(G) q S for token tile `wave`
-    u32x4 sh[4], sl[4];
+  auto rec_of = [&](int cl) { return a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecBytes; };
+  // S hi / lo operands of the k-steps over the 128 state rows
+  auto read_s = [&](u32x4 (&sh)[4], u32x4 (&sl)[4]) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       sh[s] = lds16(STh[4 * s + g4][n]);
       sl[s] = lds16(STl[4 * s + g4][n]);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // q is exact in bf16: q S takes two products (q S_hi + q S_lo), then fq
-    // scales each token row
-    f32x4 vn0 = o.u, vn1 = {0.f, 0.f, 0.f, 0.f}, vn2 = vn1, oq0 = vn1, oq1 = vn1;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      vn0 = BF::mfma_k32(o.wn[s][0], sh[s], vn0);
-      oq0 = BF::mfma_k32(o.qt[s], sh[s], oq0);
-      vn1 = BF::mfma_k32(o.wn[s][0], sl[s], vn1);
-      oq1 = BF::mfma_k32(o.qt[s], sl[s], oq1);
-      vn2 = BF::mfma_k32(o.wn[s][1], sh[s], vn2);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    const f32x4 vn = (vn0 + vn1) + vn2;
-    f32x4 vk;
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) vk[i4] = mul_rn(vn[i4], o.fk[i4]);
-    store_hl(VTh, VTl, 2 * wave + (g4 >> 1), vn);
-    store_hl(VKh, VKl, 2 * wave + (g4 >> 1), vk);
-    f32x4 oi0, oi1 = {0.f, 0.f, 0.f, 0.f}, oi2 = oi1;
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) oi0[i4] = mul_rn(oq0[i4] + oq1[i4], o.fq[i4]);
-    lds_barrier();
-    // v' and fk v' hi / lo operands, and this lane's S rows
-    u32x4 vh[2], vl[2], kh[2], kl[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      vh[s] = lds16(VTh[4 * s + g4][n]);
-      vl[s] = lds16(VTl[4 * s + g4][n]);
-      kh[s] = lds16(VKh[4 * s + g4][n]);
-      kl[s] = lds16(VKl[4 * s + g4][n]);
-    }
-    f32x4 sn[2];
-#pragma unroll
-    for (int tk = 0; tk < 2; ++tk) sn[tk] = *reinterpret_cast<const f32x4*>(S32[(16 * (2 * wave + tk) + 4 * g4) >> 2][n]);
-    __builtin_amdgcn_sched_barrier(0);
-    // (ii) o = o_inter + ((q k^T) o D) v'   (lower triangular: token tiles <= wave)
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      if (32 * s <= 16 * wave + 15) {
-        oi0 = BF::mfma_k32(o.qk[s][0], vh[s], oi0);
-        oi1 = BF::mfma_k32(o.qk[s][0], vl[s], oi1);
-        oi2 = BF::mfma_k32(o.qk[s][1], vh[s], oi2);
-      }
-    }
-    // (iii) S <- exp(G_C) S + k^T (fk v') for dk tiles 2 wave, 2 wave + 1
-    // (k is exact in bf16: two products per k-step)
-    f32x4 sa[2], sb[2];
-#pragma unroll
-    for (int tk = 0; tk < 2; ++tk) {
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) sa[tk][i4] = o.gl * sn[tk][i4];
-      sb[tk] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int tk = 0; tk < 2; ++tk) {
-        sa[tk] = BF::mfma_k32(o.kt[tk][s], kh[s], sa[tk]);
-        sb[tk] = BF::mfma_k32(o.kt[tk][s], kl[s], sb[tk]);
-      }
-    __builtin_amdgcn_sched_barrier(0);
-    const f32x4 oi = (oi0 + oi1) + oi2;
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const int t = chunk * kChunk + 16 * wave + 4 * g4 + i4;
-      if (t < a.length)
-        store_act<OT>(a.out, ((int64_t)(t - a.out_tok0) * a.num_v_heads + h) * kDim + cb * 16 + n, oi[i4]);
-    }
-#pragma unroll
-    for (int tk = 0; tk < 2; ++tk) {
-      const int r0 = 16 * (2 * wave + tk) + 4 * g4;
-      const f32x4 snew = sa[tk] + sb[tk];
-      *reinterpret_cast<f32x4*>(S32[r0 >> 2][n]) = snew;
-      store_hl(STh, STl, r0 >> 3, snew);
-    }
-    lds_barrier();
   };
 
   // Chunk cl + 2's record is pulled into L2 (one load per 128-byte line,
   // spread over the workgroup) while chunk cl computes, so the operand loads
   // of chunk cl + 1, issued at the same time, find their lines in L2: from
-  // HBM a chunk's 147 KB arrives in about the time a chunk computes, and the
+  // HBM a chunk's record arrives in about the time a chunk computes, and the
   // scan waited for it.  A touched value is consumed (an empty asm use) one
   // chunk later, when it has long arrived, so no wait is spent on it.
   // The 8 column-block workgroups of a head share an L2, so each touches
-  // every 8th line (its own eighth of the record).
+  // every 8th line (its own eighth of the record); the state role's 256
+  // threads do the touching.
   constexpr int kRecLines = kRecBytes / 128;
   constexpr int kTouch = (kRecLines + 8 * 256 - 1) / (8 * 256);
   auto touch = [&](int cl, uint32_t (&tv)[kTouch]) {
-    const char* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecBytes;
+    const char* rec = rec_of(cl);
 #pragma unroll
     for (int i = 0; i < kTouch; ++i)
       tv[i] = *reinterpret_cast<const uint32_t*>(rec + (int64_t)min(8 * (tid + 256 * i) + cb, kRecLines - 1) * 128);
@@ -806,24 +705,186 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // The prefetch is unconditional (the last chunk is simply loaded again):
   // a conditional one splits the loop into paths the compiler's wait
   // analysis merges conservatively, draining the prefetch every chunk.
-  ChunkOps A, B;
-  uint32_t tX[kTouch], tY[kTouch];
-#pragma unroll
-  for (int i = 0; i < kTouch; ++i) tY[i] = 0u;
-  load_ops(0, A);
   const int last = a.seg_chunks - 1;
-  for (int cl = 0; cl < a.seg_chunks; cl += 2) {
-    load_ops(min(cl + 1, last), B);
-    touch(min(cl + 2, last), tX);
-    process(cl, A);
-    consume(tY);
-    if (cl + 1 >= a.seg_chunks) break;
-    load_ops(min(cl + 2, last), A);
-    touch(min(cl + 3, last), tY);
-    process(cl + 1, B);
-    consume(tX);
+  auto scan = [&](auto& A, auto& B, auto load_ops, auto process, auto touching) {
+    constexpr bool kTouching = decltype(touching)::value;
+    uint32_t tX[kTouch], tY[kTouch];
+#pragma unroll
+    for (int i = 0; i < kTouch; ++i) tY[i] = 0u;
+    load_ops(0, A);
+    for (int cl = 0; cl < a.seg_chunks; cl += 2) {
+      load_ops(min(cl + 1, last), B);
+      if constexpr (kTouching) touch(min(cl + 2, last), tX);
+      process(cl, A);
+      if constexpr (kTouching) consume(tY);
+      if (cl + 1 >= a.seg_chunks) break;
+      load_ops(min(cl + 2, last), A);
+      if constexpr (kTouching) touch(min(cl + 3, last), tY);
+      process(cl + 1, B);
+      if constexpr (kTouching) consume(tX);
+    }
+  };
+
+  // Each phase reads all of its LDS operands first, then runs its MFMAs; the
+  // three products of a hi/lo pair (hi*hi, hi*lo, lo*hi) go to three
+  // accumulators that are added at the end, so the MFMAs of a phase form
+  // short independent chains.
+  using BF = Kv16<RIA_DT_BF16>;
+  if (state_role) {
+    auto load_ops = [&](int cl, StateOps& o) {
+      const char* rec = rec_of(cl);
+      const u32x4* wn = reinterpret_cast<const u32x4*>(rec + kRecWn);
+      const u32x4* kt = reinterpret_cast<const u32x4*>(rec + kRecKt);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) o.wn[s][p] = wn[((w * 4 + s) * 2 + p) * 64 + lane];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int tk = 0; tk < 2; ++tk) o.kt[tk][s] = kt[((2 * w + tk) * 2 + s) * 64 + lane];
+      o.u = reinterpret_cast<const f32x4*>(rec + kRecU)[(w * 8 + cb) * 64 + lane];
+      o.fk = reinterpret_cast<const f32x4*>(rec + kRecFk)[4 * w + g4];
+      // a vector load (opaque zero lane offset): a scalar load here would be
+      // waited for by the next lds_barrier (lgkmcnt), exposing its latency
+      int zero = 0;
+      asm volatile("" : "+v"(zero));
+      o.gl = reinterpret_cast<const float*>(rec + kRecGl)[zero];
+    };
+    auto process = [&](int, const StateOps& o) {
+      // (i) v' = U - W S for token tile w, and fk v'
+      u32x4 sh[4], sl[4];
+      read_s(sh, sl);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 vn0 = o.u, vn1 = {0.f, 0.f, 0.f, 0.f}, vn2 = vn1;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        vn0 = BF::mfma_k32(o.wn[s][0], sh[s], vn0);
+        vn1 = BF::mfma_k32(o.wn[s][0], sl[s], vn1);
+        vn2 = BF::mfma_k32(o.wn[s][1], sh[s], vn2);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const f32x4 vn = (vn0 + vn1) + vn2;
+      f32x4 vk;
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) vk[i4] = mul_rn(vn[i4], o.fk[i4]);
+      store_hl(VTh, VTl, 2 * w + (g4 >> 1), vn);
+      store_hl(VKh, VKl, 2 * w + (g4 >> 1), vk);
+      lds_barrier();
+      // (iii) S <- exp(G_C) S + k^T (fk v') for dk tiles 2 w, 2 w + 1
+      // (k is exact in bf16: two products per k-step)
+      u32x4 kh[2], kl[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        kh[s] = lds16(VKh[4 * s + g4][n]);
+        kl[s] = lds16(VKl[4 * s + g4][n]);
+      }
+      f32x4 sn[2];
+#pragma unroll
+      for (int tk = 0; tk < 2; ++tk) sn[tk] = *reinterpret_cast<const f32x4*>(S32[(16 * (2 * w + tk) + 4 * g4) >> 2][n]);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 sa[2], sb[2];
+#pragma unroll
+      for (int tk = 0; tk < 2; ++tk) {
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) sa[tk][i4] = o.gl * sn[tk][i4];
+        sb[tk] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int tk = 0; tk < 2; ++tk) {
+          sa[tk] = BF::mfma_k32(o.kt[tk][s], kh[s], sa[tk]);
+          sb[tk] = BF::mfma_k32(o.kt[tk][s], kl[s], sb[tk]);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int tk = 0; tk < 2; ++tk) {
+        const int r0 = 16 * (2 * w + tk) + 4 * g4;
+        const f32x4 snew = sa[tk] + sb[tk];
+        *reinterpret_cast<f32x4*>(S32[r0 >> 2][n]) = snew;
+        store_hl(STh, STl, r0 >> 3, snew);
+      }
+      lds_barrier();
+    };
+    StateOps A, B;
+    scan(A, B, load_ops, process, std::true_type{});
+  } else {
+    auto load_ops = [&](int cl, OutOps& o) {
+      const char* rec = rec_of(cl);
+      const u32x4* qt = reinterpret_cast<const u32x4*>(rec + kRecQt);
+      const u32x4* qk = reinterpret_cast<const u32x4*>(rec + kRecQK);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) o.qt[s] = qt[(w * 4 + s) * 64 + lane];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) o.qk[s][p] = qk[((w * 2 + s) * 2 + p) * 64 + lane];
+      o.fq = reinterpret_cast<const f32x4*>(rec + kRecFq)[4 * w + g4];
+    };
+    auto process = [&](int cl, const OutOps& o) {
+      const int chunk = a.chunk0 + cl;
+      // o_inter = fq (q S): q is exact in bf16, so two products (q S_hi +
+      // q S_lo), then fq scales each token row
+      u32x4 sh[4], sl[4];
+      read_s(sh, sl);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 oq0 = {0.f, 0.f, 0.f, 0.f}, oq1 = oq0;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        oq0 = BF::mfma_k32(o.qt[s], sh[s], oq0);
+        oq1 = BF::mfma_k32(o.qt[s], sl[s], oq1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 oi0, oi1 = {0.f, 0.f, 0.f, 0.f}, oi2 = oi1;
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) oi0[i4] = mul_rn(oq0[i4] + oq1[i4], o.fq[i4]);
+      lds_barrier();
+      // (ii) o = o_inter + ((q k^T) o D) v'   (lower triangular: token tiles <= w)
+      u32x4 vh[2], vl[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        vh[s] = lds16(VTh[4 * s + g4][n]);
+        vl[s] = lds16(VTl[4 * s + g4][n]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (32 * s <= 16 * w + 15) {
+          oi0 = BF::mfma_k32(o.qk[s][0], vh[s], oi0);
+          oi1 = BF::mfma_k32(o.qk[s][0], vl[s], oi1);
+          oi2 = BF::mfma_k32(o.qk[s][1], vh[s], oi2);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const f32x4 oi = (oi0 + oi1) + oi2;
+      // The chunk's output rows through a buffer resource that ends at the
+      // prompt's last token: the hardware drops stores past it, so every lane
+      // stores without a branch (branches around the stores leave the
+      // compiler unsure how many are in flight, and its wait for the
+      // prefetched record then drains every load, the prefetch included).
+      constexpr int kEsz = OT == RIA_DT_F32 ? 4 : 2;
+      const int t0 = chunk * kChunk;
+      const int row = a.num_v_heads * kDim;
+      char* obase = static_cast<char*>(a.out) + (int64_t)(t0 - a.out_tok0) * row * kEsz;
+      const __amdgpu_buffer_rsrc_t orsrc =
+          __builtin_amdgcn_make_buffer_rsrc(obase, 0, min(kChunk, a.length - t0) * row * kEsz, kBufferWord3);
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int off = ((16 * w + 4 * g4 + i4) * row + h * kDim + cb * 16 + n) * kEsz;
+        if constexpr (OT == RIA_DT_F32)
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(oi[i4]), orsrc, off, 0, 0);
+        else if constexpr (OT == RIA_DT_BF16)
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(oi[i4]), orsrc, off, 0, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_f16_bits(oi[i4]), orsrc, off, 0, 0);
+      }
+      lds_barrier();
+    };
+    OutOps A, B;
+    scan(A, B, load_ops, process, std::false_type{});
   }
-  for (int e = tid; e < kDim * 16; e += 256) {
+  for (int e = tid; e < kDim * 16; e += 512) {
     const int r = e >> 4, c = e & 15;
     Sg[r * kDim + c] = S32[r >> 2][c][r & 3];
   }
@@ -943,7 +1004,7 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
       PrefillArgs sa = a;
       sa.out = a.post;
       sa.out_tok0 = a.tok0;
-      hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F32>), sgrid, dim3(256), 0, st, sa);
+      hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F32>), sgrid, dim3(512), 0, st, sa);
       int rc = check_launch("ria_gdn_prefill");
       if (rc != RIA_OK) return rc;
       const int64_t head_row = (int64_t)num_v_heads * kDim;
@@ -955,11 +1016,11 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
       if (rc != RIA_OK) return rc;
     } else {
       if (out_dtype == RIA_DT_BF16)
-        hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_BF16>), sgrid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_BF16>), sgrid, dim3(512), 0, st, a);
       else if (out_dtype == RIA_DT_F16)
-        hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F16>), sgrid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F16>), sgrid, dim3(512), 0, st, a);
       else
-        hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F32>), sgrid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((chunk_scan_kernel<RIA_DT_F32>), sgrid, dim3(512), 0, st, a);
       int rc = check_launch("ria_gdn_prefill");
       if (rc != RIA_OK) return rc;
     }

@@ -39,9 +39,6 @@
 namespace ria {
 
 constexpr int kFp8Block = 128;  // scale block edge (qwen36_dequant.py:13)
-// Word 3 of a raw buffer resource on gfx9-family parts: data format 32 bits
-// (a zero format makes every load return zero), no swizzle, no index stride.
-constexpr int kBufferWord3 = 0x00020000;
 constexpr int kLinRing = 12;    // weight chunks in flight per workgroup
 constexpr int kXAhead = 2;      // chunks of x loaded ahead of the MFMAs
 constexpr int kLinRows = 128;   // most rows of x per workgroup (4 consumer waves x 32)

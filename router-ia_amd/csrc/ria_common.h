@@ -335,6 +335,11 @@ __device__ __forceinline__ void st_stream(f32x4* p, f32x4 v) { __builtin_nontemp
 // Workgroup barrier for LDS traffic only: it waits for this wave's LDS (and
 // scalar) operations but not for outstanding global loads or stores, which
 // __syncthreads() would also drain (exposing prefetches and store latency).
+// Word 3 of a raw buffer resource on gfx9-family parts: data format 32 bits
+// (a zero format makes every load return zero), no swizzle, no index stride.
+// Accesses past the resource's byte range are dropped (stores) or read zero.
+constexpr int kBufferWord3 = 0x00020000;
+
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -105,14 +105,6 @@ __device__ __forceinline__ void split8(const float* v, u32x4& hi, u32x4& lo) {
   lo = u32x4{l[0], l[1], l[2], l[3]};
 }
 
-// acc += A B with both operands as hi/lo pairs (the lo*lo term is dropped).
-__device__ __forceinline__ f32x4 mfma3(u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl, f32x4 acc) {
-  acc = Kv16<RIA_DT_BF16>::mfma_k32(ah, bh, acc);
-  acc = Kv16<RIA_DT_BF16>::mfma_k32(ah, bl, acc);
-  acc = Kv16<RIA_DT_BF16>::mfma_k32(al, bh, acc);
-  return acc;
-}
-
 __device__ __forceinline__ u32x4 lds16(const uint16_t* p) {
   const uint4 v = *reinterpret_cast<const uint4*>(p);
   return u32x4{v.x, v.y, v.z, v.w};
@@ -215,13 +207,17 @@ __global__ __launch_bounds__(256) void conv_ring_tail_kernel(PrefillArgs a) {
 
 
 // Step 3 of phase A for wave W: row tile W of Q K^T (A operand = the wave's
-// own q rows, split on the fly) and row tile 3 - W of K K^T (A operand from
-// the k rows in LDS), 5 tiles in all; B operands are the k rows of tiles tj.
-// Each tile runs the MFMA sequence of one tile alone; the epilogue applies the
-// decay mask and writes (q k^T) o D and L = strict_lower(beta k k^T o D).
+// own q rows) and row tile 3 - W of K K^T (A operand from the k rows in LDS),
+// 5 tiles in all; B operands are the k rows of tiles tj.  q and k enter as
+// the conv's bf16 values, exact MFMA operands, so each product is one MFMA;
+// the epilogue applies the rows' norms (fq_s: |q|^-1 / sqrt(128), fk_s:
+// |k|^-1) with the decay mask and writes (q k^T) o D and
+// L = strict_lower(beta k k^T o D).
 template <int W>
-__device__ __forceinline__ void prep_qk_kk_tiles(const float (&qv)[4][8], const uint16_t* khl, const float* G_s,
-                                                 const float* beta_s, float* Lm, float* QKs, int n, int g4) {
+__device__ __forceinline__ void prep_qk_kk_tiles(const uint4 (&rq)[4], const uint16_t* kr, const float* G_s,
+                                                 const float* beta_s, const float* fq_s, const float* fk_s,
+                                                 float* Lm, float* QKs, int n, int g4) {
+  using BF = Kv16<RIA_DT_BF16>;
   constexpr int RQ = W, RK = 3 - W;
   constexpr int NB = (RQ > RK ? RQ : RK) + 1;
   f32x4 aq[RQ + 1], ak[RK + 1];
@@ -232,50 +228,46 @@ __device__ __forceinline__ void prep_qk_kk_tiles(const float (&qv)[4][8], const 
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int d = 32 * s + 8 * g4;
-    u32x4 qh, ql;
-    split8(qv[s], qh, ql);
-    const u32x4 kh = lds16(khl + (16 * RK + n) * 136 + d), kl = lds16(khl + 64 * 136 + (16 * RK + n) * 136 + d);
-    u32x4 bh[NB], bl[NB];
+    const u32x4 qa = u32x4{rq[s].x, rq[s].y, rq[s].z, rq[s].w};
+    const u32x4 ka = lds16(kr + (16 * RK + n) * 136 + d);
+    u32x4 bk[NB];
 #pragma unroll
-    for (int tj = 0; tj < NB; ++tj) {
-      bh[tj] = lds16(khl + (16 * tj + n) * 136 + d);
-      bl[tj] = lds16(khl + 64 * 136 + (16 * tj + n) * 136 + d);
-    }
+    for (int tj = 0; tj < NB; ++tj) bk[tj] = lds16(kr + (16 * tj + n) * 136 + d);
 #pragma unroll
-    for (int tj = 0; tj <= RQ; ++tj) aq[tj] = mfma3(qh, ql, bh[tj], bl[tj], aq[tj]);
+    for (int tj = 0; tj <= RQ; ++tj) aq[tj] = BF::mfma_k32(qa, bk[tj], aq[tj]);
 #pragma unroll
-    for (int tj = 0; tj <= RK; ++tj) ak[tj] = mfma3(kh, kl, bh[tj], bl[tj], ak[tj]);
+    for (int tj = 0; tj <= RK; ++tj) ak[tj] = BF::mfma_k32(ka, bk[tj], ak[tj]);
   }
 #pragma unroll
   for (int tj = 0; tj <= RQ; ++tj)
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int i = 16 * RQ + 4 * g4 + i4, j = 16 * tj + n;
-      QKs[i * 68 + j] = j <= i ? aq[tj][i4] * expf(G_s[i] - G_s[j]) : 0.f;
+      QKs[i * 68 + j] = j <= i ? aq[tj][i4] * (fq_s[i] * fk_s[j]) * expf(G_s[i] - G_s[j]) : 0.f;
     }
 #pragma unroll
   for (int tj = 0; tj <= RK; ++tj)
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int i = 16 * RK + 4 * g4 + i4, j = 16 * tj + n;
-      Lm[i * 68 + j] = j < i ? beta_s[i] * ak[tj][i4] * expf(G_s[i] - G_s[j]) : 0.f;
+      Lm[i * 68 + j] = j < i ? beta_s[i] * (ak[tj][i4] * (fk_s[i] * fk_s[j])) * expf(G_s[i] - G_s[j]) : 0.f;
     }
 }
 
 // ---------------------------------------------------------------- phase A
-// LDS regions (bytes) and what they hold over the kernel's steps; 74.5 KB in
+// LDS regions (bytes) and what they hold over the kernel's steps; 75 KB in
 // all, so two workgroups share a CU and one's loads and barriers overlap the
 // other's arithmetic.
-//   RA: k hi/lo rows [2][64][136] bf16 (steps 2-3) -> T fp32 [64][68] (4-5)
-//       -> (beta v)^T hi/lo [2][128][68] bf16 (6U) -> (beta e^G k)^T hi/lo (6W)
-//       -> -W fp32 [64][132] (7)
+//   RA: k rows [64][136] bf16 (steps 2-3) -> T fp32 [64][68] (4-5)
+//       -> v^T | k^T bf16 [128][68] each (6) -> -W fp32 [64][132] (7)
 //   RB: k^T bf16 [128][72] (2) -> L fp32 [64][68] | (q k^T) o D
-//       fp32 [64][68] (3-4) -> T hi/lo [2][64][68] bf16 | - (5-6)
+//       fp32 [64][68] (3-4) -> (T o beta) hi/lo | (T o beta e^G |k|^-1)
+//       hi/lo [64][68] bf16 each (5-6)
 constexpr int kRA = 0;
 constexpr int kKtPitch = 72;  // bf16 per k^T row in RB (16-byte aligned rows)
 constexpr int kRB = kRA + 34816;
 constexpr int kRScal = kRB + 34816;  // beta, G, inverse scratch
-constexpr int kPrepLdsBytes = kRScal + 4 * 64 * 2 + 4 * 4 * 16 * 17;
+constexpr int kPrepLdsBytes = kRScal + 4 * 64 * 5 + 4 * 4 * 16 * 17;
 
 template <int XT, int GM>
 __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
@@ -289,13 +281,16 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   const int kdim = a.num_k_heads * kDim;
 
   __shared__ __attribute__((aligned(16))) unsigned char lds[kPrepLdsBytes];
-  uint16_t* khl = reinterpret_cast<uint16_t*>(lds + kRA);  // hi at [0, 64*136), lo after
+  uint16_t* kr = reinterpret_cast<uint16_t*>(lds + kRA);  // k rows [64][136] (bf16 conv values)
   uint16_t* KtB = reinterpret_cast<uint16_t*>(lds + kRB);  // k^T bf16 [128][kKtPitch]
   float* Lm = reinterpret_cast<float*>(lds + kRB);
   float* QKs = Lm + 64 * 68;
   float* beta_s = reinterpret_cast<float*>(lds + kRScal);
   float* G_s = beta_s + 64;
-  float* Xs = G_s + 64;  // [4][16][17]
+  float* fq_s = G_s + 64;  // per-token factors: |q|^-1 / sqrt(128)
+  float* fk_s = fq_s + 64;  // |k|^-1
+  float* fw_s = fk_s + 64;  // beta e^G |k|^-1 (the k side of W)
+  float* Xs = fw_s + 64;    // [4][16][17]
   char* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecBytes;
 
   // Step 1: lane (n, g4) of wave w loads token 16w + n, dims 32s + 8g4 .. +8 of
@@ -303,11 +298,10 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   const int row = 16 * wave + n;
   const int t = t0 + row;
   const bool valid = t < a.length;
-  float qv[4][8], kv[4][8], vv[4][8];
-  uint4 rq[4], rk[4];  // the conv outputs of q and k (bf16), kept for the record
+  float qv[4][8], kv[4][8];
+  uint4 rq[4], rk[4], rv[4];  // the conv outputs (bf16): the MFMA operands and the record's q and k
   {
     const uint16_t* base = a.post + (int64_t)(t - a.tok0) * a.conv_dim;
-    uint4 rv[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int d = 32 * s + 8 * g4;
@@ -331,7 +325,6 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
     for (int s = 0; s < 4; ++s) {
       unpack(rq[s], qv[s]);
       unpack(rk[s], kv[s]);
-      unpack(rv[s], vv[s]);
     }
   }
   // Gates and the cumulative decay.
@@ -380,32 +373,27 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   sk += __shfl_xor(sk, 16, 64);
   sk += __shfl_xor(sk, 32, 64);
   const float iq = 1.0f / sqrtf(sq + 1e-6f), ik = 1.0f / sqrtf(sk + 1e-6f);
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      qv[s][j] = mul_rn(mul_rn(qv[s][j], iq), 0.08838834764831845f);
-      kv[s][j] = mul_rn(kv[s][j], ik);
-    }
   lds_barrier();  // G_s, beta_s ready
   const float eg = expf(G_s[row]);                    // e^{G_t}
   const float ekl = expf(G_s[kChunk - 1] - G_s[row]);  // e^{G_C - G_t}
   const float bt = beta_s[row];
-  // k hi/lo rows into RA; q (bf16) and the per-token factors straight to the
-  // record (A-operand order); k^T (bf16) into RB.
+  // k rows (bf16) into RA; q (bf16) and the per-token factors straight to
+  // the record (A-operand order); k^T (bf16) into RB; the rows' factors for
+  // the products' epilogues into LDS.
   {
     u32x4* q_rec = reinterpret_cast<u32x4*>(rec + kRecQt);
+    const float fq = mul_rn(iq, 0.08838834764831845f);
     if (g4 == 0) {
-      reinterpret_cast<float*>(rec + kRecFq)[row] = mul_rn(mul_rn(iq, 0.08838834764831845f), eg);
+      reinterpret_cast<float*>(rec + kRecFq)[row] = mul_rn(fq, eg);
       reinterpret_cast<float*>(rec + kRecFk)[row] = mul_rn(ik, ekl);
+      fq_s[row] = fq;
+      fk_s[row] = ik;
+      fw_s[row] = mul_rn(mul_rn(bt, eg), ik);
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int d = 32 * s + 8 * g4;
-      u32x4 hi, lo;
-      split8(kv[s], hi, lo);
-      *reinterpret_cast<u32x4*>(khl + row * 136 + d) = hi;
-      *reinterpret_cast<u32x4*>(khl + 64 * 136 + row * 136 + d) = lo;
+      *reinterpret_cast<uint4*>(kr + row * 136 + d) = rk[s];
       q_rec[(wave * 4 + s) * 64 + lane] = u32x4{rq[s].x, rq[s].y, rq[s].z, rq[s].w};
       const uint32_t kw[4] = {rk[s].x, rk[s].y, rk[s].z, rk[s].w};
 #pragma unroll
@@ -427,10 +415,10 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   }
   lds_barrier();  // RB free for L and (q k^T) o D
   // Step 3: Q K^T -> (q k^T) o D and K K^T -> L, 5 tiles per wave.
-  if (wave == 0) prep_qk_kk_tiles<0>(qv, khl, G_s, beta_s, Lm, QKs, n, g4);
-  else if (wave == 1) prep_qk_kk_tiles<1>(qv, khl, G_s, beta_s, Lm, QKs, n, g4);
-  else if (wave == 2) prep_qk_kk_tiles<2>(qv, khl, G_s, beta_s, Lm, QKs, n, g4);
-  else prep_qk_kk_tiles<3>(qv, khl, G_s, beta_s, Lm, QKs, n, g4);
+  if (wave == 0) prep_qk_kk_tiles<0>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
+  else if (wave == 1) prep_qk_kk_tiles<1>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
+  else if (wave == 2) prep_qk_kk_tiles<2>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
+  else prep_qk_kk_tiles<3>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
   for (int e = tid; e < kChunk * kChunk; e += 256) {  // upper tiles of (q k^T) o D are zero
     const int i = e >> 6, j = e & 63;
     if ((j >> 4) > (i >> 4)) QKs[i * 68 + j] = 0.f;
@@ -492,78 +480,79 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
     }
     lds_barrier();
   }
-  // Step 5: T hi/lo into RB (L and (q k^T) o D are dead), then (beta v)^T
-  // hi/lo into RA (T fp32 is dead) from the rows still in registers.
-  uint16_t* Thl = reinterpret_cast<uint16_t*>(lds + kRB);  // hi [64][68], lo after
+  // Step 5: T with its columns scaled by the tokens' factors, as hi/lo
+  // pairs into RB (L and (q k^T) o D are dead): Tv = T o beta for U and
+  // Tw = T o (beta e^G |k|^-1) for W, so that v and k enter the products as
+  // the conv's bf16 values; then v^T and k^T (bf16) into RA (T is dead).
+  uint16_t* Tv = reinterpret_cast<uint16_t*>(lds + kRB);  // hi [64][68], lo after
+  uint16_t* Tw = Tv + 2 * 64 * 68;
   for (int e = tid; e < kChunk * kChunk; e += 256) {
     const int i = e >> 6, j = e & 63;
     const float v = (j >> 4) > (i >> 4) ? 0.f : Tm[i * 68 + j];
-    const uint16_t hb = f32_to_bf16_bits(v);
-    Thl[i * 68 + j] = hb;
-    Thl[64 * 68 + i * 68 + j] = f32_to_bf16_bits(v - bf16_bits_to_f32(hb));
+    const float xv = v * beta_s[j], xw = v * fw_s[j];
+    const uint16_t hv = f32_to_bf16_bits(xv), hw = f32_to_bf16_bits(xw);
+    Tv[i * 68 + j] = hv;
+    Tv[64 * 68 + i * 68 + j] = f32_to_bf16_bits(xv - bf16_bits_to_f32(hv));
+    Tw[i * 68 + j] = hw;
+    Tw[64 * 68 + i * 68 + j] = f32_to_bf16_bits(xw - bf16_bits_to_f32(hw));
   }
-  uint16_t* BT = reinterpret_cast<uint16_t*>(lds + kRA);  // (beta v)^T, then (beta e^G k)^T: hi [128][68], lo after
+  uint16_t* VtR = reinterpret_cast<uint16_t*>(lds + kRA);  // v^T [128][68]
+  uint16_t* KtR = VtR + 128 * 68;                          // k^T [128][68]
   lds_barrier();
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
+  for (int s = 0; s < 4; ++s) {
+    const uint32_t vw[4] = {rv[s].x, rv[s].y, rv[s].z, rv[s].w};
+    const uint32_t kw[4] = {rk[s].x, rk[s].y, rk[s].z, rk[s].w};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = 32 * s + 8 * g4 + j;
-      const float vb = vv[s][j] * bt;
-      const uint16_t hb = f32_to_bf16_bits(vb);
-      BT[d * 68 + row] = hb;
-      BT[128 * 68 + d * 68 + row] = f32_to_bf16_bits(vb - bf16_bits_to_f32(hb));
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * s + 8 * g4 + 2 * j;
+      VtR[d * 68 + row] = static_cast<uint16_t>(vw[j] & 0xffffu);
+      VtR[(d + 1) * 68 + row] = static_cast<uint16_t>(vw[j] >> 16);
+      KtR[d * 68 + row] = static_cast<uint16_t>(kw[j] & 0xffffu);
+      KtR[(d + 1) * 68 + row] = static_cast<uint16_t>(kw[j] >> 16);
     }
+  }
   lds_barrier();
-  // Step 6: U = T (beta v), then W = T (beta e^G k).  Wave w takes column
-  // tiles td = w and w + 4 for every token tile; the tiles of a token tile
-  // share the T operand reads.
+  // Step 6: U = Tv v and W = Tw k.  Wave w takes column tiles td = w and
+  // w + 4 for every token tile; the hi and lo products go to separate
+  // accumulators, added at the end.
   constexpr int kSteps[4] = {1, 1, 2, 2};  // T is lower triangular: k-steps of 32 up to column 16 tt + 15
-  auto t_times_bt = [&](int tt, f32x4 (&acc)[2]) {
+  using BF = Kv16<RIA_DT_BF16>;
+  auto t_times = [&](const uint16_t* Th, const uint16_t* Bt, int tt, f32x4 (&acc)[2]) {
+    f32x4 ah_acc[2], al_acc[2];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < 2; ++q) ah_acc[q] = al_acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       if (s >= kSteps[tt]) break;
       const int kofs = 32 * s + 8 * g4;
-      const u32x4 ah = lds16(Thl + (16 * tt + n) * 68 + kofs), al = lds16(Thl + 64 * 68 + (16 * tt + n) * 68 + kofs);
-      u32x4 bh[2], bl[2];
+      const u32x4 ah = lds16(Th + (16 * tt + n) * 68 + kofs), al = lds16(Th + 64 * 68 + (16 * tt + n) * 68 + kofs);
+      u32x4 bq[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) bq[q] = lds16(Bt + (16 * (wave + 4 * q) + n) * 68 + kofs);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const int td = wave + 4 * q;
-        bh[q] = lds16(BT + (16 * td + n) * 68 + kofs);
-        bl[q] = lds16(BT + 128 * 68 + (16 * td + n) * 68 + kofs);
+        ah_acc[q] = BF::mfma_k32(ah, bq[q], ah_acc[q]);
+        al_acc[q] = BF::mfma_k32(al, bq[q], al_acc[q]);
       }
-#pragma unroll
-      for (int q = 0; q < 2; ++q) acc[q] = mfma3(ah, al, bh[q], bl[q], acc[q]);
     }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) acc[q] = ah_acc[q] + al_acc[q];
   };
   {
     f32x4* u_rec = reinterpret_cast<f32x4*>(rec + kRecU);
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       f32x4 acc[2];
-      t_times_bt(tt, acc);
+      t_times(Tv, VtR, tt, acc);
 #pragma unroll
       for (int q = 0; q < 2; ++q) u_rec[(tt * 8 + wave + 4 * q) * 64 + lane] = acc[q];
     }
   }
-  lds_barrier();  // (beta v)^T read: RA takes (beta e^G k)^T
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = 32 * s + 8 * g4 + j;
-      const float kb = kv[s][j] * (bt * eg);
-      const uint16_t hb = f32_to_bf16_bits(kb);
-      BT[d * 68 + row] = hb;
-      BT[128 * 68 + d * 68 + row] = f32_to_bf16_bits(kb - bf16_bits_to_f32(hb));
-    }
-  lds_barrier();
   f32x4 wacc[4][2];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) t_times_bt(tt, wacc[tt]);
-  lds_barrier();  // (beta e^G k)^T read: RA takes the -W staging
+  for (int tt = 0; tt < 4; ++tt) t_times(Tw, KtR, tt, wacc[tt]);
+  lds_barrier();  // v^T and k^T read: RA takes the -W staging
   float* Wst = reinterpret_cast<float*>(lds + kRA);  // -W [64][132]
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)

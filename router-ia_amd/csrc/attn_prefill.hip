@@ -302,23 +302,32 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
         for (int i = 0; i < 4; ++i)
           if (32 * b + 8 * g4 + 4 * m + i > qlim) s[4 * m + i] = -INFINITY;
     }
-    float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-    mx = swap_max(mx, true);
-    mx = swap_max(mx, false);
-    // m_run is finite from the first block on (key 0 is visible to every
-    // column), so masked scores give exp2(-inf) = 0
-    const bool grow = mx > m_run + 8.0f;
-    if (__any(grow)) {
+    // The probabilities against the running max go out at once; only a
+    // block with a score more than 2^8 above it (every column's first block
+    // among them) needs the column max (permlane swaps), the rescale and the
+    // probabilities again.  m_run is the same in the four lanes of a column,
+    // so a lane's own max decides as the column max would.
+    const float mloc = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    float pr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pr[j] = __builtin_amdgcn_exp2f(s[j] - m_run);
+      asm volatile("" : "+v"(pr[j]));  // computed here, beside the vote, not sunk past the branch
+    }
+    if (__any(mloc > m_run + 8.0f)) {
+      const float mx = swap_max(swap_max(mloc, true), false);
+      // m_run is finite from the first block on (key 0 is visible to every
+      // column), so masked scores give exp2(-inf) = 0
+      const bool grow = mx > m_run + 8.0f;
       const float m_new = grow ? mx : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block, where o and l are 0
       l_run *= alpha;
 #pragma unroll
       for (int dt = 0; dt < 16; ++dt) o[dt] *= alpha;
       m_run = m_new;
-    }
-    float pr[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) pr[j] = __builtin_amdgcn_exp2f(s[j] - m_run);
+      for (int j = 0; j < 8; ++j) pr[j] = __builtin_amdgcn_exp2f(s[j] - m_run);
+    }
     l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
     u32x4 ph, pl;
     pack(pr, ph, pl);

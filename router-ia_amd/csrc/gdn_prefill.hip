@@ -295,9 +295,21 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
 
   // Step 1: lane (n, g4) of wave w loads token 16w + n, dims 32s + 8g4 .. +8 of
   // q, k and v: the MFMA A-operand order, so no transpose is needed later.
+  // Wave 0's gate inputs (lane t: token t of the chunk) go out first, so
+  // their latency overlaps the rows'.
   const int row = 16 * wave + n;
   const int t = t0 + row;
   const bool valid = t < a.length;
+  float gin_a = 0.f, gin_b = 0.f, alog = 0.f, dtb = 0.f;
+  const bool gate_ok = t0 + lane < a.length;
+  if (wave == 0 && gate_ok) {
+    gin_a = a.gate_a[(int64_t)(t0 + lane) * a.gate_stride + h];
+    gin_b = a.gate_b[(int64_t)(t0 + lane) * a.gate_stride + h];
+    if constexpr (GM == RIA_GATE_RAW) {
+      alog = a.A_log[h];
+      dtb = a.dt_bias[h];
+    }
+  }
   float qv[4][8], kv[4][8];
   uint4 rq[4], rk[4], rv[4];  // the conv outputs (bf16): the MFMA operands and the record's q and k
   {
@@ -329,17 +341,14 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   }
   // Gates and the cumulative decay.
   if (wave == 0) {
-    const int tt = t0 + lane;
     float beta = 0.f, g = 0.f;
-    if (tt < a.length) {
-      const float ga = a.gate_a[(int64_t)tt * a.gate_stride + h];
-      const float gb = a.gate_b[(int64_t)tt * a.gate_stride + h];
+    if (gate_ok) {
       if constexpr (GM == RIA_GATE_RAW) {
-        beta = sigmoid_f(gb);
-        g = -expf(a.A_log[h]) * softplus_f(ga + a.dt_bias[h]);
+        beta = sigmoid_f(gin_b);
+        g = -expf(alog) * softplus_f(gin_a + dtb);
       } else {
-        beta = gb;
-        g = ga;
+        beta = gin_b;
+        g = gin_a;
       }
     }
     beta_s[lane] = beta;
@@ -419,10 +428,6 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   else if (wave == 1) prep_qk_kk_tiles<1>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
   else if (wave == 2) prep_qk_kk_tiles<2>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
   else prep_qk_kk_tiles<3>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
-  for (int e = tid; e < kChunk * kChunk; e += 256) {  // upper tiles of (q k^T) o D are zero
-    const int i = e >> 6, j = e & 63;
-    if ((j >> 4) > (i >> 4)) QKs[i * 68 + j] = 0.f;
-  }
   lds_barrier();  // k rows dead: RA takes T
   // Step 4: QK operand to the record; T = (I + L)^-1 into RA (blocked 4x4 of 16x16).
   float* Tm = reinterpret_cast<float*>(lds + kRA);
@@ -432,6 +437,10 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
       const int w = job >> 1, s = job & 1;
       float tmp[8];
       load8(QKs + (16 * w + n) * 68 + 32 * s + 8 * g4, tmp);
+      if (((32 * s + 8 * g4) >> 4) > w) {  // upper tiles of (q k^T) o D are zero (never written)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tmp[j] = 0.f;
+      }
       u32x4 hi, lo;
       split8(tmp, hi, lo);
       qk_rec[((w * 2 + s) * 2 + 0) * 64 + lane] = hi;
@@ -486,15 +495,34 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   // the conv's bf16 values; then v^T and k^T (bf16) into RA (T is dead).
   uint16_t* Tv = reinterpret_cast<uint16_t*>(lds + kRB);  // hi [64][68], lo after
   uint16_t* Tw = Tv + 2 * 64 * 68;
-  for (int e = tid; e < kChunk * kChunk; e += 256) {
-    const int i = e >> 6, j = e & 63;
-    const float v = (j >> 4) > (i >> 4) ? 0.f : Tm[i * 68 + j];
-    const float xv = v * beta_s[j], xw = v * fw_s[j];
-    const uint16_t hv = f32_to_bf16_bits(xv), hw = f32_to_bf16_bits(xw);
-    Tv[i * 68 + j] = hv;
-    Tv[64 * 68 + i * 68 + j] = f32_to_bf16_bits(xv - bf16_bits_to_f32(hv));
-    Tw[i * 68 + j] = hw;
-    Tw[64 * 68 + i * 68 + j] = f32_to_bf16_bits(xw - bf16_bits_to_f32(hw));
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {  // 8 consecutive columns per thread
+    const int e8 = tid + 256 * r;
+    const int i = e8 >> 3, j0 = (e8 & 7) * 8;
+    float tv[8], bj[8], wj[8];
+    load8(Tm + i * 68 + j0, tv);
+    load8(beta_s + j0, bj);
+    load8(fw_s + j0, wj);
+    const bool upper = (j0 >> 4) > (i >> 4);  // T's upper tiles are zero (never written)
+    float xv[8], xw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = upper ? 0.f : tv[j];
+      xv[j] = v * bj[j];
+      xw[j] = v * wj[j];
+    }
+    u32x4 vh, vl, wh, wl;
+    split8(xv, vh, vl);
+    split8(xw, wh, wl);
+    // rows are 136 bytes apart: 8-byte stores keep every access aligned
+    auto st8x2 = [](uint16_t* p, const u32x4& x) {
+      reinterpret_cast<uint2*>(p)[0] = uint2{x[0], x[1]};
+      reinterpret_cast<uint2*>(p)[1] = uint2{x[2], x[3]};
+    };
+    st8x2(Tv + i * 68 + j0, vh);
+    st8x2(Tv + 64 * 68 + i * 68 + j0, vl);
+    st8x2(Tw + i * 68 + j0, wh);
+    st8x2(Tw + 64 * 68 + i * 68 + j0, wl);
   }
   uint16_t* VtR = reinterpret_cast<uint16_t*>(lds + kRA);  // v^T [128][68]
   uint16_t* KtR = VtR + 128 * 68;                          // k^T [128][68]

@@ -708,11 +708,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // threads do the touching.
   constexpr int kRecLines = kRecBytes / 128;
   constexpr int kTouch = (kRecLines + 8 * 256 - 1) / (8 * 256);
-  auto touch = [&](int cl, uint32_t (&tv)[kTouch]) {
-    const char* rec = rec_of(cl);
+  // Record loads go through a buffer resource based at the chunk's record
+  // (built in scalar registers per chunk): every load is a loop-invariant
+  // 32-bit lane offset plus a constant.  With 64-bit per-lane addresses the
+  // loop reused a load's destination registers as address temporaries, and
+  // the wait that reuse needs drained the record loads in flight every chunk.
+  auto rec_rsrc = [&](int cl) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(rec_of(cl)), 0, kRecBytes, kBufferWord3);
+  };
+  auto bload16 = [](__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  };
+  int touch_off[kTouch];
 #pragma unroll
-    for (int i = 0; i < kTouch; ++i)
-      tv[i] = *reinterpret_cast<const uint32_t*>(rec + (int64_t)min(8 * (tid + 256 * i) + cb, kRecLines - 1) * 128);
+  for (int i = 0; i < kTouch; ++i) touch_off[i] = min(8 * (tid + 256 * i) + cb, kRecLines - 1) * 128;
+  auto touch = [&](int cl, uint32_t (&tv)[kTouch]) {
+    const auto r = rec_rsrc(cl);
+#pragma unroll
+    for (int i = 0; i < kTouch; ++i) tv[i] = __builtin_amdgcn_raw_buffer_load_b32(r, touch_off[i], 0, 0);
   };
   auto consume = [](const uint32_t (&tv)[kTouch]) {
 #pragma unroll
@@ -748,25 +761,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // short independent chains.
   using BF = Kv16<RIA_DT_BF16>;
   if (state_role) {
+    const int l16 = 16 * lane;
     auto load_ops = [&](int cl, StateOps& o) {
-      const char* rec = rec_of(cl);
-      const u32x4* wn = reinterpret_cast<const u32x4*>(rec + kRecWn);
-      const u32x4* kt = reinterpret_cast<const u32x4*>(rec + kRecKt);
+      const auto r = rec_rsrc(cl);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) o.wn[s][p] = wn[((w * 4 + s) * 2 + p) * 64 + lane];
+        for (int p = 0; p < 2; ++p) o.wn[s][p] = bload16(r, l16, kRecWn + ((w * 4 + s) * 2 + p) * 1024);
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int tk = 0; tk < 2; ++tk) o.kt[tk][s] = kt[((2 * w + tk) * 2 + s) * 64 + lane];
-      o.u = reinterpret_cast<const f32x4*>(rec + kRecU)[(w * 8 + cb) * 64 + lane];
-      o.fk = reinterpret_cast<const f32x4*>(rec + kRecFk)[4 * w + g4];
-      // a vector load (opaque zero lane offset): a scalar load here would be
-      // waited for by the next lds_barrier (lgkmcnt), exposing its latency
-      int zero = 0;
-      asm volatile("" : "+v"(zero));
-      o.gl = reinterpret_cast<const float*>(rec + kRecGl)[zero];
+        for (int tk = 0; tk < 2; ++tk) o.kt[tk][s] = bload16(r, l16, kRecKt + ((2 * w + tk) * 2 + s) * 1024);
+      o.u = __builtin_bit_cast(f32x4, bload16(r, l16, kRecU + (w * 8 + cb) * 1024));
+      o.fk = __builtin_bit_cast(f32x4, bload16(r, 16 * g4, kRecFk + 64 * w));
+      // a vector load: a scalar load here would be waited for by the next
+      // lds_barrier (lgkmcnt), exposing its latency
+      o.gl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, 0, kRecGl, 0));
     };
     auto process = [&](int, const StateOps& o) {
       // (i) v' = U - W S for token tile w, and fk v'
@@ -827,17 +837,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     StateOps A, B;
     scan(A, B, load_ops, process, std::true_type{});
   } else {
+    const int l16 = 16 * lane;
     auto load_ops = [&](int cl, OutOps& o) {
-      const char* rec = rec_of(cl);
-      const u32x4* qt = reinterpret_cast<const u32x4*>(rec + kRecQt);
-      const u32x4* qk = reinterpret_cast<const u32x4*>(rec + kRecQK);
+      const auto r = rec_rsrc(cl);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) o.qt[s] = qt[(w * 4 + s) * 64 + lane];
+      for (int s = 0; s < 4; ++s) o.qt[s] = bload16(r, l16, kRecQt + (w * 4 + s) * 1024);
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) o.qk[s][p] = qk[((w * 2 + s) * 2 + p) * 64 + lane];
-      o.fq = reinterpret_cast<const f32x4*>(rec + kRecFq)[4 * w + g4];
+        for (int p = 0; p < 2; ++p) o.qk[s][p] = bload16(r, l16, kRecQK + ((w * 2 + s) * 2 + p) * 1024);
+      o.fq = __builtin_bit_cast(f32x4, bload16(r, 16 * g4, kRecFq + 64 * w));
     };
     auto process = [&](int cl, const OutOps& o) {
       const int chunk = a.chunk0 + cl;

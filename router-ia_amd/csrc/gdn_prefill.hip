@@ -20,13 +20,17 @@
 //                         l2norm, cumulative decay, K K^T and Q K^T on MFMA,
 //                         blocked fp32 triangular inverse, U and W on MFMA.
 //   chunk_scan_kernel     phase B, one workgroup per (V head, 16 state
-//                         columns), sequential over chunks; the fp32 state
-//                         block stays in LDS.
+//                         columns), sequential over chunks, waves in two
+//                         roles (state, read-out); the fp32 state block
+//                         stays in LDS.
 //   conv_ring_tail_kernel writes the last inputs into the conv ring.
 //
-// MFMA precision: every product runs on bf16 MFMA 16x16x32 with both fp32
-// operands split as hi + lo bf16 (hi*hi + hi*lo + lo*hi, ~2^-16 relative);
-// the cumulative decay, exponentials and the triangular inverse are fp32.
+// MFMA precision: products run on bf16 MFMA 16x16x32.  The conv outputs q, k
+// and v are bf16 values, exact operands, and enter the products as they are
+// (their norms and gates as fp32 factors outside); an fp32 operand is split
+// as hi + lo bf16: one product with an exact operand becomes two (x*hi +
+// x*lo), two fp32 operands three (hi*hi + hi*lo + lo*hi, ~2^-16 relative).
+// The cumulative decay, exponentials and the triangular inverse are fp32.
 #include <math.h>
 #include <algorithm>
 #include <type_traits>

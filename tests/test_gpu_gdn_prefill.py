@@ -3,6 +3,8 @@ reference's token-by-token recurrence, restated in the oracle.
 
 Covers a ragged last chunk with a non-zero starting state and conv history,
 segmenting (a workspace of one chunk gives the same bits as one pass),
+bf16 / fp16 outputs (the fp32 read-out rounded once, no row written past the
+prompt),
 prefill followed by decode, and the single-layer 16384-token prefill
 (zero state, seed 3) checked on every output and the final state.
 """
@@ -73,6 +75,35 @@ def test_prefill_segmenting_is_bit_identical(gpu):
     a, sa, ra = _gpu_prefill(gpu, params, inputs, 200, state0, ring0, 0)
     b, sb, rb = _gpu_prefill(gpu, params, inputs, 200, state0, ring0, 0, ws_tokens=64)
     assert torch.equal(a, b) and torch.equal(sa, sb) and torch.equal(ra, rb)
+
+
+@pytest.mark.parametrize("length,ws_tokens", [(130, None), (777, 192)])
+def test_prefill_16bit_outputs_round_the_fp32_read_out(gpu, length, ws_tokens):
+    """bf16 and fp16 outputs are the fp32 read-out rounded once, bit for bit,
+    and nothing is written past the prompt's last row: the scan stores each
+    chunk's rows through a buffer range that ends at the last token, so the
+    last chunk's rows past it are dropped by the hardware (checked on a
+    ragged last chunk, in one pass and in segments of three chunks)."""
+    announce(f"gdn_prefill: {length} tokens, bf16 / fp16 outputs against the fp32 read-out, guard rows untouched")
+    params = W.gdn_layer_params(61)
+    inputs = W.gdn_step_inputs(62, length, 1)
+    state0, ring0 = _init(63)
+    ref, s_ref, _ = _gpu_prefill(gpu, params, inputs, length, state0, ring0, 5, ws_tokens=ws_tokens)
+    for dt in (torch.bfloat16, torch.float16):
+        guard = 64  # rows after the prompt in the same allocation
+        big = torch.full((length + guard, 32, 128), 7.0, dtype=dt, device=gpu)
+        state = state0.clone().to(gpu)
+        ring = ring0.clone().to(gpu)
+        ws = torch.empty(K.gdn_prefill_workspace_bytes(16, 32, ws_tokens or length), dtype=torch.uint8, device=gpu)
+        K.gdn_prefill(inputs["mixed"][:length, 0].to(gpu), state, inputs["a_raw"][:length, 0].to(gpu),
+                      inputs["b_raw"][:length, 0].to(gpu), big[:length], num_k_heads=16, num_v_heads=32,
+                      conv_weight=params["conv_weight"].to(gpu), conv_ring=ring, conv_pos=5, workspace=ws,
+                      gate_mode=nat.RIA_GATE_RAW, A_log=params["A_log"].to(gpu), dt_bias=params["dt_bias"].to(gpu))
+        torch.cuda.synchronize()
+        got = big.cpu()
+        assert torch.equal(got[:length], ref.to(dt)), f"{dt} outputs"
+        assert torch.equal(got[length:], torch.full((guard, 32, 128), 7.0, dtype=dt)), f"{dt} rows past the prompt"
+        assert torch.equal(state.cpu(), s_ref), f"state with {dt} outputs"
 
 
 @pytest.mark.parametrize("length", [1, 3, 64])

@@ -259,22 +259,28 @@ __device__ __forceinline__ void prep_qk_kk_tiles(const uint4 (&rq)[4], const uin
 }
 
 // ---------------------------------------------------------------- phase A
-// LDS regions (bytes) and what they hold over the kernel's steps; 75 KB in
-// all, so two workgroups share a CU and one's loads and barriers overlap the
-// other's arithmetic.
-//   RA: k rows [64][136] bf16 (steps 2-3) -> T fp32 [64][68] (4-5)
-//       -> v^T | k^T bf16 [128][68] each (6) -> -W fp32 [64][132] (7)
-//   RB: k^T bf16 [128][72] (2) -> L fp32 [64][68] | (q k^T) o D
-//       fp32 [64][68] (3-4) -> (T o beta) hi/lo | (T o beta e^G |k|^-1)
-//       hi/lo [64][68] bf16 each (5-6)
-constexpr int kRA = 0;
-constexpr int kKtPitch = 72;  // bf16 per k^T row in RB (16-byte aligned rows)
-constexpr int kRB = kRA + 34816;
-constexpr int kRScal = kRB + 34816;  // beta, G, inverse scratch
-constexpr int kPrepLdsBytes = kRScal + 4 * 64 * 5 + 4 * 4 * 16 * 17;
+// LDS: three 17 KB slots and the per-token factors, 52.3 KB in all, so three
+// workgroups share a CU and their loads and barriers overlap each other's
+// arithmetic (at 75 KB and two per CU phase A took 438 us per 16k tokens).
+// What each slot holds over the kernel's steps:
+//   S0: k rows [64][136] bf16 (steps 2-3) -> T fp32 [64][68] (4-6)
+//       -> -W fp32 [64][132] (7, with S1)
+//   S1: k^T bf16 [128][72] (2, into S2) -> L fp32 [64][68] (3-4)
+//       -> (T o beta) hi/lo (6U) -> (T o beta e^G |k|^-1) hi/lo (6W)
+//   S2: (q k^T) o D fp32 [64][68] (3-4) -> inverse scratch (4) -> v^T bf16
+//       [128][68] (6U) -> k^T bf16 [128][68] (6W)
+constexpr int kSlot = 17408;
+constexpr int kS0 = 0;
+constexpr int kS1 = kS0 + kSlot;
+constexpr int kS2 = kS1 + kSlot;
+constexpr int kKtPitch = 72;  // bf16 per k^T row in S1 (16-byte aligned rows)
+constexpr int kRScal = kS2 + kSlot;  // beta, G and the per-token factors
+constexpr int kPrepLdsBytes = kRScal + 4 * 64 * 5;
+static_assert(128 * kKtPitch * 2 <= 2 * kSlot && 64 * 132 * 4 <= 2 * kSlot, "two-slot arrays");
+static_assert(3 * kPrepLdsBytes <= 160 * 1024, "three workgroups per CU");
 
 template <int XT, int GM>
-__global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, 3) void chunk_prep_kernel(PrefillArgs a) {
   const int cl = blockIdx.x;  // chunk within the segment
   const int h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -285,16 +291,16 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
   const int kdim = a.num_k_heads * kDim;
 
   __shared__ __attribute__((aligned(16))) unsigned char lds[kPrepLdsBytes];
-  uint16_t* kr = reinterpret_cast<uint16_t*>(lds + kRA);  // k rows [64][136] (bf16 conv values)
-  uint16_t* KtB = reinterpret_cast<uint16_t*>(lds + kRB);  // k^T bf16 [128][kKtPitch]
-  float* Lm = reinterpret_cast<float*>(lds + kRB);
-  float* QKs = Lm + 64 * 68;
+  uint16_t* kr = reinterpret_cast<uint16_t*>(lds + kS0);  // k rows [64][136] (bf16 conv values)
+  uint16_t* KtB = reinterpret_cast<uint16_t*>(lds + kS1);  // k^T bf16 [128][kKtPitch]
+  float* Lm = reinterpret_cast<float*>(lds + kS1);
+  float* QKs = reinterpret_cast<float*>(lds + kS2);
   float* beta_s = reinterpret_cast<float*>(lds + kRScal);
   float* G_s = beta_s + 64;
   float* fq_s = G_s + 64;  // per-token factors: |q|^-1 / sqrt(128)
   float* fk_s = fq_s + 64;  // |k|^-1
   float* fw_s = fk_s + 64;  // beta e^G |k|^-1 (the k side of W)
-  float* Xs = fw_s + 64;    // [4][16][17]
+  float* Xs = reinterpret_cast<float*>(lds + kS2);  // [4][16][17], once (q k^T) o D is in the record
   char* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecBytes;
 
   // Step 1: lane (n, g4) of wave w loads token 16w + n, dims 32s + 8g4 .. +8 of
@@ -426,15 +432,15 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
       k_rec[(dt * 2 + s) * 64 + lane] = lds16(KtB + (16 * dt + n) * kKtPitch + 32 * s + 8 * g4);
     }
   }
-  lds_barrier();  // RB free for L and (q k^T) o D
+  lds_barrier();  // S1, S2 free for L and (q k^T) o D
   // Step 3: Q K^T -> (q k^T) o D and K K^T -> L, 5 tiles per wave.
   if (wave == 0) prep_qk_kk_tiles<0>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
   else if (wave == 1) prep_qk_kk_tiles<1>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
   else if (wave == 2) prep_qk_kk_tiles<2>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
   else prep_qk_kk_tiles<3>(rq, kr, G_s, beta_s, fq_s, fk_s, Lm, QKs, n, g4);
-  lds_barrier();  // k rows dead: RA takes T
-  // Step 4: QK operand to the record; T = (I + L)^-1 into RA (blocked 4x4 of 16x16).
-  float* Tm = reinterpret_cast<float*>(lds + kRA);
+  lds_barrier();  // k rows dead: S0 takes T
+  // Step 4: QK operand to the record; T = (I + L)^-1 into S0 (blocked 4x4 of 16x16).
+  float* Tm = reinterpret_cast<float*>(lds + kS0);
   {
     u32x4* qk_rec = reinterpret_cast<u32x4*>(rec + kRecQK);
     for (int job = wave; job < 8; job += 4) {
@@ -493,64 +499,50 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
     }
     lds_barrier();
   }
-  // Step 5: T with its columns scaled by the tokens' factors, as hi/lo
-  // pairs into RB (L and (q k^T) o D are dead): Tv = T o beta for U and
-  // Tw = T o (beta e^G |k|^-1) for W, so that v and k enter the products as
-  // the conv's bf16 values; then v^T and k^T (bf16) into RA (T is dead).
-  uint16_t* Tv = reinterpret_cast<uint16_t*>(lds + kRB);  // hi [64][68], lo after
-  uint16_t* Tw = Tv + 2 * 64 * 68;
+  // Steps 5 and 6, once for U and once for W: T with its columns scaled by
+  // the tokens' factors, as hi/lo pairs into S1 (T o beta for U, then
+  // T o beta e^G |k|^-1 for W), so that v and k enter the products as the
+  // conv's bf16 values, transposed as raw bf16 into S2; then the product.
+  // Wave w takes column tiles td = w and w + 4 for every token tile; the hi
+  // and lo products go to separate accumulators, added at the end.
+  uint16_t* Th = reinterpret_cast<uint16_t*>(lds + kS1);  // hi [64][68], lo after
+  uint16_t* Bt = reinterpret_cast<uint16_t*>(lds + kS2);  // v^T or k^T [128][68]
+  auto stage = [&](const float* fac, const uint4 (&raw)[4]) {
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {  // 8 consecutive columns per thread
-    const int e8 = tid + 256 * r;
-    const int i = e8 >> 3, j0 = (e8 & 7) * 8;
-    float tv[8], bj[8], wj[8];
-    load8(Tm + i * 68 + j0, tv);
-    load8(beta_s + j0, bj);
-    load8(fw_s + j0, wj);
-    const bool upper = (j0 >> 4) > (i >> 4);  // T's upper tiles are zero (never written)
-    float xv[8], xw[8];
+    for (int r = 0; r < 2; ++r) {  // 8 consecutive columns per thread
+      const int e8 = tid + 256 * r;
+      const int i = e8 >> 3, j0 = (e8 & 7) * 8;
+      float tv[8], fj[8];
+      load8(Tm + i * 68 + j0, tv);
+      load8(fac + j0, fj);
+      const bool upper = (j0 >> 4) > (i >> 4);  // T's upper tiles are zero (never written)
+      float x[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float v = upper ? 0.f : tv[j];
-      xv[j] = v * bj[j];
-      xw[j] = v * wj[j];
+      for (int j = 0; j < 8; ++j) x[j] = (upper ? 0.f : tv[j]) * fj[j];
+      u32x4 hi, lo;
+      split8(x, hi, lo);
+      // rows are 136 bytes apart: 8-byte stores keep every access aligned
+      auto st8x2 = [](uint16_t* p, const u32x4& v) {
+        reinterpret_cast<uint2*>(p)[0] = uint2{v[0], v[1]};
+        reinterpret_cast<uint2*>(p)[1] = uint2{v[2], v[3]};
+      };
+      st8x2(Th + i * 68 + j0, hi);
+      st8x2(Th + 64 * 68 + i * 68 + j0, lo);
     }
-    u32x4 vh, vl, wh, wl;
-    split8(xv, vh, vl);
-    split8(xw, wh, wl);
-    // rows are 136 bytes apart: 8-byte stores keep every access aligned
-    auto st8x2 = [](uint16_t* p, const u32x4& x) {
-      reinterpret_cast<uint2*>(p)[0] = uint2{x[0], x[1]};
-      reinterpret_cast<uint2*>(p)[1] = uint2{x[2], x[3]};
-    };
-    st8x2(Tv + i * 68 + j0, vh);
-    st8x2(Tv + 64 * 68 + i * 68 + j0, vl);
-    st8x2(Tw + i * 68 + j0, wh);
-    st8x2(Tw + 64 * 68 + i * 68 + j0, wl);
-  }
-  uint16_t* VtR = reinterpret_cast<uint16_t*>(lds + kRA);  // v^T [128][68]
-  uint16_t* KtR = VtR + 128 * 68;                          // k^T [128][68]
-  lds_barrier();
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const uint32_t vw[4] = {rv[s].x, rv[s].y, rv[s].z, rv[s].w};
-    const uint32_t kw[4] = {rk[s].x, rk[s].y, rk[s].z, rk[s].w};
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t bw[4] = {raw[s].x, raw[s].y, raw[s].z, raw[s].w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = 32 * s + 8 * g4 + 2 * j;
-      VtR[d * 68 + row] = static_cast<uint16_t>(vw[j] & 0xffffu);
-      VtR[(d + 1) * 68 + row] = static_cast<uint16_t>(vw[j] >> 16);
-      KtR[d * 68 + row] = static_cast<uint16_t>(kw[j] & 0xffffu);
-      KtR[(d + 1) * 68 + row] = static_cast<uint16_t>(kw[j] >> 16);
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * s + 8 * g4 + 2 * j;
+        Bt[d * 68 + row] = static_cast<uint16_t>(bw[j] & 0xffffu);
+        Bt[(d + 1) * 68 + row] = static_cast<uint16_t>(bw[j] >> 16);
+      }
     }
-  }
-  lds_barrier();
-  // Step 6: U = Tv v and W = Tw k.  Wave w takes column tiles td = w and
-  // w + 4 for every token tile; the hi and lo products go to separate
-  // accumulators, added at the end.
+  };
   constexpr int kSteps[4] = {1, 1, 2, 2};  // T is lower triangular: k-steps of 32 up to column 16 tt + 15
   using BF = Kv16<RIA_DT_BF16>;
-  auto t_times = [&](const uint16_t* Th, const uint16_t* Bt, int tt, f32x4 (&acc)[2]) {
+  auto t_times = [&](int tt, f32x4 (&acc)[2]) {
     f32x4 ah_acc[2], al_acc[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) ah_acc[q] = al_acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -571,21 +563,26 @@ __global__ __launch_bounds__(256, 2) void chunk_prep_kernel(PrefillArgs a) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) acc[q] = ah_acc[q] + al_acc[q];
   };
+  stage(beta_s, rv);  // L and the inverse scratch are dead
+  lds_barrier();
   {
     f32x4* u_rec = reinterpret_cast<f32x4*>(rec + kRecU);
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       f32x4 acc[2];
-      t_times(Tv, VtR, tt, acc);
+      t_times(tt, acc);
 #pragma unroll
       for (int q = 0; q < 2; ++q) u_rec[(tt * 8 + wave + 4 * q) * 64 + lane] = acc[q];
     }
   }
+  lds_barrier();  // T o beta and v^T read
+  stage(fw_s, rk);
+  lds_barrier();
   f32x4 wacc[4][2];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) t_times(Tw, KtR, tt, wacc[tt]);
-  lds_barrier();  // v^T and k^T read: RA takes the -W staging
-  float* Wst = reinterpret_cast<float*>(lds + kRA);  // -W [64][132]
+  for (int tt = 0; tt < 4; ++tt) t_times(tt, wacc[tt]);
+  lds_barrier();  // T, its W scaling and k^T read: S0 and S1 take the -W staging
+  float* Wst = reinterpret_cast<float*>(lds + kS0);  // -W [64][132]
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
 #pragma unroll

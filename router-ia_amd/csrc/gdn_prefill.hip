@@ -127,9 +127,10 @@ __device__ __forceinline__ void load8(const float* p, float* v) {
 // per token for the two channels), then the arithmetic runs: issued in
 // batches, each batch's latency was exposed (187 -> 144 us per 16k-token
 // prompt in one process).  Other input dtypes load tokens in batches of 8.
-// SiLU keeps the accurate fp32 form: on the hardware exp2 and reciprocal the
-// launch took 96 us, but the final state of a 130-token prefill then missed
-// its 1e-4 bound (1.8e-3).
+// The launch is VALU-bound (the 16k-token prompt moves 0.54 GB, 67 us at
+// 8 TB/s): SiLU takes silu_to_bf16, the same bits as the accurate form at
+// about a third of its instructions, and the bf16 tile path addresses rows
+// through buffer resources with the row in the scalar offset (146 -> 125 us).
 constexpr int kConvTile = 64;
 
 template <int XT>
@@ -155,7 +156,10 @@ __global__ __launch_bounds__(256) void prefill_conv_kernel(PrefillArgs a) {
   };
   float ha[3], hb[3];
   for (int i = 0; i < 3; ++i) input(t_begin - 3 + i, ha[i], hb[i]);
-  auto emit = [&](int t, float xa, float xb) {
+  // conv + SiLU of one token for both channels as packed bf16 (channel c in
+  // the low half); shifts the history
+  using B16 = Kv16<RIA_DT_BF16>;
+  auto step = [&](float xa, float xb) -> uint32_t {
     float acc_a = wa[0] * ha[0], acc_b = wb[0] * hb[0];
     acc_a = fmaf(wa[1], ha[1], acc_a);
     acc_b = fmaf(wb[1], hb[1], acc_b);
@@ -163,24 +167,31 @@ __global__ __launch_bounds__(256) void prefill_conv_kernel(PrefillArgs a) {
     acc_b = fmaf(wb[2], hb[2], acc_b);
     acc_a = fmaf(wa[3], xa, acc_a);
     acc_b = fmaf(wb[3], xb, acc_b);
-    const uint32_t y = f32_to_bf16_bits(silu_f(round_bf16(acc_a))) |
-                       (uint32_t(f32_to_bf16_bits(silu_f(round_bf16(acc_b)))) << 16);
-    *reinterpret_cast<uint32_t*>(a.post + (int64_t)(t - a.tok0) * a.conv_dim + c) = y;
+    const uint32_t r = B16::pack2(acc_a, acc_b);  // the bf16 conv output
     ha[0] = ha[1]; ha[1] = ha[2]; ha[2] = xa;
     hb[0] = hb[1]; hb[1] = hb[2]; hb[2] = xb;
+    return B16::pack2(silu_to_bf16(B16::lo_f32(r)), silu_to_bf16(B16::hi_f32(r)));
   };
   if (XT == RIA_DT_BF16 && a.x_pairs) {
-    // every load of the tile at once (token index clamped to the segment)
+    // Every load of the tile at once.  Buffer resources over the tile's rows
+    // take the row in the scalar offset, so no per-token address arithmetic
+    // (x rows clamped to the segment; x_stride < 2^24 elements).
+    const int rows = t_end - t_begin;
+    const uint16_t* xt = static_cast<const uint16_t*>(a.x) + (int64_t)t_begin * a.x_stride;
+    const auto xs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(xt), 0, rows * (int)a.x_stride * 2,
+                                                      kBufferWord3);
+    const auto ps = __builtin_amdgcn_make_buffer_rsrc(a.post + (int64_t)(t_begin - a.tok0) * a.conv_dim, 0,
+                                                      rows * a.conv_dim * 2, kBufferWord3);
+    const int voff = c * 2;
     uint32_t xr[kConvTile];
-    const uint16_t* xp = static_cast<const uint16_t*>(a.x) + c;
 #pragma unroll
     for (int u = 0; u < kConvTile; ++u)
-      xr[u] = *reinterpret_cast<const uint32_t*>(xp + (int64_t)min(t_begin + u, t_end - 1) * a.x_stride);
+      xr[u] = __builtin_amdgcn_raw_buffer_load_b32(xs, voff, min(u, rows - 1) * (int)a.x_stride * 2, 0);
 #pragma unroll
-    for (int u = 0; u < kConvTile; ++u) {
-      if (t_begin + u >= t_end) break;
-      emit(t_begin + u, bf16_bits_to_f32(xr[u] & 0xffffu), bf16_bits_to_f32(xr[u] >> 16));
-    }
+    for (int u = 0; u < kConvTile; ++u)
+      if (u < rows)
+        __builtin_amdgcn_raw_buffer_store_b32(step(B16::lo_f32(xr[u]), B16::hi_f32(xr[u])), ps, voff,
+                                              u * a.conv_dim * 2, 0);
   } else {
     for (int tb = t_begin; tb < t_end; tb += 8) {
       float xa[8], xb[8];
@@ -192,7 +203,7 @@ __global__ __launch_bounds__(256) void prefill_conv_kernel(PrefillArgs a) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         if (tb + u >= t_end) break;
-        emit(tb + u, xa[u], xb[u]);
+        *reinterpret_cast<uint32_t*>(a.post + (int64_t)(tb + u - a.tok0) * a.conv_dim + c) = step(xa[u], xb[u]);
       }
     }
   }
@@ -982,7 +993,8 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
   PrefillArgs a{};
   a.x = mixed_qkv;
   a.x_stride = x_row_stride;
-  a.x_pairs = x_dtype == RIA_DT_BF16 && reinterpret_cast<uintptr_t>(mixed_qkv) % 4 == 0 && x_row_stride % 2 == 0;
+  a.x_pairs = x_dtype == RIA_DT_BF16 && reinterpret_cast<uintptr_t>(mixed_qkv) % 4 == 0 && x_row_stride % 2 == 0 &&
+              x_row_stride < (int64_t(1) << 24);
   a.conv_w = static_cast<const uint16_t*>(conv_weight);
   a.conv_ring = static_cast<uint16_t*>(conv_ring);
   a.n0 = conv_pos;

@@ -249,6 +249,22 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
+// A float that rounds to the same bf16 as silu_f(x), for a bf16 value x (a
+// post-conv activation), at a fraction of the accurate form's VALU cost.  For
+// x > -16 the hardware exp2 and reciprocal put y within kSiluTieGuard / 2
+// fp32 ulps of silu_f(x) (most of it from rounding -x log2(e) before exp2,
+// which grows with |x|).  Where y lies more than kSiluTieGuard ulps from a
+// bf16 rounding midpoint (low 16 bits 0x8000) both round to the same bf16;
+// lanes nearer a midpoint, about 1 in 1000, and x <= -16 or NaN take the
+// accurate form.  Checked over all 65536 bf16 inputs.
+constexpr uint32_t kSiluTieGuard = 32;
+__device__ __forceinline__ float silu_to_bf16(float x) {
+  const float y = x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504f));
+  const uint32_t lo = (__float_as_uint(y) & 0xffffu) - (0x8000u - kSiluTieGuard);
+  if (lo <= 2 * kSiluTieGuard || !(x > -16.0f)) return silu_f(x);
+  return y;
+}
+
 // RMSNorm pieces shared by the standalone and the fused forms.  eps is the
 // model's 1e-6 (qwen36_op_probe.py:32, qwen36_gated_norm_probe.py:16).
 constexpr float kNormEps = 1e-6f;

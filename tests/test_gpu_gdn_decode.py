@@ -7,6 +7,7 @@ dtypes, both gate modes and the unfused (post-conv input) form.
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -174,3 +175,58 @@ def test_conv1d_step_standalone(gpu):
             torch.testing.assert_close(out[b:b + 1].cpu(), want, rtol=8e-3, atol=1e-6)
     for b in range(3):
         assert torch.equal(ring_to_window(ring[b].cpu(), 6), convs[b])
+
+
+def _bf16_rne(bits32: np.ndarray) -> np.ndarray:
+    return ((bits32 + 0x7FFF + ((bits32 >> 16) & 1)) >> 16).astype(np.uint32)
+
+
+def test_conv1d_step_silu_every_bf16_input(gpu):
+    """The SiLU after the conv over all 65536 bf16 values.
+
+    Conv weights (0, 0, 0, 1) and a zero history make the conv output the
+    input itself (-0 becomes +0 in the sum), so row r, channel c takes the
+    bf16 value with bits r * 8192 + c.  The bar is the fp32 SiLU torch computes
+    (x / (1 + exp(-x)), exp overflowing past x = -88.7) rounded to bf16: the
+    float64 SiLU, rounded to fp32 and then to bf16, wherever that fp32 value
+    is not itself a bf16 rounding midpoint (258 inputs, where either
+    neighbour is accepted), and torch's CPU bf16 F.silu (the oracle's conv
+    activation) on the same inputs.  The hardware exp2 and reciprocal alone,
+    without the accurate form near midpoints, fail it at x = 5.9375.
+    """
+    announce("conv1d_step: SiLU over all 65536 bf16 inputs")
+    dev = gpu
+    rows, ch = 8, W.CONV_DIM
+    bits = torch.arange(rows * ch, dtype=torch.int32)
+    x = bits.to(torch.int16).view(torch.bfloat16).reshape(rows, ch)
+    cw = torch.zeros((ch, 1, 4), dtype=torch.bfloat16)
+    cw[:, 0, 3] = 1.0
+    ring = torch.zeros((rows, 4, ch), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((rows, ch), dtype=torch.bfloat16, device=dev)
+    K.conv1d_step(x.to(dev), cw.to(dev), ring, out, conv_pos=0)
+    got = out.cpu().reshape(-1).view(torch.int16).numpy().astype(np.uint32) & 0xFFFF
+
+    with np.errstate(over="ignore", invalid="ignore"):
+        v = x.reshape(-1).float().numpy().astype(np.float64) + 0.0
+        e = np.exp(-v)
+        e[-v > np.log(np.finfo(np.float32).max)] = np.inf
+        y32 = (v / (1.0 + e)).astype(np.float32)
+    b32 = y32.view(np.uint32).astype(np.int64)
+    nan = np.isnan(y32)
+    near = ((b32 & 0xFFFF) == 0x8000) & ~nan
+    want = _bf16_rne(b32.astype(np.uint32)) & 0xFFFF
+    got_nan = (got & 0x7F80) == 0x7F80
+    got_nan &= (got & 0x7F) != 0
+    assert np.array_equal(got_nan, nan), "NaN results differ"
+    ok = ~nan & ~near
+    bad = np.nonzero(got[ok] != want[ok])[0]
+    assert bad.size == 0, f"{bad.size} inputs differ from the rounded fp32 SiLU, first bits " \
+                          f"{hex(int(bits.numpy()[ok][bad[0]]))}"
+    # on a midpoint: one bf16 step at most from the float64 rounding
+    diff = np.abs(got[near].astype(np.int64) - want[near].astype(np.int64))
+    assert diff.max(initial=0) <= 1
+    torch_bits = torch.nn.functional.silu(x.reshape(-1) + 0.0).view(torch.int16).numpy().astype(np.uint32) & 0xFFFF
+    off = np.nonzero((torch_bits != got) & ~nan & ~near)[0]
+    assert off.size == 0, f"{off.size} inputs differ from torch's bf16 SiLU away from midpoints"
+    print(f"{int(near.sum())} inputs on a midpoint; {int((torch_bits[near] != got[near]).sum())} of them "
+          f"differ from torch's CPU bf16 SiLU")

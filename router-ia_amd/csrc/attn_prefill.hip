@@ -81,6 +81,14 @@ struct PrefillAttnArgs {
 __device__ __forceinline__ int tile_row_page(int r) { return r >> 3; }
 __device__ __forceinline__ int tile_row_token(int m, int r) { return 8 * ((r >> 2) & 1) + 4 * m + (r & 3); }
 
+// max of three scores (never NaN: finite products, or -inf where masked) in
+// one instruction; fmaxf would first quiet each MFMA result for IEEE NaN rules
+__device__ __forceinline__ float max3_f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 __device__ __forceinline__ float swap_max(float x, bool rows16) {
   const auto s = rows16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
                         : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -122,11 +130,18 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
   // ---- q operands: column n, dims 32 kd + 8 g4 + j, RoPE'd, scaled by
   //      scale * log2(e) (scores come out in log2 units), as hi + lo pairs
   u32x4 qh[8], ql[8];
-  auto pack = [&](const float (&x)[8], u32x4& hi, u32x4& lo) {
+  // SEP: fp16 values converted one at a time, so hipcc folds the multiply
+  // that produced each (q times its scale) into the conversion
+  // (v_fma_mixlo_f16, one rounding); the probabilities, which no multiply
+  // produces, take the paired conversion.
+  auto pack = [&](const float (&x)[8], u32x4& hi, u32x4& lo, auto sep) {
     uint32_t h4[4], l4[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      h4[j] = KV::pack2(x[2 * j], x[2 * j + 1]);
+      if constexpr (decltype(sep)::value && KVT == RIA_DT_F16)
+        h4[j] = uint32_t(f32_to_f16_bits(x[2 * j])) | (uint32_t(f32_to_f16_bits(x[2 * j + 1])) << 16);
+      else
+        h4[j] = KV::pack2(x[2 * j], x[2 * j + 1]);
       l4[j] = KV::pack2(x[2 * j] - KV::lo_f32(h4[j]), x[2 * j + 1] - KV::hi_f32(h4[j]));
     }
     hi = u32x4{h4[0], h4[1], h4[2], h4[3]};
@@ -189,7 +204,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     for (int kd = 0; kd < 2; ++kd) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) x[kd][j] *= sl2;
-      pack(x[kd], qh[kd], ql[kd]);
+      pack(x[kd], qh[kd], ql[kd], std::true_type{});
     }
 #pragma unroll
     for (int kd = 2; kd < 8; ++kd) {
@@ -197,7 +212,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
       load_qn(kd, y);
 #pragma unroll
       for (int j = 0; j < 8; ++j) y[j] *= sl2;
-      pack(y, qh[kd], ql[kd]);
+      pack(y, qh[kd], ql[kd], std::true_type{});
     }
   }
 
@@ -274,8 +289,8 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    sc[0] = acc[0] + acc[2];
-    sc[1] = acc[1] + acc[3];
+    sc[0] = kSplit ? acc[0] + acc[2] : acc[0];
+    sc[1] = kSplit ? acc[1] + acc[3] : acc[1];
   };
 
   auto load_v = [&](int b, u32x4 (&vop)[16]) {
@@ -307,7 +322,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     // among them) needs the column max (permlane swaps), the rescale and the
     // probabilities again.  m_run is the same in the four lanes of a column,
     // so a lane's own max decides as the column max would.
-    const float mloc = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    const float mloc = max3_f(max3_f(s[0], s[1], s[2]), max3_f(s[3], s[4], s[5]), max3_f(s[6], s[7], s[7]));
     float pr[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -330,7 +345,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     }
     l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
     u32x4 ph, pl;
-    pack(pr, ph, pl);
+    pack(pr, ph, pl, std::false_type{});
     __builtin_amdgcn_sched_barrier(0);
     // all hi products, then all lo products: 16 MFMAs between dependent ones
 #pragma unroll

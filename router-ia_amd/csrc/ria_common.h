@@ -31,6 +31,7 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
@@ -322,8 +323,9 @@ template <>
 struct Kv16<RIA_DT_F16> {
   static __device__ __forceinline__ uint16_t from_f32(float f) { return f32_to_f16_bits(f); }
   static __device__ __forceinline__ float to_f32(uint16_t b) { return f16_bits_to_f32(b); }
+  // two values rounded to nearest-even in one instruction: a in the low half
   static __device__ __forceinline__ uint32_t pack2(float a, float b) {
-    return static_cast<uint32_t>(f32_to_f16_bits(a)) | (static_cast<uint32_t>(f32_to_f16_bits(b)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
   }
   static __device__ __forceinline__ float lo_f32(uint32_t w) { return f16_bits_to_f32(static_cast<uint16_t>(w)); }
   static __device__ __forceinline__ float hi_f32(uint32_t w) { return f16_bits_to_f32(static_cast<uint16_t>(w >> 16)); }

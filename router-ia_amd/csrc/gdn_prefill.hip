@@ -15,10 +15,13 @@
 // Kernels (one sequence per call; the host walks segments of chunks):
 //   prefill_conv_kernel   causal depthwise conv + SiLU over the segment's
 //                         tokens (bf16, the reference's rounding), history
-//                         from the conv ring for tokens before the prompt.
+//                         from the conv ring for tokens before the prompt;
+//                         one more workgroup per chunk computes the gates
+//                         (beta, the cumulative decay G and its exponentials)
+//                         into the chunk's records.
 //   chunk_prep_kernel     phase A, one workgroup per (chunk, V head):
-//                         l2norm, cumulative decay, K K^T and Q K^T on MFMA,
-//                         blocked fp32 triangular inverse, U and W on MFMA.
+//                         l2norm, K K^T and Q K^T on MFMA, blocked fp32
+//                         triangular inverse, U and W on MFMA.
 //   chunk_scan_kernel     phase B, one workgroup per (V head, 16 state
 //                         columns), sequential over chunks, waves in two
 //                         roles (state, read-out); the fp32 state block
@@ -56,6 +59,8 @@ constexpr int kDim = kGdnHeadDim;  // 128
 //   fq  exp(G_t) / |q_t| / sqrt(128), per token (exp(G) q = fq q)
 //   fk  exp(G_C - G_t) / |k_t|, per token (the k of S's update = fk k)
 //   gl  exp(G_C)
+//   Gt  per token {beta, G, exp(G), exp(G_C - G)} from the conv launch's gate
+//       pass, read by phase A
 constexpr int kRecQt = 0;
 constexpr int kRecWn = kRecQt + 4 * 4 * 64 * 16;
 constexpr int kRecQK = kRecWn + 4 * 4 * 2 * 64 * 16;
@@ -64,7 +69,8 @@ constexpr int kRecU = kRecKt + 8 * 2 * 64 * 16;
 constexpr int kRecFq = kRecU + 4 * 8 * 64 * 16;
 constexpr int kRecFk = kRecFq + 64 * 4;
 constexpr int kRecGl = kRecFk + 64 * 4;
-constexpr int kRecBytes = kRecGl + 256;
+constexpr int kRecGate = kRecGl + 256;
+constexpr int kRecBytes = kRecGate + 64 * 16;
 
 struct PrefillArgs {
   const void* x;  // [L, conv_dim] projection output (pre-conv), x_dtype
@@ -91,6 +97,7 @@ struct PrefillArgs {
   int num_v_heads;
   int conv_dim;
   int x_pairs;  // bf16 x, 4-byte aligned rows: a thread's two channels are one 32-bit load
+  int gate_raw;  // gate_a / gate_b are the raw projections (RIA_GATE_RAW), else g and beta
 };
 
 // ---------------------------------------------------------------- helpers
@@ -132,9 +139,64 @@ __device__ __forceinline__ void load8(const float* p, float* v) {
 // about a third of its instructions, and the bf16 tile path addresses rows
 // through buffer resources with the row in the scalar offset (146 -> 125 us).
 constexpr int kConvTile = 64;
+static_assert(kConvTile == kChunk, "a conv tile is a chunk: the gate pass takes one per workgroup");
+
+// Gate pass of chunk blockIdx.y (the conv launch's last workgroup column):
+// wave w takes V heads w, w + 4, ..; lane t token t of the chunk.  beta =
+// sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) (qwen36_attention_cache.py:
+// 243-247), or both given; G = the sequential cumulative sum of g inside the
+// chunk (tokens past the prompt add 0); then exp(G_t), exp(G_C - G_t) and
+// exp(G_C) for phase A and the scan.  Off phase A's path, where it was a
+// chain of transcendental and dependent adds on one wave (about 15% of an
+// item) while the other three waited at the barrier.
+__device__ __forceinline__ void prefill_gates(const PrefillArgs& a, float* gsh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cl = blockIdx.y;
+  const int t = (a.chunk0 + cl) * kChunk + lane;
+  const bool ok = t < a.length;
+  float* gw = gsh + wave * kChunk;
+  for (int h = wave; h < a.num_v_heads; h += 4) {
+    float beta = 0.f, g = 0.f;
+    if (ok) {
+      const float ga = a.gate_a[(int64_t)t * a.gate_stride + h], gb = a.gate_b[(int64_t)t * a.gate_stride + h];
+      if (a.gate_raw) {
+        beta = sigmoid_f(gb);
+        g = -expf(a.A_log[h]) * softplus_f(ga + a.dt_bias[h]);
+      } else {
+        beta = gb;
+        g = ga;
+      }
+    }
+    gw[lane] = g;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // lane t adds g_0 .. g_t one at a time, the order of a sequential cumsum
+    // (the masked terms add +0, which leaves the sum unchanged)
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kChunk; i += 4) {
+      const float4 gv = *reinterpret_cast<const float4*>(gw + i);
+      acc += i + 0 <= lane ? gv.x : 0.f;
+      acc += i + 1 <= lane ? gv.y : 0.f;
+      acc += i + 2 <= lane ? gv.z : 0.f;
+      acc += i + 3 <= lane ? gv.w : 0.f;
+    }
+    const float gc = __shfl(acc, kChunk - 1, 64);
+    char* rec = a.rec + ((int64_t)cl * a.num_v_heads + h) * kRecBytes;
+    reinterpret_cast<float4*>(rec + kRecGate)[lane] = float4{beta, acc, expf(acc), expf(gc - acc)};
+    if (lane == 0) *reinterpret_cast<float*>(rec + kRecGl) = expf(gc);
+    __builtin_amdgcn_wave_barrier();  // gw is read by every lane before the next head writes it
+  }
+}
 
 template <int XT>
 __global__ __launch_bounds__(256) void prefill_conv_kernel(PrefillArgs a) {
+  if (blockIdx.x == gridDim.x - 1) {
+    __shared__ __attribute__((aligned(16))) float gsh[4 * kChunk];
+    prefill_gates(a, gsh);
+    return;
+  }
   const int c = 2 * (blockIdx.x * 256 + threadIdx.x);
   if (c >= a.conv_dim) return;
   const int t_begin = a.tok0 + blockIdx.y * kConvTile;
@@ -290,7 +352,7 @@ constexpr int kPrepLdsBytes = kRScal + 4 * 64 * 5;
 static_assert(128 * kKtPitch * 2 <= 2 * kSlot && 64 * 132 * 4 <= 2 * kSlot, "two-slot arrays");
 static_assert(3 * kPrepLdsBytes <= 160 * 1024, "three workgroups per CU");
 
-template <int XT, int GM>
+template <int XT>
 __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(PrefillArgs a) {
   const int cl = blockIdx.x;  // chunk within the segment
   const int h = blockIdx.y;
@@ -316,21 +378,12 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(PrefillArgs a) {
 
   // Step 1: lane (n, g4) of wave w loads token 16w + n, dims 32s + 8g4 .. +8 of
   // q, k and v: the MFMA A-operand order, so no transpose is needed later.
-  // Wave 0's gate inputs (lane t: token t of the chunk) go out first, so
-  // their latency overlaps the rows'.
+  // The row's gates {beta, G, exp(G), exp(G_C - G)} (the conv launch's gate
+  // pass) go out first.
   const int row = 16 * wave + n;
   const int t = t0 + row;
   const bool valid = t < a.length;
-  float gin_a = 0.f, gin_b = 0.f, alog = 0.f, dtb = 0.f;
-  const bool gate_ok = t0 + lane < a.length;
-  if (wave == 0 && gate_ok) {
-    gin_a = a.gate_a[(int64_t)(t0 + lane) * a.gate_stride + h];
-    gin_b = a.gate_b[(int64_t)(t0 + lane) * a.gate_stride + h];
-    if constexpr (GM == RIA_GATE_RAW) {
-      alog = a.A_log[h];
-      dtb = a.dt_bias[h];
-    }
-  }
+  const float4 gt = reinterpret_cast<const float4*>(rec + kRecGate)[row];
   float qv[4][8], kv[4][8];
   uint4 rq[4], rk[4], rv[4];  // the conv outputs (bf16): the MFMA operands and the record's q and k
   {
@@ -360,34 +413,9 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(PrefillArgs a) {
       unpack(rk[s], kv[s]);
     }
   }
-  // Gates and the cumulative decay.
-  if (wave == 0) {
-    float beta = 0.f, g = 0.f;
-    if (gate_ok) {
-      if constexpr (GM == RIA_GATE_RAW) {
-        beta = sigmoid_f(gin_b);
-        g = -expf(alog) * softplus_f(gin_a + dtb);
-      } else {
-        beta = gin_b;
-        g = gin_a;
-      }
-    }
-    beta_s[lane] = beta;
-    G_s[lane] = g;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    // Lane t adds g_0 .. g_t one at a time, the order of a sequential
-    // cumsum (the masked terms add +0, which leaves the sum unchanged).
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < kChunk; i += 4) {
-      const float4 gv = *reinterpret_cast<const float4*>(G_s + i);
-      acc += i + 0 <= lane ? gv.x : 0.f;
-      acc += i + 1 <= lane ? gv.y : 0.f;
-      acc += i + 2 <= lane ? gv.z : 0.f;
-      acc += i + 3 <= lane ? gv.w : 0.f;
-    }
-    G_s[lane] = acc;
+  if (g4 == 0) {
+    beta_s[row] = gt.x;
+    G_s[row] = gt.y;
   }
   // Step 2: l2norm of the q and k rows (a row is spread over the 4 lane groups).
   float sq = 0.f, sk = 0.f;
@@ -404,9 +432,9 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(PrefillArgs a) {
   sk += __shfl_xor(sk, 32, 64);
   const float iq = 1.0f / sqrtf(sq + 1e-6f), ik = 1.0f / sqrtf(sk + 1e-6f);
   lds_barrier();  // G_s, beta_s ready
-  const float eg = expf(G_s[row]);                    // e^{G_t}
-  const float ekl = expf(G_s[kChunk - 1] - G_s[row]);  // e^{G_C - G_t}
-  const float bt = beta_s[row];
+  const float eg = gt.z;   // e^{G_t}
+  const float ekl = gt.w;  // e^{G_C - G_t}
+  const float bt = gt.x;
   // k rows (bf16) into RA; q (bf16) and the per-token factors straight to
   // the record (A-operand order); k^T (bf16) into RB; the rows' factors for
   // the products' epilogues into LDS.
@@ -614,7 +642,6 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(PrefillArgs a) {
       wn_rec[((w * 4 + s) * 2 + 1) * 64 + lane] = lo;
     }
   }
-  if (tid == 0) *reinterpret_cast<float*>(rec + kRecGl) = expf(G_s[kChunk - 1]);
 }
 
 // ---------------------------------------------------------------- phase B
@@ -1005,6 +1032,7 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
   a.gate_stride = gate_row_stride;
   a.A_log = A_log;
   a.dt_bias = dt_bias;
+  a.gate_raw = gate_mode == RIA_GATE_RAW;
   a.out = out;
   a.num_k_heads = num_k_heads;
   a.num_v_heads = num_v_heads;
@@ -1020,15 +1048,12 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
     a.seg_chunks = min(seg_chunks, total_chunks - c0);
     a.tok0 = c0 * kChunk;
     a.seg_tokens = min(a.seg_chunks * kChunk, length - a.tok0);
-    dim3 cgrid((conv_dim / 2 + 255) / 256, (a.seg_tokens + kConvTile - 1) / kConvTile);
+    dim3 cgrid((conv_dim / 2 + 255) / 256 + 1, (a.seg_tokens + kConvTile - 1) / kConvTile);  // + the gate pass
     dim3 pgrid(a.seg_chunks, num_v_heads);
     dim3 sgrid(num_v_heads * (kDim / 16));
 #define RIA_PREFILL_PHASES(XT_)                                                                          \
   hipLaunchKernelGGL((prefill_conv_kernel<XT_>), cgrid, dim3(256), 0, st, a);                           \
-  if (gate_mode == RIA_GATE_RAW)                                                                        \
-    hipLaunchKernelGGL((chunk_prep_kernel<XT_, RIA_GATE_RAW>), pgrid, dim3(256), 0, st, a);      \
-  else                                                                                                  \
-    hipLaunchKernelGGL((chunk_prep_kernel<XT_, RIA_GATE_PRECOMPUTED>), pgrid, dim3(256), 0, st, a)
+  hipLaunchKernelGGL((chunk_prep_kernel<XT_>), pgrid, dim3(256), 0, st, a)
     if (x_dtype == RIA_DT_BF16) {
       RIA_PREFILL_PHASES(RIA_DT_BF16);
     } else if (x_dtype == RIA_DT_F16) {

@@ -244,10 +244,15 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     }
   };
 
-  f32x4 o[16];  // O^T tiles: dims 16 dt + 4 g4 + i, column n
+  // O^T tiles: dims 16 dt + 4 g4 + i, column n; o[16] is the product with an
+  // all-ones V^T tile, every row the sum of the column's probabilities as
+  // the MFMAs weighted V with them (the softmax's normaliser, no VALU adds
+  // and no cross-lane sum)
+  f32x4 o[17];
 #pragma unroll
-  for (int dt = 0; dt < 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
+  for (int dt = 0; dt < 17; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;
+  constexpr uint32_t kOne2 = KVT == RIA_DT_F16 ? 0x3C003C00u : 0x3F803F80u;  // two 16-bit 1.0
 
   // K operand rows of this lane (row n of both score tiles): vector offset of
   // token tile_row_token(m, n) of page tile_row_page(n); dims 32 kd + 8 g4 ..
@@ -293,7 +298,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     sc[1] = kSplit ? acc[1] + acc[3] : acc[1];
   };
 
-  auto load_v = [&](int b, u32x4 (&vop)[16]) {
+  auto load_v = [&](int b, u32x4 (&vop)[17]) {
     const u32x4* slot = slot_of(b);
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) vop[dt] = slot[v_vec + 16 * dt];
@@ -301,8 +306,9 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
 
   // ---- online softmax of block b (log2 units), then O^T += V^T P^T over its 32 keys
   auto softmax_pv = [&](int b, const f32x4 (&sc)[2]) {
-    u32x4 vop[16];
+    u32x4 vop[17];
     load_v(b, vop);
+    vop[16] = u32x4{kOne2, kOne2, kOne2, kOne2};
     __builtin_amdgcn_sched_barrier(0);
     float s[8];
 #pragma unroll
@@ -336,23 +342,21 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
       const bool grow = mx > m_run + 8.0f;
       const float m_new = grow ? mx : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block, where o and l are 0
-      l_run *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 16; ++dt) o[dt] *= alpha;
+      for (int dt = 0; dt < 17; ++dt) o[dt] *= alpha;
       m_run = m_new;
 #pragma unroll
       for (int j = 0; j < 8; ++j) pr[j] = __builtin_amdgcn_exp2f(s[j] - m_run);
     }
-    l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
     u32x4 ph, pl;
     pack(pr, ph, pl, std::false_type{});
     __builtin_amdgcn_sched_barrier(0);
-    // all hi products, then all lo products: 16 MFMAs between dependent ones
+    // all hi products, then all lo products: 17 MFMAs between dependent ones
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) o[dt] = KV::mfma_k32(vop[dt], ph, o[dt]);
+    for (int dt = 0; dt < 17; ++dt) o[dt] = KV::mfma_k32(vop[dt], ph, o[dt]);
     if (kSplit) {
 #pragma unroll
-      for (int dt = 0; dt < 16; ++dt) o[dt] = KV::mfma_k32(vop[dt], pl, o[dt]);
+      for (int dt = 0; dt < 17; ++dt) o[dt] = KV::mfma_k32(vop[dt], pl, o[dt]);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -405,7 +409,7 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
 
   // ---- normalise, stage (the ring is dead once every wave has left the loop), gate, store
   lds_barrier();
-  const float l_tot = swap_sum(swap_sum(l_run, true), false);
+  const float l_tot = o[16][0];
   const float inv = 1.0f / l_tot;  // every valid query sees at least itself
   float* st = stage + (wave * 16 + n) * kStagePitch;
 #pragma unroll

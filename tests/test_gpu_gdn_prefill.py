@@ -2,7 +2,7 @@
 reference's token-by-token recurrence, restated in the oracle.
 
 Covers a ragged last chunk with a non-zero starting state and conv history,
-segmenting (a workspace of one chunk gives the same bits as one pass),
+precomputed gates, segmenting (a workspace of one chunk gives the same bits as one pass),
 bf16 / fp16 outputs (the fp32 read-out rounded once, no row written past the
 prompt),
 prefill followed by decode, and the single-layer 16384-token prefill
@@ -33,16 +33,26 @@ def _oracle_tokens(params, inputs, length, state=None, conv=None):
     return torch.stack(outs), state, conv
 
 
-def _gpu_prefill(dev, params, inputs, length, state0, ring0, pos0, ws_tokens=None, out_dtype=torch.float32):
+def _gpu_prefill(dev, params, inputs, length, state0, ring0, pos0, ws_tokens=None, out_dtype=torch.float32,
+                 precomputed=False):
     state = state0.clone().to(dev)
     ring = ring0.clone().to(dev)
     seg = ws_tokens or length
     ws = torch.empty(K.gdn_prefill_workspace_bytes(16, 32, seg), dtype=torch.uint8, device=dev)
     out = torch.empty((length, 32, 128), dtype=out_dtype, device=dev)
-    K.gdn_prefill(inputs["mixed"][:length, 0].to(dev), state, inputs["a_raw"][:length, 0].to(dev),
-                  inputs["b_raw"][:length, 0].to(dev), out, num_k_heads=16, num_v_heads=32,
-                  conv_weight=params["conv_weight"].to(dev), conv_ring=ring, conv_pos=pos0, workspace=ws,
-                  gate_mode=nat.RIA_GATE_RAW, A_log=params["A_log"].to(dev), dt_bias=params["dt_bias"].to(dev))
+    if precomputed:
+        # g and beta from the oracle's gating (the reference's sigmoid / softplus prologue)
+        gates = [O.gating(inputs["a_raw"][t], inputs["b_raw"][t], params["A_log"], params["dt_bias"])
+                 for t in range(length)]
+        ga = torch.cat([g for _, g in gates]).float().contiguous()
+        gb = torch.cat([b for b, _ in gates]).float().contiguous()
+        gate_kw = dict(gate_mode=nat.RIA_GATE_PRECOMPUTED)
+    else:
+        ga, gb = inputs["a_raw"][:length, 0], inputs["b_raw"][:length, 0]
+        gate_kw = dict(gate_mode=nat.RIA_GATE_RAW, A_log=params["A_log"].to(dev), dt_bias=params["dt_bias"].to(dev))
+    K.gdn_prefill(inputs["mixed"][:length, 0].to(dev), state, ga.to(dev), gb.to(dev), out, num_k_heads=16,
+                  num_v_heads=32, conv_weight=params["conv_weight"].to(dev), conv_ring=ring, conv_pos=pos0,
+                  workspace=ws, **gate_kw)
     torch.cuda.synchronize()
     return out.cpu(), state.cpu(), ring.cpu()
 
@@ -65,6 +75,25 @@ def test_prefill_ragged_chunks_with_history(gpu):
     assert_act_close(got, want, "prefill outputs")
     assert_state_close(state[None], s_want, "final state")
     assert torch.equal(ring_to_window(ring, pos0 + 130), c_want)
+
+
+def test_prefill_precomputed_gates(gpu):
+    """g and beta passed in (RIA_GATE_PRECOMPUTED) instead of derived from the
+    raw projections, over segments of two chunks: the gate pass reads them as
+    given and the cumulative decay restarts in every chunk."""
+    announce("gdn_prefill: precomputed g / beta, 200 tokens, 128-token segments, random state and history")
+    params = W.gdn_layer_params(37)
+    inputs = W.gdn_step_inputs(38, 200, 1)
+    state0, ring0 = _init(39)
+    pos0 = 2
+    got, state, ring = _gpu_prefill(gpu, params, inputs, 200, state0, ring0, pos0, ws_tokens=128, precomputed=True)
+    want, s_want, c_want = _oracle_tokens(params, inputs, 200, state0[None], ring_to_window(ring0, pos0))
+    assert_act_close(got, want, "prefill outputs")
+    assert_state_close(state[None], s_want, "final state")
+    assert torch.equal(ring_to_window(ring, pos0 + 200), c_want)
+    raw, s_raw, _ = _gpu_prefill(gpu, params, inputs, 200, state0, ring0, pos0, ws_tokens=128)
+    assert_act_close(got, raw, "precomputed against raw gates")
+    assert_state_close(state[None], s_raw[None], "precomputed against raw gates, state")
 
 
 def test_prefill_segmenting_is_bit_identical(gpu):

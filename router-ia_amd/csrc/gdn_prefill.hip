@@ -150,7 +150,7 @@ static_assert(kConvTile == kChunk, "a conv tile is a chunk: the gate pass takes 
 // chain of transcendental and dependent adds on one wave (about 15% of an
 // item) while the other three waited at the barrier.
 __device__ __forceinline__ void prefill_gates(const PrefillArgs& a, float* gsh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int cl = blockIdx.y;
   const int t = (a.chunk0 + cl) * kChunk + lane;
   const bool ok = t < a.length;
@@ -356,7 +356,9 @@ template <int XT>
 __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(PrefillArgs a) {
   const int cl = blockIdx.x;  // chunk within the segment
   const int h = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave in a scalar register: the per-wave branches and job loops below are
+  // then scalar
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g4 = lane >> 4;
   const int t0 = (a.chunk0 + cl) * kChunk;  // absolute first token of the chunk
   const int group = a.num_v_heads / a.num_k_heads;
@@ -662,6 +664,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // run on one XCD; id = 32 * cb + h), so its records are fetched once per L2.
   const int h = blockIdx.x % a.num_v_heads;
   const int cb = blockIdx.x / a.num_v_heads;
+  // wave stays in a vector register here, so each record load whose scalar
+  // offset derives from it is issued through a one-pass waterfall loop; with
+  // wave scalar (no loops) the scan measured 446-453 against 417-423 us per
+  // 16k-token layer, bit-identical (the loops pace the 84 KB of loads per
+  // chunk that queue in the CU's vector memory path)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g4 = lane >> 4;
   // Two roles, one wave of each per SIMD (waves w and w + 4 share SIMD w):

@@ -252,13 +252,14 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x));
 
 // A float that rounds to the same bf16 as silu_f(x), for a bf16 value x (a
 // post-conv activation), at a fraction of the accurate form's VALU cost.  For
-// x > -16 the hardware exp2 and reciprocal put y within kSiluTieGuard / 2
-// fp32 ulps of silu_f(x) (most of it from rounding -x log2(e) before exp2,
-// which grows with |x|).  Where y lies more than kSiluTieGuard ulps from a
-// bf16 rounding midpoint (low 16 bits 0x8000) both round to the same bf16;
-// lanes nearer a midpoint, about 1 in 1000, and x <= -16 or NaN take the
-// accurate form.  Checked over all 65536 bf16 inputs.
-constexpr uint32_t kSiluTieGuard = 32;
+// x > -16 the hardware exp2 and reciprocal put y within 14 fp32 ulps of
+// silu_f(x) (measured over every bf16 input; most of it from rounding
+// -x log2(e) before exp2, which grows with |x|: 3 ulps for -2 <= x < 0).
+// Where y lies more than kSiluTieGuard ulps from a bf16 rounding midpoint
+// (low 16 bits 0x8000) both round to the same bf16; lanes nearer a midpoint,
+// about 1 in 1600, and x <= -16 or NaN take the accurate form.  Checked over
+// all 65536 bf16 inputs.
+constexpr uint32_t kSiluTieGuard = 20;
 __device__ __forceinline__ float silu_to_bf16(float x) {
   const float y = x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504f));
   const uint32_t lo = (__float_as_uint(y) & 0xffffu) - (0x8000u - kSiluTieGuard);

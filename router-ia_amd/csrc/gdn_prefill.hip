@@ -354,8 +354,14 @@ static_assert(3 * kPrepLdsBytes <= 160 * 1024, "three workgroups per CU");
 
 template <int XT>
 __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(PrefillArgs a) {
-  const int cl = blockIdx.x;  // chunk within the segment
-  const int h = blockIdx.y;
+  // Heads vary fastest, so a round of workgroups reads a few chunks' whole
+  // rows rather than pieces of every chunk.  With Hv a multiple of 8, x ->
+  // head (Hv / 8) (x % 8) + x / 8 puts consecutive V heads (those sharing a K
+  // head) on one XCD (workgroup ids congruent mod 8 share an XCD), so their
+  // q and k rows are fetched once per L2.
+  const int cl = blockIdx.y;  // chunk within the segment
+  const int x = blockIdx.x;
+  const int h = a.num_v_heads % 8 == 0 ? (a.num_v_heads / 8) * (x % 8) + x / 8 : x;
   // wave in a scalar register: the per-wave branches and job loops below are
   // then scalar
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1056,7 +1062,7 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
     a.tok0 = c0 * kChunk;
     a.seg_tokens = min(a.seg_chunks * kChunk, length - a.tok0);
     dim3 cgrid((conv_dim / 2 + 255) / 256 + 1, (a.seg_tokens + kConvTile - 1) / kConvTile);  // + the gate pass
-    dim3 pgrid(a.seg_chunks, num_v_heads);
+    dim3 pgrid(num_v_heads, a.seg_chunks);
     dim3 sgrid(num_v_heads * (kDim / 16));
 #define RIA_PREFILL_PHASES(XT_)                                                                          \
   hipLaunchKernelGGL((prefill_conv_kernel<XT_>), cgrid, dim3(256), 0, st, a);                           \

@@ -439,7 +439,8 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(PrefillArgs a) {
   sk += __shfl_xor(sk, 16, 64);
   sk += __shfl_xor(sk, 32, 64);
   const float iq = 1.0f / sqrtf(sq + 1e-6f), ik = 1.0f / sqrtf(sk + 1e-6f);
-  lds_barrier();  // G_s, beta_s ready
+  // No barrier here: beta_s and G_s are first read in step 3, after the next
+  // one, and until then each wave writes only its own rows.
   const float eg = gt.z;   // e^{G_t}
   const float ekl = gt.w;  // e^{G_C - G_t}
   const float bt = gt.x;

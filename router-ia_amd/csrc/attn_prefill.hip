@@ -427,7 +427,8 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     float g[4], y[4];
     load_act4<AT>(a.gate, (int64_t)t * a.gate_stride + (int64_t)head * kAttnHeadDim + d, g);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = mul_rn(row[i], sigmoid_f(g[i]));
+    for (int i = 0; i < 4; ++i)
+      y[i] = AT == RIA_DT_BF16 ? gate_mul_to_bf16(row[i], g[i]) : mul_rn(row[i], sigmoid_f(g[i]));
     store_act4<AT>(a.out, ((int64_t)t * a.num_q_heads + head) * kAttnHeadDim + d, y);
   }
 }

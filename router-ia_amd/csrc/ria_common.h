@@ -267,6 +267,21 @@ __device__ __forceinline__ float silu_to_bf16(float x) {
   return y;
 }
 
+// x sigmoid(g) as a float that rounds to the same bf16 as mul_rn(x,
+// sigmoid_f(g)), for a bf16 gate g and any fp32 x.  For g > -16 the
+// hardware exp2 and reciprocal put the sigmoid within 12 fp32 ulps of
+// sigmoid_f(g) (measured over every bf16 gate), so the two products lie
+// within 25 ulps of each other; where the product lies more than
+// kGateTieGuard ulps from a bf16 rounding midpoint both round to the same
+// bf16, and lanes nearer one, g <= -16 or NaN take the accurate form.
+constexpr uint32_t kGateTieGuard = 32;
+__device__ __forceinline__ float gate_mul_to_bf16(float x, float g) {
+  const float y = mul_rn(x, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504f)));
+  const uint32_t lo = (__float_as_uint(y) & 0xffffu) - (0x8000u - kGateTieGuard);
+  if (lo <= 2 * kGateTieGuard || !(g > -16.0f)) return mul_rn(x, sigmoid_f(g));
+  return y;
+}
+
 // RMSNorm pieces shared by the standalone and the fused forms.  eps is the
 // model's 1e-6 (qwen36_op_probe.py:32, qwen36_gated_norm_probe.py:16).
 constexpr float kNormEps = 1e-6f;

@@ -423,7 +423,8 @@ __global__ __launch_bounds__(kPrefillThreads) __attribute__((amdgpu_waves_per_eu
     const int t = 16 * qb + r;
     if (t >= a.length) break;
     const int d = 4 * lane;
-    const float* row = stage + (wave * 16 + r) * kStagePitch + d;
+    // one 16-byte read of the staged row (element reads would hit 4-way bank conflicts)
+    const f32x4 row = *reinterpret_cast<const f32x4*>(stage + (wave * 16 + r) * kStagePitch + d);
     float g[4], y[4];
     load_act4<AT>(a.gate, (int64_t)t * a.gate_stride + (int64_t)head * kAttnHeadDim + d, g);
 #pragma unroll

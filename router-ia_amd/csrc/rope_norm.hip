@@ -122,11 +122,10 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
   const int64_t xo = t * a.x_stride + hoff;
   const int64_t oo = t * a.out_stride + hoff;
   const int64_t zo = t * a.z_stride + hoff;
-  auto finish = [&](int c, const float (&v)[4], float rs, f32x4 w) {
+  // z: the gate's 4 values at c (gated), loaded by the caller
+  auto finish = [&](int c, const float (&v)[4], float rs, f32x4 w, const float (&z)[4]) {
     float y[4];
     if constexpr (GATED) {
-      float z[4];
-      load_act4_dt(a.z, zo + c, a.z_dtype, z);
 #pragma unroll
       for (int j = 0; j < 4; ++j) y[j] = gated_norm_elem<XT>(v[j], rs, w[j], z[j]);
     } else {
@@ -140,13 +139,17 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
     // dim == 4 RL NCH: the lane's NCH chunks are loaded at once and kept in
     // registers for the second pass (the squares are summed in the same order
     // as the loop below, so both give the same bits)
-    float v[NCH][4];
-    f32x4 w[NCH];  // the weights too, so their loads overlap the reduction
+    float v[NCH][4], z[NCH][4] = {};
+    f32x4 w[NCH];  // the weights and the gate too, so their loads overlap the reduction
     if (ok) {
 #pragma unroll
       for (int q = 0; q < NCH; ++q) load_act4<XT>(a.x, xo + 4 * li + 4 * RL * q, v[q]);
 #pragma unroll
       for (int q = 0; q < NCH; ++q) w[q] = *reinterpret_cast<const f32x4*>(a.weight + 4 * li + 4 * RL * q);
+      if constexpr (GATED) {
+#pragma unroll
+        for (int q = 0; q < NCH; ++q) load_act4_dt(a.z, zo + 4 * li + 4 * RL * q, a.z_dtype, z[q]);
+      }
 #pragma unroll
       for (int q = 0; q < NCH; ++q)
 #pragma unroll
@@ -157,7 +160,7 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
     if (!ok) return;
     const float rs = rms_scale(ss, a.dim, a.eps);
 #pragma unroll
-    for (int q = 0; q < NCH; ++q) finish(4 * li + 4 * RL * q, v[q], rs, w[q]);
+    for (int q = 0; q < NCH; ++q) finish(4 * li + 4 * RL * q, v[q], rs, w[q], z[q]);
   } else {
     if (ok) {
       for (int c = 4 * li; c < a.dim; c += 4 * RL) {
@@ -172,9 +175,10 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
     if (!ok) return;
     const float rs = rms_scale(ss, a.dim, a.eps);
     for (int c = 4 * li; c < a.dim; c += 4 * RL) {
-      float v[4];
+      float v[4], z[4] = {};
       load_act4<XT>(a.x, xo + c, v);
-      finish(c, v, rs, *reinterpret_cast<const f32x4*>(a.weight + c));
+      if constexpr (GATED) load_act4_dt(a.z, zo + c, a.z_dtype, z);
+      finish(c, v, rs, *reinterpret_cast<const f32x4*>(a.weight + c), z);
     }
   }
 }

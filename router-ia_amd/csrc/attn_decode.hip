@@ -179,9 +179,8 @@ __global__ __launch_bounds__(256) void kv_append_page_kernel(AppendArgs a) {
   const int s0 = pg * kPageTokens;
   const int t_lo = max(a.pos_scalar, s0) - s0, t_hi = min(a.pos_scalar + a.seq_len, s0 + kPageTokens) - s0;
   const int phys = a.page_table[pg];
-  if (phys < 0 || phys >= a.num_pages) return;  // host guarantees allocation; never write out of the pool
-  const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
   __shared__ float k_s[kPageTokens][kAttnHeadDim];
+  __shared__ float cos_s[kPageTokens][32], sin_s[kPageTokens][32];  // the page's rotary table (rope_dim <= 64)
   __shared__ float ss_s[kPageTokens][4];
   __shared__ __attribute__((aligned(16))) uint16_t kt_s[kTileElems];
   __shared__ __attribute__((aligned(16))) uint16_t kt16_s[kTileElems];  // the fp16 copy (stage)
@@ -195,6 +194,24 @@ __global__ __launch_bounds__(256) void kv_append_page_kernel(AppendArgs a) {
     const float vx = load_act<VT>(a.v, r * a.v_stride + kvh * kAttnHeadDim + d);
     kv[i] = in ? kx : 0.f;
     vv[i] = in ? vx : 0.f;
+  }
+  // checked after the row loads are out, so they do not wait for the entry
+  if (phys < 0 || phys >= a.num_pages) return;  // host guarantees allocation; never write out of the pool
+  const int64_t tile = (int64_t)phys * a.num_kv_heads + kvh;
+  // cos / sin of the page's 16 positions x 32 frequencies, two per thread
+  // (rope_elem's angle and functions), instead of 32 on each of wave 0's
+  // lanes while the other waves wait
+  const bool rope_table = a.rope_dim <= 64;
+  if (rope_table) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = 8 * h + (d >> 5), f = d & 31;
+      if (2 * f < a.rope_dim) {
+        const float ang = mul_rn(static_cast<float>(s0 + i), a.inv_freq[f]);
+        cos_s[i][f] = cosf(ang);
+        sin_s[i][f] = sinf(ang);
+      }
+    }
   }
   if (a.norm_w) {  // per token: one sum of squares over the 256 dims, waves in order
     const float wn = a.norm_w[d];
@@ -217,7 +234,14 @@ __global__ __launch_bounds__(256) void kv_append_page_kernel(AppendArgs a) {
 #pragma unroll
   for (int i = 0; i < kPageTokens; ++i) {
     const float partner = d < a.rope_dim ? k_s[i][pd] : 0.f;
-    const float kr = rope_elem(kv[i], partner, d, a.rope_dim, static_cast<float>(s0 + i), a.inv_freq);
+    float kr;
+    if (rope_table) {
+      const int f = d < half ? d : d - half;
+      kr = d < a.rope_dim ? add_rn(mul_rn(kv[i], cos_s[i][f]), mul_rn(d < half ? -partner : partner, sin_s[i][f]))
+                          : kv[i];
+    } else {
+      kr = rope_elem(kv[i], partner, d, a.rope_dim, static_cast<float>(s0 + i), a.inv_freq);
+    }
     kt_s[k_tile_offset(i, d)] = Kv16<KVT>::from_f32(kr);
     if (a.stage_k) kt16_s[k_tile_offset(i, d)] = Kv16<RIA_DT_F16>::from_f32(kr);
   }

@@ -26,7 +26,8 @@
 //                         columns), sequential over chunks, waves in two
 //                         roles (state, read-out); the fp32 state block
 //                         stays in LDS.
-//   conv_ring_tail_kernel writes the last inputs into the conv ring.
+//   (phase A of the prompt's last chunk also writes the last inputs into the
+//   conv ring.)
 //
 // MFMA precision: products run on bf16 MFMA 16x16x32.  The conv outputs q, k
 // and v are bf16 values, exact operands, and enter the products as they are
@@ -269,17 +270,6 @@ __global__ __launch_bounds__(256) void prefill_conv_kernel(PrefillArgs a) {
       }
     }
   }
-}
-
-// The inputs of the last min(L, 4) tokens go to their ring slots (after every
-// conv tile has read the old history).
-template <int XT>
-__global__ __launch_bounds__(256) void conv_ring_tail_kernel(PrefillArgs a) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= a.conv_dim) return;
-  for (int t = max(0, a.length - 4); t < a.length; ++t)
-    a.conv_ring[((a.n0 + t) & 3) * a.conv_dim + c] =
-        f32_to_bf16_bits(load_act<XT>(a.x, (int64_t)t * a.x_stride + c));
 }
 
 
@@ -650,6 +640,16 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(PrefillArgs a) {
       wn_rec[((w * 4 + s) * 2 + 0) * 64 + lane] = hi;
       wn_rec[((w * 4 + s) * 2 + 1) * 64 + lane] = lo;
     }
+  }
+  // The conv ring takes the inputs of the prompt's last min(L, 4) tokens:
+  // the workgroups of the last segment's last chunk share the channels (the
+  // conv launches, the only readers of its old contents, have finished).
+  if (a.tok0 + a.seg_tokens == a.length && cl == a.seg_chunks - 1) {
+    const int per = (a.conv_dim + gridDim.x - 1) / gridDim.x;
+    const int c_end = min(x * per + per, a.conv_dim);
+    for (int t = max(0, a.length - 4); t < a.length; ++t)
+      for (int c = x * per + tid; c < c_end; c += 256)
+        a.conv_ring[((a.n0 + t) & 3) * a.conv_dim + c] = f32_to_bf16_bits(load_act<XT>(a.x, (int64_t)t * a.x_stride + c));
   }
 }
 
@@ -1103,12 +1103,5 @@ extern "C" int ria_gdn_prefill(int length, int num_k_heads, int num_v_heads, con
       if (rc != RIA_OK) return rc;
     }
   }
-  dim3 rgrid((conv_dim + 255) / 256);
-  if (x_dtype == RIA_DT_BF16)
-    hipLaunchKernelGGL((conv_ring_tail_kernel<RIA_DT_BF16>), rgrid, dim3(256), 0, st, a);
-  else if (x_dtype == RIA_DT_F16)
-    hipLaunchKernelGGL((conv_ring_tail_kernel<RIA_DT_F16>), rgrid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((conv_ring_tail_kernel<RIA_DT_F32>), rgrid, dim3(256), 0, st, a);
-  return check_launch("ria_gdn_prefill (conv ring)");
+  return RIA_OK;
 }
